@@ -1,0 +1,147 @@
+#!/usr/bin/env python3
+"""Benchmark of the three-layer multi-head GAT forward on one MI355X.
+
+A step is one full forward D_in -> 8x32 -> 8x32 -> 1xC over the whole graph,
+inputs resident in HBM.  Default workload: the 64.3M-edge power-law graph
+(2,449,029 nodes, 100 -> 8x32 -> 8x32 -> 1x47, bf16 storage with FP32
+softmax/accumulation).  Prints ONE JSON line (rank 0).
+
+  python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload large|arxiv|smoke]
+                  [--precision bf16|fp32] [--no-cpu-baseline]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT / "gat-tfs_amd"))
+
+METRIC = "3-layer GAT fwd latency (ms), GEdge/s & % HBM roofline, 2.5M/64M-edge graphs"
+HBM_PEAK_GBS = 8000.0
+MFMA_BF16_PEAK_TFLOPS = 2500.0
+
+
+def agg_bytes(n, e, heads, dim, s_z, s_out):
+    """Algorithmic bytes of one transform-first aggregation launch: rowptr,
+    col, R gathers (K floats per edge), L/M/den per node, the gathered Z rows
+    and the output rows."""
+    return 8 * (n + 1) + 4 * e + 4 * heads * e + 4 * heads * n + e * heads * dim * s_z + n * heads * dim * s_out
+
+
+def cpu_baseline(w, row, col, x, model, precision, threads):
+    """The oracle's B0 restatement (standard_bf16 / standard_fp32 semantics,
+    baseline/src/baseline_standard.cpp) on the host cores: one untimed warm-up
+    layer, then one timed three-layer forward."""
+    sys.path.insert(0, str(ROOT))
+    import oracle
+
+    bf16 = precision == "bf16"
+    wq = [oracle.quantize_bf16(p["w"]) if bf16 else None for p in model]
+    oracle.standard_layer(row, col, x, model[0], True, bf16, threads, wq[0])  # warm-up (page-in)
+    t0 = time.perf_counter()
+    h = x
+    for l, p in enumerate(model):
+        st, _ = oracle.standard_layer(row, col, h, p, l < 2, bf16, threads, wq[l])
+        h = st["out"]
+    dt = time.perf_counter() - t0
+    e = int(row[-1])
+    return {"value": round(3 * e / dt / 1e9, 6), "unit": "GEdge/s", "cores": threads, "kind": "port",
+            "sample": f"full {w.name} graph, 1 three-layer B0 forward ({'standard_bf16' if bf16 else 'standard_fp32'}) "
+                      f"after a 1-layer warm-up, {dt * 1e3:.1f} ms",
+            "ms_per_forward": round(dt * 1e3, 3)}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--workload", default="large")
+    ap.add_argument("--precision", default="bf16", choices=["bf16", "fp32"])
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-threads", type=int, default=int(os.environ.get("OMP_NUM_THREADS", "0") or 0))
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path (run with --gpus 1).", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    import gatgpu
+    from gatgpu import inputs
+
+    w = inputs.WORKLOADS[args.workload]
+    t0 = time.perf_counter()
+    row, col = w.graph()
+    x = w.features()
+    model = w.model()
+    gen_s = time.perf_counter() - t0
+    n, e = w.n, int(row[-1])
+    prec = gatgpu.BF16 if args.precision == "bf16" else gatgpu.FP32
+
+    ctx = gatgpu.Context(0)
+    ctx.set_graph(row, col)
+    ctx.set_model(model)
+    ctx.set_input(x)
+    print(f"# workload {w.name}: N={n} E={e} gen {gen_s:.1f}s", file=sys.stderr, flush=True)
+
+    for _ in range(args.warmup):
+        ctx.model_forward(prec, gatgpu.AUTO, want_logits=False, timed=False)
+    torch.cuda.synchronize()
+    ctx.synchronize()
+    step_ms, layer_times = [], []
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        _, times, total = ctx.model_forward(prec, gatgpu.AUTO, want_logits=False, timed=True)
+        step_ms.append(total)
+        layer_times.append(times)
+    ctx.synchronize()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms = float(np.mean(step_ms))  # HIP-event model time (first kernel of layer 1 to last of layer 3)
+    value = 3 * e / (ms * 1e-3) / 1e9
+
+    # Dominant kernel: the layer-2 aggregation (fused prescan/softmax/SpMM/ELU), 8x32 heads.
+    s_z = 2 if prec == gatgpu.BF16 else 4
+    L2 = model[1]
+    agg_ms = float(np.mean([t[1]["aggregate_ms"] for t in layer_times]))
+    b2 = agg_bytes(n, e, L2["heads"], L2["dim"], s_z, s_z)
+    achieved = b2 / (agg_ms * 1e-3) / 1e9
+    per_layer = [{k: round(float(np.mean([t[l][k] for t in layer_times])), 4)
+                  for k in ("convert_ms", "projection_ms", "aggregate_ms", "total_ms")} for l in range(3)]
+    out = {
+        "metric": METRIC,
+        "value": round(value, 4),
+        "unit": "GEdge/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16" if prec == gatgpu.BF16 else "f32",
+        "data": "synthetic",
+        "config": {"workload": f"{w.name}: 3-layer GAT {w.din}->{w.heads}x{w.dim}->{w.heads}x{w.dim}->1x{w.classes}, "
+                               f"N={n}, E={e} (incl. self-loops), max in-degree {int(np.diff(row).max())}",
+                   "precision": args.precision, "wall_ms_per_step": round(wall / args.steps * 1e3, 4),
+                   "layers": per_layer},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "layer-2 aggregation", "algorithmic_bytes": int(b2), "avg_ms": round(agg_ms, 4)},
+    }
+    ctx.close()
+    if not args.no_cpu_baseline:
+        threads = args.cpu_threads or os.cpu_count()
+        out["cpu_baseline"] = cpu_baseline(w, row, col, x, model, args.precision, threads)
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

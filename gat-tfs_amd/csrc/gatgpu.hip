@@ -1,0 +1,579 @@
+// C ABI of the gfx950 GAT forward: context, device buffers, layer and model
+// orchestration, HIP-event stage timing.  Declarations: include/gatgpu.h.
+#include "gatgpu.h"
+
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "internal.hpp"
+
+using namespace gatgpu;
+
+namespace {
+
+std::string g_create_error;  // message for failures before a context exists
+
+struct DevBuf {
+    void* p = nullptr;
+    size_t bytes = 0;
+    DevBuf() = default;
+    DevBuf(const DevBuf&) = delete;
+    DevBuf& operator=(const DevBuf&) = delete;
+    ~DevBuf() { release(); }
+    void release() {
+        if (p) (void)hipFree(p);
+        p = nullptr;
+        bytes = 0;
+    }
+    // Grows to at least `b` bytes; contents are not preserved.
+    hipError_t ensure(size_t b) {
+        if (b <= bytes && p) return hipSuccess;
+        release();
+        if (b == 0) b = 1;
+        hipError_t e = hipMalloc(&p, b);
+        if (e == hipSuccess) bytes = b;
+        else p = nullptr;
+        return e;
+    }
+    template <class T>
+    T* as() const {
+        return static_cast<T*>(p);
+    }
+};
+
+struct LayerState {
+    bool set = false;
+    int in = 0, heads = 0, dim = 0;
+    std::vector<float> w_host;
+    DevBuf w32, wq32, al, ar, blr;
+    DevBuf z32, zbf, zscratch, left, right, mx, den, out32, outbf, in32, inbf;
+    // What the last forward of this layer produced.
+    bool ran = false, z_valid = false, out32_valid = false, outbf_valid = false;
+    int precision = -1;
+    int width() const { return heads * dim; }
+};
+
+}  // namespace
+
+struct gatgpu_ctx {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    std::string err;
+    // graph and schedule
+    bool graph = false;
+    uint64_t n = 0, e = 0;
+    DevBuf row, col, keys_a, keys_b, vals_a, vals_b, hist, scan_tmp, prow, pcol, small;
+    uint32_t* sorted_deg = nullptr;
+    uint32_t* perm = nullptr;
+    uint64_t neighbor_steps = 0;
+    uint32_t max_degree = 0;
+    RowBins bins;
+    // input
+    bool input = false;
+    int din = 0;
+    DevBuf x32, xbf;
+    LayerState L[3];
+    // options (in-degree thresholds)
+    uint32_t small_max = 0;          // rows <= this share a wave (0: off)
+    uint32_t block_min = 512;        // rows >= this take a block
+    uint32_t split_min = 0xffffffffu;  // rows >= this are split over blocks
+    uint32_t split_chunk = 2048;
+    hipEvent_t ev[16] = {};
+};
+
+namespace {
+
+int fail(gatgpu_ctx* c, int code, const std::string& msg) {
+    if (c) c->err = msg;
+    else g_create_error = msg;
+    return code;
+}
+int hip_fail(gatgpu_ctx* c, const char* what, hipError_t e) {
+    return fail(c, e == hipErrorOutOfMemory ? GATGPU_ENOMEM : GATGPU_EDEVICE,
+                std::string(what) + ": " + hipGetErrorString(e));
+}
+#define HIPCHECK(ctx, expr)                                         \
+    do {                                                            \
+        hipError_t _e = (expr);                                     \
+        if (_e != hipSuccess) return hip_fail((ctx), #expr, _e);    \
+    } while (0)
+
+bool mul_overflows(uint64_t a, uint64_t b) { return b && a > UINT64_MAX / b; }
+
+bool all_finite(const float* p, uint64_t count, uint64_t* bad) {
+    for (uint64_t i = 0; i < count; ++i)
+        if (!std::isfinite(p[i])) {
+            *bad = i;
+            return false;
+        }
+    return true;
+}
+
+int bind(gatgpu_ctx* c) {
+    HIPCHECK(c, hipSetDevice(c->device));
+    return GATGPU_OK;
+}
+
+// Sorted-position boundaries of the degree bins.
+int compute_bins(gatgpu_ctx* c) {
+    uint32_t thr[3] = {c->small_max, c->block_min ? c->block_min - 1 : 0,
+                       c->split_min ? c->split_min - 1 : 0};
+    // small (0) disables the shared-wave bin; block_min 0 means every row takes a block.
+    HIPCHECK(c, c->small.ensure(64));
+    // small[]: [0,4) max degree, [8,16) neighbor steps, [16,28) thresholds, [32,56) positions
+    uint32_t* dthr = reinterpret_cast<uint32_t*>(c->small.as<char>() + 16);
+    uint64_t* dpos = reinterpret_cast<uint64_t*>(c->small.as<char>() + 32);
+    HIPCHECK(c, hipMemcpyAsync(dthr, thr, sizeof(thr), hipMemcpyHostToDevice, c->stream));
+    HIPCHECK(c, launch_count_le(c->sorted_deg, c->n, dthr, 3, dpos, c->stream));
+    uint64_t pos[3];
+    HIPCHECK(c, hipMemcpyAsync(pos, dpos, sizeof(pos), hipMemcpyDeviceToHost, c->stream));
+    HIPCHECK(c, hipStreamSynchronize(c->stream));
+    RowBins b;
+    b.n = c->n;
+    b.small_end = c->small_max ? pos[0] : 0;
+    b.block_begin = c->block_min ? pos[1] : 0;
+    b.split_begin = c->split_min ? pos[2] : 0;
+    if (b.block_begin < b.small_end) b.block_begin = b.small_end;
+    if (b.split_begin < b.block_begin) b.split_begin = b.block_begin;
+    c->bins = b;
+    return GATGPU_OK;
+}
+
+int build_schedule(gatgpu_ctx* c) {
+    const uint64_t n = c->n;
+    HIPCHECK(c, c->keys_a.ensure(n * 4));
+    HIPCHECK(c, c->keys_b.ensure(n * 4));
+    HIPCHECK(c, c->vals_a.ensure(n * 4));
+    HIPCHECK(c, c->vals_b.ensure(n * 4));
+    HIPCHECK(c, c->hist.ensure(radix_tile_hist_elems(n) * 4));
+    HIPCHECK(c, c->scan_tmp.ensure(scan_tmp_bytes(n)));
+    HIPCHECK(c, c->small.ensure(64));
+    uint32_t* dmax = c->small.as<uint32_t>();
+    HIPCHECK(c, hipMemsetAsync(dmax, 0, 4, c->stream));
+    HIPCHECK(c, launch_degrees_and_ids(c->row.as<uint64_t>(), c->keys_a.as<uint32_t>(),
+                                       c->vals_a.as<uint32_t>(), n, dmax, c->stream));
+    uint32_t maxdeg = 0;
+    HIPCHECK(c, hipMemcpyAsync(&maxdeg, dmax, 4, hipMemcpyDeviceToHost, c->stream));
+    HIPCHECK(c, hipStreamSynchronize(c->stream));
+    c->max_degree = maxdeg;
+    int bits = 0;
+    while (bits < 32 && (maxdeg >> bits)) ++bits;
+    const int passes = bits == 0 ? 1 : (bits + 7) / 8;
+    HIPCHECK(c, radix_sort_by_degree(c->keys_a.as<uint32_t>(), c->vals_a.as<uint32_t>(),
+                                     c->keys_b.as<uint32_t>(), c->vals_b.as<uint32_t>(),
+                                     c->hist.as<uint32_t>(), n, passes, c->scan_tmp.p, c->stream,
+                                     &c->sorted_deg, &c->perm));
+    HIPCHECK(c, c->prow.ensure((n + 1) * 8));
+    HIPCHECK(c, c->pcol.ensure(c->e * 4));
+    HIPCHECK(c, exclusive_scan_u32_to_u64(c->sorted_deg, c->prow.as<uint64_t>(), n, c->scan_tmp.p,
+                                          c->stream));
+    HIPCHECK(c, hipMemcpyAsync(c->prow.as<uint64_t>() + n, &c->e, 8, hipMemcpyHostToDevice, c->stream));
+    HIPCHECK(c, launch_permute_cols(c->row.as<uint64_t>(), c->col.as<uint32_t>(), c->perm,
+                                    c->prow.as<uint64_t>(), c->pcol.as<uint32_t>(), n, c->e, c->stream));
+    uint64_t* dsteps = reinterpret_cast<uint64_t*>(c->small.as<char>() + 8);
+    HIPCHECK(c, hipMemsetAsync(dsteps, 0, 8, c->stream));
+    HIPCHECK(c, launch_neighbor_steps(c->sorted_deg, n, dsteps, c->stream));
+    HIPCHECK(c, hipMemcpyAsync(&c->neighbor_steps, dsteps, 8, hipMemcpyDeviceToHost, c->stream));
+    HIPCHECK(c, hipStreamSynchronize(c->stream));
+    return compute_bins(c);
+}
+
+float ms_between(hipEvent_t a, hipEvent_t b) {
+    float ms = 0.0f;
+    if (hipEventElapsedTime(&ms, a, b) != hipSuccess) return 0.0f;
+    return ms;
+}
+
+// Runs layer l on the device.  ev_base: first of 4 events (start, after
+// convert, after projection, after aggregate) or -1 for no timing.
+int run_layer(gatgpu_ctx* c, int l, int precision, int dataflow, bool hidden, const float* host_input,
+              int ev_base) {
+    LayerState& Ls = c->L[l];
+    const uint64_t n = c->n;
+    const int K = Ls.heads, dim = Ls.dim, W = Ls.width(), D = Ls.in;
+    if (dataflow == GATGPU_AGGREGATE_FIRST)
+        return fail(c, GATGPU_EINVAL, "aggregate-first dataflow is not available in this build");
+    // ---- input (explicit host input is uploaded before the timed region)
+    const float* src32 = nullptr;
+    const uint16_t* srcbf = nullptr;
+    if (host_input) {
+        HIPCHECK(c, Ls.in32.ensure(n * D * 4));
+        HIPCHECK(c, hipMemcpyAsync(Ls.in32.p, host_input, n * D * 4, hipMemcpyHostToDevice, c->stream));
+        src32 = Ls.in32.as<float>();
+    } else if (l == 0) {
+        if (!c->input) return fail(c, GATGPU_ESTATE, "node features not set");
+        if (c->din != D) return fail(c, GATGPU_EINVAL, "layer 0 input width differs from the features");
+        src32 = c->x32.as<float>();
+    } else {
+        LayerState& P = c->L[l - 1];
+        if (!P.ran || P.precision != precision)
+            return fail(c, GATGPU_ESTATE, "previous layer has no output in this precision");
+        if (P.width() != D) return fail(c, GATGPU_EINVAL, "layer input width differs from the previous output");
+        if (precision == GATGPU_BF16 && P.outbf_valid) srcbf = P.outbf.as<uint16_t>();
+        else if (P.out32_valid) src32 = P.out32.as<float>();
+        else return fail(c, GATGPU_ESTATE, "previous layer output missing");
+    }
+    // ---- outputs
+    HIPCHECK(c, Ls.left.ensure(n * K * 4));
+    HIPCHECK(c, Ls.right.ensure(n * K * 4));
+    HIPCHECK(c, Ls.mx.ensure(n * K * 4));
+    HIPCHECK(c, Ls.den.ensure(n * K * 4));
+    const bool bf16 = precision == GATGPU_BF16;
+    const bool want_outbf = bf16 && hidden;
+    if (want_outbf) HIPCHECK(c, Ls.outbf.ensure(n * W * 2));
+    else HIPCHECK(c, Ls.out32.ensure(n * W * 4));
+    if (bf16) {
+        HIPCHECK(c, Ls.zbf.ensure(n * W * 2));
+        HIPCHECK(c, Ls.zscratch.ensure(n * W * 4));
+    } else {
+        HIPCHECK(c, Ls.z32.ensure(n * W * 4));
+    }
+    if (bf16 && src32) HIPCHECK(c, Ls.inbf.ensure(n * D * 2));
+    if (ev_base >= 0) HIPCHECK(c, hipEventRecord(c->ev[ev_base], c->stream));
+    // ---- convert (bf16 path, FP32 source only; a bf16 source was rounded in
+    // the previous layer's epilogue, which equals convert() of that output)
+    if (bf16 && src32) {
+        HIPCHECK(c, launch_to_bf16(src32, Ls.inbf.as<uint16_t>(), n * D, c->stream));
+        srcbf = Ls.inbf.as<uint16_t>();
+        src32 = nullptr;
+    }
+    if (ev_base >= 0) HIPCHECK(c, hipEventRecord(c->ev[ev_base + 1], c->stream));
+    // ---- projection + L/R
+    HIPCHECK(c, launch_projection(src32, srcbf, bf16 ? Ls.wq32.as<float>() : Ls.w32.as<float>(), n, D, K,
+                                  dim, Ls.al.as<float>(), Ls.ar.as<float>(), bf16 ? nullptr : Ls.z32.as<float>(),
+                                  bf16 ? Ls.zbf.as<uint16_t>() : nullptr, Ls.left.as<float>(),
+                                  Ls.right.as<float>(), Ls.zscratch.as<float>(), c->stream));
+    if (ev_base >= 0) HIPCHECK(c, hipEventRecord(c->ev[ev_base + 2], c->stream));
+    // ---- fused prescan + softmax + aggregation + normalise + ELU
+    AggArgs a{};
+    a.prow = c->prow.as<uint64_t>();
+    a.pcol = c->pcol.as<uint32_t>();
+    a.perm = c->perm;
+    a.left = Ls.left.as<float>();
+    a.right = Ls.right.as<float>();
+    a.feat = bf16 ? static_cast<const void*>(Ls.zbf.p) : Ls.z32.p;
+    a.feat_bf16 = bf16;
+    a.heads = K;
+    a.dim = dim;
+    a.hidden = hidden;
+    a.mx = Ls.mx.as<float>();
+    a.den = Ls.den.as<float>();
+    a.out32 = want_outbf ? nullptr : Ls.out32.as<float>();
+    a.outbf = want_outbf ? Ls.outbf.as<uint16_t>() : nullptr;
+    a.n = c->n;
+    a.e = c->e;
+    HIPCHECK(c, launch_aggregate_tf(a, c->bins, c->split_chunk, c->stream));
+    if (ev_base >= 0) HIPCHECK(c, hipEventRecord(c->ev[ev_base + 3], c->stream));
+    Ls.ran = true;
+    Ls.precision = precision;
+    Ls.z_valid = true;
+    Ls.out32_valid = !want_outbf;
+    Ls.outbf_valid = want_outbf;
+    return GATGPU_OK;
+}
+
+void fill_times(gatgpu_ctx* c, int ev_base, gatgpu_times* t) {
+    std::memset(t, 0, sizeof(*t));
+    t->convert_ms = ms_between(c->ev[ev_base], c->ev[ev_base + 1]);
+    t->projection_ms = ms_between(c->ev[ev_base + 1], c->ev[ev_base + 2]);
+    t->aggregate_ms = ms_between(c->ev[ev_base + 2], c->ev[ev_base + 3]);
+    t->total_ms = ms_between(c->ev[ev_base], c->ev[ev_base + 3]);
+}
+
+int check_ctx(gatgpu_ctx* c) {
+    if (!c) return fail(nullptr, GATGPU_EINVAL, "null context");
+    return bind(c);
+}
+
+}  // namespace
+
+extern "C" {
+
+int gatgpu_create(int device, gatgpu_ctx** out) {
+    if (!out) return fail(nullptr, GATGPU_EINVAL, "null output pointer");
+    *out = nullptr;
+    int count = 0;
+    if (hipGetDeviceCount(&count) != hipSuccess || count == 0)
+        return fail(nullptr, GATGPU_ENODEV, "no HIP device");
+    if (device < 0 || device >= count) return fail(nullptr, GATGPU_ENODEV, "device ordinal out of range");
+    hipDeviceProp_t prop;
+    if (hipGetDeviceProperties(&prop, device) != hipSuccess)
+        return fail(nullptr, GATGPU_ENODEV, "cannot query device");
+    if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+        return fail(nullptr, GATGPU_ENODEV, std::string("device is ") + prop.gcnArchName + ", need gfx950");
+    auto* c = new (std::nothrow) gatgpu_ctx;
+    if (!c) return fail(nullptr, GATGPU_ENOMEM, "host allocation failed");
+    c->device = device;
+    if (hipSetDevice(device) != hipSuccess || hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking) != hipSuccess) {
+        delete c;
+        return fail(nullptr, GATGPU_EDEVICE, "cannot create stream");
+    }
+    for (auto& e : c->ev)
+        if (hipEventCreate(&e) != hipSuccess) {
+            gatgpu_destroy(c);
+            return fail(nullptr, GATGPU_EDEVICE, "cannot create events");
+        }
+    *out = c;
+    return GATGPU_OK;
+}
+
+int gatgpu_destroy(gatgpu_ctx* c) {
+    if (!c) return GATGPU_OK;
+    (void)hipSetDevice(c->device);
+    if (c->stream) (void)hipStreamSynchronize(c->stream);
+    for (auto& e : c->ev)
+        if (e) (void)hipEventDestroy(e);
+    if (c->stream) (void)hipStreamDestroy(c->stream);
+    delete c;
+    return GATGPU_OK;
+}
+
+const char* gatgpu_last_error(const gatgpu_ctx* c) { return c ? c->err.c_str() : g_create_error.c_str(); }
+
+int gatgpu_set_graph(gatgpu_ctx* c, uint64_t n, uint64_t e, const uint64_t* row, const uint32_t* col) {
+    if (int r = check_ctx(c)) return r;
+    if (!row || (e && !col)) return fail(c, GATGPU_EINVAL, "null CSR pointer");
+    if (n == 0 || n > uint64_t(INT32_MAX)) return fail(c, GATGPU_EINVAL, "invalid graph sizes");
+    if (e > (uint64_t(1) << 40)) return fail(c, GATGPU_EOVERFLOW, "edge count too large");
+    if (row[0] != 0 || row[n] != e) return fail(c, GATGPU_EINVAL, "bad CSR bounds");
+    for (uint64_t i = 0; i < n; ++i)
+        if (row[i] > row[i + 1]) return fail(c, GATGPU_EINVAL, "nonmonotone CSR");
+    for (uint64_t k = 0; k < e; ++k)
+        if (col[k] >= n) return fail(c, GATGPU_EINVAL, "source index out of bounds");
+    if (c->input && c->n != n) c->input = false;
+    c->graph = false;
+    for (auto& L : c->L) L.ran = false;
+    c->n = n;
+    c->e = e;
+    HIPCHECK(c, c->row.ensure((n + 1) * 8));
+    HIPCHECK(c, c->col.ensure(e * 4));
+    HIPCHECK(c, hipMemcpyAsync(c->row.p, row, (n + 1) * 8, hipMemcpyHostToDevice, c->stream));
+    if (e) HIPCHECK(c, hipMemcpyAsync(c->col.p, col, e * 4, hipMemcpyHostToDevice, c->stream));
+    if (int r = build_schedule(c)) return r;
+    c->graph = true;
+    return GATGPU_OK;
+}
+
+int gatgpu_set_layer(gatgpu_ctx* c, int layer, int in, int heads, int dim, const float* w,
+                     const float* al, const float* ar) {
+    if (int r = check_ctx(c)) return r;
+    if (layer < 0 || layer > 2) return fail(c, GATGPU_EINVAL, "layer must be 0, 1 or 2");
+    if (in <= 0 || heads <= 0 || heads > 8 || dim <= 0 || dim > 64)
+        return fail(c, GATGPU_EINVAL, "invalid parameter shape (heads <=8, head_dim <=64)");
+    if (!w || !al || !ar) return fail(c, GATGPU_EINVAL, "null weight pointer");
+    const uint64_t W = uint64_t(heads) * dim, wn = uint64_t(in) * W;
+    uint64_t bad = 0;
+    if (!all_finite(w, wn, &bad)) return fail(c, GATGPU_ENONFINITE, "nonfinite W index=" + std::to_string(bad));
+    if (!all_finite(al, W, &bad)) return fail(c, GATGPU_ENONFINITE, "nonfinite aL index=" + std::to_string(bad));
+    if (!all_finite(ar, W, &bad)) return fail(c, GATGPU_ENONFINITE, "nonfinite aR index=" + std::to_string(bad));
+    LayerState& L = c->L[layer];
+    L.set = false;
+    L.ran = false;
+    L.in = in;
+    L.heads = heads;
+    L.dim = dim;
+    // Static preparation (prepare(), baseline/src/common.cpp:97-119): bf16
+    // copy of W (kept as FP32 values) and B_LR = W a for the reordered front end.
+    std::vector<float> wq(wn), blr(size_t(in) * 2 * heads);
+    for (uint64_t i = 0; i < wn; ++i) wq[i] = bf16_widen(bf16_rne(w[i]));
+    for (int k = 0; k < in; ++k)
+        for (int h = 0; h < heads; ++h) {
+            float l = 0, r = 0;
+            for (int d = 0; d < dim; ++d) {
+                const float wv = w[size_t(k) * W + h * dim + d];
+                l += wv * al[h * dim + d];
+                r += wv * ar[h * dim + d];
+            }
+            blr[size_t(k) * 2 * heads + h] = l;
+            blr[size_t(k) * 2 * heads + heads + h] = r;
+        }
+    HIPCHECK(c, L.w32.ensure(wn * 4));
+    HIPCHECK(c, L.wq32.ensure(wn * 4));
+    HIPCHECK(c, L.al.ensure(W * 4));
+    HIPCHECK(c, L.ar.ensure(W * 4));
+    HIPCHECK(c, L.blr.ensure(blr.size() * 4));
+    HIPCHECK(c, hipMemcpyAsync(L.w32.p, w, wn * 4, hipMemcpyHostToDevice, c->stream));
+    HIPCHECK(c, hipMemcpyAsync(L.wq32.p, wq.data(), wn * 4, hipMemcpyHostToDevice, c->stream));
+    HIPCHECK(c, hipMemcpyAsync(L.al.p, al, W * 4, hipMemcpyHostToDevice, c->stream));
+    HIPCHECK(c, hipMemcpyAsync(L.ar.p, ar, W * 4, hipMemcpyHostToDevice, c->stream));
+    HIPCHECK(c, hipMemcpyAsync(L.blr.p, blr.data(), blr.size() * 4, hipMemcpyHostToDevice, c->stream));
+    HIPCHECK(c, hipStreamSynchronize(c->stream));
+    L.set = true;
+    return GATGPU_OK;
+}
+
+int gatgpu_set_input(gatgpu_ctx* c, uint64_t n, int din, const float* x) {
+    if (int r = check_ctx(c)) return r;
+    if (!c->graph) return fail(c, GATGPU_ESTATE, "graph not set");
+    if (n != c->n || din <= 0 || !x) return fail(c, GATGPU_EINVAL, "feature matrix does not match the graph");
+    if (mul_overflows(n, uint64_t(din) * 4)) return fail(c, GATGPU_EOVERFLOW, "size overflow");
+    uint64_t bad = 0;
+    if (!all_finite(x, n * din, &bad)) return fail(c, GATGPU_ENONFINITE, "nonfinite graph input index=" + std::to_string(bad));
+    HIPCHECK(c, c->x32.ensure(n * din * 4));
+    HIPCHECK(c, hipMemcpyAsync(c->x32.p, x, n * din * 4, hipMemcpyHostToDevice, c->stream));
+    HIPCHECK(c, hipStreamSynchronize(c->stream));
+    c->din = din;
+    c->input = true;
+    c->L[0].ran = false;
+    return GATGPU_OK;
+}
+
+int gatgpu_degree_schedule(gatgpu_ctx* c, uint32_t* perm, uint64_t* steps) {
+    if (int r = check_ctx(c)) return r;
+    if (!c->graph) return fail(c, GATGPU_ESTATE, "graph not set");
+    if (perm) HIPCHECK(c, hipMemcpy(perm, c->perm, c->n * 4, hipMemcpyDeviceToHost));
+    if (steps) *steps = c->neighbor_steps;
+    return GATGPU_OK;
+}
+
+int gatgpu_permuted_csr(gatgpu_ctx* c, uint64_t* prow, uint32_t* pcol) {
+    if (int r = check_ctx(c)) return r;
+    if (!c->graph) return fail(c, GATGPU_ESTATE, "graph not set");
+    if (prow) HIPCHECK(c, hipMemcpy(prow, c->prow.p, (c->n + 1) * 8, hipMemcpyDeviceToHost));
+    if (pcol && c->e) HIPCHECK(c, hipMemcpy(pcol, c->pcol.p, c->e * 4, hipMemcpyDeviceToHost));
+    return GATGPU_OK;
+}
+
+int gatgpu_choose_R(gatgpu_ctx* c, int* r_out) {
+    if (int r = check_ctx(c)) return r;
+    if (!c->graph || !r_out) return fail(c, GATGPU_ESTATE, "graph not set");
+    const double avg = double(c->e) / double(c->n);
+    const double rho = avg ? c->max_degree / avg : 1.0;
+    *r_out = rho < 32 ? 128 : rho < 1024 ? 64 : rho < 20000 ? 32 : 16;
+    return GATGPU_OK;
+}
+
+int gatgpu_layer_forward(gatgpu_ctx* c, int layer, int precision, int dataflow, int hidden,
+                         const float* input, gatgpu_times* times) {
+    if (int r = check_ctx(c)) return r;
+    if (layer < 0 || layer > 2) return fail(c, GATGPU_EINVAL, "layer must be 0, 1 or 2");
+    if (precision != GATGPU_FP32 && precision != GATGPU_BF16) return fail(c, GATGPU_EINVAL, "bad precision");
+    if (dataflow < GATGPU_AUTO || dataflow > GATGPU_AGGREGATE_FIRST) return fail(c, GATGPU_EINVAL, "bad dataflow");
+    if (!c->graph) return fail(c, GATGPU_ESTATE, "graph not set");
+    if (!c->L[layer].set) return fail(c, GATGPU_ESTATE, "layer weights not set");
+    if (input) {
+        uint64_t bad = 0;
+        if (!all_finite(input, c->n * uint64_t(c->L[layer].in), &bad))
+            return fail(c, GATGPU_ENONFINITE, "nonfinite layer input index=" + std::to_string(bad));
+    }
+    const int flow = dataflow == GATGPU_AUTO ? GATGPU_TRANSFORM_FIRST : dataflow;
+    if (int r = run_layer(c, layer, precision, flow, hidden != 0, input, times ? 0 : -1)) return r;
+    HIPCHECK(c, hipStreamSynchronize(c->stream));
+    HIPCHECK(c, hipGetLastError());
+    if (times) fill_times(c, 0, times);
+    return GATGPU_OK;
+}
+
+int gatgpu_model_forward(gatgpu_ctx* c, int precision, int dataflow, float* logits, gatgpu_times* times,
+                         double* total_ms) {
+    if (int r = check_ctx(c)) return r;
+    if (precision != GATGPU_FP32 && precision != GATGPU_BF16) return fail(c, GATGPU_EINVAL, "bad precision");
+    if (dataflow < GATGPU_AUTO || dataflow > GATGPU_AGGREGATE_FIRST) return fail(c, GATGPU_EINVAL, "bad dataflow");
+    if (!c->graph || !c->input) return fail(c, GATGPU_ESTATE, "graph or features not set");
+    for (int l = 0; l < 3; ++l)
+        if (!c->L[l].set) return fail(c, GATGPU_ESTATE, "layer weights not set");
+    if (c->L[0].in != c->din || c->L[1].in != c->L[0].width() || c->L[2].in != c->L[1].width())
+        return fail(c, GATGPU_EINVAL, "layer widths do not chain");
+    const bool timed = times || total_ms;
+    for (int l = 0; l < 3; ++l) {
+        const int flow = dataflow == GATGPU_AUTO ? GATGPU_TRANSFORM_FIRST : dataflow;
+        if (int r = run_layer(c, l, precision, flow, l < 2, nullptr, timed ? 4 * l : -1)) return r;
+    }
+    HIPCHECK(c, hipStreamSynchronize(c->stream));
+    HIPCHECK(c, hipGetLastError());
+    if (times)
+        for (int l = 0; l < 3; ++l) fill_times(c, 4 * l, &times[l]);
+    if (total_ms) *total_ms = ms_between(c->ev[0], c->ev[11]);
+    if (logits) {
+        const LayerState& L = c->L[2];
+        HIPCHECK(c, hipMemcpy(logits, L.out32.p, c->n * L.width() * 4, hipMemcpyDeviceToHost));
+    }
+    return GATGPU_OK;
+}
+
+int gatgpu_stage_size(gatgpu_ctx* c, int layer, int which, uint64_t* count) {
+    if (int r = check_ctx(c)) return r;
+    if (layer < 0 || layer > 2 || !count) return fail(c, GATGPU_EINVAL, "bad stage request");
+    const LayerState& L = c->L[layer];
+    *count = 0;
+    if (!L.ran) return GATGPU_OK;
+    switch (which) {
+        case GATGPU_STAGE_Z:
+            *count = L.z_valid ? c->n * L.width() : 0;
+            break;
+        case GATGPU_STAGE_LEFT:
+        case GATGPU_STAGE_RIGHT:
+        case GATGPU_STAGE_MAX:
+        case GATGPU_STAGE_DEN:
+            *count = c->n * L.heads;
+            break;
+        case GATGPU_STAGE_OUT:
+            *count = c->n * L.width();
+            break;
+        default:
+            return fail(c, GATGPU_EINVAL, "bad stage selector");
+    }
+    return GATGPU_OK;
+}
+
+int gatgpu_get_stage(gatgpu_ctx* c, int layer, int which, float* host) {
+    uint64_t count = 0;
+    if (int r = gatgpu_stage_size(c, layer, which, &count)) return r;
+    if (!count) return fail(c, GATGPU_ESTATE, "stage not available");
+    if (!host) return fail(c, GATGPU_EINVAL, "null output");
+    const LayerState& L = c->L[layer];
+    const void* src = nullptr;
+    bool bf = false;
+    switch (which) {
+        case GATGPU_STAGE_Z:
+            bf = L.precision == GATGPU_BF16;
+            src = bf ? L.zbf.p : L.z32.p;
+            break;
+        case GATGPU_STAGE_LEFT: src = L.left.p; break;
+        case GATGPU_STAGE_RIGHT: src = L.right.p; break;
+        case GATGPU_STAGE_MAX: src = L.mx.p; break;
+        case GATGPU_STAGE_DEN: src = L.den.p; break;
+        case GATGPU_STAGE_OUT:
+            bf = !L.out32_valid;
+            src = bf ? L.outbf.p : L.out32.p;
+            break;
+    }
+    if (bf) {
+        std::vector<uint16_t> tmp(count);
+        HIPCHECK(c, hipMemcpy(tmp.data(), src, count * 2, hipMemcpyDeviceToHost));
+        for (uint64_t i = 0; i < count; ++i) host[i] = bf16_widen(tmp[i]);
+    } else {
+        HIPCHECK(c, hipMemcpy(host, src, count * 4, hipMemcpyDeviceToHost));
+    }
+    return GATGPU_OK;
+}
+
+int gatgpu_set_option(gatgpu_ctx* c, int key, int64_t value) {
+    if (int r = check_ctx(c)) return r;
+    if (value < 0 || value > int64_t(UINT32_MAX)) return fail(c, GATGPU_EINVAL, "option value out of range");
+    switch (key) {
+        case GATGPU_OPT_BLOCK_ROW_MIN_DEGREE: c->block_min = uint32_t(value); break;
+        case GATGPU_OPT_SPLIT_ROW_MIN_DEGREE: c->split_min = uint32_t(value); break;
+        case GATGPU_OPT_SPLIT_CHUNK_EDGES:
+            if (value < 64) return fail(c, GATGPU_EINVAL, "split chunk must be >= 64 edges");
+            c->split_chunk = uint32_t(value);
+            break;
+        case GATGPU_OPT_SMALL_ROW_MAX_DEGREE: c->small_max = uint32_t(value); break;
+        default: return fail(c, GATGPU_EINVAL, "unknown option");
+    }
+    if (c->graph) return compute_bins(c);
+    return GATGPU_OK;
+}
+
+int gatgpu_synchronize(gatgpu_ctx* c) {
+    if (int r = check_ctx(c)) return r;
+    HIPCHECK(c, hipStreamSynchronize(c->stream));
+    return GATGPU_OK;
+}
+
+void* gatgpu_stream(gatgpu_ctx* c) { return c ? static_cast<void*>(c->stream) : nullptr; }
+
+}  // extern "C"

@@ -1,0 +1,101 @@
+// Internal declarations shared by the HIP translation units of libgatgpu.
+#pragma once
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <string>
+
+namespace gatgpu {
+
+constexpr int kWave = 64;  // CDNA4 wavefront
+
+// ---------------------------------------------------------------- bf16 bits
+// FP32 -> bf16 round-to-nearest-even, NaN quieted to (u>>16)|0x40; the
+// conversion of baseline/src/common.cpp:80-83, written on raw bits so NaN
+// payloads and ties match the reference exactly.
+__host__ __device__ inline uint16_t bf16_rne(float x) {
+    uint32_t u = __builtin_bit_cast(uint32_t, x);
+    if ((u & 0x7f800000u) == 0x7f800000u && (u & 0x7fffffu)) return uint16_t((u >> 16) | 0x40u);
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return uint16_t(u >> 16);
+}
+__host__ __device__ inline float bf16_widen(uint16_t b) {
+    return __builtin_bit_cast(float, uint32_t(b) << 16);
+}
+__device__ inline float leaky(float x) { return x >= 0.0f ? x : 0.2f * x; }
+__device__ inline float elu(float x) { return x >= 0.0f ? x : expm1f(x); }
+
+// Wave-local ordering of LDS traffic between lanes of one wavefront.
+__device__ inline void wave_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// ---------------------------------------------------------------- launches
+// Every launcher returns hipSuccess or the launch error.
+
+// schedule.hip
+// deg[i] = row[i+1]-row[i], ids[i] = i, *maxdeg = max degree (atomicMax).
+hipError_t launch_degrees_and_ids(const uint64_t* row, uint32_t* deg, uint32_t* ids, uint64_t n,
+                                  uint32_t* maxdeg, hipStream_t s);
+hipError_t radix_sort_by_degree(uint32_t* keys, uint32_t* vals, uint32_t* keys_alt,
+                                uint32_t* vals_alt, uint32_t* tile_hist, uint64_t n, int passes,
+                                void* scan_tmp, hipStream_t s, uint32_t** keys_out,
+                                uint32_t** vals_out);
+size_t radix_tile_hist_elems(uint64_t n);
+size_t scan_tmp_bytes(uint64_t n);
+hipError_t exclusive_scan_u32_to_u64(const uint32_t* in, uint64_t* out, uint64_t n, void* tmp,
+                                     hipStream_t s);
+hipError_t launch_permute_cols(const uint64_t* row, const uint32_t* col, const uint32_t* perm,
+                               const uint64_t* prow, uint32_t* pcol, uint64_t n, uint64_t e,
+                               hipStream_t s);
+hipError_t launch_neighbor_steps(const uint32_t* sorted_deg, uint64_t n, uint64_t* steps,
+                                 hipStream_t s);
+hipError_t launch_count_le(const uint32_t* sorted_deg, uint64_t n, const uint32_t* thresholds,
+                           int count, uint64_t* positions, hipStream_t s);
+
+// projection.hip
+hipError_t launch_to_bf16(const float* x, uint16_t* y, uint64_t count, hipStream_t s);
+hipError_t launch_widen_bf16(const uint16_t* x, float* y, uint64_t count, hipStream_t s);
+// Z = X W with the L/R attention dots and the store of Z (FP32 or bf16).
+// X is FP32 (x32 != null) or bf16 bits (xbf != null); W is FP32 values (for
+// the bf16 path: bf16-rounded values).
+hipError_t launch_projection(const float* x32, const uint16_t* xbf, const float* w, uint64_t n,
+                             int in, int heads, int dim, const float* al, const float* ar,
+                             float* z32, uint16_t* zbf, float* left, float* right, float* zscratch,
+                             hipStream_t s);
+// L/R only (aggregate-first front end): LR = X B_LR with B_LR = W a.
+hipError_t launch_lr_reordered(const float* x32, const uint16_t* xbf, const float* blr,
+                               uint64_t n, int in, int heads, float* left, float* right,
+                               hipStream_t s);
+
+// aggregate.hip
+struct RowBins {
+    // Sorted positions [0, n) split by degree: [0, small_end) share waves,
+    // [small_end, block_begin) one wave per row, [block_begin, split_begin)
+    // one block per row, [split_begin, n) several blocks per row.
+    uint64_t small_end = 0, block_begin = 0, split_begin = 0, n = 0;
+};
+struct AggArgs {
+    const uint64_t* prow;
+    const uint32_t* pcol;
+    const uint32_t* perm;
+    const float* left;   // [n][K]
+    const float* right;  // [n][K]
+    const void* feat;    // Z [n][W] (TF) or X [n][D] (AF); FP32 or bf16
+    bool feat_bf16;
+    int heads, dim;
+    bool hidden;
+    float* mx;       // [n][K]
+    float* den;      // [n][K]
+    float* out32;    // [n][W] or null
+    uint16_t* outbf; // [n][W] or null
+    uint64_t n, e;           // nodes and CSR entries (bounds of perm/prow values)
+    float* acc_scratch;      // split rows: [n_split_rows][W] + [n_split_rows][K]
+    uint32_t* split_counter; // split rows: [n_split_rows]
+};
+hipError_t launch_aggregate_tf(const AggArgs& a, const RowBins& bins, uint32_t split_chunk,
+                               hipStream_t s);
+
+}  // namespace gatgpu

@@ -1,0 +1,206 @@
+"""Python binding of libgatgpu (the gfx950 GAT forward) over its C ABI.
+
+The binding is a thin ctypes layer over ``include/gatgpu.h``: host arrays are
+NumPy, every device buffer is owned by the library context.  There is no
+fallback: if ``lib/libgatgpu.so`` is missing or no gfx950 device is present,
+the calls raise.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from pathlib import Path
+
+import numpy as np
+
+PKG_ROOT = Path(__file__).resolve().parent.parent  # gat-tfs_amd/
+LIB_PATH = PKG_ROOT / "lib" / "libgatgpu.so"
+
+OK, EINVAL, ESTATE, ENODEV, ENOMEM, EDEVICE, ENONFINITE, EOVERFLOW = 0, -1, -2, -3, -4, -5, -6, -7
+FP32, BF16 = 0, 1
+AUTO, TRANSFORM_FIRST, AGGREGATE_FIRST = 0, 1, 2
+STAGE_Z, STAGE_LEFT, STAGE_RIGHT, STAGE_MAX, STAGE_DEN, STAGE_OUT = range(6)
+OPT_BLOCK_ROW_MIN_DEGREE, OPT_SPLIT_ROW_MIN_DEGREE, OPT_SPLIT_CHUNK_EDGES, OPT_SMALL_ROW_MAX_DEGREE = 1, 2, 3, 4
+
+STAGE_NAMES = {"z": STAGE_Z, "left": STAGE_LEFT, "right": STAGE_RIGHT, "max": STAGE_MAX,
+               "den": STAGE_DEN, "out": STAGE_OUT}
+
+# Every symbol include/gatgpu.h declares.
+EXPORTS = (
+    "gatgpu_create", "gatgpu_destroy", "gatgpu_last_error", "gatgpu_set_graph", "gatgpu_set_layer",
+    "gatgpu_set_input", "gatgpu_degree_schedule", "gatgpu_permuted_csr", "gatgpu_choose_R",
+    "gatgpu_layer_forward", "gatgpu_model_forward", "gatgpu_get_stage", "gatgpu_stage_size",
+    "gatgpu_set_option", "gatgpu_synchronize", "gatgpu_stream",
+)
+
+
+class Times(ctypes.Structure):
+    """gatgpu_times (field names of gat::Times, baseline/include/gat.hpp:68-76)."""
+    _fields_ = [(name, ctypes.c_double) for name in (
+        "convert_ms", "projection_ms", "lr_ms", "max_prescan_ms", "aggregate_ms", "normalize_ms",
+        "activation_ms", "total_ms")]
+
+    def as_dict(self):
+        return {name: getattr(self, name) for name, _ in self._fields_}
+
+
+class GatGpuError(RuntimeError):
+    def __init__(self, code, msg):
+        super().__init__(f"gatgpu error {code}: {msg}")
+        self.code = code
+
+
+_LIB = None
+
+
+def load_library(path: os.PathLike | None = None):
+    """Loads libgatgpu.so (raises if it has not been built)."""
+    global _LIB
+    if _LIB is not None and path is None:
+        return _LIB
+    p = Path(path) if path else LIB_PATH
+    if not p.exists():
+        raise FileNotFoundError(f"{p} is not built; run `make -C {PKG_ROOT}` (or __graft_entry__.build())")
+    L = ctypes.CDLL(str(p))
+    P, u64, i32, i64 = ctypes.c_void_p, ctypes.c_uint64, ctypes.c_int, ctypes.c_int64
+    L.gatgpu_create.argtypes = [i32, ctypes.POINTER(P)]
+    L.gatgpu_destroy.argtypes = [P]
+    L.gatgpu_last_error.argtypes = [P]
+    L.gatgpu_last_error.restype = ctypes.c_char_p
+    L.gatgpu_set_graph.argtypes = [P, u64, u64, P, P]
+    L.gatgpu_set_layer.argtypes = [P, i32, i32, i32, i32, P, P, P]
+    L.gatgpu_set_input.argtypes = [P, u64, i32, P]
+    L.gatgpu_degree_schedule.argtypes = [P, P, P]
+    L.gatgpu_permuted_csr.argtypes = [P, P, P]
+    L.gatgpu_choose_R.argtypes = [P, ctypes.POINTER(i32)]
+    L.gatgpu_layer_forward.argtypes = [P, i32, i32, i32, i32, P, P]
+    L.gatgpu_model_forward.argtypes = [P, i32, i32, P, P, ctypes.POINTER(ctypes.c_double)]
+    L.gatgpu_get_stage.argtypes = [P, i32, i32, P]
+    L.gatgpu_stage_size.argtypes = [P, i32, i32, ctypes.POINTER(u64)]
+    L.gatgpu_set_option.argtypes = [P, i32, i64]
+    L.gatgpu_synchronize.argtypes = [P]
+    L.gatgpu_stream.argtypes = [P]
+    L.gatgpu_stream.restype = P
+    for name in EXPORTS:
+        if name not in ("gatgpu_last_error", "gatgpu_stream"):
+            getattr(L, name).restype = i32
+    if path is None:
+        _LIB = L
+    return L
+
+
+def _ptr(a):
+    return None if a is None else a.ctypes.data
+
+
+class Context:
+    """One device context (gatgpu_ctx)."""
+
+    def __init__(self, device: int = 0):
+        self.lib = load_library()
+        h = ctypes.c_void_p()
+        rc = self.lib.gatgpu_create(device, ctypes.byref(h))
+        if rc != OK:
+            raise GatGpuError(rc, self.lib.gatgpu_last_error(None).decode())
+        self.h = h
+        self.n = 0
+        self.e = 0
+        self.layers = [None, None, None]
+
+    def _check(self, rc):
+        if rc != OK:
+            raise GatGpuError(rc, self.lib.gatgpu_last_error(self.h).decode())
+
+    def close(self):
+        if self.h:
+            self.lib.gatgpu_destroy(self.h)
+            self.h = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    # -- static inputs
+    def set_graph(self, row, col):
+        row = np.ascontiguousarray(row, np.uint64)
+        col = np.ascontiguousarray(col, np.uint32)
+        n = row.size - 1
+        self._check(self.lib.gatgpu_set_graph(self.h, n, col.size, _ptr(row), _ptr(col)))
+        self.n, self.e = n, col.size
+
+    def set_layer(self, layer, p):
+        w = np.ascontiguousarray(p["w"], np.float32)
+        al = np.ascontiguousarray(p["al"], np.float32)
+        ar = np.ascontiguousarray(p["ar"], np.float32)
+        self._check(self.lib.gatgpu_set_layer(self.h, layer, p["in"], p["heads"], p["dim"], _ptr(w), _ptr(al),
+                                              _ptr(ar)))
+        self.layers[layer] = (p["in"], p["heads"], p["dim"])
+
+    def set_model(self, model):
+        for l, p in enumerate(model):
+            self.set_layer(l, p)
+
+    def set_input(self, x):
+        x = np.ascontiguousarray(x, np.float32)
+        self._check(self.lib.gatgpu_set_input(self.h, x.shape[0], x.shape[1], _ptr(x)))
+
+    def set_option(self, key, value):
+        self._check(self.lib.gatgpu_set_option(self.h, key, int(value)))
+
+    # -- schedule
+    def degree_schedule(self):
+        perm = np.empty(self.n, np.uint32)
+        steps = np.zeros(1, np.uint64)
+        self._check(self.lib.gatgpu_degree_schedule(self.h, _ptr(perm), _ptr(steps)))
+        return perm, int(steps[0])
+
+    def permuted_csr(self):
+        prow = np.empty(self.n + 1, np.uint64)
+        pcol = np.empty(self.e, np.uint32)
+        self._check(self.lib.gatgpu_permuted_csr(self.h, _ptr(prow), _ptr(pcol)))
+        return prow, pcol
+
+    def choose_R(self):
+        r = ctypes.c_int()
+        self._check(self.lib.gatgpu_choose_R(self.h, ctypes.byref(r)))
+        return r.value
+
+    # -- forward
+    def layer_forward(self, layer, precision=FP32, dataflow=AUTO, hidden=True, input=None):
+        t = Times()
+        inp = None if input is None else np.ascontiguousarray(input, np.float32)
+        self._check(self.lib.gatgpu_layer_forward(self.h, layer, precision, dataflow, int(hidden), _ptr(inp),
+                                                  ctypes.byref(t)))
+        return t.as_dict()
+
+    def model_forward(self, precision=FP32, dataflow=AUTO, want_logits=True, timed=True):
+        logits = None
+        if want_logits:
+            logits = np.empty((self.n, self.layers[2][1] * self.layers[2][2]), np.float32)
+        times = (Times * 3)() if timed else None
+        total = ctypes.c_double(0.0)
+        self._check(self.lib.gatgpu_model_forward(self.h, precision, dataflow, _ptr(logits),
+                                                  times if timed else None,
+                                                  ctypes.byref(total) if timed else None))
+        return logits, ([t.as_dict() for t in times] if timed else None), total.value
+
+    def stage(self, layer, which):
+        code = STAGE_NAMES[which] if isinstance(which, str) else which
+        cnt = ctypes.c_uint64()
+        self._check(self.lib.gatgpu_stage_size(self.h, layer, code, ctypes.byref(cnt)))
+        if cnt.value == 0:
+            return None
+        out = np.empty(cnt.value, np.float32)
+        self._check(self.lib.gatgpu_get_stage(self.h, layer, code, _ptr(out)))
+        return out.reshape(self.n, -1)
+
+    def synchronize(self):
+        self._check(self.lib.gatgpu_synchronize(self.h))

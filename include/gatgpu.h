@@ -1,0 +1,170 @@
+/*
+ * gatgpu.h -- C ABI of the MI355X (gfx950) three-layer multi-head GAT forward.
+ *
+ * One opaque context per device owns every device buffer: the destination-row
+ * CSR graph, its degree schedule, three layers of weights and the per-layer
+ * activations.  Host buffers stay owned by the caller.  No function throws;
+ * each returns 0 (GATGPU_OK) or a negative error class, and
+ * gatgpu_last_error() describes the failure.  A context is used by one host
+ * thread at a time.
+ *
+ * The entry points replace the per-layer "paths" of the reference harness:
+ *   run_path(path, g, p, q, s, input, w, hidden, panel, t, policy)
+ *     baseline/bench/main.cpp:21-25 (path whitelist main.cpp:30)
+ *   X_layer(const Graph&, const Param&, const Prepared&, [const Schedule&,]
+ *           const std::vector<float>& input, Workspace&, bool hidden, Times&)
+ *     baseline/include/gat.hpp:107-117
+ * The graph container (u64 rowptr, u32 col, f32 x; baseline/include/gat.hpp:32-39)
+ * and the weight layout (W[in][heads*dim] row-major, head h = columns
+ * [h*dim,(h+1)*dim), aL/aR[heads*dim]; baseline/include/gat.hpp:42-48) are
+ * taken unchanged.
+ */
+#ifndef GATGPU_H
+#define GATGPU_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct gatgpu_ctx gatgpu_ctx;
+
+/* Return codes.  The reference throws std::runtime_error for each of these
+ * (baseline/src/common.cpp:6-49); its harness maps them to "FAIL msg", exit 1
+ * (baseline/bench/main.cpp:184). */
+enum {
+    GATGPU_OK = 0,
+    GATGPU_EINVAL = -1,     /* malformed argument, CSR, shape or option       */
+    GATGPU_ESTATE = -2,     /* call order: graph/layer/input not set yet      */
+    GATGPU_ENODEV = -3,     /* no usable HIP device / wrong architecture      */
+    GATGPU_ENOMEM = -4,     /* device allocation failed                       */
+    GATGPU_EDEVICE = -5,    /* a HIP call or kernel launch failed             */
+    GATGPU_ENONFINITE = -6, /* NaN/Inf in features or weights                 */
+    GATGPU_EOVERFLOW = -7   /* size product overflows (common.cpp:6-9)        */
+};
+
+/* Precision of a forward.  FP32: FP32 X, W, Z and softmax state (the
+ * reference's ref_fp32 / standard_fp32).  BF16: RNE-rounded bf16 X and W,
+ * FP32 MFMA accumulation, L/R from the FP32 accumulators, Z stored bf16,
+ * FP32 score/max/exp/denominator/output accumulation (standard_bf16 with a
+ * bf16 copy of Z; IMPLEMENTATION_CONTRACT.md section 3). */
+enum { GATGPU_FP32 = 0, GATGPU_BF16 = 1 };
+
+/* Dataflow of one layer.  TRANSFORM_FIRST projects Z = X W then aggregates Z
+ * rows (standard_layer, baseline/src/baseline_standard.cpp:98-108).
+ * AGGREGATE_FIRST aggregates X rows per head and projects afterwards
+ * (tfs_online_fused, implementation/src/gat_tfs_online.cpp:200-283).  AUTO
+ * picks aggregate-first when the gathered row is narrower (in*sizeof(x) <
+ * heads*dim*sizeof(z)). */
+enum { GATGPU_AUTO = 0, GATGPU_TRANSFORM_FIRST = 1, GATGPU_AGGREGATE_FIRST = 2 };
+
+/* Stage selectors for gatgpu_get_stage (Workspace fields, gat.hpp:96-106). */
+enum {
+    GATGPU_STAGE_Z = 0,    /* [n][heads*dim] projected features (TF only)   */
+    GATGPU_STAGE_LEFT = 1, /* [n][heads]                                     */
+    GATGPU_STAGE_RIGHT = 2,/* [n][heads]                                     */
+    GATGPU_STAGE_MAX = 3,  /* [n][heads] exact row max M = leaky(L + max R)  */
+    GATGPU_STAGE_DEN = 4,  /* [n][heads] sum of exp(score - M)               */
+    GATGPU_STAGE_OUT = 5   /* [n][heads*dim] normalised (+ELU) layer output  */
+};
+
+/* Per-layer stage times in milliseconds, measured with HIP events on the
+ * context's stream.  Field names follow gat::Times (baseline/include/gat.hpp:68-76).
+ * normalize and activation are fused into the aggregation kernel on the GPU,
+ * so their time is inside aggregate_ms and their fields read 0. */
+typedef struct gatgpu_times {
+    double convert_ms;
+    double projection_ms;
+    double lr_ms;
+    double max_prescan_ms;
+    double aggregate_ms;
+    double normalize_ms;
+    double activation_ms;
+    double total_ms;
+} gatgpu_times;
+
+/* Options (gatgpu_set_option).  Thresholds are in-degrees. */
+enum {
+    GATGPU_OPT_BLOCK_ROW_MIN_DEGREE = 1, /* rows at/above use a block per row  */
+    GATGPU_OPT_SPLIT_ROW_MIN_DEGREE = 2, /* rows at/above are split over blocks */
+    GATGPU_OPT_SPLIT_CHUNK_EDGES = 3,    /* edges per block for split rows      */
+    GATGPU_OPT_SMALL_ROW_MAX_DEGREE = 4  /* rows at/below share one wave        */
+};
+
+/* ---- lifetime -------------------------------------------------------- */
+/* Opens `device` (HIP ordinal), checks it is a gfx950, creates the stream. */
+int gatgpu_create(int device, gatgpu_ctx** out);
+/* Frees every device buffer; accepts NULL. */
+int gatgpu_destroy(gatgpu_ctx* ctx);
+/* Message of the last failure on ctx (or of the last failed create when ctx
+ * is NULL).  Valid until the next call on the same context. */
+const char* gatgpu_last_error(const gatgpu_ctx* ctx);
+
+/* ---- static inputs (untimed, like load_graph/prepare: README.md:52) ---- */
+/* Validates and uploads the CSR, then builds the degree schedule on the GPU.
+ * Replaces load_graph + Graph::validate (baseline/src/common.cpp:23-39) and
+ * degree_schedule (common.cpp:120-125).  Checks row[0]==0, row[n]==e,
+ * monotone rows, col[k] < n, 0 < n <= INT32_MAX. */
+int gatgpu_set_graph(gatgpu_ctx* ctx, uint64_t n, uint64_t e, const uint64_t* row,
+                     const uint32_t* col);
+/* Uploads one layer (0..2) of weights and prepares its bf16 copy.  Replaces
+ * Param::validate + prepare (common.cpp:45-49, 97-119): 0 < heads <= 8,
+ * 0 < dim <= 64, 0 < in, all values finite. */
+int gatgpu_set_layer(gatgpu_ctx* ctx, int layer, int in, int heads, int dim, const float* w,
+                     const float* al, const float* ar);
+/* Uploads the node features x[n][din] (Graph::x); all values finite. */
+int gatgpu_set_input(gatgpu_ctx* ctx, uint64_t n, int din, const float* x);
+
+/* ---- schedule -------------------------------------------------------- */
+/* Copies the degree permutation (perm[sorted] = original row, ascending
+ * (degree, id)) and neighbor_steps (sum over 16-row tiles of the last row's
+ * degree), both computed on the GPU.  Either pointer may be NULL.
+ * Replaces degree_schedule (baseline/src/common.cpp:120-125) and degree_perm
+ * (implementation/src/gat_tfs_online.cpp:180-189). */
+int gatgpu_degree_schedule(gatgpu_ctx* ctx, uint32_t* perm, uint64_t* neighbor_steps);
+/* Copies the CSR in degree-sorted order: prow[k] = sum of degrees of
+ * perm[0..k), pcol[prow[k]..prow[k+1]) = col[row[perm[k]]..row[perm[k]+1]). */
+int gatgpu_permuted_csr(gatgpu_ctx* ctx, uint64_t* prow, uint32_t* pcol);
+/* choose_R (implementation/src/gat_tfs_online.cpp:191-199) from the device
+ * max degree: 128 if rho<32, 64 if rho<1024, 32 if rho<20000, else 16. */
+int gatgpu_choose_R(gatgpu_ctx* ctx, int* r_out);
+
+/* ---- forward --------------------------------------------------------- */
+/* One layer (0..2).  `input` NULL chains from the device-resident output of
+ * layer-1 run with the same precision (layer 0 reads the graph features);
+ * non-NULL uploads a host FP32 [n][in] matrix first (outside the timing),
+ * as run_path takes any `input` vector.  hidden != 0 applies ELU
+ * (layers 0 and 1 of the model).  times may be NULL.
+ * Replaces standard_layer / ref_layer / tfs_layer (gat.hpp:107-117) and
+ * reference / tfs_online_fused (implementation/src/gat_online.cpp:167,
+ * implementation/src/gat_tfs_online.cpp:200-202). */
+int gatgpu_layer_forward(gatgpu_ctx* ctx, int layer, int precision, int dataflow, int hidden,
+                         const float* input, gatgpu_times* times);
+/* The three layers chained on device (hidden = layer < 2), timed from the
+ * first kernel of layer 0 to the last of layer 2 with HIP events (the model
+ * timer of baseline/bench/main.cpp:171-174).  logits (NULL allowed) receives
+ * layer 2's FP32 [n][dim] output after the timer stops.  times (NULL allowed)
+ * points at 3 per-layer records; total_ms (NULL allowed) gets the model time.
+ * dataflow applies to every layer (AUTO decides per layer). */
+int gatgpu_model_forward(gatgpu_ctx* ctx, int precision, int dataflow, float* logits,
+                         gatgpu_times* times, double* total_ms);
+/* Copies a stage of the last forward of `layer` as FP32 (bf16 stages are
+ * widened exactly). */
+int gatgpu_get_stage(gatgpu_ctx* ctx, int layer, int which, float* host_out);
+/* Size in floats of a stage buffer (0 if absent). */
+int gatgpu_stage_size(gatgpu_ctx* ctx, int layer, int which, uint64_t* count);
+
+/* ---- misc ------------------------------------------------------------ */
+int gatgpu_set_option(gatgpu_ctx* ctx, int key, int64_t value);
+/* Blocks until all work on the context's stream is done. */
+int gatgpu_synchronize(gatgpu_ctx* ctx);
+/* The context's HIP stream (hipStream_t) for callers that order their own
+ * work against it. */
+void* gatgpu_stream(gatgpu_ctx* ctx);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* GATGPU_H */

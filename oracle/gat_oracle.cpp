@@ -1,0 +1,474 @@
+// CPU oracle for the three-layer multi-head GAT forward (TEST INFRASTRUCTURE).
+//
+// This library is the checker and the CPU baseline, never the product: only
+// tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may load it.
+// Every function restates the reference algorithm it cites (paths relative to
+// the reference root).  It is compiled with g++ so that libstdc++'s mt19937 and
+// normal/uniform distributions reproduce the reference's random weights.
+//
+// Parity status of each function (how it is pinned) is listed in oracle/README.md.
+#include <algorithm>
+#include <chrono>
+#include <cmath>
+#include <cstdint>
+#include <cstring>
+#include <limits>
+#include <numeric>
+#include <random>
+#include <vector>
+#include <omp.h>
+
+namespace {
+using Clock = std::chrono::steady_clock;
+double ms_since(Clock::time_point a) {
+    return std::chrono::duration<double, std::milli>(Clock::now() - a).count();
+}
+inline float leak(float x) { return x >= 0 ? x : 0.2f * x; }  // baseline/include/gat.hpp:52
+inline float elu(float x) { return x >= 0 ? x : std::expm1(x); }  // baseline/include/gat.hpp:53
+
+// FP32 -> BF16 round-to-nearest-even with NaN quieting: baseline/src/common.cpp:80-83.
+inline uint16_t rne(float x) {
+    uint32_t u;
+    std::memcpy(&u, &x, 4);
+    if ((u & 0x7f800000u) == 0x7f800000u && (u & 0x7fffffu)) return uint16_t((u >> 16) | 0x40u);
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return uint16_t(u >> 16);
+}
+inline float expand(uint16_t b) {  // baseline/src/common.cpp:84
+    uint32_t u = uint32_t(b) << 16;
+    float x;
+    std::memcpy(&x, &u, 4);
+    return x;
+}
+
+// Vectorisable exp for the CPU baseline (the reference uses icpx SVML
+// _mm512_exp_ps, absent here).  Method: Cody & Waite (1980) argument
+// reduction x = n*ln2 + r with ln2 split in a short-mantissa high part and a
+// low part, then the degree-7 Taylor polynomial of e^r on |r| <= ln2/2
+// (truncation error |r|^8/8! < 1.2e-8 relative), then scaling by 2^n through
+// the exponent field.  Arguments below -87.33 return 0 (the softmax only
+// evaluates x <= 0, where such values are below FP32's normal range).
+inline float exp_cw(float x) {
+    if (x < -87.33f) return 0.0f;
+    if (x > 88.7f) x = 88.7f;
+    const float log2e = 1.44269504088896341f;
+    const float ln2_hi = 0.693359375f;          // 0x3f318000: 9 significant bits
+    const float ln2_lo = -2.12194440e-4f;       // ln2 - ln2_hi
+    float n = std::nearbyint(x * log2e);
+    float r = x - n * ln2_hi;
+    r = r - n * ln2_lo;
+    // Taylor coefficients 1/k!, k = 7..0, Horner form.
+    float p = 1.0f / 5040.0f;
+    p = p * r + 1.0f / 720.0f;
+    p = p * r + 1.0f / 120.0f;
+    p = p * r + 1.0f / 24.0f;
+    p = p * r + 1.0f / 6.0f;
+    p = p * r + 0.5f;
+    p = p * r + 1.0f;
+    p = p * r + 1.0f;
+    int32_t e = int32_t(n) + 127;
+    if (e <= 0) {  // result in the subnormal range: scale in two steps
+        uint32_t b1 = uint32_t(e + 64) << 23;
+        float s1;
+        std::memcpy(&s1, &b1, 4);
+        return p * s1 * 5.42101086e-20f;  // 2^-64
+    }
+    uint32_t bits = uint32_t(e) << 23;
+    float s;
+    std::memcpy(&s, &bits, 4);
+    return p * s;
+}
+// expm1 for x < 0 (ELU branch): series for small |x| avoids cancellation.
+inline float expm1_neg(float x) {
+    if (x > -0.25f) {
+        // Taylor series of e^x - 1 to x^8/8!: |x|^9/9! < 1e-11 for |x| <= 0.25.
+        float p = 1.0f / 40320.0f;
+        p = p * x + 1.0f / 5040.0f;
+        p = p * x + 1.0f / 720.0f;
+        p = p * x + 1.0f / 120.0f;
+        p = p * x + 1.0f / 24.0f;
+        p = p * x + 1.0f / 6.0f;
+        p = p * x + 0.5f;
+        p = p * x + 1.0f;
+        return p * x;
+    }
+    return exp_cw(x) - 1.0f;
+}
+}  // namespace
+
+extern "C" {
+
+// ---------------------------------------------------------------- conversion
+void or_rne(const float* x, uint16_t* out, uint64_t n) {
+    for (uint64_t i = 0; i < n; ++i) out[i] = rne(x[i]);
+}
+float or_exp_cw(float x) { return exp_cw(x); }
+float or_expm1_neg(float x) { return expm1_neg(x); }
+
+// ---------------------------------------------------------------- weights
+// One layer of random_model: baseline/src/common.cpp:50-62.  The caller passes
+// rng_seed = seed + 11*layer, exactly as common.cpp:55 seeds mt19937.
+void or_random_param(int in, int heads, int dim, int rng_seed, float* w, float* al, float* ar) {
+    std::mt19937 rng(rng_seed);
+    std::normal_distribution<float> norm;
+    const size_t width = size_t(heads) * dim;
+    for (size_t i = 0; i < size_t(in) * width; ++i) w[i] = norm(rng) / std::sqrt(float(in));
+    for (size_t i = 0; i < width; ++i) al[i] = norm(rng) / std::sqrt(float(dim));
+    for (size_t i = 0; i < width; ++i) ar[i] = norm(rng) / std::sqrt(float(dim));
+}
+// Boundary-test parameters: baseline/tests/boundaries.cpp:8-9.
+void or_boundary_param(int D, int K, int d, float* w, float* al, float* ar) {
+    std::mt19937 rng(D + K + d);
+    std::uniform_real_distribution<float> rnd(-.3f, .3f);
+    for (size_t i = 0; i < size_t(D) * K * d; ++i) w[i] = rnd(rng);
+    for (int i = 0; i < K * d; ++i) al[i] = rnd(rng);
+    for (int i = 0; i < K * d; ++i) ar[i] = rnd(rng);
+}
+// Boundary-test features: baseline/tests/boundaries.cpp:13 (float sin).
+void or_boundary_features(uint64_t count, float* x) {
+    for (uint64_t i = 0; i < count; ++i) x[i] = std::sin(float(i) * .17f) * .5f;
+}
+
+// ---------------------------------------------------------------- R0 oracle
+// R0 FP32 layer: baseline/src/ref_fp32.cpp:3-26.  The SGEMM is restated as a
+// float dot product in ascending k (oneMKL's blocking order is not known; the
+// difference is tolerance-level, pinned by the FP64 oracle below).  L/R follow
+// lr_from_z(scalar=true) (baseline/src/baseline_standard.cpp:7-20).  score, p
+// and alpha are [E][K]; any of them may be null.
+void or_ref_layer(uint64_t n, const uint64_t* row, const uint32_t* col, const float* x, int in,
+                  int heads, int dim, const float* w, const float* al, const float* ar, int hidden,
+                  float* z, float* left, float* right, float* mx, float* den, float* score, float* p,
+                  float* alpha, float* out) {
+    const int K = heads, W = heads * dim;
+    #pragma omp parallel for schedule(static)
+    for (uint64_t i = 0; i < n; ++i) {
+        float* zi = z + i * W;
+        for (int c = 0; c < W; ++c) zi[c] = 0.0f;
+        for (int k = 0; k < in; ++k) {
+            const float a = x[i * in + k];
+            const float* wk = w + size_t(k) * W;
+            for (int c = 0; c < W; ++c) zi[c] += a * wk[c];
+        }
+        for (int h = 0; h < K; ++h) {
+            float l = 0, r = 0;
+            for (int d = 0; d < dim; ++d) {
+                l += zi[h * dim + d] * al[h * dim + d];
+                r += zi[h * dim + d] * ar[h * dim + d];
+            }
+            left[i * K + h] = l;
+            right[i * K + h] = r;
+        }
+    }
+    #pragma omp parallel
+    {
+        std::vector<float> sc, pv;
+        #pragma omp for schedule(dynamic, 64)
+        for (uint64_t i = 0; i < n; ++i) {
+            const uint64_t b = row[i], e_end = row[i + 1], deg = e_end - b;
+            sc.resize(deg * K);
+            pv.resize(deg * K);
+            float* oi = out + i * W;
+            for (int c = 0; c < W; ++c) oi[c] = 0.0f;
+            for (int h = 0; h < K; ++h) {
+                float m = -std::numeric_limits<float>::infinity();
+                for (uint64_t e = 0; e < deg; ++e) {
+                    float s = leak(left[i * K + h] + right[size_t(col[b + e]) * K + h]);
+                    sc[e * K + h] = s;
+                    m = std::max(m, s);
+                }
+                mx[i * K + h] = deg == 0 ? 0.0f : m;
+                float dn = 0;
+                for (uint64_t e = 0; e < deg; ++e) {
+                    float v = std::exp(sc[e * K + h] - m);
+                    pv[e * K + h] = v;
+                    dn += v;
+                }
+                den[i * K + h] = dn;
+                for (uint64_t e = 0; e < deg; ++e) {
+                    if (score) score[(b + e) * K + h] = sc[e * K + h];
+                    if (p) p[(b + e) * K + h] = pv[e * K + h];
+                    if (alpha) alpha[(b + e) * K + h] = pv[e * K + h] / dn;
+                }
+            }
+            // ref_fp32.cpp:17-21 aggregates with alpha = p/den in edge order.
+            for (uint64_t e = 0; e < deg; ++e) {
+                const float* zj = z + size_t(col[b + e]) * W;
+                for (int h = 0; h < K; ++h) {
+                    const float a = pv[e * K + h] / den[i * K + h];
+                    for (int d = 0; d < dim; ++d) oi[h * dim + d] += a * zj[h * dim + d];
+                }
+            }
+            if (hidden)
+                for (int c = 0; c < W; ++c) oi[c] = elu(oi[c]);
+        }
+    }
+}
+
+// ---------------------------------------------------------------- FP64 oracle
+// Independent FP64 layer: baseline/tests/boundaries.cpp:15-21 (scalar
+// projection/attention/softmax in double) plus the ELU of
+// baseline/tests/oracle.py:53-54 when hidden.  Outputs are double.
+void or_fp64_layer(uint64_t n, const uint64_t* row, const uint32_t* col, const float* x, int in,
+                   int heads, int dim, const float* w, const float* al, const float* ar, int hidden,
+                   double* z, double* left, double* right, double* mx, double* den, double* out) {
+    const int K = heads, W = heads * dim;
+    #pragma omp parallel for schedule(static)
+    for (uint64_t i = 0; i < n; ++i) {
+        for (int h = 0; h < K; ++h) {
+            double l = 0, r = 0;
+            for (int d = 0; d < dim; ++d) {
+                double v = 0;
+                for (int k = 0; k < in; ++k) v += double(x[i * in + k]) * w[size_t(k) * W + h * dim + d];
+                z[i * W + h * dim + d] = v;
+                l += v * al[h * dim + d];
+                r += v * ar[h * dim + d];
+            }
+            left[i * K + h] = l;
+            right[i * K + h] = r;
+        }
+    }
+    #pragma omp parallel
+    {
+        std::vector<double> sc;
+        #pragma omp for schedule(dynamic, 64)
+        for (uint64_t i = 0; i < n; ++i) {
+            const uint64_t b = row[i], deg = row[i + 1] - b;
+            for (int h = 0; h < K; ++h) {
+                sc.assign(deg, 0.0);
+                double m = -INFINITY, dn = 0;
+                for (uint64_t e = 0; e < deg; ++e) {
+                    double v = left[i * K + h] + right[size_t(col[b + e]) * K + h];
+                    v = v >= 0 ? v : .2 * v;
+                    sc[e] = v;
+                    m = std::max(m, v);
+                }
+                for (auto& v : sc) {
+                    v = std::exp(v - m);
+                    dn += v;
+                }
+                mx[i * K + h] = deg ? m : 0.0;
+                den[i * K + h] = dn;
+                for (int d = 0; d < dim; ++d) {
+                    double s = 0;
+                    for (uint64_t e = 0; e < deg; ++e) s += sc[e] * z[size_t(col[b + e]) * W + h * dim + d];
+                    double o = dn > 0 ? s / dn : 0.0;
+                    if (hidden && o < 0) o = std::expm1(o);
+                    out[i * W + h * dim + d] = o;
+                }
+            }
+        }
+    }
+}
+
+// ---------------------------------------------------------------- B0 (CPU baseline)
+// Strong standard GAT layer: baseline/src/baseline_standard.cpp:98-108 stage
+// order: convert (bf16 only) -> projection -> lr_from_z -> max_prescan ->
+// standard_aggregate -> finish.  bf16 != 0 is the standard_bf16 semantics
+// (RNE X and W, FP32 accumulate, FP32 Z and softmax state); bf16 == 0 is
+// standard_fp32.  times[7] receives convert, projection, lr, max_prescan,
+// aggregate, finish, total in milliseconds.  threads <= 0 keeps OpenMP's default.
+// wq (bf16 weights as FP32 values) is prepared by the caller outside the timer,
+// as prepare() does in baseline/src/common.cpp:97-119.
+void or_standard_layer(uint64_t n, const uint64_t* row, const uint32_t* col, const float* x, int in,
+                       int heads, int dim, const float* w, const float* al, const float* ar, int hidden,
+                       int bf16, int threads, float* xq_scratch, float* z, float* left, float* right,
+                       float* mx, float* den, float* out, double* times) {
+    if (threads > 0) omp_set_num_threads(threads);
+    const int K = heads, W = heads * dim;
+    const float* xin = x;
+    auto t0 = Clock::now(), t = t0;
+    // convert: common.cpp:85-93 (the bf16 value is kept widened to FP32).
+    if (bf16) {
+        const uint64_t cnt = n * uint64_t(in);
+        #pragma omp parallel for schedule(static)
+        for (uint64_t i = 0; i < cnt; ++i) xq_scratch[i] = expand(rne(x[i]));
+        xin = xq_scratch;
+    }
+    times[0] = ms_since(t);
+    t = Clock::now();
+    // projection: register-blocked FP32 GEMM, 4 rows x 32 columns per step.
+    // bf16 products are exact in FP32, so this equals BF16xBF16->FP32 up to
+    // the accumulation order.
+    {
+        const int RB = 4, CB = 32;
+        const uint64_t row_blocks = (n + RB - 1) / RB;
+        const int col_blocks = (W + CB - 1) / CB;
+        #pragma omp parallel for schedule(static) collapse(2)
+        for (uint64_t rb = 0; rb < row_blocks; ++rb)
+            for (int cb = 0; cb < col_blocks; ++cb) {
+                const uint64_t r0 = rb * RB;
+                const int rows = int(std::min<uint64_t>(RB, n - r0));
+                const int c0 = cb * CB, cols = std::min(CB, W - c0);
+                float acc[RB][CB] = {};
+                for (int k = 0; k < in; ++k) {
+                    const float* wk = w + size_t(k) * W + c0;
+                    for (int r = 0; r < RB; ++r) {
+                        const float a = r < rows ? xin[(r0 + r) * in + k] : 0.0f;
+                        #pragma omp simd
+                        for (int c = 0; c < CB; ++c) acc[r][c] += a * (c < cols ? wk[c] : 0.0f);
+                    }
+                }
+                for (int r = 0; r < rows; ++r)
+                    for (int c = 0; c < cols; ++c) z[(r0 + r) * W + c0 + c] = acc[r][c];
+            }
+    }
+    times[1] = ms_since(t);
+    t = Clock::now();
+    // lr_from_z: baseline_standard.cpp:7-20.
+    #pragma omp parallel for schedule(static)
+    for (uint64_t i = 0; i < n; ++i)
+        for (int h = 0; h < K; ++h) {
+            float l = 0, r = 0;
+            #pragma omp simd reduction(+ : l, r)
+            for (int d = 0; d < dim; ++d) {
+                l += z[i * W + h * dim + d] * al[h * dim + d];
+                r += z[i * W + h * dim + d] * ar[h * dim + d];
+            }
+            left[i * K + h] = l;
+            right[i * K + h] = r;
+        }
+    times[2] = ms_since(t);
+    t = Clock::now();
+    // max_prescan: baseline_standard.cpp:44-51 (exact max; empty row -> 0).
+    #pragma omp parallel for schedule(dynamic, 64)
+    for (uint64_t i = 0; i < n; ++i) {
+        float m[8];
+        for (int h = 0; h < K; ++h) m[h] = -std::numeric_limits<float>::infinity();
+        for (uint64_t e = row[i]; e < row[i + 1]; ++e)
+            for (int h = 0; h < K; ++h) m[h] = std::max(m[h], right[size_t(col[e]) * K + h]);
+        for (int h = 0; h < K; ++h) mx[i * K + h] = row[i] == row[i + 1] ? 0.0f : leak(m[h] + left[i * K + h]);
+    }
+    times[3] = ms_since(t);
+    t = Clock::now();
+    // standard_aggregate: baseline_standard.cpp:52-84 (one owner per row,
+    // unnormalised sum and FP32 denominator).
+    #pragma omp parallel
+    {
+        std::vector<float> acc(W);
+        #pragma omp for schedule(dynamic, 64)
+        for (uint64_t i = 0; i < n; ++i) {
+            std::fill(acc.begin(), acc.end(), 0.0f);
+            float dn[8] = {}, l[8], m[8], wgt[8];
+            for (int h = 0; h < K; ++h) {
+                l[h] = left[i * K + h];
+                m[h] = mx[i * K + h];
+            }
+            for (uint64_t e = row[i]; e < row[i + 1]; ++e) {
+                const size_t j = col[e];
+                for (int h = 0; h < K; ++h) {
+                    wgt[h] = exp_cw(leak(l[h] + right[j * K + h]) - m[h]);
+                    dn[h] += wgt[h];
+                }
+                const float* zj = z + j * W;
+                for (int h = 0; h < K; ++h) {
+                    const float f = wgt[h];
+                    float* a = acc.data() + h * dim;
+                    const float* zz = zj + h * dim;
+                    #pragma omp simd
+                    for (int d = 0; d < dim; ++d) a[d] += f * zz[d];
+                }
+            }
+            for (int h = 0; h < K; ++h) den[i * K + h] = dn[h];
+            std::copy(acc.begin(), acc.end(), out + i * W);
+        }
+    }
+    times[4] = ms_since(t);
+    t = Clock::now();
+    // finish: baseline_standard.cpp:85-97 (normalise, then ELU on hidden layers).
+    #pragma omp parallel for schedule(static)
+    for (uint64_t i = 0; i < n; ++i)
+        for (int h = 0; h < K; ++h) {
+            const float dn = den[i * K + h];
+            const float s = dn > 0 ? 1 / dn : 0;
+            float* o = out + i * W + h * dim;
+            for (int d = 0; d < dim; ++d) {
+                float v = o[d] * s;
+                if (hidden && v < 0) v = expm1_neg(v);
+                o[d] = v;
+            }
+        }
+    times[5] = ms_since(t);
+    times[6] = ms_since(t0);
+}
+
+// ---------------------------------------------------------------- schedule
+// degree_schedule: baseline/src/common.cpp:120-125 (perm[sorted]=original row,
+// ascending (degree, id); neighbor_steps = sum over 16-row tiles of the last
+// row's degree).  Same order as degree_perm in
+// implementation/src/gat_tfs_online.cpp:180-189.
+void or_degree_schedule(uint64_t n, const uint64_t* row, uint32_t* perm, uint64_t* neighbor_steps) {
+    std::iota(perm, perm + n, 0u);
+    std::sort(perm, perm + n, [&](uint32_t a, uint32_t b) {
+        auto da = row[a + 1] - row[a], db = row[b + 1] - row[b];
+        return da != db ? da < db : a < b;
+    });
+    uint64_t steps = 0;
+    for (uint64_t base = 0; base < n; base += 16) {
+        uint32_t r = perm[std::min<uint64_t>(n, base + 16) - 1];
+        steps += row[r + 1] - row[r];
+    }
+    *neighbor_steps = steps;
+}
+// CSR in degree-sorted order: prow[k] = sum of degrees of perm[0..k),
+// pcol[prow[k]..prow[k+1]) = col[row[perm[k]]..row[perm[k]+1]).
+void or_permute_csr(uint64_t n, const uint64_t* row, const uint32_t* col, const uint32_t* perm,
+                    uint64_t* prow, uint32_t* pcol) {
+    prow[0] = 0;
+    for (uint64_t k = 0; k < n; ++k) {
+        const uint64_t b = row[perm[k]], deg = row[perm[k] + 1] - b;
+        std::copy(col + b, col + b + deg, pcol + prow[k]);
+        prow[k + 1] = prow[k] + deg;
+    }
+}
+// choose_R: implementation/src/gat_tfs_online.cpp:191-199.
+int or_choose_R(uint64_t n, uint64_t e, const uint64_t* row) {
+    uint64_t maxdeg = 0;
+    for (uint64_t i = 0; i < n; ++i) maxdeg = std::max(maxdeg, row[i + 1] - row[i]);
+    double avg = double(e) / n, rho = avg ? maxdeg / avg : 1.0;
+    if (rho < 32) return 128;
+    if (rho < 1024) return 64;
+    if (rho < 20000) return 32;
+    return 16;
+}
+
+// ---------------------------------------------------------------- metrics
+// errors(): baseline/src/common.cpp:141-150.  out = {max_abs, mean_abs,
+// relative_l2, rmse, p50, p90, p99}; returns 1 if every value is finite.
+int or_errors(const float* ref, const float* got, uint64_t n, double* out) {
+    std::vector<double> a;
+    a.reserve(n);
+    double sq = 0, dsum = 0, mx = 0, mean = 0;
+    bool finite = true;
+    for (uint64_t i = 0; i < n; ++i) {
+        if (!std::isfinite(ref[i]) || !std::isfinite(got[i])) {
+            finite = false;
+            continue;
+        }
+        double d = double(got[i]) - ref[i], v = std::abs(d);
+        mx = std::max(mx, v);
+        mean += v;
+        sq += d * d;
+        dsum += double(ref[i]) * ref[i];
+        a.push_back(v);
+    }
+    if (!finite || n == 0) {
+        for (int k = 0; k < 7; ++k) out[k] = std::numeric_limits<double>::infinity();
+        return 0;
+    }
+    out[0] = mx;
+    out[1] = mean / n;
+    out[2] = dsum > 0 ? std::sqrt(sq / dsum) : (sq == 0 ? 0 : std::numeric_limits<double>::infinity());
+    out[3] = std::sqrt(sq / n);
+    auto pct = [&](double q) {
+        size_t k = std::min(a.size() - 1, size_t(std::ceil(q * a.size()) - 1));
+        std::nth_element(a.begin(), a.begin() + k, a.end());
+        return a[k];
+    };
+    out[4] = pct(.5);
+    out[5] = pct(.9);
+    out[6] = pct(.99);
+    return 1;
+}
+
+int or_max_threads() { return omp_get_max_threads(); }
+}

@@ -1,0 +1,216 @@
+"""Parity of the gfx950 path (through the C ABI) with the CPU oracle.
+
+Gates: FP32 path max-abs <= 1e-4 (and rel-L2 <= 1e-4 where the reference's
+boundary test uses it) against R0; bf16 path rel-L2 <= 1e-2 against R0 FP32;
+the degree permutation, neighbor_steps and the permuted CSR bit-exact.
+"""
+import numpy as np
+import pytest
+
+import gatgpu
+import oracle
+from gatgpu import inputs
+from make_smoke1024 import smoke1024
+
+pytestmark = pytest.mark.gpu
+
+FP32_MAX_ABS = 1e-4
+BF16_REL_L2 = 1e-2
+
+
+def run_layer(ctx, row, col, x, p, hidden, precision, block_min=None):
+    ctx.set_graph(row, col)
+    if block_min is not None:
+        ctx.set_option(gatgpu.OPT_BLOCK_ROW_MIN_DEGREE, block_min)
+    ctx.set_layer(0, p)
+    ctx.set_input(x)
+    ctx.layer_forward(0, precision, gatgpu.TRANSFORM_FIRST, hidden)
+    out = {k: ctx.stage(0, k) for k in ("left", "right", "max", "den", "out")}
+    if block_min is not None:
+        ctx.set_option(gatgpu.OPT_BLOCK_ROW_MIN_DEGREE, 512)
+    return out
+
+
+# ---------------------------------------------------------------- schedule
+def schedule_graphs():
+    yield "boundary35", oracle.boundary_graph(17)["row"], oracle.boundary_graph(17)["col"]
+    g = smoke1024()
+    yield "smoke1024", g["row"], g["col"]
+    for name in ("smoke", "arxiv", "large"):
+        row, col = inputs.WORKLOADS[name].graph()
+        yield name, row, col
+
+
+@pytest.mark.parametrize("case", ["boundary35", "smoke1024", "smoke", "arxiv", "large"])
+def test_degree_schedule_bit_exact(gpu_ctx, case):
+    row, col = next((r, c) for n, r, c in schedule_graphs() if n == case)
+    gpu_ctx.set_graph(row, col)
+    perm, steps = gpu_ctx.degree_schedule()
+    operm, osteps = oracle.degree_schedule(row)
+    assert np.array_equal(perm, operm)
+    assert steps == osteps
+    prow, pcol = gpu_ctx.permuted_csr()
+    oprow, opcol = oracle.permute_csr(row, col, operm)
+    assert np.array_equal(prow, oprow)
+    assert np.array_equal(pcol, opcol)
+    assert gpu_ctx.choose_R() == oracle.choose_R(row)
+
+
+# ---------------------------------------------------------------- boundary shapes
+SHAPES = [(D, K, d) for D in (17, 33, 128, 256) for K in (1, 2, 4, 8) for d in (7, 32, 40, 47)]
+
+
+@pytest.mark.parametrize("D,K,d", SHAPES)
+def test_boundary_shapes_fp32(gpu_ctx, D, K, d):
+    """baseline/tests/boundaries.cpp:27-35 on the GPU path: FP32 within 1e-4 of
+    R0 (max-abs and rel-L2), exact zeros for the empty row, and the row max
+    equal bit for bit to the scalar max of LeakyReLU(L+R) over the GPU's own L/R."""
+    g = oracle.boundary_graph(D)
+    p = oracle.boundary_param(D, K, d)
+    r = oracle.ref_layer(g["row"], g["col"], g["x"], p, False)
+    for block_min in (512, 1):
+        got = run_layer(gpu_ctx, g["row"], g["col"], g["x"], p, False, gatgpu.FP32, block_min)
+        e = oracle.errors(r["out"], got["out"])
+        assert e["finite"] and e["max_abs"] < FP32_MAX_ABS and e["relative_l2"] < FP32_MAX_ABS, (block_min, e)
+        for k in ("left", "right", "max"):
+            assert oracle.errors(r[k], got[k])["max_abs"] < FP32_MAX_ABS, k
+        assert oracle.errors(r["den"], got["den"])["relative_l2"] < 1e-5
+        assert np.all(got["out"][0] == 0) and np.all(got["den"][0] == 0)
+        row, col = g["row"], g["col"]
+        L, R = got["left"], got["right"]
+        for i in range(g["n"]):
+            b, e_ = int(row[i]), int(row[i + 1])
+            sc = L[i][None, :] + R[col[b:e_]]
+            sc = np.where(sc >= 0, sc, np.float32(0.2) * sc).astype(np.float32)
+            m = np.zeros(K, np.float32) if b == e_ else sc.max(axis=0)
+            assert np.array_equal(m, got["max"][i])
+
+
+@pytest.mark.parametrize("D,K,d", [(17, 8, 7), (128, 8, 32), (256, 1, 47), (33, 4, 40)])
+def test_boundary_shapes_bf16_and_hidden(gpu_ctx, D, K, d):
+    g = oracle.boundary_graph(D)
+    p = oracle.boundary_param(D, K, d)
+    for hidden in (False, True):
+        r = oracle.ref_layer(g["row"], g["col"], g["x"], p, hidden)
+        got = run_layer(gpu_ctx, g["row"], g["col"], g["x"], p, hidden, gatgpu.FP32)
+        assert oracle.errors(r["out"], got["out"])["max_abs"] < FP32_MAX_ABS
+        got = run_layer(gpu_ctx, g["row"], g["col"], g["x"], p, hidden, gatgpu.BF16)
+        e = oracle.errors(r["out"], got["out"])
+        assert e["finite"] and e["relative_l2"] < BF16_REL_L2, e
+        assert np.all(got["out"][0] == 0)
+
+
+def test_adversarial_scores(gpu_ctx):
+    """boundaries.cpp:44-52 through inputs (see test_oracle.adversarial_layer)."""
+    from test_oracle import adversarial_layer
+
+    g = oracle.boundary_graph(2)
+    deg = np.diff(g["row"])
+    for scenario in range(5):
+        x, p = adversarial_layer(g["n"], scenario)
+        got = run_layer(gpu_ctx, g["row"], g["col"], x, p, False, gatgpu.FP32)
+        assert np.isfinite(got["out"]).all(), scenario
+        assert np.all(got["den"][deg == 0] == 0)
+        assert np.all(got["den"][deg > 0] >= 1), scenario
+        r = oracle.ref_layer(g["row"], g["col"], x, p, False)
+        scale = max(1.0, float(np.abs(r["out"]).max()))
+        assert oracle.errors(r["out"], got["out"])["max_abs"] < FP32_MAX_ABS * scale, scenario
+
+
+# ---------------------------------------------------------------- full models
+def model_parity(ctx, row, col, x, model, precision):
+    ctx.set_graph(row, col)
+    ctx.set_model(model)
+    ctx.set_input(x)
+    logits, times, total = ctx.model_forward(precision, gatgpu.AUTO)
+    ref = oracle.ref_model(row, col, x, model)
+    return logits, ref, times, total
+
+
+def test_smoke1024_model_fp32_and_checksum(gpu_ctx):
+    g = smoke1024()
+    m = oracle.random_model(128, 40, 11)
+    logits, ref, times, total = model_parity(gpu_ctx, g["row"], g["col"], g["x"], m, gatgpu.FP32)
+    e = oracle.errors(ref[2]["out"], logits)
+    assert e["finite"] and e["max_abs"] < FP32_MAX_ABS, e
+    assert abs(float(logits.astype(np.float64).sum()) - 221.971286) < 1e-3
+    assert total > 0 and all(t["aggregate_ms"] > 0 for t in times)
+    for l in range(3):
+        for k in ("left", "right", "max", "den"):
+            s = gpu_ctx.stage(l, k)
+            assert oracle.errors(ref[l][k], s)["relative_l2"] < 1e-5, (l, k)
+
+
+def test_smoke1024_model_bf16(gpu_ctx):
+    g = smoke1024()
+    m = oracle.random_model(128, 40, 11)
+    logits, ref, _, _ = model_parity(gpu_ctx, g["row"], g["col"], g["x"], m, gatgpu.BF16)
+    e = oracle.errors(ref[2]["out"], logits)
+    assert e["finite"] and e["relative_l2"] < BF16_REL_L2, e
+
+
+@pytest.mark.parametrize("name", ["smoke", "arxiv"])
+@pytest.mark.parametrize("precision", [gatgpu.FP32, gatgpu.BF16])
+def test_workload_model_parity(gpu_ctx, name, precision):
+    w = inputs.WORKLOADS[name]
+    row, col = w.graph()
+    x = w.features()
+    m = w.model()
+    logits, ref, _, _ = model_parity(gpu_ctx, row, col, x, m, precision)
+    e = oracle.errors(ref[2]["out"], logits)
+    if precision == gatgpu.FP32:
+        assert e["finite"] and e["max_abs"] < FP32_MAX_ABS, e
+    else:
+        assert e["finite"] and e["relative_l2"] < BF16_REL_L2, e
+
+
+def test_layer2_micro_fp32(gpu_ctx):
+    """Single layer 256 -> 8x32 on the arxiv-sized graph, N(0,1) input."""
+    w = inputs.WORKLOADS["arxiv"]
+    row, col = w.graph()
+    x = inputs.normal((w.n, 256), 5)
+    p = inputs.glorot_param(256, 8, 32, 6)
+    gpu_ctx.set_graph(row, col)
+    gpu_ctx.set_layer(1, p)
+    gpu_ctx.layer_forward(1, gatgpu.FP32, gatgpu.TRANSFORM_FIRST, True, input=x)
+    got = gpu_ctx.stage(1, "out")
+    r = oracle.ref_layer(row, col, x, p, True)
+    e = oracle.errors(r["out"], got)
+    assert e["finite"] and e["max_abs"] < FP32_MAX_ABS, e
+
+
+# ---------------------------------------------------------------- error codes
+def test_error_codes(gpu_ctx):
+    g = oracle.boundary_graph(17)
+    row, col = g["row"].copy(), g["col"].copy()
+    bad = row.copy()
+    bad[3] = bad[-1] + 1
+    with pytest.raises(gatgpu.GatGpuError) as err:
+        gpu_ctx.set_graph(bad, col)
+    assert err.value.code == gatgpu.EINVAL
+    badc = col.copy()
+    badc[0] = g["n"]
+    with pytest.raises(gatgpu.GatGpuError) as err:
+        gpu_ctx.set_graph(row, badc)
+    assert err.value.code == gatgpu.EINVAL
+    gpu_ctx.set_graph(row, col)
+    x = g["x"].copy()
+    x[0, 0] = np.nan
+    with pytest.raises(gatgpu.GatGpuError) as err:
+        gpu_ctx.set_input(x)
+    assert err.value.code == gatgpu.ENONFINITE
+    p = oracle.boundary_param(17, 8, 7)
+    for heads, dim in ((9, 7), (8, 65)):
+        q = dict(p, heads=heads, dim=dim, w=np.zeros((17, heads * dim), np.float32),
+                 al=np.zeros(heads * dim, np.float32), ar=np.zeros(heads * dim, np.float32))
+        with pytest.raises(gatgpu.GatGpuError) as err:
+            gpu_ctx.set_layer(0, q)
+        assert err.value.code == gatgpu.EINVAL
+    with pytest.raises(gatgpu.GatGpuError) as err:
+        gpu_ctx.set_layer(3, p)
+    assert err.value.code == gatgpu.EINVAL
+    ctx2 = gatgpu.Context(0)
+    with pytest.raises(gatgpu.GatGpuError) as err:
+        ctx2.layer_forward(0)
+    assert err.value.code == gatgpu.ESTATE
+    ctx2.close()
