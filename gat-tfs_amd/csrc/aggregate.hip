@@ -60,7 +60,7 @@ __device__ inline float range_max(uint64_t beg, uint64_t end, const uint32_t* __
 template <class ZT, int NF>
 __device__ inline void range_accumulate(uint64_t beg, uint64_t end, const uint32_t* __restrict__ pcol,
                                         const float* __restrict__ R, const ZT* __restrict__ Z, int K,
-                                        int W, float Lh, float Mh, const Lanes& ln, float* pbuf,
+                                        int W, int zs, float Lh, float Mh, const Lanes& ln, float* pbuf,
                                         uint32_t* jbuf, const int (&fhead)[NF], float (&acc)[NF],
                                         float& dloc) {
     const int lane = threadIdx.x % kWave;
@@ -77,7 +77,7 @@ __device__ inline void range_accumulate(uint64_t beg, uint64_t end, const uint32
         const uint64_t rem = end - base;
         const int cnt = rem < uint64_t(ln.eb_count) ? int(rem) : ln.eb_count;
         for (int t = 0; t < cnt; ++t) {
-            const ZT* zr = Z + uint64_t(jbuf[t]) * W;
+            const ZT* zr = Z + uint64_t(jbuf[t]) * zs;
 #pragma unroll
             for (int q = 0; q < NF; ++q) {
                 const int f = lane + kWave * q;
@@ -112,7 +112,7 @@ struct KArgs {
     const float* L;
     const float* R;
     const ZT* Z;
-    int K, dim;
+    int K, dim, zs;
     bool hidden;
     float* mx;
     float* den;
@@ -149,7 +149,7 @@ __global__ void __launch_bounds__(kThreads) k_agg_wave(KArgs<ZT> a, uint64_t k_b
         acc[q] = 0.0f;
     }
     float dloc = 0.0f;
-    range_accumulate<ZT, NF>(beg, end, a.pcol, a.R, a.Z, K, W, Lh, Mh, ln, pbuf[w], jbuf[w], fhead, acc,
+    range_accumulate<ZT, NF>(beg, end, a.pcol, a.R, a.Z, K, W, a.zs, Lh, Mh, ln, pbuf[w], jbuf[w], fhead, acc,
                              dloc);
     for (int off = ln.kp; off < kWave; off <<= 1) dloc += __shfl_xor(dloc, off);
     if (lane < K) {
@@ -196,7 +196,7 @@ __global__ void __launch_bounds__(kThreads) k_agg_block(KArgs<ZT> a, uint64_t k_
         acc[q] = 0.0f;
     }
     float dloc = 0.0f;
-    range_accumulate<ZT, NF>(q0, q1, a.pcol, a.R, a.Z, K, W, Lh, Mh, ln, pbuf[w], jbuf[w], fhead, acc,
+    range_accumulate<ZT, NF>(q0, q1, a.pcol, a.R, a.Z, K, W, a.zs, Lh, Mh, ln, pbuf[w], jbuf[w], fhead, acc,
                              dloc);
     for (int off = ln.kp; off < kWave; off <<= 1) dloc += __shfl_xor(dloc, off);
     if (lane < K) dsh[w][lane] = dloc;
@@ -225,7 +225,7 @@ __global__ void __launch_bounds__(kThreads) k_agg_block(KArgs<ZT> a, uint64_t k_
 template <class ZT, int NF>
 hipError_t dispatch(const AggArgs& g, const RowBins& bins, hipStream_t s) {
     KArgs<ZT> a{g.prow, g.pcol, g.perm, g.left, g.right, static_cast<const ZT*>(g.feat), g.heads, g.dim,
-                g.hidden, g.mx, g.den, g.out32, g.outbf, g.n, g.e};
+                g.fstride, g.hidden, g.mx, g.den, g.out32, g.outbf, g.n, g.e};
     // v1: every row below block_begin takes a wave; the rest a block each.
     const uint64_t wave_rows = bins.block_begin;
     if (wave_rows) {
@@ -249,10 +249,12 @@ hipError_t dispatch_nf(const AggArgs& g, const RowBins& bins, hipStream_t s) {
 
 }  // namespace
 
-hipError_t launch_aggregate_tf(const AggArgs& a, const RowBins& bins, uint32_t split_chunk,
+hipError_t launch_aggregate_tf(const AggArgs& a, const RowBins& bins, const SplitTable& split,
                                hipStream_t s) {
-    (void)split_chunk;
     if (a.heads < 1 || a.heads > 8 || a.dim < 1 || a.heads * a.dim > 512) return hipErrorInvalidValue;
+    if (aggregate_vec_supported(a)) return launch_aggregate_vec(a, bins, split, s);
+    // Generic path: a wave per row below block_begin, a block per row above
+    // (split rows included).
     return a.feat_bf16 ? dispatch_nf<uint16_t>(a, bins, s) : dispatch_nf<float>(a, bins, s);
 }
 

@@ -53,6 +53,9 @@ struct LayerState {
     // What the last forward of this layer produced.
     bool ran = false, z_valid = false, out32_valid = false, outbf_valid = false;
     int precision = -1;
+    // bf16 MFMA projection weights (pack_projection_weights order)
+    DevBuf wpk;
+    int ksteps = 0, groups = 0, nmb = 0;
     int width() const { return heads * dim; }
 };
 
@@ -79,9 +82,12 @@ struct gatgpu_ctx {
     // options (in-degree thresholds)
     uint32_t small_max = 0;          // rows <= this share a wave (0: off)
     uint32_t block_min = 512;        // rows >= this take a block
-    uint32_t split_min = 0xffffffffu;  // rows >= this are split over blocks
-    uint32_t split_chunk = 2048;
+    uint32_t split_min = 1024;         // rows >= this are split into chunks
+    uint32_t split_chunk = 256;        // edges per chunk of a split row
+    DevBuf split_k, split_first, mchunk, part, counter;
+    SplitTable split;
     hipEvent_t ev[16] = {};
+    int cus = 256;  // compute units of the device
 };
 
 namespace {
@@ -139,6 +145,41 @@ int compute_bins(gatgpu_ctx* c) {
     if (b.block_begin < b.small_end) b.block_begin = b.small_end;
     if (b.split_begin < b.block_begin) b.split_begin = b.block_begin;
     c->bins = b;
+    // Chunk table of the split rows, heaviest row first.
+    const uint64_t nsplit = b.n - b.split_begin;
+    std::vector<uint64_t> prow(nsplit + 1);
+    if (nsplit)
+        HIPCHECK(c, hipMemcpy(prow.data(), c->prow.as<uint64_t>() + b.split_begin, (nsplit + 1) * 8,
+                              hipMemcpyDeviceToHost));
+    std::vector<uint32_t> ck, cf;
+    for (uint64_t q = nsplit; q-- > 0;) {
+        const uint64_t deg = prow[q + 1] - prow[q];
+        const uint64_t nch = (deg + c->split_chunk - 1) / c->split_chunk;
+        const uint32_t first = uint32_t(ck.size());
+        for (uint64_t t = 0; t < nch; ++t) {
+            ck.push_back(uint32_t(b.split_begin + q));
+            cf.push_back(first);
+        }
+    }
+    SplitTable& t = c->split;
+    t = SplitTable{};
+    t.chunks = ck.size();
+    t.chunk_edges = c->split_chunk;
+    if (t.chunks) {
+        HIPCHECK(c, c->split_k.ensure(ck.size() * 4));
+        HIPCHECK(c, c->split_first.ensure(cf.size() * 4));
+        HIPCHECK(c, c->mchunk.ensure(ck.size() * 8 * 4));
+        HIPCHECK(c, c->part.ensure(ck.size() * (512 + 8) * 4));
+        HIPCHECK(c, c->counter.ensure(ck.size() * 4));
+        HIPCHECK(c, hipMemcpy(c->split_k.p, ck.data(), ck.size() * 4, hipMemcpyHostToDevice));
+        HIPCHECK(c, hipMemcpy(c->split_first.p, cf.data(), cf.size() * 4, hipMemcpyHostToDevice));
+        HIPCHECK(c, hipMemset(c->counter.p, 0, ck.size() * 4));
+        t.chunk_k = c->split_k.as<uint32_t>();
+        t.chunk_first = c->split_first.as<uint32_t>();
+        t.mchunk = c->mchunk.as<float>();
+        t.part = c->part.as<float>();
+        t.counter = c->counter.as<uint32_t>();
+    }
     return GATGPU_OK;
 }
 
@@ -225,27 +266,55 @@ int run_layer(gatgpu_ctx* c, int l, int precision, int dataflow, bool hidden, co
     const bool want_outbf = bf16 && hidden;
     if (want_outbf) HIPCHECK(c, Ls.outbf.ensure(n * W * 2));
     else HIPCHECK(c, Ls.out32.ensure(n * W * 4));
+    // bf16 path: X as [n][xs] bf16 (xs = ksteps*16, zero-padded), Z as [n][zs]
+    // bf16 (zs = W rounded up to 8 for aligned vector stores).
+    const int xs = Ls.ksteps * 16;
+    const int zs = bf16 ? (W + 7) / 8 * 8 : W;
     if (bf16) {
-        HIPCHECK(c, Ls.zbf.ensure(n * W * 2));
-        HIPCHECK(c, Ls.zscratch.ensure(n * W * 4));
+        HIPCHECK(c, Ls.zbf.ensure(n * zs * 2));
+        if (srcbf && D != xs) {  // chained bf16 input without the padded layout
+            HIPCHECK(c, Ls.in32.ensure(n * D * 4));
+            HIPCHECK(c, launch_widen_bf16(srcbf, Ls.in32.as<float>(), n * D, c->stream));
+            src32 = Ls.in32.as<float>();
+            srcbf = nullptr;
+        }
+        if (src32) HIPCHECK(c, Ls.inbf.ensure(n * xs * 2));
     } else {
         HIPCHECK(c, Ls.z32.ensure(n * W * 4));
     }
-    if (bf16 && src32) HIPCHECK(c, Ls.inbf.ensure(n * D * 2));
     if (ev_base >= 0) HIPCHECK(c, hipEventRecord(c->ev[ev_base], c->stream));
     // ---- convert (bf16 path, FP32 source only; a bf16 source was rounded in
     // the previous layer's epilogue, which equals convert() of that output)
     if (bf16 && src32) {
-        HIPCHECK(c, launch_to_bf16(src32, Ls.inbf.as<uint16_t>(), n * D, c->stream));
+        HIPCHECK(c, launch_to_bf16_pad(src32, Ls.inbf.as<uint16_t>(), n, D, xs, c->stream));
         srcbf = Ls.inbf.as<uint16_t>();
         src32 = nullptr;
     }
     if (ev_base >= 0) HIPCHECK(c, hipEventRecord(c->ev[ev_base + 1], c->stream));
     // ---- projection + L/R
-    HIPCHECK(c, launch_projection(src32, srcbf, bf16 ? Ls.wq32.as<float>() : Ls.w32.as<float>(), n, D, K,
-                                  dim, Ls.al.as<float>(), Ls.ar.as<float>(), bf16 ? nullptr : Ls.z32.as<float>(),
-                                  bf16 ? Ls.zbf.as<uint16_t>() : nullptr, Ls.left.as<float>(),
-                                  Ls.right.as<float>(), Ls.zscratch.as<float>(), c->stream));
+    if (bf16) {
+        ProjArgs pa{};
+        pa.x = srcbf;
+        pa.n = n;
+        pa.xs = xs;
+        pa.ksteps = Ls.ksteps;
+        pa.wpk = Ls.wpk.as<uint4>();
+        pa.groups = Ls.groups;
+        pa.head_blocks = (W + 31) / 32;
+        pa.nmb = Ls.nmb;
+        pa.width = W;
+        pa.heads = K;
+        pa.z = Ls.zbf.as<uint16_t>();
+        pa.zs = zs;
+        pa.left = Ls.left.as<float>();
+        pa.right = Ls.right.as<float>();
+        pa.tiles = (n + 31) / 32;
+        HIPCHECK(c, launch_projection_mfma(pa, c->stream, c->cus));
+    } else {
+        HIPCHECK(c, launch_projection(src32, nullptr, Ls.w32.as<float>(), n, D, K, dim, Ls.al.as<float>(),
+                                      Ls.ar.as<float>(), Ls.z32.as<float>(), nullptr, Ls.left.as<float>(),
+                                      Ls.right.as<float>(), nullptr, c->stream));
+    }
     if (ev_base >= 0) HIPCHECK(c, hipEventRecord(c->ev[ev_base + 2], c->stream));
     // ---- fused prescan + softmax + aggregation + normalise + ELU
     AggArgs a{};
@@ -256,6 +325,7 @@ int run_layer(gatgpu_ctx* c, int l, int precision, int dataflow, bool hidden, co
     a.right = Ls.right.as<float>();
     a.feat = bf16 ? static_cast<const void*>(Ls.zbf.p) : Ls.z32.p;
     a.feat_bf16 = bf16;
+    a.fstride = zs;
     a.heads = K;
     a.dim = dim;
     a.hidden = hidden;
@@ -265,7 +335,7 @@ int run_layer(gatgpu_ctx* c, int l, int precision, int dataflow, bool hidden, co
     a.outbf = want_outbf ? Ls.outbf.as<uint16_t>() : nullptr;
     a.n = c->n;
     a.e = c->e;
-    HIPCHECK(c, launch_aggregate_tf(a, c->bins, c->split_chunk, c->stream));
+    HIPCHECK(c, launch_aggregate_tf(a, c->bins, c->split, c->stream));
     if (ev_base >= 0) HIPCHECK(c, hipEventRecord(c->ev[ev_base + 3], c->stream));
     Ls.ran = true;
     Ls.precision = precision;
@@ -307,6 +377,7 @@ int gatgpu_create(int device, gatgpu_ctx** out) {
     auto* c = new (std::nothrow) gatgpu_ctx;
     if (!c) return fail(nullptr, GATGPU_ENOMEM, "host allocation failed");
     c->device = device;
+    c->cus = prop.multiProcessorCount;
     if (hipSetDevice(device) != hipSuccess || hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking) != hipSuccess) {
         delete c;
         return fail(nullptr, GATGPU_EDEVICE, "cannot create stream");
@@ -390,6 +461,10 @@ int gatgpu_set_layer(gatgpu_ctx* c, int layer, int in, int heads, int dim, const
             blr[size_t(k) * 2 * heads + h] = l;
             blr[size_t(k) * 2 * heads + heads + h] = r;
         }
+    std::vector<uint16_t> packed;
+    pack_projection_weights(wq.data(), al, ar, in, heads, dim, packed, L.ksteps, L.groups, L.nmb);
+    HIPCHECK(c, L.wpk.ensure(packed.size() * 2));
+    HIPCHECK(c, hipMemcpyAsync(L.wpk.p, packed.data(), packed.size() * 2, hipMemcpyHostToDevice, c->stream));
     HIPCHECK(c, L.w32.ensure(wn * 4));
     HIPCHECK(c, L.wq32.ensure(wn * 4));
     HIPCHECK(c, L.al.ensure(W * 4));
@@ -541,7 +616,13 @@ int gatgpu_get_stage(gatgpu_ctx* c, int layer, int which, float* host) {
             src = bf ? L.outbf.p : L.out32.p;
             break;
     }
-    if (bf) {
+    if (bf && which == GATGPU_STAGE_Z) {
+        const int W = L.width(), zs = (W + 7) / 8 * 8;
+        std::vector<uint16_t> tmp(c->n * zs);
+        HIPCHECK(c, hipMemcpy(tmp.data(), src, tmp.size() * 2, hipMemcpyDeviceToHost));
+        for (uint64_t i = 0; i < c->n; ++i)
+            for (int f = 0; f < W; ++f) host[i * W + f] = bf16_widen(tmp[i * zs + f]);
+    } else if (bf) {
         std::vector<uint16_t> tmp(count);
         HIPCHECK(c, hipMemcpy(tmp.data(), src, count * 2, hipMemcpyDeviceToHost));
         for (uint64_t i = 0; i < count; ++i) host[i] = bf16_widen(tmp[i]);
@@ -556,7 +637,10 @@ int gatgpu_set_option(gatgpu_ctx* c, int key, int64_t value) {
     if (value < 0 || value > int64_t(UINT32_MAX)) return fail(c, GATGPU_EINVAL, "option value out of range");
     switch (key) {
         case GATGPU_OPT_BLOCK_ROW_MIN_DEGREE: c->block_min = uint32_t(value); break;
-        case GATGPU_OPT_SPLIT_ROW_MIN_DEGREE: c->split_min = uint32_t(value); break;
+        case GATGPU_OPT_SPLIT_ROW_MIN_DEGREE:
+            if (value < 1) return fail(c, GATGPU_EINVAL, "split threshold must be >= 1 edge");
+            c->split_min = uint32_t(value);
+            break;
         case GATGPU_OPT_SPLIT_CHUNK_EDGES:
             if (value < 64) return fail(c, GATGPU_EINVAL, "split chunk must be >= 64 edges");
             c->split_chunk = uint32_t(value);

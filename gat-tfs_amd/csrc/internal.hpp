@@ -4,6 +4,7 @@
 
 #include <cstdint>
 #include <string>
+#include <vector>
 
 namespace gatgpu {
 
@@ -58,6 +59,8 @@ hipError_t launch_count_le(const uint32_t* sorted_deg, uint64_t n, const uint32_
 // projection.hip
 hipError_t launch_to_bf16(const float* x, uint16_t* y, uint64_t count, hipStream_t s);
 hipError_t launch_widen_bf16(const uint16_t* x, float* y, uint64_t count, hipStream_t s);
+// x [n][d] FP32 -> y [n][dp] bf16 with zero columns d..dp-1.
+hipError_t launch_to_bf16_pad(const float* x, uint16_t* y, uint64_t n, int d, int dp, hipStream_t s);
 // Z = X W with the L/R attention dots and the store of Z (FP32 or bf16).
 // X is FP32 (x32 != null) or bf16 bits (xbf != null); W is FP32 values (for
 // the bf16 path: bf16-rounded values).
@@ -69,6 +72,25 @@ hipError_t launch_projection(const float* x32, const uint16_t* xbf, const float*
 hipError_t launch_lr_reordered(const float* x32, const uint16_t* xbf, const float* blr,
                                uint64_t n, int in, int heads, float* left, float* right,
                                hipStream_t s);
+
+// projection_mfma.hip: bf16 MFMA projection with the fused L/R block.
+struct ProjArgs {
+    const uint16_t* x;   // [n][xs] bf16 input, zero-padded to ksteps*16 columns
+    uint64_t n;
+    int xs;              // row stride of x (elements, multiple of 8)
+    int ksteps;          // ceil(in / 16)
+    const uint4* wpk;    // packed weights, pack_projection_weights() order
+    int groups, head_blocks, nmb, width, heads;
+    uint16_t* z;         // [n][zs] bf16 output
+    int zs;              // row stride of z (elements, multiple of 8, >= width)
+    float* left;         // [n][heads]
+    float* right;        // [n][heads]
+    uint64_t tiles;      // ceil(n / 32)
+};
+int proj_blocks_per_group(int width);
+void pack_projection_weights(const float* wq, const float* al, const float* ar, int in, int heads, int dim,
+                             std::vector<uint16_t>& out, int& ksteps, int& groups, int& nmb);
+hipError_t launch_projection_mfma(const ProjArgs& a, hipStream_t s, int cus);
 
 // aggregate.hip
 struct RowBins {
@@ -85,6 +107,7 @@ struct AggArgs {
     const float* right;  // [n][K]
     const void* feat;    // Z [n][W] (TF) or X [n][D] (AF); FP32 or bf16
     bool feat_bf16;
+    int fstride;         // row stride of feat in elements (>= W)
     int heads, dim;
     bool hidden;
     float* mx;       // [n][K]
@@ -92,10 +115,23 @@ struct AggArgs {
     float* out32;    // [n][W] or null
     uint16_t* outbf; // [n][W] or null
     uint64_t n, e;           // nodes and CSR entries (bounds of perm/prow values)
-    float* acc_scratch;      // split rows: [n_split_rows][W] + [n_split_rows][K]
-    uint32_t* split_counter; // split rows: [n_split_rows]
 };
-hipError_t launch_aggregate_tf(const AggArgs& a, const RowBins& bins, uint32_t split_chunk,
+// Split rows (sorted positions [split_begin, n)) cut into chunks of
+// chunk_edges edges, heaviest rows first; built on the host from prow.
+struct SplitTable {
+    uint64_t chunks = 0;
+    const uint32_t* chunk_k = nullptr;      // [chunks] sorted position of the row
+    const uint32_t* chunk_first = nullptr;  // [chunks] first chunk of that row
+    uint32_t chunk_edges = 256;
+    float* mchunk = nullptr;                // [chunks][8] per-chunk max of R
+    float* part = nullptr;                  // [chunks][W + 8] partial sums
+    uint32_t* counter = nullptr;            // [chunks] arrival counters, zero between launches
+};
+hipError_t launch_aggregate_tf(const AggArgs& a, const RowBins& bins, const SplitTable& split,
                                hipStream_t s);
+// aggregate_vec.hip: 16-byte vector path for 8 heads x (32 | 64).
+bool aggregate_vec_supported(const AggArgs& a);
+hipError_t launch_aggregate_vec(const AggArgs& a, const RowBins& bins, const SplitTable& split,
+                                hipStream_t s);
 
 }  // namespace gatgpu

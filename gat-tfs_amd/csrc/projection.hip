@@ -21,6 +21,18 @@ k_to_bf16(const float* __restrict__ x, uint16_t* __restrict__ y, uint64_t count)
         y[i] = bf16_rne(x[i]);
 }
 
+// x [n][d] FP32 -> y [n][dp] bf16, columns d..dp-1 zero.
+__global__ void __launch_bounds__(kThreads)
+k_to_bf16_pad(const float* __restrict__ x, uint16_t* __restrict__ y, uint64_t n, int d, int dp) {
+    const uint64_t count = n * uint64_t(dp);
+    for (uint64_t i = blockIdx.x * uint64_t(kThreads) + threadIdx.x; i < count;
+         i += uint64_t(gridDim.x) * kThreads) {
+        const uint64_t r = i / dp;
+        const int c = int(i - r * dp);
+        y[i] = c < d ? bf16_rne(x[r * d + c]) : uint16_t(0);
+    }
+}
+
 __global__ void __launch_bounds__(kThreads)
 k_widen_bf16(const uint16_t* __restrict__ x, float* __restrict__ y, uint64_t count) {
     for (uint64_t i = blockIdx.x * uint64_t(kThreads) + threadIdx.x; i < count;
@@ -126,6 +138,12 @@ uint32_t grid_for(uint64_t items, uint32_t cap) {
 
 hipError_t launch_to_bf16(const float* x, uint16_t* y, uint64_t count, hipStream_t s) {
     k_to_bf16<<<grid_for(count, 1u << 16), kThreads, 0, s>>>(x, y, count);
+    return hipGetLastError();
+}
+
+hipError_t launch_to_bf16_pad(const float* x, uint16_t* y, uint64_t n, int d, int dp, hipStream_t s) {
+    if (dp == d) return launch_to_bf16(x, y, n * uint64_t(d), s);
+    k_to_bf16_pad<<<grid_for(n * uint64_t(dp), 1u << 16), kThreads, 0, s>>>(x, y, n, d, dp);
     return hipGetLastError();
 }
 

@@ -1,0 +1,207 @@
+// bf16 MFMA projection: Z = X W_all (bf16 in, FP32 accumulate, bf16 out)
+// fused with the attention dots L = Z aL, R = Z aR.
+//
+// Reference: projection via cblas_gemm_bf16bf16f32 and lr_from_z
+// (baseline/src/baseline_standard.cpp:3-20).  The dots are taken as one more
+// MFMA output block against B_LR = W_bf16 a (the reordered contraction of
+// lr_reordered, baseline_standard.cpp:29-43), with B_LR split into a bf16
+// high part and a bf16 low part so the result carries ~16 mantissa bits of
+// B_LR and FP32 accumulation -- the same value as the FP32 dot of the FP32 Z
+// row with a up to rounding order.
+//
+// The product is computed transposed, Z^T = W^T X^T, on
+// v_mfma_f32_32x32x16_bf16: A = 32 output features x 16 k of W^T (packed on
+// the host in fragment order, read from LDS), B = 16 k x 32 graph rows of X^T
+// (one 16-byte load per lane straight from the row-major X), D = 32 features
+// x 32 rows, so each lane's accumulators hold 4 consecutive features of one
+// graph row -- stored as 8-byte bf16 vectors without a transpose.
+//
+// Work split: one wave per 32-row tile, 8 waves per workgroup, persistent
+// workgroups that copy their group's packed W into LDS once.  Output features
+// are cut into groups of up to 8 blocks of 32; the last group also carries the
+// L/R block.
+#include "internal.hpp"
+
+namespace gatgpu {
+namespace {
+
+typedef __bf16 bf16x8 __attribute__((__vector_size__(8 * sizeof(__bf16))));
+typedef float f32x16 __attribute__((__vector_size__(16 * sizeof(float))));
+
+constexpr int kThreads = 512;
+constexpr int kWaves = kThreads / kWave;
+constexpr int kChunk = 16;  // X fragments held in registers at once (k = 256)
+
+template <int NMB, bool LDS_A>
+__global__ void __launch_bounds__(kThreads) k_proj_mfma(ProjArgs a) {
+    extern __shared__ uint4 wlds[];
+    const int w = threadIdx.x / kWave, l = threadIdx.x % kWave;
+    const int g = blockIdx.y;
+    const size_t gblocks = size_t(a.ksteps) * NMB * kWave;
+    const uint4* wg = a.wpk + size_t(g) * gblocks;
+    if constexpr (LDS_A) {
+        for (size_t q = threadIdx.x; q < gblocks; q += kThreads) wlds[q] = wg[q];
+        __syncthreads();
+    }
+    const uint4* wsrc = LDS_A ? wlds : wg;
+    const int head_blocks = a.head_blocks - 8 * g < 8 ? a.head_blocks - 8 * g : 8;
+    const bool has_lr = g == a.groups - 1;
+    const int nblk = head_blocks + (has_lr ? 1 : 0);
+    const int half = l / 32, col = l % 32;
+    for (uint64_t tile = uint64_t(blockIdx.x) * kWaves + w; tile < a.tiles;
+         tile += uint64_t(gridDim.x) * kWaves) {
+        const uint64_t row = tile * 32 + col;
+        const bool row_ok = row < a.n;
+        f32x16 acc[NMB];
+#pragma unroll
+        for (int mb = 0; mb < NMB; ++mb)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[mb][r] = 0.0f;
+        const uint16_t* xrow = a.x + row * a.xs + 8 * half;
+        for (int k0 = 0; k0 < a.ksteps; k0 += kChunk) {
+            uint4 xf[kChunk];
+#pragma unroll
+            for (int q = 0; q < kChunk; ++q)
+                xf[q] = (row_ok && k0 + q < a.ksteps) ? *reinterpret_cast<const uint4*>(xrow + (k0 + q) * 16)
+                                                      : make_uint4(0, 0, 0, 0);
+#pragma unroll
+            for (int q = 0; q < kChunk; ++q) {
+                if (k0 + q < a.ksteps) {
+                    const bf16x8 b = __builtin_bit_cast(bf16x8, xf[q]);
+                    const uint4* wk = wsrc + size_t(k0 + q) * NMB * kWave + l;
+#pragma unroll
+                    for (int mb = 0; mb < NMB; ++mb) {
+                        if (mb < nblk) {
+                            const bf16x8 av = __builtin_bit_cast(bf16x8, wk[mb * kWave]);
+                            acc[mb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, b, acc[mb], 0, 0, 0);
+                        }
+                    }
+                }
+            }
+        }
+        if (!row_ok) continue;
+        // Z: lane (half, col) holds features 32*gb + 8*gq + 4*half + {0..3} of row.
+#pragma unroll
+        for (int mb = 0; mb < NMB; ++mb) {
+            if (mb >= head_blocks) continue;
+            const int gb = 8 * g + mb;
+#pragma unroll
+            for (int gq = 0; gq < 4; ++gq) {
+                const int f0 = gb * 32 + 8 * gq + 4 * half;
+                if (f0 >= a.width) continue;
+                const uint32_t w0 = uint32_t(bf16_rne(acc[mb][4 * gq])) | (uint32_t(bf16_rne(acc[mb][4 * gq + 1])) << 16);
+                const uint32_t w1 = uint32_t(bf16_rne(acc[mb][4 * gq + 2])) | (uint32_t(bf16_rne(acc[mb][4 * gq + 3])) << 16);
+                *reinterpret_cast<uint2*>(a.z + row * a.zs + f0) = make_uint2(w0, w1);
+            }
+        }
+        if (has_lr) {
+            // LR block columns: [0,8) L hi, [8,16) R hi, [16,24) L lo, [24,32) R lo;
+            // lane half h4 holds heads 4*h4 + {0..3} of each quarter in regs
+            // {0..3}, {4..7}, {8..11}, {12..15}.
+#pragma unroll
+            for (int mb = 0; mb < NMB; ++mb) {
+                if (mb != head_blocks) continue;
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const int h = 4 * half + q;
+                    if (h < a.heads) {
+                        a.left[row * a.heads + h] = acc[mb][q] + acc[mb][8 + q];
+                        a.right[row * a.heads + h] = acc[mb][4 + q] + acc[mb][12 + q];
+                    }
+                }
+            }
+        }
+    }
+}
+
+template <int NMB>
+hipError_t launch_nmb(const ProjArgs& a, hipStream_t s, int cus) {
+    const size_t lds = size_t(a.ksteps) * NMB * kWave * sizeof(uint4);
+    const uint64_t wg_needed = (a.tiles + kWaves - 1) / kWaves;
+    if (lds <= 160 * 1024) {
+        const int per_cu = lds <= 80 * 1024 ? 2 : 1;
+        uint64_t gx = uint64_t(cus) * per_cu;
+        if (gx > wg_needed) gx = wg_needed;
+        if (gx < 1) gx = 1;
+        if (lds > 64 * 1024) {
+            hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_proj_mfma<NMB, true>),
+                                               hipFuncAttributeMaxDynamicSharedMemorySize, int(lds));
+            if (e != hipSuccess) return e;
+        }
+        k_proj_mfma<NMB, true><<<dim3(uint32_t(gx), uint32_t(a.groups)), kThreads, lds, s>>>(a);
+    } else {
+        uint64_t gx = wg_needed < 65535 * 16 ? wg_needed : 65535 * 16;
+        if (gx < 1) gx = 1;
+        k_proj_mfma<NMB, false><<<dim3(uint32_t(gx), uint32_t(a.groups)), kThreads, 0, s>>>(a);
+    }
+    return hipGetLastError();
+}
+
+}  // namespace
+
+int proj_blocks_per_group(int width) {
+    const int head_blocks = (width + 31) / 32;
+    if (head_blocks >= 8) return 9;
+    const int need = head_blocks + 1;
+    return need <= 2 ? 2 : need <= 3 ? 3 : need <= 5 ? 5 : 9;
+}
+
+hipError_t launch_projection_mfma(const ProjArgs& a, hipStream_t s, int cus) {
+    switch (a.nmb) {
+        case 2: return launch_nmb<2>(a, s, cus);
+        case 3: return launch_nmb<3>(a, s, cus);
+        case 5: return launch_nmb<5>(a, s, cus);
+        case 9: return launch_nmb<9>(a, s, cus);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+// Packs W (bf16-rounded, [in][width]) and B_LR = W_bf16 a (hi/lo) into the
+// A-fragment order [group][kstep][block][lane][8]: lane l of block b at k step
+// ks holds W^T[32 b + l % 32][16 ks + 8 (l / 32) + j], j = 0..7.
+void pack_projection_weights(const float* wq, const float* al, const float* ar, int in, int heads, int dim,
+                             std::vector<uint16_t>& out, int& ksteps, int& groups, int& nmb) {
+    const int width = heads * dim;
+    const int head_blocks = (width + 31) / 32;
+    nmb = proj_blocks_per_group(width);
+    groups = head_blocks >= 8 ? (head_blocks + 7) / 8 : 1;
+    ksteps = (in + 15) / 16;
+    // B_LR columns from the bf16 W in double, split into bf16 hi + lo.
+    std::vector<float> lrcol(size_t(in) * 32, 0.0f);
+    for (int k = 0; k < in; ++k)
+        for (int h = 0; h < heads; ++h) {
+            double l = 0, r = 0;
+            for (int d = 0; d < dim; ++d) {
+                const double wv = wq[size_t(k) * width + h * dim + d];
+                l += wv * al[h * dim + d];
+                r += wv * ar[h * dim + d];
+            }
+            const float lf = float(l), rf = float(r);
+            const float lh = bf16_widen(bf16_rne(lf)), rh = bf16_widen(bf16_rne(rf));
+            lrcol[size_t(k) * 32 + h] = lh;
+            lrcol[size_t(k) * 32 + 8 + h] = rh;
+            lrcol[size_t(k) * 32 + 16 + h] = bf16_widen(bf16_rne(lf - lh));
+            lrcol[size_t(k) * 32 + 24 + h] = bf16_widen(bf16_rne(rf - rh));
+        }
+    out.assign(size_t(groups) * ksteps * nmb * kWave * 8, 0);
+    for (int g = 0; g < groups; ++g) {
+        const int hb = head_blocks - 8 * g < 8 ? head_blocks - 8 * g : 8;
+        for (int ks = 0; ks < ksteps; ++ks)
+            for (int b = 0; b < nmb; ++b) {
+                const bool lr = g == groups - 1 && b == hb;
+                if (b > hb || (b == hb && !lr)) continue;
+                for (int l = 0; l < kWave; ++l)
+                    for (int j = 0; j < 8; ++j) {
+                        const int k = 16 * ks + 8 * (l / 32) + j, c = l % 32;
+                        float v = 0.0f;
+                        if (k < in) {
+                            if (lr) v = lrcol[size_t(k) * 32 + c];
+                            else if (32 * (8 * g + b) + c < width) v = wq[size_t(k) * width + 32 * (8 * g + b) + c];
+                        }
+                        out[((((size_t(g) * ksteps + ks) * nmb + b) * kWave + l) * 8) + j] = bf16_rne(v);
+                    }
+            }
+    }
+}
+
+}  // namespace gatgpu

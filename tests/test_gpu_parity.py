@@ -18,16 +18,24 @@ FP32_MAX_ABS = 1e-4
 BF16_REL_L2 = 1e-2
 
 
-def run_layer(ctx, row, col, x, p, hidden, precision, block_min=None):
+DEFAULT_OPTIONS = {gatgpu.OPT_BLOCK_ROW_MIN_DEGREE: 512, gatgpu.OPT_SPLIT_ROW_MIN_DEGREE: 1024,
+                   gatgpu.OPT_SPLIT_CHUNK_EDGES: 256}
+# Schedules that route the small graphs' rows through every kernel variant:
+# default, every row a block (generic path), rows >= 16 split into 64-edge chunks.
+SCHEDULES = [{}, {gatgpu.OPT_BLOCK_ROW_MIN_DEGREE: 1},
+             {gatgpu.OPT_SPLIT_ROW_MIN_DEGREE: 16, gatgpu.OPT_SPLIT_CHUNK_EDGES: 64}]
+
+
+def run_layer(ctx, row, col, x, p, hidden, precision, options=None):
     ctx.set_graph(row, col)
-    if block_min is not None:
-        ctx.set_option(gatgpu.OPT_BLOCK_ROW_MIN_DEGREE, block_min)
+    for k, v in (options or {}).items():
+        ctx.set_option(k, v)
     ctx.set_layer(0, p)
     ctx.set_input(x)
     ctx.layer_forward(0, precision, gatgpu.TRANSFORM_FIRST, hidden)
     out = {k: ctx.stage(0, k) for k in ("left", "right", "max", "den", "out")}
-    if block_min is not None:
-        ctx.set_option(gatgpu.OPT_BLOCK_ROW_MIN_DEGREE, 512)
+    for k in options or {}:
+        ctx.set_option(k, DEFAULT_OPTIONS[k])
     return out
 
 
@@ -68,10 +76,10 @@ def test_boundary_shapes_fp32(gpu_ctx, D, K, d):
     g = oracle.boundary_graph(D)
     p = oracle.boundary_param(D, K, d)
     r = oracle.ref_layer(g["row"], g["col"], g["x"], p, False)
-    for block_min in (512, 1):
-        got = run_layer(gpu_ctx, g["row"], g["col"], g["x"], p, False, gatgpu.FP32, block_min)
+    for opts in SCHEDULES:
+        got = run_layer(gpu_ctx, g["row"], g["col"], g["x"], p, False, gatgpu.FP32, opts)
         e = oracle.errors(r["out"], got["out"])
-        assert e["finite"] and e["max_abs"] < FP32_MAX_ABS and e["relative_l2"] < FP32_MAX_ABS, (block_min, e)
+        assert e["finite"] and e["max_abs"] < FP32_MAX_ABS and e["relative_l2"] < FP32_MAX_ABS, (opts, e)
         for k in ("left", "right", "max"):
             assert oracle.errors(r[k], got[k])["max_abs"] < FP32_MAX_ABS, k
         assert oracle.errors(r["den"], got["den"])["relative_l2"] < 1e-5
@@ -86,18 +94,20 @@ def test_boundary_shapes_fp32(gpu_ctx, D, K, d):
             assert np.array_equal(m, got["max"][i])
 
 
-@pytest.mark.parametrize("D,K,d", [(17, 8, 7), (128, 8, 32), (256, 1, 47), (33, 4, 40)])
+@pytest.mark.parametrize("D,K,d", [(17, 8, 7), (128, 8, 32), (256, 1, 47), (33, 4, 40), (128, 8, 64),
+                                   (256, 8, 64)])
 def test_boundary_shapes_bf16_and_hidden(gpu_ctx, D, K, d):
     g = oracle.boundary_graph(D)
     p = oracle.boundary_param(D, K, d)
     for hidden in (False, True):
         r = oracle.ref_layer(g["row"], g["col"], g["x"], p, hidden)
-        got = run_layer(gpu_ctx, g["row"], g["col"], g["x"], p, hidden, gatgpu.FP32)
-        assert oracle.errors(r["out"], got["out"])["max_abs"] < FP32_MAX_ABS
-        got = run_layer(gpu_ctx, g["row"], g["col"], g["x"], p, hidden, gatgpu.BF16)
-        e = oracle.errors(r["out"], got["out"])
-        assert e["finite"] and e["relative_l2"] < BF16_REL_L2, e
-        assert np.all(got["out"][0] == 0)
+        for opts in SCHEDULES:
+            got = run_layer(gpu_ctx, g["row"], g["col"], g["x"], p, hidden, gatgpu.FP32, opts)
+            assert oracle.errors(r["out"], got["out"])["max_abs"] < FP32_MAX_ABS, opts
+            got = run_layer(gpu_ctx, g["row"], g["col"], g["x"], p, hidden, gatgpu.BF16, opts)
+            e = oracle.errors(r["out"], got["out"])
+            assert e["finite"] and e["relative_l2"] < BF16_REL_L2, (opts, e)
+            assert np.all(got["out"][0] == 0)
 
 
 def test_adversarial_scores(gpu_ctx):
@@ -214,3 +224,37 @@ def test_error_codes(gpu_ctx):
         ctx2.layer_forward(0)
     assert err.value.code == gatgpu.ESTATE
     ctx2.close()
+
+
+@pytest.mark.parametrize("D,K,d", [(128, 8, 32), (100, 8, 32), (256, 8, 32), (256, 1, 47), (128, 8, 64), (33, 4, 40)])
+def test_bf16_projection_stages(gpu_ctx, D, K, d):
+    """bf16 MFMA projection against R0 run on bf16-rounded X and W: Z within one
+    bf16 ulp of RNE(FP32 Z) (accumulation order may flip a rounding), L/R from
+    the hi/lo B_LR block within 1e-5 relative L2 of the FP32 dots of Z."""
+    w = inputs.WORKLOADS["smoke"]
+    row, col = w.graph()
+    x = inputs.normal((w.n, D), 3)
+    p = inputs.glorot_param(D, K, d, 4)
+    qp = dict(p, w=oracle.quantize_bf16(p["w"]))
+    r = oracle.ref_layer(row, col, oracle.quantize_bf16(x), qp, False)
+    gpu_ctx.set_graph(row, col)
+    gpu_ctx.set_layer(0, p)
+    gpu_ctx.set_input(x)
+    gpu_ctx.layer_forward(0, gatgpu.BF16, gatgpu.TRANSFORM_FIRST, False)
+    z = gpu_ctx.stage(0, "z").astype(np.float64)
+    zref = oracle.quantize_bf16(r["z"]).astype(np.float64)
+    # One bf16 ulp of the result plus the FP32 accumulation-order bound
+    # (D * 2^-24 * sum |x w|, with margin) for results that cancel.
+    expo = np.frexp(np.abs(zref))[1]
+    ulp = np.ldexp(1.0, expo - 8)
+    absdot = np.abs(oracle.quantize_bf16(x)).astype(np.float64) @ np.abs(qp["w"]).astype(np.float64)
+    tol = ulp + 4 * D * 2.0 ** -24 * absdot
+    bad = np.abs(z - zref) > tol
+    if bad.any():
+        i, f = np.argwhere(bad)[0]
+        pytest.fail(f"{int(bad.sum())} Z entries off, first [{i},{f}] gpu={z[i, f]!r} ref={zref[i, f]!r} "
+                    f"fp32={r['z'][i, f]!r} tol={tol[i, f]!r}")
+    assert np.mean(z != zref) < 0.01
+    for k in ("left", "right"):
+        e = oracle.errors(r[k], gpu_ctx.stage(0, k))
+        assert e["relative_l2"] < 1e-5, (k, e)
