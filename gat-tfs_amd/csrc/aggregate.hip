@@ -253,6 +253,7 @@ hipError_t launch_aggregate_tf(const AggArgs& a, const RowBins& bins, const Spli
                                hipStream_t s) {
     if (a.heads < 1 || a.heads > 8 || a.dim < 1 || a.heads * a.dim > 512) return hipErrorInvalidValue;
     if (aggregate_vec_supported(a)) return launch_aggregate_vec(a, bins, split, s);
+    if (aggregate_k1_supported(a)) return launch_aggregate_k1(a, bins, split, s);
     // Generic path: a wave per row below block_begin, a block per row above
     // (split rows included).
     return a.feat_bf16 ? dispatch_nf<uint16_t>(a, bins, s) : dispatch_nf<float>(a, bins, s);

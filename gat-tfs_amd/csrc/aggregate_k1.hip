@@ -1,0 +1,242 @@
+// Single-head aggregation for narrow rows (the output layer, 1 head x C <= 64
+// classes).  Same mathematics as aggregate.hip (baseline_standard.cpp:44-97).
+//
+// A group of G lanes owns one destination row, so a wave works on 64/G rows
+// at once.  Rows are taken in degree-sorted order, which gives the rows of a
+// wave the same in-degree and therefore the same trip count.  Per batch of G
+// edges, lane `sub` of the group scores edge `sub` (one exp per edge) and the
+// group then walks the batch: source id and score are broadcast by a lane
+// shuffle, and each lane gathers 16 bytes of the source's Z row (Z rows are
+// padded to ZS = G*VEC... elements >= C, so the loads are aligned).  Rows at or
+// above the split threshold are cut into chunks; a chunk takes a whole wave
+// (each group a contiguous piece), and chunks merge exactly as in
+// aggregate_vec.hip: exact row max from the per-chunk maxima, partial sums to
+// scratch, the last arrival adds them in chunk order.
+#include "internal.hpp"
+
+namespace gatgpu {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kWavesPerBlock = kThreads / kWave;
+
+template <class ZT, int G_>
+struct K1 {
+    static constexpr int G = G_;                      // lanes per row group (power of two)
+    static constexpr int VEC = 16 / int(sizeof(ZT));  // features per lane
+    static constexpr int GPW = kWave / G;             // row groups per wave
+    static constexpr int MAXW = G * VEC;              // widest row handled
+};
+
+template <class ZT>
+struct K1Args {
+    const uint64_t* prow;
+    const uint32_t* pcol;
+    const uint32_t* perm;
+    const float* L;
+    const float* R;
+    const ZT* Z;
+    int W, zs;
+    bool hidden;
+    float* mx;
+    float* den;
+    float* out32;
+    uint16_t* outbf;
+    uint64_t n, e, rows;
+    uint64_t chunks;
+    const uint32_t* chunk_k;
+    const uint32_t* chunk_first;
+    uint32_t chunk_edges;
+    const float* mchunk;
+    float* part;
+    uint32_t* counter;
+};
+
+__device__ inline void unpack(const uint4& v, float (&f)[8]) {
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        f[2 * q] = __builtin_bit_cast(float, w[q] << 16);
+        f[2 * q + 1] = __builtin_bit_cast(float, w[q] & 0xffff0000u);
+    }
+}
+__device__ inline void unpack(const uint4& v, float (&f)[4]) {
+    f[0] = __builtin_bit_cast(float, v.x);
+    f[1] = __builtin_bit_cast(float, v.y);
+    f[2] = __builtin_bit_cast(float, v.z);
+    f[3] = __builtin_bit_cast(float, v.w);
+}
+
+// Max of R over [beg, end), reduced over the G lanes of the group.
+template <class C>
+__device__ inline float group_max(uint64_t beg, uint64_t end, const uint32_t* __restrict__ pcol,
+                                  const float* __restrict__ R, int sub) {
+    float m = -INFINITY;
+    for (uint64_t e = beg + sub; e < end; e += C::G) m = fmaxf(m, R[pcol[e]]);
+    for (int off = 1; off < C::G; off <<= 1) m = fmaxf(m, __shfl_xor(m, off));
+    return m;
+}
+
+// Edges [beg, end) of one row into the group's accumulators.
+template <class C, class ZT>
+__device__ inline void group_accumulate(uint64_t beg, uint64_t end, const uint32_t* __restrict__ pcol,
+                                        const float* __restrict__ R, const ZT* __restrict__ Z, int zs, int W,
+                                        float Li, float Mi, int gbase, int sub, float (&acc)[C::VEC],
+                                        float& dloc) {
+    const bool reader = sub * C::VEC < W;
+    for (uint64_t base = beg; base < end; base += C::G) {
+        const uint64_t e = base + sub;
+        const bool ev = e < end;
+        const uint32_t j = ev ? pcol[e] : 0u;
+        const float p = ev ? expf(leaky(Li + R[j]) - Mi) : 0.0f;
+        dloc += p;
+        const uint64_t rem = end - base;
+        const int cnt = rem < uint64_t(C::G) ? int(rem) : C::G;
+        uint4 raw[C::G];
+        float pt[C::G];
+#pragma unroll
+        for (int t = 0; t < C::G; ++t) {
+            const uint32_t jt = __shfl(j, gbase + t);
+            pt[t] = __shfl(p, gbase + t);
+            raw[t] = (t < cnt && reader) ? *reinterpret_cast<const uint4*>(Z + uint64_t(jt) * zs + sub * C::VEC)
+                                         : make_uint4(0, 0, 0, 0);
+        }
+#pragma unroll
+        for (int t = 0; t < C::G; ++t) {
+            float f[C::VEC];
+            unpack(raw[t], f);
+#pragma unroll
+            for (int x = 0; x < C::VEC; ++x) acc[x] += pt[t] * f[x];
+        }
+    }
+}
+
+template <class C>
+__device__ inline void store_row(uint32_t i, int W, int sub, const float (&acc)[C::VEC], float d, bool hidden,
+                                 float* out32, uint16_t* outbf) {
+    const float scale = d > 0.0f ? 1.0f / d : 0.0f;
+#pragma unroll
+    for (int x = 0; x < C::VEC; ++x) {
+        const int f = sub * C::VEC + x;
+        if (f >= W) continue;
+        float y = acc[x] * scale;
+        if (hidden) y = elu(y);
+        if (out32) out32[uint64_t(i) * W + f] = y;
+        if (outbf) outbf[uint64_t(i) * W + f] = bf16_rne(y);
+    }
+}
+
+template <class C, class ZT>
+__global__ void __launch_bounds__(kThreads) k_agg_k1(K1Args<ZT> a) {
+    const int w = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+    const int g = lane / C::G, sub = lane % C::G, gbase = g * C::G;
+    const uint64_t wave = uint64_t(blockIdx.x) * kWavesPerBlock + w;
+    float acc[C::VEC];
+#pragma unroll
+    for (int x = 0; x < C::VEC; ++x) acc[x] = 0.0f;
+    float dloc = 0.0f;
+    if (wave < a.chunks) {
+        // ---------------- one chunk of a split row per wave
+        const uint64_t c = wave;
+        const uint32_t k = a.chunk_k[c], first = a.chunk_first[c];
+        const uint64_t rbeg = a.prow[k], rend = a.prow[k + 1];
+        const uint32_t i = a.perm[k];
+        if (i >= a.n || rbeg > rend || rend > a.e) return;
+        const uint32_t nch = uint32_t((rend - rbeg + a.chunk_edges - 1) / a.chunk_edges);
+        const uint64_t cbeg = rbeg + uint64_t(c - first) * a.chunk_edges;
+        const uint64_t cend = cbeg + a.chunk_edges < rend ? cbeg + a.chunk_edges : rend;
+        float m = -INFINITY;
+        for (uint32_t q = lane; q < nch; q += kWave) m = fmaxf(m, a.mchunk[(first + q) * 8]);
+        for (int off = 1; off < kWave; off <<= 1) m = fmaxf(m, __shfl_xor(m, off));
+        const float Li = a.L[i];
+        const float Mi = leaky(Li + m);
+        const uint64_t len = cend - cbeg;
+        const uint64_t pb = cbeg + len * g / C::GPW, pe = cbeg + len * (g + 1) / C::GPW;
+        group_accumulate<C, ZT>(pb, pe, a.pcol, a.R, a.Z, a.zs, a.W, Li, Mi, gbase, sub, acc, dloc);
+        for (int off = C::G; off < kWave; off <<= 1) {
+#pragma unroll
+            for (int x = 0; x < C::VEC; ++x) acc[x] += __shfl_xor(acc[x], off);
+        }
+        for (int off = 1; off < kWave; off <<= 1) dloc += __shfl_xor(dloc, off);
+        float* part = a.part + c * (512 + 8);
+        if (g == 0)
+#pragma unroll
+            for (int x = 0; x < C::VEC; ++x) part[sub * C::VEC + x] = acc[x];
+        if (lane == 0) part[512] = dloc;
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+        uint32_t old = 0;
+        if (lane == 0)
+            old = __hip_atomic_fetch_add(a.counter + first, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        old = __shfl(old, 0);
+        if (old + 1 != nch) return;
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+        float tot[C::VEC];
+#pragma unroll
+        for (int x = 0; x < C::VEC; ++x) tot[x] = 0.0f;
+        float dtot = 0.0f;
+        for (uint32_t q = 0; q < nch; ++q) {
+            const float* pq = a.part + uint64_t(first + q) * (512 + 8);
+#pragma unroll
+            for (int x = 0; x < C::VEC; ++x) tot[x] += pq[sub * C::VEC + x];
+            dtot += pq[512];
+        }
+        if (lane == 0) {
+            a.mx[i] = Mi;
+            a.den[i] = dtot;
+            a.counter[first] = 0;
+        }
+        if (g == 0) store_row<C>(i, a.W, sub, tot, dtot, a.hidden, a.out32, a.outbf);
+        return;
+    }
+    // ---------------- 64/G whole rows per wave, heaviest first
+    const uint64_t idx = (wave - a.chunks) * C::GPW + g;
+    if (idx >= a.rows) return;  // whole groups exit; no wave-wide sync follows
+    const uint64_t k = a.rows - 1 - idx;
+    const uint32_t i = a.perm[k];
+    const uint64_t beg = a.prow[k], end = a.prow[k + 1];
+    if (i >= a.n || beg > end || end > a.e) return;
+    const float Li = a.L[i];
+    const float m = group_max<C>(beg, end, a.pcol, a.R, sub);
+    const float Mi = end > beg ? leaky(Li + m) : 0.0f;
+    group_accumulate<C, ZT>(beg, end, a.pcol, a.R, a.Z, a.zs, a.W, Li, Mi, gbase, sub, acc, dloc);
+    for (int off = 1; off < C::G; off <<= 1) dloc += __shfl_xor(dloc, off);
+    if (sub == 0) {
+        a.mx[i] = Mi;
+        a.den[i] = dloc;
+    }
+    store_row<C>(i, a.W, sub, acc, dloc, a.hidden, a.out32, a.outbf);
+}
+
+template <int G, class ZT>
+hipError_t run(const AggArgs& g, const RowBins& bins, const SplitTable& t, hipStream_t s) {
+    using C = K1<ZT, G>;
+    K1Args<ZT> a{g.prow, g.pcol, g.perm, g.left, g.right, static_cast<const ZT*>(g.feat), g.heads * g.dim,
+                 g.fstride, g.hidden, g.mx, g.den, g.out32, g.outbf, g.n, g.e, bins.split_begin, t.chunks,
+                 t.chunk_k, t.chunk_first, t.chunk_edges, t.mchunk, t.part, t.counter};
+    if (t.chunks) {
+        hipError_t e = launch_split_prescan(g.prow, g.pcol, g.right, 1, t, g.e, s);
+        if (e != hipSuccess) return e;
+    }
+    const uint64_t waves = t.chunks + (bins.split_begin + C::GPW - 1) / C::GPW;
+    if (waves)
+        k_agg_k1<C, ZT><<<dim3(uint32_t((waves + kWavesPerBlock - 1) / kWavesPerBlock)), kThreads, 0, s>>>(a);
+    return hipGetLastError();
+}
+
+}  // namespace
+
+bool aggregate_k1_supported(const AggArgs& g) {
+    const int W = g.dim;
+    if (g.heads != 1 || W > 64) return false;
+    const int vec = g.feat_bf16 ? 8 : 4;
+    return g.fstride % vec == 0 && g.fstride >= W;
+}
+
+hipError_t launch_aggregate_k1(const AggArgs& g, const RowBins& bins, const SplitTable& t, hipStream_t s) {
+    const int W = g.dim;
+    if (g.feat_bf16) return W <= 64 ? run<8, uint16_t>(g, bins, t, s) : hipErrorInvalidValue;
+    if (W <= 32) return run<8, float>(g, bins, t, s);
+    return run<16, float>(g, bins, t, s);
+}
+
+}  // namespace gatgpu

@@ -335,8 +335,8 @@ hipError_t run(const AggArgs& g, const RowBins& bins, const SplitTable& t, hipSt
                 g.out32, g.outbf, g.n, g.e, bins.split_begin,
                 SplitArgs{t.chunks, t.chunk_k, t.chunk_first, t.chunk_edges, t.mchunk, t.part, t.counter}};
     if (t.chunks) {
-        k_split_prescan<C::K><<<dim3(uint32_t((t.chunks + kWavesPerBlock - 1) / kWavesPerBlock)), kThreads, 0, s>>>(
-            g.prow, g.pcol, g.right, a.sp, g.e);
+        hipError_t e = launch_split_prescan(g.prow, g.pcol, g.right, C::K, t, g.e, s);
+        if (e != hipSuccess) return e;
     }
     const uint64_t items = t.chunks + bins.split_begin;
     if (items)
@@ -345,6 +345,21 @@ hipError_t run(const AggArgs& g, const RowBins& bins, const SplitTable& t, hipSt
 }
 
 }  // namespace
+
+hipError_t launch_split_prescan(const uint64_t* prow, const uint32_t* pcol, const float* right, int heads,
+                                const SplitTable& t, uint64_t e, hipStream_t s) {
+    if (!t.chunks) return hipSuccess;
+    const SplitArgs sp{t.chunks, t.chunk_k, t.chunk_first, t.chunk_edges, t.mchunk, t.part, t.counter};
+    const dim3 grid(uint32_t((t.chunks + kWavesPerBlock - 1) / kWavesPerBlock));
+    switch (heads) {
+        case 1: k_split_prescan<1><<<grid, kThreads, 0, s>>>(prow, pcol, right, sp, e); break;
+        case 2: k_split_prescan<2><<<grid, kThreads, 0, s>>>(prow, pcol, right, sp, e); break;
+        case 4: k_split_prescan<4><<<grid, kThreads, 0, s>>>(prow, pcol, right, sp, e); break;
+        case 8: k_split_prescan<8><<<grid, kThreads, 0, s>>>(prow, pcol, right, sp, e); break;
+        default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
 
 bool aggregate_vec_supported(const AggArgs& g) {
     const int W = g.heads * g.dim;

@@ -269,7 +269,7 @@ int run_layer(gatgpu_ctx* c, int l, int precision, int dataflow, bool hidden, co
     // bf16 path: X as [n][xs] bf16 (xs = ksteps*16, zero-padded), Z as [n][zs]
     // bf16 (zs = W rounded up to 8 for aligned vector stores).
     const int xs = Ls.ksteps * 16;
-    const int zs = bf16 ? (W + 7) / 8 * 8 : W;
+    const int zs = bf16 ? (W + 7) / 8 * 8 : (W + 3) / 4 * 4;
     if (bf16) {
         HIPCHECK(c, Ls.zbf.ensure(n * zs * 2));
         if (srcbf && D != xs) {  // chained bf16 input without the padded layout
@@ -280,7 +280,7 @@ int run_layer(gatgpu_ctx* c, int l, int precision, int dataflow, bool hidden, co
         }
         if (src32) HIPCHECK(c, Ls.inbf.ensure(n * xs * 2));
     } else {
-        HIPCHECK(c, Ls.z32.ensure(n * W * 4));
+        HIPCHECK(c, Ls.z32.ensure(n * zs * 4));
     }
     if (ev_base >= 0) HIPCHECK(c, hipEventRecord(c->ev[ev_base], c->stream));
     // ---- convert (bf16 path, FP32 source only; a bf16 source was rounded in
@@ -313,7 +313,7 @@ int run_layer(gatgpu_ctx* c, int l, int precision, int dataflow, bool hidden, co
     } else {
         HIPCHECK(c, launch_projection(src32, nullptr, Ls.w32.as<float>(), n, D, K, dim, Ls.al.as<float>(),
                                       Ls.ar.as<float>(), Ls.z32.as<float>(), nullptr, Ls.left.as<float>(),
-                                      Ls.right.as<float>(), nullptr, c->stream));
+                                      Ls.right.as<float>(), nullptr, zs, c->stream));
     }
     if (ev_base >= 0) HIPCHECK(c, hipEventRecord(c->ev[ev_base + 2], c->stream));
     // ---- fused prescan + softmax + aggregation + normalise + ELU
@@ -622,6 +622,12 @@ int gatgpu_get_stage(gatgpu_ctx* c, int layer, int which, float* host) {
         HIPCHECK(c, hipMemcpy(tmp.data(), src, tmp.size() * 2, hipMemcpyDeviceToHost));
         for (uint64_t i = 0; i < c->n; ++i)
             for (int f = 0; f < W; ++f) host[i * W + f] = bf16_widen(tmp[i * zs + f]);
+    } else if (which == GATGPU_STAGE_Z) {
+        const int W = L.width(), zs = (W + 3) / 4 * 4;
+        std::vector<float> tmp(c->n * zs);
+        HIPCHECK(c, hipMemcpy(tmp.data(), src, tmp.size() * 4, hipMemcpyDeviceToHost));
+        for (uint64_t i = 0; i < c->n; ++i)
+            for (int f = 0; f < W; ++f) host[i * W + f] = tmp[i * zs + f];
     } else if (bf) {
         std::vector<uint16_t> tmp(count);
         HIPCHECK(c, hipMemcpy(tmp.data(), src, count * 2, hipMemcpyDeviceToHost));

@@ -67,7 +67,7 @@ hipError_t launch_to_bf16_pad(const float* x, uint16_t* y, uint64_t n, int d, in
 hipError_t launch_projection(const float* x32, const uint16_t* xbf, const float* w, uint64_t n,
                              int in, int heads, int dim, const float* al, const float* ar,
                              float* z32, uint16_t* zbf, float* left, float* right, float* zscratch,
-                             hipStream_t s);
+                             int zs, hipStream_t s);
 // L/R only (aggregate-first front end): LR = X B_LR with B_LR = W a.
 hipError_t launch_lr_reordered(const float* x32, const uint16_t* xbf, const float* blr,
                                uint64_t n, int in, int heads, float* left, float* right,
@@ -128,6 +128,13 @@ struct SplitTable {
     uint32_t* counter = nullptr;            // [chunks] arrival counters, zero between launches
 };
 hipError_t launch_aggregate_tf(const AggArgs& a, const RowBins& bins, const SplitTable& split,
+                               hipStream_t s);
+// Per-chunk maxima of R for split rows (heads 1, 2, 4 or 8).
+hipError_t launch_split_prescan(const uint64_t* prow, const uint32_t* pcol, const float* right, int heads,
+                                const SplitTable& t, uint64_t e, hipStream_t s);
+// aggregate_k1.hip: one head, rows of at most 64 features.
+bool aggregate_k1_supported(const AggArgs& a);
+hipError_t launch_aggregate_k1(const AggArgs& a, const RowBins& bins, const SplitTable& split,
                                hipStream_t s);
 // aggregate_vec.hip: 16-byte vector path for 8 heads x (32 | 64).
 bool aggregate_vec_supported(const AggArgs& a);

@@ -48,7 +48,7 @@ __device__ inline float ldx(const float* x32, const uint16_t* xbf, uint64_t idx)
 // X rows index blockIdx.x (2^31 limit), output column tiles blockIdx.y.
 __global__ void __launch_bounds__(kThreads)
 k_gemm_tiled(const float* __restrict__ x32, const uint16_t* __restrict__ xbf, const float* __restrict__ w,
-             float* __restrict__ z, uint64_t n, int D, int W) {
+             float* __restrict__ z, uint64_t n, int D, int W, int zs) {
     __shared__ float As[16][64 + 4];
     __shared__ float Bs[16][64];
     const int tx = threadIdx.x % 16, ty = threadIdx.x / 16;
@@ -90,20 +90,20 @@ k_gemm_tiled(const float* __restrict__ x32, const uint16_t* __restrict__ xbf, co
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             const int gc = col0 + tx * 4 + j;
-            if (gc < W) z[gr * W + gc] = acc[i][j];
+            if (gc < W) z[gr * zs + gc] = acc[i][j];
         }
     }
 }
 
 // One thread per (row, head): the dots of lr_from_z, then the optional bf16 store of Z.
 __global__ void __launch_bounds__(kThreads)
-k_lr_from_z(const float* __restrict__ z, uint64_t n, int K, int dim, const float* __restrict__ al,
+k_lr_from_z(const float* __restrict__ z, uint64_t n, int K, int dim, int zs, const float* __restrict__ al,
             const float* __restrict__ ar, float* __restrict__ left, float* __restrict__ right) {
     const uint64_t t = blockIdx.x * uint64_t(kThreads) + threadIdx.x;
     if (t >= n * K) return;
     const uint64_t i = t / K;
-    const int h = int(t % K), W = K * dim;
-    const float* zi = z + i * W + h * dim;
+    const int h = int(t % K);
+    const float* zi = z + i * zs + h * dim;
     float l = 0.0f, r = 0.0f;
     for (int d = 0; d < dim; ++d) {
         l += zi[d] * al[h * dim + d];
@@ -155,19 +155,19 @@ hipError_t launch_widen_bf16(const uint16_t* x, float* y, uint64_t count, hipStr
 hipError_t launch_projection(const float* x32, const uint16_t* xbf, const float* w, uint64_t n,
                              int in, int heads, int dim, const float* al, const float* ar,
                              float* z32, uint16_t* zbf, float* left, float* right, float* zscratch,
-                             hipStream_t s) {
+                             int zs, hipStream_t s) {
     const int W = heads * dim;
     float* zf = z32 ? z32 : zscratch;
     if (!zf) return hipErrorInvalidValue;
     dim3 grid(uint32_t((n + 63) / 64), uint32_t((W + 63) / 64));
-    k_gemm_tiled<<<grid, kThreads, 0, s>>>(x32, xbf, w, zf, n, in, W);
+    k_gemm_tiled<<<grid, kThreads, 0, s>>>(x32, xbf, w, zf, n, in, W, zs);
     hipError_t err = hipGetLastError();
     if (err != hipSuccess) return err;
     const uint64_t pairs = n * uint64_t(heads);
-    k_lr_from_z<<<dim3(uint32_t((pairs + kThreads - 1) / kThreads)), kThreads, 0, s>>>(zf, n, heads, dim, al,
-                                                                                       ar, left, right);
+    k_lr_from_z<<<dim3(uint32_t((pairs + kThreads - 1) / kThreads)), kThreads, 0, s>>>(zf, n, heads, dim, zs,
+                                                                                       al, ar, left, right);
     if ((err = hipGetLastError()) != hipSuccess) return err;
-    if (zbf) return launch_to_bf16(zf, zbf, n * uint64_t(W), s);
+    if (zbf) return launch_to_bf16(zf, zbf, n * uint64_t(zs), s);
     return hipSuccess;
 }
 
