@@ -222,28 +222,37 @@ def rne_bits(a):
     return bits
 
 
-def standard_layer(row, col, x, p, hidden, bf16, threads=0, wq=None):
+def standard_workspace(n, p):
+    """Stage buffers of one B0 layer, allocated and touched once (the
+    Workspace::allocate of baseline/src/common.cpp:126-134, outside timing)."""
+    K, W = p["heads"], p["heads"] * p["dim"]
+    ws = {"z": np.zeros((n, W), np.float32), "out": np.zeros((n, W), np.float32),
+          "xq": np.zeros((n, p["in"]), np.float32)}
+    for k in ("left", "right", "max", "den"):
+        ws[k] = np.zeros((n, K), np.float32)
+    return ws
+
+
+def standard_layer(row, col, x, p, hidden, bf16, threads=0, wq=None, ws=None):
     """B0 strong standard layer (baseline/src/baseline_standard.cpp:98-108).
 
     Returns (stages, times_ms) with times = convert, projection, lr,
     max_prescan, aggregate, finish, total.  ``wq`` is the bf16-rounded W
-    (prepared outside the timer, like prepare() in common.cpp:97-119).
+    (prepared outside the timer, like prepare() in common.cpp:97-119); ``ws``
+    a standard_workspace() reused across calls.
     """
     row, col = _graph_args(row, col)
     x = np.ascontiguousarray(x, np.float32)
     n = row.size - 1
-    K, W = p["heads"], p["heads"] * p["dim"]
     w = p["w"]
     if bf16:
         w = quantize_bf16(w) if wq is None else wq
-    xq = np.empty_like(x) if bf16 else None
-    st = {"z": np.empty((n, W), np.float32), "out": np.empty((n, W), np.float32)}
-    for k in ("left", "right", "max", "den"):
-        st[k] = np.empty((n, K), np.float32)
+    st = ws if ws is not None else standard_workspace(n, p)
     t = np.zeros(7, np.float64)
-    lib().or_standard_layer(n, _p(row), _p(col), _p(x), p["in"], K, p["dim"], _p(np.ascontiguousarray(w)),
-                            _p(p["al"]), _p(p["ar"]), int(hidden), int(bf16), int(threads), _p(xq), _p(st["z"]),
-                            _p(st["left"]), _p(st["right"]), _p(st["max"]), _p(st["den"]), _p(st["out"]), _p(t))
+    lib().or_standard_layer(n, _p(row), _p(col), _p(x), p["in"], p["heads"], p["dim"],
+                            _p(np.ascontiguousarray(w, np.float32)), _p(p["al"]), _p(p["ar"]), int(hidden),
+                            int(bf16), int(threads), _p(st["xq"]), _p(st["z"]), _p(st["left"]), _p(st["right"]),
+                            _p(st["max"]), _p(st["den"]), _p(st["out"]), _p(t))
     return st, t
 
 

@@ -20,6 +20,12 @@
 
 namespace {
 using Clock = std::chrono::steady_clock;
+typedef float v16 __attribute__((vector_size(64)));
+#ifdef __AVX512F__
+constexpr int kMR = 6;  // 12 zmm accumulators
+#else
+constexpr int kMR = 3;  // 12 ymm accumulators (each v16 is two ymm)
+#endif
 double ms_since(Clock::time_point a) {
     return std::chrono::duration<double, std::milli>(Clock::now() - a).count();
 }
@@ -49,12 +55,13 @@ inline float expand(uint16_t b) {  // baseline/src/common.cpp:84
 // the exponent field.  Arguments below -87.33 return 0 (the softmax only
 // evaluates x <= 0, where such values are below FP32's normal range).
 inline float exp_cw(float x) {
-    if (x < -87.33f) return 0.0f;
-    if (x > 88.7f) x = 88.7f;
+    const bool under = x < -87.33f;  // e^x below 2^-126: returned as 0
+    x = std::min(std::max(x, -87.33f), 88.7f);
     const float log2e = 1.44269504088896341f;
     const float ln2_hi = 0.693359375f;          // 0x3f318000: 9 significant bits
     const float ln2_lo = -2.12194440e-4f;       // ln2 - ln2_hi
-    float n = std::nearbyint(x * log2e);
+    const float shifter = 12582912.0f;          // 1.5 * 2^23: adding it rounds to an integer
+    const float n = (x * log2e + shifter) - shifter;
     float r = x - n * ln2_hi;
     r = r - n * ln2_lo;
     // Taylor coefficients 1/k!, k = 7..0, Horner form.
@@ -66,33 +73,26 @@ inline float exp_cw(float x) {
     p = p * r + 0.5f;
     p = p * r + 1.0f;
     p = p * r + 1.0f;
-    int32_t e = int32_t(n) + 127;
-    if (e <= 0) {  // result in the subnormal range: scale in two steps
-        uint32_t b1 = uint32_t(e + 64) << 23;
-        float s1;
-        std::memcpy(&s1, &b1, 4);
-        return p * s1 * 5.42101086e-20f;  // 2^-64
-    }
-    uint32_t bits = uint32_t(e) << 23;
-    float s;
-    std::memcpy(&s, &bits, 4);
-    return p * s;
+    const int32_t e = int32_t(n) + 127;  // >= 1 after the clamp: always a normal power of two
+    const uint32_t bits = uint32_t(e) << 23;
+    float sc;
+    std::memcpy(&sc, &bits, 4);
+    return under ? 0.0f : p * sc;
 }
 // expm1 for x < 0 (ELU branch): series for small |x| avoids cancellation.
 inline float expm1_neg(float x) {
-    if (x > -0.25f) {
-        // Taylor series of e^x - 1 to x^8/8!: |x|^9/9! < 1e-11 for |x| <= 0.25.
-        float p = 1.0f / 40320.0f;
-        p = p * x + 1.0f / 5040.0f;
-        p = p * x + 1.0f / 720.0f;
-        p = p * x + 1.0f / 120.0f;
-        p = p * x + 1.0f / 24.0f;
-        p = p * x + 1.0f / 6.0f;
-        p = p * x + 0.5f;
-        p = p * x + 1.0f;
-        return p * x;
-    }
-    return exp_cw(x) - 1.0f;
+    // Taylor series of e^x - 1 to x^8/8! for |x| <= 0.25 (|x|^9/9! < 1e-11),
+    // exp(x) - 1 below; both evaluated and selected so the loop vectorises.
+    float p = 1.0f / 40320.0f;
+    p = p * x + 1.0f / 5040.0f;
+    p = p * x + 1.0f / 720.0f;
+    p = p * x + 1.0f / 120.0f;
+    p = p * x + 1.0f / 24.0f;
+    p = p * x + 1.0f / 6.0f;
+    p = p * x + 0.5f;
+    p = p * x + 1.0f;
+    const float series = p * x;
+    return x > -0.25f ? series : exp_cw(x) - 1.0f;
 }
 }  // namespace
 
@@ -275,6 +275,12 @@ void or_standard_layer(uint64_t n, const uint64_t* row, const uint32_t* col, con
                        float* mx, float* den, float* out, double* times) {
     if (threads > 0) omp_set_num_threads(threads);
     const int K = heads, W = heads * dim;
+    // Static weight preparation outside the stage timers (prepare(),
+    // common.cpp:97-119): W in 32-column panels [panel][k][32], zero-padded.
+    std::vector<float> wpanel_buf(size_t((W + 31) / 32) * in * 32, 0.0f);
+    for (int k = 0; k < in; ++k)
+        for (int c = 0; c < W; ++c) wpanel_buf[(size_t(c / 32) * in + k) * 32 + c % 32] = w[size_t(k) * W + c];
+    const float* wpanel = wpanel_buf.data();
     const float* xin = x;
     auto t0 = Clock::now(), t = t0;
     // convert: common.cpp:85-93 (the bf16 value is kept widened to FP32).
@@ -286,31 +292,42 @@ void or_standard_layer(uint64_t n, const uint64_t* row, const uint32_t* col, con
     }
     times[0] = ms_since(t);
     t = Clock::now();
-    // projection: register-blocked FP32 GEMM, 4 rows x 32 columns per step.
-    // bf16 products are exact in FP32, so this equals BF16xBF16->FP32 up to
-    // the accumulation order.
+    // projection: FP32 GEMM on the prepacked 32-column panels of W, MR rows x
+    // 32 columns of accumulators per step (vector registers).  bf16 products
+    // are exact in FP32, so this equals BF16xBF16->FP32 up to the
+    // accumulation order.
     {
-        const int RB = 4, CB = 32;
-        const uint64_t row_blocks = (n + RB - 1) / RB;
-        const int col_blocks = (W + CB - 1) / CB;
-        #pragma omp parallel for schedule(static) collapse(2)
-        for (uint64_t rb = 0; rb < row_blocks; ++rb)
-            for (int cb = 0; cb < col_blocks; ++cb) {
-                const uint64_t r0 = rb * RB;
-                const int rows = int(std::min<uint64_t>(RB, n - r0));
-                const int c0 = cb * CB, cols = std::min(CB, W - c0);
-                float acc[RB][CB] = {};
+        const int panels = (W + 31) / 32;
+        const uint64_t row_blocks = (n + kMR - 1) / kMR;
+        #pragma omp parallel for schedule(static)
+        for (uint64_t rb = 0; rb < row_blocks; ++rb) {
+            const uint64_t r0 = rb * kMR;
+            const int rows = int(std::min<uint64_t>(kMR, n - r0));
+            const float* arow[kMR];
+            for (int r = 0; r < kMR; ++r) arow[r] = xin + (r0 + std::min(r, rows - 1)) * in;
+            for (int pnl = 0; pnl < panels; ++pnl) {
+                const float* bp = wpanel + size_t(pnl) * in * 32;
+                v16 c[kMR][2];
+                for (int r = 0; r < kMR; ++r) c[r][0] = c[r][1] = v16{};
                 for (int k = 0; k < in; ++k) {
-                    const float* wk = w + size_t(k) * W + c0;
-                    for (int r = 0; r < RB; ++r) {
-                        const float a = r < rows ? xin[(r0 + r) * in + k] : 0.0f;
-                        #pragma omp simd
-                        for (int c = 0; c < CB; ++c) acc[r][c] += a * (c < cols ? wk[c] : 0.0f);
+                    v16 b0, b1;
+                    std::memcpy(&b0, bp + size_t(k) * 32, 64);
+                    std::memcpy(&b1, bp + size_t(k) * 32 + 16, 64);
+                    for (int r = 0; r < kMR; ++r) {
+                        const float a = arow[r][k];
+                        c[r][0] += a * b0;
+                        c[r][1] += a * b1;
                     }
                 }
-                for (int r = 0; r < rows; ++r)
-                    for (int c = 0; c < cols; ++c) z[(r0 + r) * W + c0 + c] = acc[r][c];
+                const int c0 = pnl * 32, cols = std::min(32, W - c0);
+                for (int r = 0; r < rows; ++r) {
+                    float tmp[32];
+                    std::memcpy(tmp, &c[r][0], 64);
+                    std::memcpy(tmp + 16, &c[r][1], 64);
+                    std::memcpy(z + (r0 + r) * W + c0, tmp, size_t(cols) * 4);
+                }
             }
+        }
     }
     times[1] = ms_since(t);
     t = Clock::now();
@@ -348,15 +365,24 @@ void or_standard_layer(uint64_t n, const uint64_t* row, const uint32_t* col, con
         #pragma omp for schedule(dynamic, 64)
         for (uint64_t i = 0; i < n; ++i) {
             std::fill(acc.begin(), acc.end(), 0.0f);
-            float dn[8] = {}, l[8], m[8], wgt[8];
+            float dn[8] = {}, l[8] = {}, m[8] = {}, wgt[8];
             for (int h = 0; h < K; ++h) {
                 l[h] = left[i * K + h];
                 m[h] = mx[i * K + h];
             }
             for (uint64_t e = row[i]; e < row[i + 1]; ++e) {
                 const size_t j = col[e];
-                for (int h = 0; h < K; ++h) {
-                    wgt[h] = exp_cw(leak(l[h] + right[j * K + h]) - m[h]);
+                // Software prefetch of the Z row PF edges ahead (random 1 KB
+                // gathers are latency-bound on one core otherwise).
+                constexpr uint64_t PF = 6;
+                if (e + PF < row[i + 1]) {
+                    const char* zp = reinterpret_cast<const char*>(z + size_t(col[e + PF]) * W);
+                    for (int off = 0; off < W * 4; off += 64) __builtin_prefetch(zp + off);
+                }
+                #pragma omp simd
+                for (int h = 0; h < 8; ++h) {
+                    const float r = right[j * K + (h < K ? h : 0)];
+                    wgt[h] = h < K ? exp_cw(leak(l[h] + r) - m[h]) : 0.0f;
                     dn[h] += wgt[h];
                 }
                 const float* zj = z + j * W;
@@ -381,10 +407,10 @@ void or_standard_layer(uint64_t n, const uint64_t* row, const uint32_t* col, con
             const float dn = den[i * K + h];
             const float s = dn > 0 ? 1 / dn : 0;
             float* o = out + i * W + h * dim;
+            #pragma omp simd
             for (int d = 0; d < dim; ++d) {
-                float v = o[d] * s;
-                if (hidden && v < 0) v = expm1_neg(v);
-                o[d] = v;
+                const float v = o[d] * s;
+                o[d] = hidden ? (v < 0 ? expm1_neg(std::min(v, 0.0f)) : v) : v;
             }
         }
     times[5] = ms_since(t);
