@@ -78,6 +78,8 @@ def main():
     ap.add_argument("--precision", default="bf16", choices=["bf16", "fp32"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-threads", type=int, default=int(os.environ.get("OMP_NUM_THREADS", "0") or 0))
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="run one 1 GiB device-to-device copy first (counter calibration under rocprofv3 --pmc)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (run with --gpus 1).", file=sys.stderr)
@@ -102,6 +104,12 @@ def main():
     ctx.set_input(x)
     print(f"# workload {w.name}: N={n} E={e} gen {gen_s:.1f}s", file=sys.stderr, flush=True)
 
+    if args.calibrate_copy:
+        src = torch.ones(1 << 28, dtype=torch.float32, device="cuda")  # 1 GiB
+        dst = torch.empty_like(src)
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
     for _ in range(args.warmup):
         ctx.model_forward(prec, gatgpu.AUTO, want_logits=False, timed=False)
     torch.cuda.synchronize()

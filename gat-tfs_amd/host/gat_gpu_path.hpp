@@ -1,0 +1,122 @@
+// C++ adapter that registers the gfx950 path in a harness built around the
+// reference's containers: gat::Graph (u64 row, u32 col, f32 x; din, classes),
+// gat::Param (in, heads, dim, w, al, ar), gat::Workspace (z, left, right, max,
+// den, out vectors) and gat::Times (convert, projection, lr, max_prescan,
+// aggregate, normalize, activation, total in seconds) --
+// baseline/include/gat.hpp:32-106.  It is templated on those types, so it
+// compiles against the reference's own header or against any structs with the
+// same field names (gat-tfs_amd/host/gat_types.hpp).
+//
+// gpu_layer() has the shape of the per-layer entry points the harness
+// dispatches to in run_path (baseline/bench/main.cpp:21-25,
+// baseline/include/gat.hpp:107-117): same inputs, same Workspace fields
+// filled, same Times fields.  Every non-zero C-ABI return becomes a
+// std::runtime_error, which the harness turns into "FAIL msg", exit 1
+// (baseline/bench/main.cpp:184).
+#pragma once
+#include <cstdint>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+#include "gatgpu.h"
+
+namespace gatgpu_host {
+
+inline void check(gatgpu_ctx* ctx, int rc, const char* what) {
+    if (rc != GATGPU_OK)
+        throw std::runtime_error(std::string(what) + ": " + gatgpu_last_error(ctx) + " (code " +
+                                 std::to_string(rc) + ")");
+}
+
+// One device context plus the identity of what it currently holds, so a
+// harness that calls the path layer by layer uploads the graph and each
+// layer's weights once.
+class GpuPath {
+   public:
+    explicit GpuPath(int device = 0) {
+        gatgpu_ctx* c = nullptr;
+        check(nullptr, gatgpu_create(device, &c), "gatgpu_create");
+        ctx_ = c;
+    }
+    ~GpuPath() { gatgpu_destroy(ctx_); }
+    GpuPath(const GpuPath&) = delete;
+    GpuPath& operator=(const GpuPath&) = delete;
+    gatgpu_ctx* ctx() const { return ctx_; }
+
+    template <class Graph>
+    void set_graph(const Graph& g) {
+        if (graph_ == static_cast<const void*>(&g) && n_ == g.n && e_ == g.e) return;
+        check(ctx_, gatgpu_set_graph(ctx_, g.n, g.e, g.row.data(), g.col.data()), "gatgpu_set_graph");
+        check(ctx_, gatgpu_set_input(ctx_, g.n, int(g.din), g.x.data()), "gatgpu_set_input");
+        graph_ = &g;
+        n_ = g.n;
+        e_ = g.e;
+    }
+
+    template <class Param>
+    void set_layer(int layer, const Param& p) {
+        if (layer_[layer] == static_cast<const void*>(&p)) return;
+        check(ctx_, gatgpu_set_layer(ctx_, layer, p.in, p.heads, p.dim, p.w.data(), p.al.data(), p.ar.data()),
+              "gatgpu_set_layer");
+        layer_[layer] = &p;
+    }
+
+    // The per-layer path: input -> w.out (plus the stage vectors the
+    // reference's correctness mode compares), times in seconds.
+    template <class Graph, class Param, class Workspace, class Times>
+    void layer(const Graph& g, const Param& p, int layer_index, const std::vector<float>& input, Workspace& w,
+               bool hidden, Times& t, int precision, int dataflow = GATGPU_AUTO) {
+        set_graph(g);
+        set_layer(layer_index, p);
+        gatgpu_times gt{};
+        check(ctx_,
+              gatgpu_layer_forward(ctx_, layer_index, precision, dataflow, hidden ? 1 : 0, input.data(), &gt),
+              "gatgpu_layer_forward");
+        t.convert = gt.convert_ms * 1e-3;
+        t.projection = gt.projection_ms * 1e-3;
+        t.lr = gt.lr_ms * 1e-3;
+        t.max_prescan = gt.max_prescan_ms * 1e-3;
+        t.aggregate = gt.aggregate_ms * 1e-3;
+        t.normalize = gt.normalize_ms * 1e-3;
+        t.activation = gt.activation_ms * 1e-3;
+        t.total = gt.total_ms * 1e-3;
+        fetch(layer_index, GATGPU_STAGE_OUT, w.out);
+        fetch(layer_index, GATGPU_STAGE_LEFT, w.left);
+        fetch(layer_index, GATGPU_STAGE_RIGHT, w.right);
+        fetch(layer_index, GATGPU_STAGE_MAX, w.max);
+        fetch(layer_index, GATGPU_STAGE_DEN, w.den);
+        fetch(layer_index, GATGPU_STAGE_Z, w.z);
+    }
+
+    // Three layers chained on the device; returns the model time in seconds
+    // (HIP events from layer 1's first kernel to layer 3's last).
+    double model(int precision, std::vector<float>* logits, int dataflow = GATGPU_AUTO) {
+        double ms = 0;
+        gatgpu_times t[3];
+        if (logits) logits->resize(size_t(n_) * classes_hint_);
+        check(ctx_, gatgpu_model_forward(ctx_, precision, dataflow, logits ? logits->data() : nullptr, t, &ms),
+              "gatgpu_model_forward");
+        return ms * 1e-3;
+    }
+    void set_classes_hint(int c) { classes_hint_ = c; }
+
+   private:
+    void fetch(int layer, int which, std::vector<float>& v) {
+        uint64_t count = 0;
+        check(ctx_, gatgpu_stage_size(ctx_, layer, which, &count), "gatgpu_stage_size");
+        if (!count) {
+            v.clear();
+            return;
+        }
+        v.resize(count);
+        check(ctx_, gatgpu_get_stage(ctx_, layer, which, v.data()), "gatgpu_get_stage");
+    }
+    gatgpu_ctx* ctx_ = nullptr;
+    const void* graph_ = nullptr;
+    const void* layer_[3] = {nullptr, nullptr, nullptr};
+    uint64_t n_ = 0, e_ = 0;
+    int classes_hint_ = 0;
+};
+
+}  // namespace gatgpu_host
