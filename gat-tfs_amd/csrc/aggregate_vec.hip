@@ -27,20 +27,21 @@ namespace {
 constexpr int kThreads = 256;
 constexpr int kWavesPerBlock = kThreads / kWave;
 
-template <class ZT, int W_, int K_, int EB_>
+template <class ZT, int W_, int K_, int BE_>
 struct Cfg {
-    static constexpr int W = W_, K = K_, EB = EB_;
-    static constexpr int VEC = 16 / int(sizeof(ZT));
+    static constexpr int W = W_, K = K_, BE = BE_;    // BE: edges scored per block
+    static constexpr int VEC = 16 / int(sizeof(ZT));  // features per 16-byte load
     static constexpr int DIM = W / K;
-    static constexpr int LPR = W / VEC;
-    static constexpr int EPI = LPR >= kWave ? 1 : kWave / LPR;
-    static constexpr int VPL = LPR <= kWave ? 1 : LPR / kWave;
-    static constexpr int NU = EB / EPI;
-    static constexpr int SPL = (EB * K + kWave - 1) / kWave;
+    static constexpr int LPR = W / VEC;               // lanes (16-byte vectors) per row
+    static constexpr int EPI = LPR >= kWave ? 1 : kWave / LPR;  // edges per load instruction
+    static constexpr int VPL = LPR <= kWave ? 1 : LPR / kWave;  // vectors per lane per edge
+    static constexpr int NUB = BE / EPI;              // load instructions of a full block
+    static constexpr int S = BE * K / kWave;          // (edge, head) scores per lane per block
+    static constexpr int G = 8;                       // load instructions in flight per group
     static constexpr int ACC = VPL * VEC;
     static_assert(W % K == 0 && DIM % VEC == 0, "a vector must not straddle two heads");
     static_assert(LPR * EPI == kWave || LPR % kWave == 0, "lanes per row must divide or fill the wave");
-    static_assert(EB % EPI == 0, "batch must fill whole load instructions");
+    static_assert(BE % EPI == 0 && (BE * K) % kWave == 0 && NUB % G == 0, "block must fill whole groups");
     static_assert(kWave % K == 0, "heads must divide the wave");
 };
 
@@ -94,69 +95,115 @@ struct RowAcc {
     float dloc;
 };
 
-// Edges [beg, end) into the lane's accumulators (Mh, Lh: this scorer lane's head).
-template <class C, class ZT>
-__device__ inline void accumulate(uint64_t beg, uint64_t end, const uint32_t* __restrict__ pcol,
-                                  const float* __restrict__ R, const ZT* __restrict__ Z, float Lh, float Mh,
-                                  float* pb, uint32_t* jb, RowAcc<C>& st) {
+// Max of R[j, head] over edges [beg, end) for this lane's head, reduced over
+// the lanes of the same head (lane l covers edges l/K, l/K + 64/K, ...).
+template <class C>
+__device__ inline float row_max(uint64_t beg, uint64_t end, const uint32_t* __restrict__ pcol,
+                                const float* __restrict__ R) {
+    const int lane = threadIdx.x % kWave, hs = lane % C::K;
+    float m = -INFINITY;
+    for (uint64_t e = beg + lane / C::K; e < end; e += kWave / C::K) m = fmaxf(m, R[uint64_t(pcol[e]) * C::K + hs]);
+    for (int off = C::K; off < kWave; off <<= 1) m = fmaxf(m, __shfl_xor(m, off));
+    return m;
+}
+
+// One block of cnt <= BE edges starting at base.  Every lane loads the source
+// ids and R values of its S (edge, head) pairs once; with FIND_MAX (a row
+// that fits one block) the exact row max comes from those registers, so R is
+// read once per edge.  Scores and ids go to LDS in reader order, then the
+// Z rows are gathered in groups of G 16-byte loads per lane, double-buffered
+// so that one group's loads are in flight while the previous group's FMAs run.
+template <class C, class ZT, bool FIND_MAX>
+__device__ inline void block(uint64_t base, int cnt, const uint32_t* __restrict__ pcol,
+                             const float* __restrict__ R, const ZT* __restrict__ Z, float Lh, float& Mh,
+                             float* pb, uint32_t* jb, RowAcc<C>& st) {
     const int lane = threadIdx.x % kWave;
+    const int hs = lane % C::K;
     const int slot = C::EPI > 1 ? lane / C::LPR : 0;
     const int sub = C::EPI > 1 ? lane % C::LPR : lane;
-    const int hs = lane % C::K;  // scorer head (same for every s since 64 % K == 0)
-    int hr[C::VPL];              // reader head of each vector
+    uint32_t jv[C::S];
+    float rv[C::S];
+#pragma unroll
+    for (int s = 0; s < C::S; ++s) {
+        const int t = lane / C::K + (kWave / C::K) * s;
+        jv[s] = t < cnt ? pcol[base + t] : 0u;
+        rv[s] = t < cnt ? R[uint64_t(jv[s]) * C::K + hs] : -INFINITY;
+    }
+    if constexpr (FIND_MAX) {
+        float m = rv[0];
+#pragma unroll
+        for (int s = 1; s < C::S; ++s) m = fmaxf(m, rv[s]);
+        for (int off = C::K; off < kWave; off <<= 1) m = fmaxf(m, __shfl_xor(m, off));
+        Mh = leaky(Lh + m);
+    }
+#pragma unroll
+    for (int s = 0; s < C::S; ++s) {
+        const int t = lane / C::K + (kWave / C::K) * s;
+        const float p = t < cnt ? expf(leaky(Lh + rv[s]) - Mh) : 0.0f;
+        st.dloc += p;
+        const int u = t / C::EPI, sl = t % C::EPI;
+        pb[(hs * C::EPI + sl) * C::NUB + u] = p;
+        if (hs == 0) jb[sl * C::NUB + u] = jv[s];
+    }
+    wave_sync();
+    int hr[C::VPL];
 #pragma unroll
     for (int v = 0; v < C::VPL; ++v) hr[v] = ((sub + kWave * v) * C::VEC) / C::DIM;
-    for (uint64_t base = beg; base < end; base += C::EB) {
-        const uint64_t rem = end - base;
-        const int cnt = rem < uint64_t(C::EB) ? int(rem) : C::EB;
-        // ---- scores
+    const int nu = (cnt + C::EPI - 1) / C::EPI;  // load instructions of this block
+    uint4 buf[2][C::G][C::VPL];
+    auto issue = [&](int b, int u0) {
 #pragma unroll
-        for (int s = 0; s < C::SPL; ++s) {
-            const int q = lane + kWave * s;
-            const int t = q / C::K;
-            if (q < C::EB * C::K) {
-                float p = 0.0f;
-                uint32_t j = 0;
-                if (t < cnt) {
-                    j = pcol[base + t];
-                    p = expf(leaky(Lh + R[uint64_t(j) * C::K + hs]) - Mh);
-                }
-                st.dloc += p;
-                const int u = t / C::EPI, sl = t % C::EPI;
-                pb[(hs * C::EPI + sl) * C::NU + u] = p;
-                if (hs == 0) jb[sl * C::NU + u] = j;
-            }
-        }
-        wave_sync();
-        // ---- gathers
-        float p[C::VPL][C::NU];
-        uint32_t j[C::NU];
-#pragma unroll
-        for (int u = 0; u < C::NU; ++u) j[u] = jb[slot * C::NU + u];
-#pragma unroll
-        for (int v = 0; v < C::VPL; ++v)
-#pragma unroll
-            for (int u = 0; u < C::NU; ++u) p[v][u] = pb[(hr[v] * C::EPI + slot) * C::NU + u];
-        uint4 raw[C::NU][C::VPL];
-#pragma unroll
-        for (int u = 0; u < C::NU; ++u) {
+        for (int q = 0; q < C::G; ++q) {
+            const int u = u0 + q;
             const bool ok = u * C::EPI + slot < cnt;
-            const ZT* row = Z + uint64_t(j[u]) * C::W;
+            const uint32_t j = jb[slot * C::NUB + (u < C::NUB ? u : 0)];
+            const ZT* row = Z + uint64_t(j) * C::W;
 #pragma unroll
             for (int v = 0; v < C::VPL; ++v)
-                raw[u][v] = ok ? *reinterpret_cast<const uint4*>(row + (sub + kWave * v) * C::VEC)
-                               : make_uint4(0, 0, 0, 0);
+                buf[b][q][v] = ok ? *reinterpret_cast<const uint4*>(row + (sub + kWave * v) * C::VEC)
+                                  : make_uint4(0, 0, 0, 0);
         }
+    };
+    auto consume = [&](int b, int u0) {
 #pragma unroll
-        for (int u = 0; u < C::NU; ++u)
+        for (int q = 0; q < C::G; ++q) {
+            const int u = u0 + q < C::NUB ? u0 + q : 0;
 #pragma unroll
             for (int v = 0; v < C::VPL; ++v) {
+                const float p = pb[(hr[v] * C::EPI + slot) * C::NUB + u];
                 float f[C::VEC];
-                unpack(raw[u][v], f);
+                unpack(buf[b][q][v], f);
 #pragma unroll
-                for (int x = 0; x < C::VEC; ++x) st.acc[v * C::VEC + x] += p[v][u] * f[x];
+                for (int x = 0; x < C::VEC; ++x) st.acc[v * C::VEC + x] += p * f[x];
             }
-        wave_sync();
+        }
+    };
+    // Groups beyond nu load nothing (ok == false) and add zeros.
+    issue(0, 0);
+    for (int u0 = 0; u0 < nu; u0 += 2 * C::G) {
+        if (u0 + C::G < nu) issue(1, u0 + C::G);
+        consume(0, u0);
+        if (u0 + C::G < nu) {
+            if (u0 + 2 * C::G < nu) issue(0, u0 + 2 * C::G);
+            consume(1, u0 + C::G);
+        }
+    }
+    wave_sync();
+}
+
+// Edges [beg, end) of a row or chunk whose max is known (Mh) or, for a row
+// that fits one block, found on the way.
+template <class C, class ZT>
+__device__ inline void accumulate(uint64_t beg, uint64_t end, bool find_max, const uint32_t* __restrict__ pcol,
+                                  const float* __restrict__ R, const ZT* __restrict__ Z, float Lh, float& Mh,
+                                  float* pb, uint32_t* jb, RowAcc<C>& st) {
+    if (find_max) {
+        block<C, ZT, true>(beg, int(end - beg), pcol, R, Z, Lh, Mh, pb, jb, st);
+        return;
+    }
+    for (uint64_t base = beg; base < end; base += C::BE) {
+        const uint64_t rem = end - base;
+        block<C, ZT, false>(base, rem < uint64_t(C::BE) ? int(rem) : C::BE, pcol, R, Z, Lh, Mh, pb, jb, st);
     }
 }
 
@@ -229,8 +276,8 @@ k_split_prescan(const uint64_t* __restrict__ prow, const uint32_t* __restrict__ 
 
 template <class C, class ZT>
 __global__ void __launch_bounds__(kThreads) k_agg_vec(VArgs<ZT> a) {
-    __shared__ float pbuf[kWavesPerBlock][C::K * C::EB];
-    __shared__ uint32_t jbuf[kWavesPerBlock][C::EB];
+    __shared__ float pbuf[kWavesPerBlock][C::K * C::BE];
+    __shared__ uint32_t jbuf[kWavesPerBlock][C::BE];
     __shared__ float dsh[kWavesPerBlock][8];
     const int w = threadIdx.x / kWave, lane = threadIdx.x % kWave;
     const uint64_t item = uint64_t(blockIdx.x) * kWavesPerBlock + w;
@@ -253,8 +300,8 @@ __global__ void __launch_bounds__(kThreads) k_agg_vec(VArgs<ZT> a) {
         for (uint32_t q = lane / C::K; q < nch; q += kWave / C::K) m = fmaxf(m, a.sp.mchunk[(first + q) * 8 + hs]);
         for (int off = C::K; off < kWave; off <<= 1) m = fmaxf(m, __shfl_xor(m, off));
         const float Lh = a.L[uint64_t(i) * C::K + hs];
-        const float Mh = leaky(Lh + m);
-        accumulate<C, ZT>(beg, end, a.pcol, a.R, a.Z, Lh, Mh, pbuf[w], jbuf[w], st);
+        float Mh = leaky(Lh + m);
+        accumulate<C, ZT>(beg, end, false, a.pcol, a.R, a.Z, Lh, Mh, pbuf[w], jbuf[w], st);
         reduce_lanes<C>(st);
         float* part = a.sp.part + c * (C::W + 8);
         const int slot = C::EPI > 1 ? lane / C::LPR : 0;
@@ -313,12 +360,11 @@ __global__ void __launch_bounds__(kThreads) k_agg_vec(VArgs<ZT> a) {
     const uint64_t beg = a.prow[k], end = a.prow[k + 1];
     if (i >= a.n || beg > end || end > a.e) return;
     const float Lh = a.L[uint64_t(i) * C::K + hs];
-    float m = -INFINITY;
-    for (uint64_t e = beg + lane / C::K; e < end; e += kWave / C::K)
-        m = fmaxf(m, a.R[uint64_t(a.pcol[e]) * C::K + hs]);
-    for (int off = C::K; off < kWave; off <<= 1) m = fmaxf(m, __shfl_xor(m, off));
-    const float Mh = end > beg ? leaky(Lh + m) : 0.0f;
-    accumulate<C, ZT>(beg, end, a.pcol, a.R, a.Z, Lh, Mh, pbuf[w], jbuf[w], st);
+    const uint64_t deg = end - beg;
+    // Empty row: max 0, denominator 0, output 0 (baseline/src/ref_fp32.cpp:11).
+    float Mh = 0.0f;
+    if (deg > uint64_t(C::BE)) Mh = leaky(Lh + row_max<C>(beg, end, a.pcol, a.R));
+    if (deg) accumulate<C, ZT>(beg, end, deg <= uint64_t(C::BE), a.pcol, a.R, a.Z, Lh, Mh, pbuf[w], jbuf[w], st);
     reduce_lanes<C>(st);
     if (lane < C::K) {
         a.mx[uint64_t(i) * C::K + lane] = Mh;
@@ -370,11 +416,11 @@ hipError_t launch_aggregate_vec(const AggArgs& g, const RowBins& bins, const Spl
     const int W = g.heads * g.dim;
     if (g.heads != 8) return hipErrorInvalidValue;
     if (g.feat_bf16) {
-        if (W == 256) return run<Cfg<uint16_t, 256, 8, 16>, uint16_t>(g, bins, t, s);
-        if (W == 512) return run<Cfg<uint16_t, 512, 8, 8>, uint16_t>(g, bins, t, s);
+        if (W == 256) return run<Cfg<uint16_t, 256, 8, 64>, uint16_t>(g, bins, t, s);
+        if (W == 512) return run<Cfg<uint16_t, 512, 8, 64>, uint16_t>(g, bins, t, s);
     } else {
-        if (W == 256) return run<Cfg<float, 256, 8, 8>, float>(g, bins, t, s);
-        if (W == 512) return run<Cfg<float, 512, 8, 8>, float>(g, bins, t, s);
+        if (W == 256) return run<Cfg<float, 256, 8, 64>, float>(g, bins, t, s);
+        if (W == 512) return run<Cfg<float, 512, 8, 64>, float>(g, bins, t, s);
     }
     return hipErrorInvalidValue;
 }

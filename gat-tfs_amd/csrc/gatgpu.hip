@@ -56,6 +56,10 @@ struct LayerState {
     // bf16 MFMA projection weights (pack_projection_weights order)
     DevBuf wpk;
     int ksteps = 0, groups = 0, nmb = 0;
+    // L/R-only block for the aggregate-first front end
+    DevBuf wlr;
+    int lr_ksteps = 0;
+    int dataflow = 0;  // dataflow of the last forward
     int width() const { return heads * dim; }
 };
 
@@ -169,7 +173,7 @@ int compute_bins(gatgpu_ctx* c) {
         HIPCHECK(c, c->split_k.ensure(ck.size() * 4));
         HIPCHECK(c, c->split_first.ensure(cf.size() * 4));
         HIPCHECK(c, c->mchunk.ensure(ck.size() * 8 * 4));
-        HIPCHECK(c, c->part.ensure(ck.size() * (512 + 8) * 4));
+        HIPCHECK(c, c->part.ensure(ck.size() * (8 * 128 + 8) * 4));  // largest partial: aggregate-first U
         HIPCHECK(c, c->counter.ensure(ck.size() * 4));
         HIPCHECK(c, hipMemcpy(c->split_k.p, ck.data(), ck.size() * 4, hipMemcpyHostToDevice));
         HIPCHECK(c, hipMemcpy(c->split_first.p, cf.data(), cf.size() * 4, hipMemcpyHostToDevice));
@@ -222,10 +226,103 @@ int build_schedule(gatgpu_ctx* c) {
     return compute_bins(c);
 }
 
+// AUTO selects transform-first: on gfx950 its aggregation plus MFMA
+// projection is faster than the aggregate-first kernel even where the input
+// row is narrower (measured: 100 -> 8x32 on the 64.3M-edge graph, 9.2 ms TF
+// against 10.7 ms AF).  Aggregate-first stays selectable per call.
+int resolve_dataflow(const LayerState& L, int precision, int dataflow) {
+    const bool af_ok = precision == GATGPU_BF16 && aggregate_af_supported(L.in, L.heads, L.dim);
+    if (dataflow == GATGPU_AUTO) return GATGPU_TRANSFORM_FIRST;
+    if (dataflow == GATGPU_AGGREGATE_FIRST && !af_ok) return -1;
+    return dataflow;
+}
+
 float ms_between(hipEvent_t a, hipEvent_t b) {
     float ms = 0.0f;
     if (hipEventElapsedTime(&ms, a, b) != hipSuccess) return 0.0f;
     return ms;
+}
+
+// Aggregate-first bf16 layer: convert the input to bf16 rows of 128, the
+// L/R-only MFMA front end (reordered contraction), then the aggregate-first
+// kernels (tiles of 32 rows + split-row chunks).
+int run_layer_af(gatgpu_ctx* c, int l, bool hidden, const float* src32, const uint16_t* srcbf, int ev_base) {
+    LayerState& Ls = c->L[l];
+    const uint64_t n = c->n;
+    const int K = Ls.heads, W = Ls.width(), D = Ls.in, xs = af_input_stride();
+    HIPCHECK(c, Ls.left.ensure(n * K * 4));
+    HIPCHECK(c, Ls.right.ensure(n * K * 4));
+    HIPCHECK(c, Ls.mx.ensure(n * K * 4));
+    HIPCHECK(c, Ls.den.ensure(n * K * 4));
+    if (hidden) HIPCHECK(c, Ls.outbf.ensure(n * W * 2));
+    else HIPCHECK(c, Ls.out32.ensure(n * W * 4));
+    if (srcbf && D != xs) {  // chained bf16 input in another row layout
+        HIPCHECK(c, Ls.in32.ensure(n * D * 4));
+        HIPCHECK(c, launch_widen_bf16(srcbf, Ls.in32.as<float>(), n * D, c->stream));
+        src32 = Ls.in32.as<float>();
+        srcbf = nullptr;
+    }
+    if (src32) HIPCHECK(c, Ls.inbf.ensure(n * xs * 2));
+    if (ev_base >= 0) HIPCHECK(c, hipEventRecord(c->ev[ev_base], c->stream));
+    if (src32) {
+        HIPCHECK(c, launch_to_bf16_pad(src32, Ls.inbf.as<uint16_t>(), n, D, xs, c->stream));
+        srcbf = Ls.inbf.as<uint16_t>();
+    }
+    if (ev_base >= 0) HIPCHECK(c, hipEventRecord(c->ev[ev_base + 1], c->stream));
+    ProjArgs pa{};
+    pa.x = srcbf;
+    pa.n = n;
+    pa.xs = xs;
+    pa.ksteps = Ls.lr_ksteps;
+    pa.wpk = Ls.wlr.as<uint4>();
+    pa.groups = 1;
+    pa.head_blocks = 0;
+    pa.nmb = 2;
+    pa.width = 0;
+    pa.heads = K;
+    pa.left = Ls.left.as<float>();
+    pa.right = Ls.right.as<float>();
+    pa.tiles = (n + 31) / 32;
+    HIPCHECK(c, launch_projection_mfma(pa, c->stream, c->cus));
+    if (ev_base >= 0) HIPCHECK(c, hipEventRecord(c->ev[ev_base + 2], c->stream));
+    AfArgs a{};
+    a.prow = c->prow.as<uint64_t>();
+    a.pcol = c->pcol.as<uint32_t>();
+    a.perm = c->perm;
+    a.L = Ls.left.as<float>();
+    a.R = Ls.right.as<float>();
+    a.X = srcbf;
+    a.wpk = Ls.wpk.as<uint4>();
+    a.nmb = Ls.nmb;
+    a.ksteps = Ls.ksteps;
+    a.wq = Ls.wq32.as<float>();
+    a.in = D;
+    a.heads = K;
+    a.hidden = hidden;
+    a.mx = Ls.mx.as<float>();
+    a.den = Ls.den.as<float>();
+    a.out32 = hidden ? nullptr : Ls.out32.as<float>();
+    a.outbf = hidden ? Ls.outbf.as<uint16_t>() : nullptr;
+    a.n = n;
+    a.e = c->e;
+    a.rows = c->bins.split_begin;
+    a.tiles = (a.rows + 31) / 32;
+    a.chunks = c->split.chunks;
+    a.chunk_k = c->split.chunk_k;
+    a.chunk_first = c->split.chunk_first;
+    a.chunk_edges = c->split.chunk_edges;
+    a.mchunk = c->split.mchunk;
+    a.part = c->split.part;
+    a.counter = c->split.counter;
+    HIPCHECK(c, launch_aggregate_af(a, c->stream, c->cus));
+    if (ev_base >= 0) HIPCHECK(c, hipEventRecord(c->ev[ev_base + 3], c->stream));
+    Ls.ran = true;
+    Ls.precision = GATGPU_BF16;
+    Ls.dataflow = GATGPU_AGGREGATE_FIRST;
+    Ls.z_valid = false;
+    Ls.out32_valid = !hidden;
+    Ls.outbf_valid = hidden;
+    return GATGPU_OK;
 }
 
 // Runs layer l on the device.  ev_base: first of 4 events (start, after
@@ -235,8 +332,6 @@ int run_layer(gatgpu_ctx* c, int l, int precision, int dataflow, bool hidden, co
     LayerState& Ls = c->L[l];
     const uint64_t n = c->n;
     const int K = Ls.heads, dim = Ls.dim, W = Ls.width(), D = Ls.in;
-    if (dataflow == GATGPU_AGGREGATE_FIRST)
-        return fail(c, GATGPU_EINVAL, "aggregate-first dataflow is not available in this build");
     // ---- input (explicit host input is uploaded before the timed region)
     const float* src32 = nullptr;
     const uint16_t* srcbf = nullptr;
@@ -257,6 +352,7 @@ int run_layer(gatgpu_ctx* c, int l, int precision, int dataflow, bool hidden, co
         else if (P.out32_valid) src32 = P.out32.as<float>();
         else return fail(c, GATGPU_ESTATE, "previous layer output missing");
     }
+    if (dataflow == GATGPU_AGGREGATE_FIRST) return run_layer_af(c, l, hidden, src32, srcbf, ev_base);
     // ---- outputs
     HIPCHECK(c, Ls.left.ensure(n * K * 4));
     HIPCHECK(c, Ls.right.ensure(n * K * 4));
@@ -339,16 +435,21 @@ int run_layer(gatgpu_ctx* c, int l, int precision, int dataflow, bool hidden, co
     if (ev_base >= 0) HIPCHECK(c, hipEventRecord(c->ev[ev_base + 3], c->stream));
     Ls.ran = true;
     Ls.precision = precision;
+    Ls.dataflow = GATGPU_TRANSFORM_FIRST;
     Ls.z_valid = true;
     Ls.out32_valid = !want_outbf;
     Ls.outbf_valid = want_outbf;
     return GATGPU_OK;
 }
 
-void fill_times(gatgpu_ctx* c, int ev_base, gatgpu_times* t) {
+void fill_times(gatgpu_ctx* c, int ev_base, gatgpu_times* t, int dataflow) {
     std::memset(t, 0, sizeof(*t));
     t->convert_ms = ms_between(c->ev[ev_base], c->ev[ev_base + 1]);
-    t->projection_ms = ms_between(c->ev[ev_base + 1], c->ev[ev_base + 2]);
+    // Transform-first: the MFMA projection with its fused L/R block.
+    // Aggregate-first: the L/R front end only; the projection runs inside the
+    // aggregation kernel and is counted in aggregate_ms.
+    if (dataflow == GATGPU_AGGREGATE_FIRST) t->lr_ms = ms_between(c->ev[ev_base + 1], c->ev[ev_base + 2]);
+    else t->projection_ms = ms_between(c->ev[ev_base + 1], c->ev[ev_base + 2]);
     t->aggregate_ms = ms_between(c->ev[ev_base + 2], c->ev[ev_base + 3]);
     t->total_ms = ms_between(c->ev[ev_base], c->ev[ev_base + 3]);
 }
@@ -465,6 +566,11 @@ int gatgpu_set_layer(gatgpu_ctx* c, int layer, int in, int heads, int dim, const
     pack_projection_weights(wq.data(), al, ar, in, heads, dim, packed, L.ksteps, L.groups, L.nmb);
     HIPCHECK(c, L.wpk.ensure(packed.size() * 2));
     HIPCHECK(c, hipMemcpyAsync(L.wpk.p, packed.data(), packed.size() * 2, hipMemcpyHostToDevice, c->stream));
+    std::vector<uint16_t> lrpacked;
+    pack_lr_weights(wq.data(), al, ar, in, heads, dim, lrpacked, L.lr_ksteps);
+    HIPCHECK(c, L.wlr.ensure(lrpacked.size() * 2));
+    HIPCHECK(c, hipMemcpyAsync(L.wlr.p, lrpacked.data(), lrpacked.size() * 2, hipMemcpyHostToDevice, c->stream));
+    HIPCHECK(c, hipStreamSynchronize(c->stream));
     HIPCHECK(c, L.w32.ensure(wn * 4));
     HIPCHECK(c, L.wq32.ensure(wn * 4));
     HIPCHECK(c, L.al.ensure(W * 4));
@@ -534,11 +640,12 @@ int gatgpu_layer_forward(gatgpu_ctx* c, int layer, int precision, int dataflow, 
         if (!all_finite(input, c->n * uint64_t(c->L[layer].in), &bad))
             return fail(c, GATGPU_ENONFINITE, "nonfinite layer input index=" + std::to_string(bad));
     }
-    const int flow = dataflow == GATGPU_AUTO ? GATGPU_TRANSFORM_FIRST : dataflow;
+    const int flow = resolve_dataflow(c->L[layer], precision, dataflow);
+    if (flow < 0) return fail(c, GATGPU_EINVAL, "aggregate-first needs bf16, head_dim 32 and in <= 128");
     if (int r = run_layer(c, layer, precision, flow, hidden != 0, input, times ? 0 : -1)) return r;
     HIPCHECK(c, hipStreamSynchronize(c->stream));
     HIPCHECK(c, hipGetLastError());
-    if (times) fill_times(c, 0, times);
+    if (times) fill_times(c, 0, times, c->L[layer].dataflow);
     return GATGPU_OK;
 }
 
@@ -554,13 +661,14 @@ int gatgpu_model_forward(gatgpu_ctx* c, int precision, int dataflow, float* logi
         return fail(c, GATGPU_EINVAL, "layer widths do not chain");
     const bool timed = times || total_ms;
     for (int l = 0; l < 3; ++l) {
-        const int flow = dataflow == GATGPU_AUTO ? GATGPU_TRANSFORM_FIRST : dataflow;
+        const int flow = resolve_dataflow(c->L[l], precision, dataflow);
+        if (flow < 0) return fail(c, GATGPU_EINVAL, "aggregate-first needs bf16, head_dim 32 and in <= 128");
         if (int r = run_layer(c, l, precision, flow, l < 2, nullptr, timed ? 4 * l : -1)) return r;
     }
     HIPCHECK(c, hipStreamSynchronize(c->stream));
     HIPCHECK(c, hipGetLastError());
     if (times)
-        for (int l = 0; l < 3; ++l) fill_times(c, 4 * l, &times[l]);
+        for (int l = 0; l < 3; ++l) fill_times(c, 4 * l, &times[l], c->L[l].dataflow);
     if (total_ms) *total_ms = ms_between(c->ev[0], c->ev[11]);
     if (logits) {
         const LayerState& L = c->L[2];

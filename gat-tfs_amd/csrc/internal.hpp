@@ -91,6 +91,8 @@ int proj_blocks_per_group(int width);
 void pack_projection_weights(const float* wq, const float* al, const float* ar, int in, int heads, int dim,
                              std::vector<uint16_t>& out, int& ksteps, int& groups, int& nmb);
 hipError_t launch_projection_mfma(const ProjArgs& a, hipStream_t s, int cus);
+void pack_lr_weights(const float* wq, const float* al, const float* ar, int in, int heads, int dim,
+                     std::vector<uint16_t>& out, int& ksteps);
 
 // aggregate.hip
 struct RowBins {
@@ -136,6 +138,37 @@ hipError_t launch_split_prescan(const uint64_t* prow, const uint32_t* pcol, cons
 bool aggregate_k1_supported(const AggArgs& a);
 hipError_t launch_aggregate_k1(const AggArgs& a, const RowBins& bins, const SplitTable& split,
                                hipStream_t s);
+// aggregate_af.hip: aggregate-first bf16 layer (input rows <= 128, 32 features per head).
+struct AfArgs {
+    const uint64_t* prow;
+    const uint32_t* pcol;
+    const uint32_t* perm;
+    const float* L;      // [n][heads] from the reordered contraction
+    const float* R;      // [n][heads]
+    const uint16_t* X;   // [n][128] bf16 layer input, zero-padded
+    const uint4* wpk;    // projection weights in pack_projection_weights() order (one group)
+    int nmb, ksteps;     // blocks per group and k steps of wpk
+    const float* wq;     // [in][heads*32] bf16-rounded W as FP32 (split rows)
+    int in, heads;
+    bool hidden;
+    float* mx;
+    float* den;
+    float* out32;
+    uint16_t* outbf;
+    uint64_t n, e;
+    uint64_t rows;       // non-split rows: sorted positions [0, rows)
+    uint64_t tiles;      // ceil(rows / 32)
+    uint64_t chunks;
+    const uint32_t* chunk_k;
+    const uint32_t* chunk_first;
+    uint32_t chunk_edges;
+    const float* mchunk;
+    float* part;         // [chunks][8*128 + 8]
+    uint32_t* counter;
+};
+bool aggregate_af_supported(int in, int heads, int dim);
+int af_input_stride();
+hipError_t launch_aggregate_af(const AfArgs& a, hipStream_t s, int cus);
 // aggregate_vec.hip: 16-byte vector path for 8 heads x (32 | 64).
 bool aggregate_vec_supported(const AggArgs& a);
 hipError_t launch_aggregate_vec(const AggArgs& a, const RowBins& bins, const SplitTable& split,

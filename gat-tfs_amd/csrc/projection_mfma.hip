@@ -204,4 +204,30 @@ void pack_projection_weights(const float* wq, const float* al, const float* ar, 
     }
 }
 
+// Only the L/R block ([kstep][2][lane][8], block 1 zero): the reordered
+// contraction LR = X (W_bf16 a) for the aggregate-first front end.
+void pack_lr_weights(const float* wq, const float* al, const float* ar, int in, int heads, int dim,
+                     std::vector<uint16_t>& out, int& ksteps) {
+    const int width = heads * dim;
+    ksteps = (in + 15) / 16;
+    out.assign(size_t(ksteps) * 2 * kWave * 8, 0);
+    for (int k = 0; k < in; ++k)
+        for (int h = 0; h < heads; ++h) {
+            double l = 0, r = 0;
+            for (int d = 0; d < dim; ++d) {
+                const double wv = wq[size_t(k) * width + h * dim + d];
+                l += wv * al[h * dim + d];
+                r += wv * ar[h * dim + d];
+            }
+            const float lf = float(l), rf = float(r);
+            const float lh = bf16_widen(bf16_rne(lf)), rh = bf16_widen(bf16_rne(rf));
+            const float cols[4] = {lh, rh, bf16_widen(bf16_rne(lf - lh)), bf16_widen(bf16_rne(rf - rh))};
+            for (int qd = 0; qd < 4; ++qd) {
+                const int c = 8 * qd + h;  // L hi, R hi, L lo, R lo at columns h, 8+h, 16+h, 24+h
+                const int ks = k / 16, half = (k % 16) / 8, j = k % 8;
+                out[((size_t(ks) * 2 + 0) * kWave + half * 32 + c) * 8 + j] = bf16_rne(cols[qd]);
+            }
+        }
+}
+
 }  // namespace gatgpu

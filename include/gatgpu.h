@@ -55,9 +55,9 @@ enum { GATGPU_FP32 = 0, GATGPU_BF16 = 1 };
 /* Dataflow of one layer.  TRANSFORM_FIRST projects Z = X W then aggregates Z
  * rows (standard_layer, baseline/src/baseline_standard.cpp:98-108).
  * AGGREGATE_FIRST aggregates X rows per head and projects afterwards
- * (tfs_online_fused, implementation/src/gat_tfs_online.cpp:200-283).  AUTO
- * picks aggregate-first when the gathered row is narrower (in*sizeof(x) <
- * heads*dim*sizeof(z)). */
+ * (tfs_online_fused, implementation/src/gat_tfs_online.cpp:200-283), bf16
+ * only, head_dim 32 and in <= 128.  AUTO selects the faster dataflow for the
+ * layer shape on gfx950 (transform-first for every shape of this build). */
 enum { GATGPU_AUTO = 0, GATGPU_TRANSFORM_FIRST = 1, GATGPU_AGGREGATE_FIRST = 2 };
 
 /* Stage selectors for gatgpu_get_stage (Workspace fields, gat.hpp:96-106). */

@@ -258,3 +258,63 @@ def test_bf16_projection_stages(gpu_ctx, D, K, d):
     for k in ("left", "right"):
         e = oracle.errors(r[k], gpu_ctx.stage(0, k))
         assert e["relative_l2"] < 1e-5, (k, e)
+
+
+AF_SHAPES = [(100, 8, 32), (128, 8, 32), (33, 4, 32), (17, 1, 32), (128, 2, 32), (64, 8, 32)]
+
+
+@pytest.mark.parametrize("D,K,d", AF_SHAPES)
+def test_aggregate_first_layer(gpu_ctx, D, K, d):
+    """Aggregate-first (tfs_online_fused semantics, exact max): equals R0 run on
+    bf16-rounded X and W (the AF path projects FP32 sums of bf16 inputs with
+    hi/lo bf16 MFMA operands), for every schedule incl. split-row chunks."""
+    w = inputs.WORKLOADS["smoke"]
+    row, col = w.graph()
+    x = inputs.normal((w.n, D), 13)
+    p = inputs.glorot_param(D, K, d, 14)
+    qp = dict(p, w=oracle.quantize_bf16(p["w"]))
+    xq = oracle.quantize_bf16(x)
+    for hidden in (False, True):
+        r = oracle.ref_layer(row, col, xq, qp, hidden)
+        r32 = oracle.ref_layer(row, col, x, p, hidden)
+        for opts in SCHEDULES:
+            gpu_ctx.set_graph(row, col)
+            for k_, v_ in opts.items():
+                gpu_ctx.set_option(k_, v_)
+            gpu_ctx.set_layer(0, p)
+            gpu_ctx.set_input(x)
+            gpu_ctx.layer_forward(0, gatgpu.BF16, gatgpu.AGGREGATE_FIRST, hidden)
+            out = gpu_ctx.stage(0, "out")
+            assert gpu_ctx.stage(0, "z") is None  # no Z in the aggregate-first dataflow
+            for k_ in opts:
+                gpu_ctx.set_option(k_, DEFAULT_OPTIONS[k_])
+            # hidden outputs are stored bf16 (the next layer's input): allow its rounding
+            e = oracle.errors(oracle.quantize_bf16(r["out"]) if hidden else r["out"], out)
+            assert e["finite"] and e["relative_l2"] < (4e-3 if hidden else 1e-4), (hidden, opts, e)
+            assert oracle.errors(r32["out"], out)["relative_l2"] < BF16_REL_L2
+            for k_ in ("max", "den"):
+                assert oracle.errors(r[k_], gpu_ctx.stage(0, k_))["relative_l2"] < 1e-4, (k_, opts)
+
+
+def test_aggregate_first_matches_transform_first_on_arxiv(gpu_ctx):
+    w = inputs.WORKLOADS["arxiv"]
+    row, col = w.graph()
+    x = w.features()
+    m = w.model()
+    gpu_ctx.set_graph(row, col)
+    gpu_ctx.set_model(m)
+    gpu_ctx.set_input(x)
+    tf, _, _ = gpu_ctx.model_forward(gatgpu.BF16, gatgpu.TRANSFORM_FIRST)
+    # layer 1 aggregate-first, layers 2-3 cannot (in = 256 > 128) and take transform-first
+    gpu_ctx.layer_forward(0, gatgpu.BF16, gatgpu.AGGREGATE_FIRST, True)
+    gpu_ctx.layer_forward(1, gatgpu.BF16, gatgpu.TRANSFORM_FIRST, True)
+    gpu_ctx.layer_forward(2, gatgpu.BF16, gatgpu.TRANSFORM_FIRST, False)
+    auto = gpu_ctx.stage(2, "out")
+    ref = oracle.ref_model(row, col, x, m)[2]["out"]
+    for got in (tf, auto):
+        e = oracle.errors(ref, got)
+        assert e["finite"] and e["relative_l2"] < BF16_REL_L2, e
+    assert oracle.errors(tf, auto)["relative_l2"] < BF16_REL_L2
+    with pytest.raises(gatgpu.GatGpuError) as err:
+        gpu_ctx.model_forward(gatgpu.FP32, gatgpu.AGGREGATE_FIRST)
+    assert err.value.code == gatgpu.EINVAL
