@@ -34,9 +34,9 @@ struct K1Args {
     const uint32_t* pcol;
     const uint32_t* perm;
     const float* L;
-    const float* R;
+    const float* R;      // R of row j at R[j * rs] (a separate array, or inside the Z row)
     const ZT* Z;
-    int W, zs;
+    int W, zs, rs;
     bool hidden;
     float* mx;
     float* den;
@@ -70,9 +70,9 @@ __device__ inline void unpack(const uint4& v, float (&f)[4]) {
 // Max of R over [beg, end), reduced over the G lanes of the group.
 template <class C>
 __device__ inline float group_max(uint64_t beg, uint64_t end, const uint32_t* __restrict__ pcol,
-                                  const float* __restrict__ R, int sub) {
+                                  const float* __restrict__ R, int rs, int sub) {
     float m = -INFINITY;
-    for (uint64_t e = beg + sub; e < end; e += C::G) m = fmaxf(m, R[pcol[e]]);
+    for (uint64_t e = beg + sub; e < end; e += C::G) m = fmaxf(m, R[uint64_t(pcol[e]) * rs]);
     for (int off = 1; off < C::G; off <<= 1) m = fmaxf(m, __shfl_xor(m, off));
     return m;
 }
@@ -80,15 +80,15 @@ __device__ inline float group_max(uint64_t beg, uint64_t end, const uint32_t* __
 // Edges [beg, end) of one row into the group's accumulators.
 template <class C, class ZT>
 __device__ inline void group_accumulate(uint64_t beg, uint64_t end, const uint32_t* __restrict__ pcol,
-                                        const float* __restrict__ R, const ZT* __restrict__ Z, int zs, int W,
-                                        float Li, float Mi, int gbase, int sub, float (&acc)[C::VEC],
+                                        const float* __restrict__ R, int rs, const ZT* __restrict__ Z, int zs,
+                                        int W, float Li, float Mi, int gbase, int sub, float (&acc)[C::VEC],
                                         float& dloc) {
     const bool reader = sub * C::VEC < W;
     for (uint64_t base = beg; base < end; base += C::G) {
         const uint64_t e = base + sub;
         const bool ev = e < end;
         const uint32_t j = ev ? pcol[e] : 0u;
-        const float p = ev ? expf(leaky(Li + R[j]) - Mi) : 0.0f;
+        const float p = ev ? expf(leaky(Li + R[uint64_t(j) * rs]) - Mi) : 0.0f;
         dloc += p;
         const uint64_t rem = end - base;
         const int cnt = rem < uint64_t(C::G) ? int(rem) : C::G;
@@ -152,7 +152,7 @@ __global__ void __launch_bounds__(kThreads) k_agg_k1(K1Args<ZT> a) {
         const float Mi = leaky(Li + m);
         const uint64_t len = cend - cbeg;
         const uint64_t pb = cbeg + len * g / C::GPW, pe = cbeg + len * (g + 1) / C::GPW;
-        group_accumulate<C, ZT>(pb, pe, a.pcol, a.R, a.Z, a.zs, a.W, Li, Mi, gbase, sub, acc, dloc);
+        group_accumulate<C, ZT>(pb, pe, a.pcol, a.R, a.rs, a.Z, a.zs, a.W, Li, Mi, gbase, sub, acc, dloc);
         for (int off = C::G; off < kWave; off <<= 1) {
 #pragma unroll
             for (int x = 0; x < C::VEC; ++x) acc[x] += __shfl_xor(acc[x], off);
@@ -196,9 +196,9 @@ __global__ void __launch_bounds__(kThreads) k_agg_k1(K1Args<ZT> a) {
     const uint64_t beg = a.prow[k], end = a.prow[k + 1];
     if (i >= a.n || beg > end || end > a.e) return;
     const float Li = a.L[i];
-    const float m = group_max<C>(beg, end, a.pcol, a.R, sub);
+    const float m = group_max<C>(beg, end, a.pcol, a.R, a.rs, sub);
     const float Mi = end > beg ? leaky(Li + m) : 0.0f;
-    group_accumulate<C, ZT>(beg, end, a.pcol, a.R, a.Z, a.zs, a.W, Li, Mi, gbase, sub, acc, dloc);
+    group_accumulate<C, ZT>(beg, end, a.pcol, a.R, a.rs, a.Z, a.zs, a.W, Li, Mi, gbase, sub, acc, dloc);
     for (int off = 1; off < C::G; off <<= 1) dloc += __shfl_xor(dloc, off);
     if (sub == 0) {
         a.mx[i] = Mi;
@@ -210,8 +210,13 @@ __global__ void __launch_bounds__(kThreads) k_agg_k1(K1Args<ZT> a) {
 template <int G, class ZT>
 hipError_t run(const AggArgs& g, const RowBins& bins, const SplitTable& t, hipStream_t s) {
     using C = K1<ZT, G>;
-    K1Args<ZT> a{g.prow, g.pcol, g.perm, g.left, g.right, static_cast<const ZT*>(g.feat), g.heads * g.dim,
-                 g.fstride, g.hidden, g.mx, g.den, g.out32, g.outbf, g.n, g.e, bins.split_begin, t.chunks,
+    // R read from the padding of the Z row when it was stored there (one
+    // 128-byte line per edge), else from the separate array.
+    const float* rptr = g.r_in_feat ? reinterpret_cast<const float*>(static_cast<const ZT*>(g.feat) + g.fstride - 2)
+                                    : g.right;
+    const int rs = g.r_in_feat ? int(g.fstride * sizeof(ZT) / 4) : 1;
+    K1Args<ZT> a{g.prow, g.pcol, g.perm, g.left, rptr, static_cast<const ZT*>(g.feat), g.heads * g.dim,
+                 g.fstride, rs, g.hidden, g.mx, g.den, g.out32, g.outbf, g.n, g.e, bins.split_begin, t.chunks,
                  t.chunk_k, t.chunk_first, t.chunk_edges, t.mchunk, t.part, t.counter};
     if (t.chunks) {
         hipError_t e = launch_split_prescan(g.prow, g.pcol, g.right, 1, t, g.e, s);

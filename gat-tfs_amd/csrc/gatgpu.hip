@@ -226,6 +226,16 @@ int build_schedule(gatgpu_ctx* c) {
     return compute_bins(c);
 }
 
+// Row stride (elements) of Z.  bf16: a multiple of 8 for 16-byte vector
+// stores; a single-head layer with at most 60 features gets a 128-byte row
+// (one cache line per gather) whose last 4 bytes hold R.  FP32: a multiple of 4.
+int z_stride(int precision, int heads, int width, bool* r_in_z) {
+    const bool rz = precision == GATGPU_BF16 && heads == 1 && width <= 60;
+    if (r_in_z) *r_in_z = rz;
+    if (rz) return 64;
+    return precision == GATGPU_BF16 ? (width + 7) / 8 * 8 : (width + 3) / 4 * 4;
+}
+
 // AUTO selects transform-first: on gfx950 its aggregation plus MFMA
 // projection is faster than the aggregate-first kernel even where the input
 // row is narrower (measured: 100 -> 8x32 on the 64.3M-edge graph, 9.2 ms TF
@@ -365,7 +375,8 @@ int run_layer(gatgpu_ctx* c, int l, int precision, int dataflow, bool hidden, co
     // bf16 path: X as [n][xs] bf16 (xs = ksteps*16, zero-padded), Z as [n][zs]
     // bf16 (zs = W rounded up to 8 for aligned vector stores).
     const int xs = Ls.ksteps * 16;
-    const int zs = bf16 ? (W + 7) / 8 * 8 : (W + 3) / 4 * 4;
+    bool r_in_z = false;
+    const int zs = z_stride(precision, K, W, &r_in_z);
     if (bf16) {
         HIPCHECK(c, Ls.zbf.ensure(n * zs * 2));
         if (srcbf && D != xs) {  // chained bf16 input without the padded layout
@@ -405,6 +416,7 @@ int run_layer(gatgpu_ctx* c, int l, int precision, int dataflow, bool hidden, co
         pa.left = Ls.left.as<float>();
         pa.right = Ls.right.as<float>();
         pa.tiles = (n + 31) / 32;
+        pa.r_in_z = r_in_z;
         HIPCHECK(c, launch_projection_mfma(pa, c->stream, c->cus));
     } else {
         HIPCHECK(c, launch_projection(src32, nullptr, Ls.w32.as<float>(), n, D, K, dim, Ls.al.as<float>(),
@@ -422,6 +434,7 @@ int run_layer(gatgpu_ctx* c, int l, int precision, int dataflow, bool hidden, co
     a.feat = bf16 ? static_cast<const void*>(Ls.zbf.p) : Ls.z32.p;
     a.feat_bf16 = bf16;
     a.fstride = zs;
+    a.r_in_feat = r_in_z;
     a.heads = K;
     a.dim = dim;
     a.hidden = hidden;
@@ -725,13 +738,13 @@ int gatgpu_get_stage(gatgpu_ctx* c, int layer, int which, float* host) {
             break;
     }
     if (bf && which == GATGPU_STAGE_Z) {
-        const int W = L.width(), zs = (W + 7) / 8 * 8;
+        const int W = L.width(), zs = z_stride(GATGPU_BF16, L.heads, W, nullptr);
         std::vector<uint16_t> tmp(c->n * zs);
         HIPCHECK(c, hipMemcpy(tmp.data(), src, tmp.size() * 2, hipMemcpyDeviceToHost));
         for (uint64_t i = 0; i < c->n; ++i)
             for (int f = 0; f < W; ++f) host[i * W + f] = bf16_widen(tmp[i * zs + f]);
     } else if (which == GATGPU_STAGE_Z) {
-        const int W = L.width(), zs = (W + 3) / 4 * 4;
+        const int W = L.width(), zs = z_stride(GATGPU_FP32, L.heads, W, nullptr);
         std::vector<float> tmp(c->n * zs);
         HIPCHECK(c, hipMemcpy(tmp.data(), src, tmp.size() * 4, hipMemcpyDeviceToHost));
         for (uint64_t i = 0; i < c->n; ++i)

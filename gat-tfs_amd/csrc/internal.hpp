@@ -86,6 +86,7 @@ struct ProjArgs {
     float* left;         // [n][heads]
     float* right;        // [n][heads]
     uint64_t tiles;      // ceil(n / 32)
+    bool r_in_z;         // one head: also store R as FP32 in z[row][zs-2..zs-1]
 };
 int proj_blocks_per_group(int width);
 void pack_projection_weights(const float* wq, const float* al, const float* ar, int in, int heads, int dim,
@@ -110,6 +111,7 @@ struct AggArgs {
     const void* feat;    // Z [n][W] (TF) or X [n][D] (AF); FP32 or bf16
     bool feat_bf16;
     int fstride;         // row stride of feat in elements (>= W)
+    bool r_in_feat;      // one head, bf16: R of row j is the FP32 at feat[j][fstride-2..fstride-1]
     int heads, dim;
     bool hidden;
     float* mx;       // [n][K]

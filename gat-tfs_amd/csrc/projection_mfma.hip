@@ -105,8 +105,10 @@ __global__ void __launch_bounds__(kThreads) k_proj_mfma(ProjArgs a) {
                 for (int q = 0; q < 4; ++q) {
                     const int h = 4 * half + q;
                     if (h < a.heads) {
+                        const float rv = acc[mb][4 + q] + acc[mb][12 + q];
                         a.left[row * a.heads + h] = acc[mb][q] + acc[mb][8 + q];
-                        a.right[row * a.heads + h] = acc[mb][4 + q] + acc[mb][12 + q];
+                        a.right[row * a.heads + h] = rv;
+                        if (a.r_in_z) *reinterpret_cast<float*>(a.z + row * a.zs + a.zs - 2) = rv;
                     }
                 }
             }
