@@ -35,6 +35,19 @@ def agg_bytes(n, e, heads, dim, s_z, s_out):
     return 8 * (n + 1) + 4 * e + 4 * heads * e + 4 * heads * n + e * heads * dim * s_z + n * heads * dim * s_out
 
 
+def pmc_traffic(workload, precision):
+    """HBM bytes per launch of the layer-2 aggregation, measured with
+    rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE and calibrated against a device
+    copy of known size; read from the committed summary (None if absent)."""
+    for f in sorted((ROOT / "profiles").glob("*pmc*.md")):
+        for line in f.read_text().splitlines():
+            if line.startswith("bench-traffic: "):
+                rec = json.loads(line[len("bench-traffic: "):])
+                if rec.get("workload") == workload and rec.get("precision") == precision:
+                    return rec
+    return None
+
+
 def cpu_baseline(w, row, col, x, model, precision, threads, reps=1):
     """The oracle's B0 restatement (standard_bf16 / standard_fp32 semantics,
     baseline/src/baseline_standard.cpp) on the host cores.  Workspaces are
@@ -132,6 +145,7 @@ def main():
     agg_ms = float(np.mean([t[1]["aggregate_ms"] for t in layer_times]))
     b2 = agg_bytes(n, e, L2["heads"], L2["dim"], s_z, s_z)
     achieved = b2 / (agg_ms * 1e-3) / 1e9
+    pmc = pmc_traffic(w.name, args.precision)
     per_layer = [{k: round(float(np.mean([t[l][k] for t in layer_times])), 4)
                   for k in ("convert_ms", "projection_ms", "aggregate_ms", "total_ms")} for l in range(3)]
     out = {
@@ -152,7 +166,8 @@ def main():
                    "precision": args.precision, "wall_ms_per_step": round(wall / args.steps * 1e3, 4),
                    "layers": per_layer},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": int(pmc["bytes_per_launch"]) if pmc else None,
                      "kernel": "layer-2 aggregation", "algorithmic_bytes": int(b2), "avg_ms": round(agg_ms, 4)},
     }
     ctx.close()

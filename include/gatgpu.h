@@ -49,7 +49,7 @@ enum {
  * reference's ref_fp32 / standard_fp32).  BF16: RNE-rounded bf16 X and W,
  * FP32 MFMA accumulation, L/R from the FP32 accumulators, Z stored bf16,
  * FP32 score/max/exp/denominator/output accumulation (standard_bf16 with a
- * bf16 copy of Z; IMPLEMENTATION_CONTRACT.md section 3). */
+ * bf16 copy of Z; baseline/IMPLEMENTATION_CONTRACT.md sections 3.2-3.3). */
 enum { GATGPU_FP32 = 0, GATGPU_BF16 = 1 };
 
 /* Dataflow of one layer.  TRANSFORM_FIRST projects Z = X W then aggregates Z
@@ -102,7 +102,7 @@ int gatgpu_destroy(gatgpu_ctx* ctx);
  * is NULL).  Valid until the next call on the same context. */
 const char* gatgpu_last_error(const gatgpu_ctx* ctx);
 
-/* ---- static inputs (untimed, like load_graph/prepare: README.md:52) ---- */
+/* ---- static inputs (untimed, like load_graph/prepare: baseline/README.md:52) ---- */
 /* Validates and uploads the CSR, then builds the degree schedule on the GPU.
  * Replaces load_graph + Graph::validate (baseline/src/common.cpp:23-39) and
  * degree_schedule (common.cpp:120-125).  Checks row[0]==0, row[n]==e,

@@ -6,7 +6,24 @@
 // the reference root).  It is compiled with g++ so that libstdc++'s mt19937 and
 // normal/uniform distributions reproduce the reference's random weights.
 //
-// Parity status of each function (how it is pinned) is listed in oracle/README.md.
+// How each function is pinned (tests/test_oracle.py):
+//   or_rne                 torch bfloat16 RNE on 2^20 random patterns, the ties of
+//                          baseline/tests/boundaries.cpp:25-26, NaN quieting
+//   or_random_param        errors of the reference's correctness log reproduced
+//                          (baseline/runs/check-10808045/correctness.log); bitwise
+//                          equality with the reference's files is parity unpinned:
+//                          its icpx/libimf logf differs from glibc in the last ulp
+//   or_boundary_*          same log; the feature bits (sinf) likewise parity unpinned
+//   or_ref_layer (R0)      FP64 oracle < 1e-4 on 64 shapes, NumPy FP64 chain < 2e-4,
+//                          smoke1024 checksum 221.971286 (+-1e-3), the logged errors
+//   or_fp64_layer          NumPy FP64 restatement of baseline/tests/oracle.py (1e-9)
+//   or_standard_layer (B0) the logged standard_bf16 stage errors and chain error
+//   or_degree_schedule,    numpy.lexsort on (degree, id); neighbor_steps definition;
+//   or_permute_csr         row-by-row copy check
+//   or_choose_R            hand-computed rho thresholds
+//   or_errors              NumPy on hand-built vectors
+// Bitwise parity with oneMKL's SGEMM order and SVML exp is parity unpinned
+// (neither is available); both are tolerance-pinned as above.
 #include <algorithm>
 #include <chrono>
 #include <cmath>
