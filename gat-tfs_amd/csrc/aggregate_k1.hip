@@ -111,6 +111,60 @@ __device__ inline void group_accumulate(uint64_t beg, uint64_t end, const uint32
     }
 }
 
+// Edges [beg, end) of one row in a single pass, for Z rows that carry R in
+// their last four bytes (lane G-1's 16-byte slice).  Each source row is
+// fetched once: the batch's R values are broadcast from lane G-1 and every lane
+// of the group scores the whole batch, so m, the accumulators and dsum stay
+// identical across the group.  The softmax is kept online (the
+// running-maximum form of tfs_online_fused, implementation/src/
+// gat_tfs_online.cpp:86-117): when a batch raises the running maximum m, the
+// accumulators and the denominator are rescaled by exp(m_old - m_new).  The
+// final m equals leaky(L + max R) bit for bit, because leaky and the addition
+// are monotone.
+template <class C>
+__device__ inline void group_online(uint64_t beg, uint64_t end, const uint32_t* __restrict__ pcol,
+                                    const uint16_t* __restrict__ Z, int zs, int W, float Li, int gbase, int sub,
+                                    float (&acc)[C::VEC], float& dsum, float& m) {
+    static_assert(C::VEC == 8, "bf16 rows only");
+    const bool reader = sub * C::VEC < W || sub == C::G - 1;
+    for (uint64_t base = beg; base < end; base += C::G) {
+        const uint64_t e = base + sub;
+        const uint32_t j = e < end ? pcol[e] : 0u;
+        const uint64_t rem = end - base;
+        const int cnt = rem < uint64_t(C::G) ? int(rem) : C::G;
+        uint4 raw[C::G];
+#pragma unroll
+        for (int t = 0; t < C::G; ++t) {
+            const uint32_t jt = __shfl(j, gbase + t);
+            raw[t] = (t < cnt && reader) ? *reinterpret_cast<const uint4*>(Z + uint64_t(jt) * zs + sub * C::VEC)
+                                         : make_uint4(0, 0, 0, 0);
+        }
+        float s[C::G];
+        float mb = -INFINITY;
+#pragma unroll
+        for (int t = 0; t < C::G; ++t) {
+            const float r = __builtin_bit_cast(float, __shfl(raw[t].w, gbase + C::G - 1));
+            s[t] = t < cnt ? leaky(Li + r) : -INFINITY;
+            mb = fmaxf(mb, s[t]);
+        }
+        const float mn = fmaxf(m, mb);
+        const float sc = expf(m - mn);  // 0 on the first batch (m = -inf)
+        m = mn;
+        dsum *= sc;
+#pragma unroll
+        for (int x = 0; x < C::VEC; ++x) acc[x] *= sc;
+#pragma unroll
+        for (int t = 0; t < C::G; ++t) {
+            const float p = t < cnt ? expf(s[t] - mn) : 0.0f;
+            dsum += p;
+            float f[C::VEC];
+            unpack(raw[t], f);
+#pragma unroll
+            for (int x = 0; x < C::VEC; ++x) acc[x] += p * f[x];
+        }
+    }
+}
+
 template <class C>
 __device__ inline void store_row(uint32_t i, int W, int sub, const float (&acc)[C::VEC], float d, bool hidden,
                                  float* out32, uint16_t* outbf) {
@@ -126,7 +180,7 @@ __device__ inline void store_row(uint32_t i, int W, int sub, const float (&acc)[
     }
 }
 
-template <class C, class ZT>
+template <class C, class ZT, bool ONE_PASS>
 __global__ void __launch_bounds__(kThreads) k_agg_k1(K1Args<ZT> a) {
     const int w = threadIdx.x / kWave, lane = threadIdx.x % kWave;
     const int g = lane / C::G, sub = lane % C::G, gbase = g * C::G;
@@ -196,10 +250,17 @@ __global__ void __launch_bounds__(kThreads) k_agg_k1(K1Args<ZT> a) {
     const uint64_t beg = a.prow[k], end = a.prow[k + 1];
     if (i >= a.n || beg > end || end > a.e) return;
     const float Li = a.L[i];
-    const float m = group_max<C>(beg, end, a.pcol, a.R, a.rs, sub);
-    const float Mi = end > beg ? leaky(Li + m) : 0.0f;
-    group_accumulate<C, ZT>(beg, end, a.pcol, a.R, a.rs, a.Z, a.zs, a.W, Li, Mi, gbase, sub, acc, dloc);
-    for (int off = 1; off < C::G; off <<= 1) dloc += __shfl_xor(dloc, off);
+    float Mi;
+    if constexpr (ONE_PASS) {
+        float m = -INFINITY;
+        group_online<C>(beg, end, a.pcol, a.Z, a.zs, a.W, Li, gbase, sub, acc, dloc, m);
+        Mi = end > beg ? m : 0.0f;
+    } else {
+        const float m = group_max<C>(beg, end, a.pcol, a.R, a.rs, sub);
+        Mi = end > beg ? leaky(Li + m) : 0.0f;
+        group_accumulate<C, ZT>(beg, end, a.pcol, a.R, a.rs, a.Z, a.zs, a.W, Li, Mi, gbase, sub, acc, dloc);
+        for (int off = 1; off < C::G; off <<= 1) dloc += __shfl_xor(dloc, off);
+    }
     if (sub == 0) {
         a.mx[i] = Mi;
         a.den[i] = dloc;
@@ -223,8 +284,16 @@ hipError_t run(const AggArgs& g, const RowBins& bins, const SplitTable& t, hipSt
         if (e != hipSuccess) return e;
     }
     const uint64_t waves = t.chunks + (bins.split_begin + C::GPW - 1) / C::GPW;
-    if (waves)
-        k_agg_k1<C, ZT><<<dim3(uint32_t((waves + kWavesPerBlock - 1) / kWavesPerBlock)), kThreads, 0, s>>>(a);
+    const dim3 grid(uint32_t((waves + kWavesPerBlock - 1) / kWavesPerBlock));
+    if (!waves) return hipSuccess;
+    if constexpr (sizeof(ZT) == 2) {
+        if (g.r_in_feat) {
+            // whole rows in one pass over their Z lines (R rides in the line)
+            k_agg_k1<C, ZT, true><<<grid, kThreads, 0, s>>>(a);
+            return hipGetLastError();
+        }
+    }
+    k_agg_k1<C, ZT, false><<<grid, kThreads, 0, s>>>(a);
     return hipGetLastError();
 }
 

@@ -1,24 +1,37 @@
-// Vectorised transform-first aggregation for rows whose width is a multiple
-// of one 16-byte vector per lane (8 bf16 or 4 FP32 features), e.g. 8 heads x
-// 32 or 8 x 64.  Same mathematics as aggregate.hip (baseline_standard.cpp:44-97):
-// exact row max first, then p = exp(LeakyReLU(L+R) - M), den = sum p,
-// out = ELU?(sum p Z / den).
+// Vectorised transform-first aggregation for rows of 8 heads whose width is a
+// multiple of one 16-byte vector per lane (8 bf16 or 4 FP32 features), i.e.
+// 8 x 32 and 8 x 64.  Same mathematics as aggregate.hip
+// (baseline_standard.cpp:44-97): p = exp(LeakyReLU(L+R) - M) with M the exact
+// row max, den = sum p, out = ELU?(sum p Z / den).
 //
-// Work items (one wave each, 4 waves per block):
-//   * chunks of split rows (in-degree >= split_min): C edges each.  A first
-//     kernel stores every chunk's per-head maximum; the aggregation kernel
-//     reads the maxima of all chunks of its row, so every chunk uses the exact
-//     row max, and the partial (sum p Z, sum p) of a chunk needs no rescaling.
-//     Partials go to scratch; the last chunk to arrive (agent-scope acq_rel
-//     counter) adds them in chunk order -- deterministic -- and finishes the row.
+// Work items, one wave each, in this order:
+//   * chunks of split rows (in-degree >= split_min), C edges each.
+//     k_split_prescan stores every chunk's per-head maximum first, so every
+//     chunk starts from the exact row max and its partial (sum p Z, sum p)
+//     needs no rescaling.  Partials go to scratch; the last chunk to arrive
+//     (agent-scope release/acquire around a relaxed counter) adds them in
+//     chunk order, which is deterministic, and finishes the row.
 //   * whole rows below split_min, heaviest first.
 //
-// Lane roles inside a wave, per batch of EB edges:
-//   scorer   pair q = lane + 64 s -> edge q / K, head q % K: one exp per (edge, head)
-//   reader   slot = lane / LPR, sub = lane % LPR: loads 16 bytes of edge
-//            (u*EPI + slot)'s row for u < NU, i.e. EPI edges per instruction.
-// Scores and source ids pass from scorers to readers through LDS, laid out so
-// that each reader fetches its NU values with 128-bit LDS reads.
+// Lane layout.  A source row is LPR 16-byte vectors.  Lane (slot, sub), with
+// slot = lane / LPR and sub = lane % LPR, reads vector sub of every edge whose
+// index within the batch is slot (mod EPI); EPI = 64 / LPR edges share one
+// load instruction, and a row wider than the wave gives a lane VPL vectors.
+// Each vector lies inside one head, so a lane scores its own (edge, head)
+// pairs: R[j][h] is one 4-byte load issued beside the lane's Z load (the
+// lanes of one edge read one 32-byte R row), and exp is evaluated by each of
+// the DIM/VEC lanes of a head.  That costs a few VALU operations per edge and
+// removes the score exchange through LDS and its barriers.  Source ids are
+// wave-uniform (one row per wave) and arrive with scalar loads, BATCH at a
+// time; pcol carries kPcolPad entries past its end for that.
+//
+// Softmax state per lane and head: the running max m, the denominator and the
+// accumulators, rescaled by exp(m_old - m_new) when a batch raises m (the
+// running-maximum form of implementation/src/gat_tfs_online.cpp:86-117).  Each
+// edge slot keeps its own state and the slots merge at the end of the row.
+// Every source row is thus read once, and the final m is max leaky(L + R_j) =
+// leaky(L + max R_j) bit for bit (leaky and the addition are monotone).  A
+// chunk starts from the exact row max, so its m never moves.
 #include "internal.hpp"
 
 namespace gatgpu {
@@ -27,22 +40,20 @@ namespace {
 constexpr int kThreads = 256;
 constexpr int kWavesPerBlock = kThreads / kWave;
 
-template <class ZT, int W_, int K_, int BE_>
+template <class ZT, int W_, int K_>
 struct Cfg {
-    static constexpr int W = W_, K = K_, BE = BE_;    // BE: edges scored per block
+    static constexpr int W = W_, K = K_;
     static constexpr int VEC = 16 / int(sizeof(ZT));  // features per 16-byte load
     static constexpr int DIM = W / K;
-    static constexpr int LPR = W / VEC;               // lanes (16-byte vectors) per row
+    static constexpr int LPR = W / VEC;               // 16-byte vectors per row
     static constexpr int EPI = LPR >= kWave ? 1 : kWave / LPR;  // edges per load instruction
     static constexpr int VPL = LPR <= kWave ? 1 : LPR / kWave;  // vectors per lane per edge
-    static constexpr int NUB = BE / EPI;              // load instructions of a full block
-    static constexpr int S = BE * K / kWave;          // (edge, head) scores per lane per block
-    static constexpr int G = 8;                       // load instructions in flight per group
+    static constexpr int U = VPL == 1 ? 8 : 4;        // load instructions per vector per batch
+    static constexpr int BATCH = U * EPI;             // edges per batch
     static constexpr int ACC = VPL * VEC;
     static_assert(W % K == 0 && DIM % VEC == 0, "a vector must not straddle two heads");
     static_assert(LPR * EPI == kWave || LPR % kWave == 0, "lanes per row must divide or fill the wave");
-    static_assert(BE % EPI == 0 && (BE * K) % kWave == 0 && NUB % G == 0, "block must fill whole groups");
-    static_assert(kWave % K == 0, "heads must divide the wave");
+    static_assert(BATCH <= int(kPcolPad), "a batch may read at most kPcolPad entries past the row");
 };
 
 struct SplitArgs {
@@ -88,153 +99,116 @@ __device__ inline void unpack(const uint4& v, float (&f)[4]) {
     f[3] = __builtin_bit_cast(float, v.w);
 }
 
-// Per-lane state of one row (or chunk) aggregation.
+// Softmax state of one lane: its VPL heads' running max, denominator, L,
+// and the ACC accumulated features.
 template <class C>
-struct RowAcc {
+struct Lane {
     float acc[C::ACC];
-    float dloc;
+    float den[C::VPL];
+    float m[C::VPL];
+    float L[C::VPL];
+    int h[C::VPL];
 };
 
-// Max of R[j, head] over edges [beg, end) for this lane's head, reduced over
-// the lanes of the same head (lane l covers edges l/K, l/K + 64/K, ...).
-template <class C>
-__device__ inline float row_max(uint64_t beg, uint64_t end, const uint32_t* __restrict__ pcol,
-                                const float* __restrict__ R) {
-    const int lane = threadIdx.x % kWave, hs = lane % C::K;
-    float m = -INFINITY;
-    for (uint64_t e = beg + lane / C::K; e < end; e += kWave / C::K) m = fmaxf(m, R[uint64_t(pcol[e]) * C::K + hs]);
-    for (int off = C::K; off < kWave; off <<= 1) m = fmaxf(m, __shfl_xor(m, off));
-    return m;
+// One batch of edges [base, base + BATCH) clipped to end.
+template <class C, class ZT>
+__device__ inline void batch(uint64_t base, uint64_t end, const uint32_t* __restrict__ pcol,
+                             const float* __restrict__ R, const ZT* __restrict__ Z, int slot, int sub,
+                             Lane<C>& st) {
+    uint32_t js[C::BATCH];
+#pragma unroll
+    for (int t = 0; t < C::BATCH; ++t) js[t] = pcol[base + t];  // wave-uniform, padded past e
+    uint4 z[C::U][C::VPL];
+    float s[C::U][C::VPL];
+    bool ok[C::U];
+#pragma unroll
+    for (int u = 0; u < C::U; ++u) {
+        uint32_t j = js[u * C::EPI];
+#pragma unroll
+        for (int q = 1; q < C::EPI; ++q) j = slot == q ? js[u * C::EPI + q] : j;
+        ok[u] = base + uint64_t(u * C::EPI + slot) < end;
+        const ZT* row = Z + uint64_t(j) * C::W;
+#pragma unroll
+        for (int v = 0; v < C::VPL; ++v) {
+            z[u][v] = ok[u] ? *reinterpret_cast<const uint4*>(row + (sub + kWave * v) * C::VEC)
+                            : make_uint4(0, 0, 0, 0);
+            const float r = ok[u] ? R[uint64_t(j) * C::K + st.h[v]] : 0.0f;
+            s[u][v] = leaky(st.L[v] + r);
+        }
+    }
+#pragma unroll
+    for (int v = 0; v < C::VPL; ++v) {
+        float mb = -INFINITY;
+#pragma unroll
+        for (int u = 0; u < C::U; ++u) mb = ok[u] ? fmaxf(mb, s[u][v]) : mb;
+        const float mn = fmaxf(st.m[v], mb);
+        const float sc = mn > st.m[v] ? expf(st.m[v] - mn) : 1.0f;  // exp(-inf) = 0 on a slot's first edge
+        st.m[v] = mn;
+        st.den[v] *= sc;
+#pragma unroll
+        for (int x = 0; x < C::VEC; ++x) st.acc[v * C::VEC + x] *= sc;
+    }
+#pragma unroll
+    for (int u = 0; u < C::U; ++u) {
+#pragma unroll
+        for (int v = 0; v < C::VPL; ++v) {
+            const float p = ok[u] ? expf(s[u][v] - st.m[v]) : 0.0f;
+            st.den[v] += p;
+            float f[C::VEC];
+            unpack(z[u][v], f);
+#pragma unroll
+            for (int x = 0; x < C::VEC; ++x) st.acc[v * C::VEC + x] += p * f[x];
+        }
+    }
 }
 
-// One block of cnt <= BE edges starting at base.  Every lane loads the source
-// ids and R values of its S (edge, head) pairs once; with FIND_MAX (a row
-// that fits one block) the exact row max comes from those registers, so R is
-// read once per edge.  Scores and ids go to LDS in reader order, then the
-// Z rows are gathered in groups of G 16-byte loads per lane, double-buffered
-// so that one group's loads are in flight while the previous group's FMAs run.
-template <class C, class ZT, bool FIND_MAX>
-__device__ inline void block(uint64_t base, int cnt, const uint32_t* __restrict__ pcol,
-                             const float* __restrict__ R, const ZT* __restrict__ Z, float Lh, float& Mh,
-                             float* pb, uint32_t* jb, RowAcc<C>& st) {
-    const int lane = threadIdx.x % kWave;
-    const int hs = lane % C::K;
-    const int slot = C::EPI > 1 ? lane / C::LPR : 0;
-    const int sub = C::EPI > 1 ? lane % C::LPR : lane;
-    uint32_t jv[C::S];
-    float rv[C::S];
-#pragma unroll
-    for (int s = 0; s < C::S; ++s) {
-        const int t = lane / C::K + (kWave / C::K) * s;
-        jv[s] = t < cnt ? pcol[base + t] : 0u;
-        rv[s] = t < cnt ? R[uint64_t(jv[s]) * C::K + hs] : -INFINITY;
-    }
-    if constexpr (FIND_MAX) {
-        float m = rv[0];
-#pragma unroll
-        for (int s = 1; s < C::S; ++s) m = fmaxf(m, rv[s]);
-        for (int off = C::K; off < kWave; off <<= 1) m = fmaxf(m, __shfl_xor(m, off));
-        Mh = leaky(Lh + m);
-    }
-#pragma unroll
-    for (int s = 0; s < C::S; ++s) {
-        const int t = lane / C::K + (kWave / C::K) * s;
-        const float p = t < cnt ? expf(leaky(Lh + rv[s]) - Mh) : 0.0f;
-        st.dloc += p;
-        const int u = t / C::EPI, sl = t % C::EPI;
-        pb[(hs * C::EPI + sl) * C::NUB + u] = p;
-        if (hs == 0) jb[sl * C::NUB + u] = jv[s];
-    }
-    wave_sync();
-    int hr[C::VPL];
-#pragma unroll
-    for (int v = 0; v < C::VPL; ++v) hr[v] = ((sub + kWave * v) * C::VEC) / C::DIM;
-    const int nu = (cnt + C::EPI - 1) / C::EPI;  // load instructions of this block
-    uint4 buf[2][C::G][C::VPL];
-    auto issue = [&](int b, int u0) {
-#pragma unroll
-        for (int q = 0; q < C::G; ++q) {
-            const int u = u0 + q;
-            const bool ok = u * C::EPI + slot < cnt;
-            const uint32_t j = jb[slot * C::NUB + (u < C::NUB ? u : 0)];
-            const ZT* row = Z + uint64_t(j) * C::W;
-#pragma unroll
-            for (int v = 0; v < C::VPL; ++v)
-                buf[b][q][v] = ok ? *reinterpret_cast<const uint4*>(row + (sub + kWave * v) * C::VEC)
-                                  : make_uint4(0, 0, 0, 0);
-        }
-    };
-    auto consume = [&](int b, int u0) {
-#pragma unroll
-        for (int q = 0; q < C::G; ++q) {
-            const int u = u0 + q < C::NUB ? u0 + q : 0;
+// Edges [beg, end) of a row or chunk, then the edge slots merged: afterwards
+// every lane holds its heads' totals and m is the max over all the edges.
+template <class C, class ZT>
+__device__ inline void aggregate(uint64_t beg, uint64_t end, const uint32_t* __restrict__ pcol,
+                                 const float* __restrict__ R, const ZT* __restrict__ Z, int slot, int sub,
+                                 Lane<C>& st) {
+    for (uint64_t base = beg; base < end; base += C::BATCH) batch<C, ZT>(base, end, pcol, R, Z, slot, sub, st);
+    if constexpr (C::EPI > 1) {
+        for (int off = C::LPR; off < kWave; off <<= 1) {
 #pragma unroll
             for (int v = 0; v < C::VPL; ++v) {
-                const float p = pb[(hr[v] * C::EPI + slot) * C::NUB + u];
-                float f[C::VEC];
-                unpack(buf[b][q][v], f);
+                const float mo = __shfl_xor(st.m[v], off);
+                const float M = fmaxf(st.m[v], mo);
+                const float f = st.m[v] == M ? 1.0f : expf(st.m[v] - M);
+                st.m[v] = M;
+                st.den[v] *= f;
+                st.den[v] += __shfl_xor(st.den[v], off);
 #pragma unroll
-                for (int x = 0; x < C::VEC; ++x) st.acc[v * C::VEC + x] += p * f[x];
+                for (int x = 0; x < C::VEC; ++x) {
+                    float a = st.acc[v * C::VEC + x] * f;
+                    st.acc[v * C::VEC + x] = a + __shfl_xor(a, off);
+                }
             }
         }
-    };
-    // Groups beyond nu load nothing (ok == false) and add zeros.
-    issue(0, 0);
-    for (int u0 = 0; u0 < nu; u0 += 2 * C::G) {
-        if (u0 + C::G < nu) issue(1, u0 + C::G);
-        consume(0, u0);
-        if (u0 + C::G < nu) {
-            if (u0 + 2 * C::G < nu) issue(0, u0 + 2 * C::G);
-            consume(1, u0 + C::G);
-        }
-    }
-    wave_sync();
-}
-
-// Edges [beg, end) of a row or chunk whose max is known (Mh) or, for a row
-// that fits one block, found on the way.
-template <class C, class ZT>
-__device__ inline void accumulate(uint64_t beg, uint64_t end, bool find_max, const uint32_t* __restrict__ pcol,
-                                  const float* __restrict__ R, const ZT* __restrict__ Z, float Lh, float& Mh,
-                                  float* pb, uint32_t* jb, RowAcc<C>& st) {
-    if (find_max) {
-        block<C, ZT, true>(beg, int(end - beg), pcol, R, Z, Lh, Mh, pb, jb, st);
-        return;
-    }
-    for (uint64_t base = beg; base < end; base += C::BE) {
-        const uint64_t rem = end - base;
-        block<C, ZT, false>(base, rem < uint64_t(C::BE) ? int(rem) : C::BE, pcol, R, Z, Lh, Mh, pb, jb, st);
     }
 }
 
-// Sum the denominators over scorer lanes of the same head (lanes < K end up
-// with head lane's total) and the accumulators over the EPI edge slots.
+// Normalise, ELU and store one output row from the slot-0 lanes; the first
+// lane of each head also stores M and den.
 template <class C>
-__device__ inline void reduce_lanes(RowAcc<C>& st) {
-    for (int off = C::K; off < kWave; off <<= 1) st.dloc += __shfl_xor(st.dloc, off);
-    if constexpr (C::EPI > 1) {
-#pragma unroll
-        for (int x = 0; x < C::ACC; ++x)
-            for (int off = C::LPR; off < kWave; off <<= 1) st.acc[x] += __shfl_xor(st.acc[x], off);
-    }
-}
-
-// Normalise, ELU, store one output row (slot-0 lanes), den/M rows (lanes < K).
-template <class C>
-__device__ inline void finish_row(uint32_t i, const float (&acc)[C::ACC], const float* dsh, bool hidden,
-                                  float* out32, uint16_t* outbf) {
-    const int lane = threadIdx.x % kWave;
-    if (C::EPI > 1 && lane >= C::LPR) return;  // slot-0 lanes hold the reduced sums
-    const int sub = lane;
+__device__ inline void finish_row(uint32_t i, const float (&acc)[C::ACC], const float (&den)[C::VPL],
+                                  const float (&M)[C::VPL], const int (&h)[C::VPL], int slot, int sub,
+                                  bool hidden, float* mx, float* dn, float* out32,
+                                  uint16_t* outbf) {
+    if (slot != 0) return;
 #pragma unroll
     for (int v = 0; v < C::VPL; ++v) {
         const int f0 = (sub + kWave * v) * C::VEC;
-        const float d = dsh[f0 / C::DIM];
-        const float scale = d > 0.0f ? 1.0f / d : 0.0f;
+        if (f0 % C::DIM == 0) {
+            mx[uint64_t(i) * C::K + h[v]] = M[v];
+            dn[uint64_t(i) * C::K + h[v]] = den[v];
+        }
+        const float scale = den[v] > 0.0f ? 1.0f / den[v] : 0.0f;
         float o[C::VEC];
 #pragma unroll
         for (int x = 0; x < C::VEC; ++x) {
-            float y = acc[v * C::VEC + x] * scale;
+            const float y = acc[v * C::VEC + x] * scale;
             o[x] = hidden ? elu(y) : y;
         }
         const uint64_t off = uint64_t(i) * C::W + f0;
@@ -276,16 +250,21 @@ k_split_prescan(const uint64_t* __restrict__ prow, const uint32_t* __restrict__ 
 
 template <class C, class ZT>
 __global__ void __launch_bounds__(kThreads) k_agg_vec(VArgs<ZT> a) {
-    __shared__ float pbuf[kWavesPerBlock][C::K * C::BE];
-    __shared__ uint32_t jbuf[kWavesPerBlock][C::BE];
-    __shared__ float dsh[kWavesPerBlock][8];
-    const int w = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+    // The wave index is made wave-uniform so that row bounds and source ids
+    // come in through scalar loads.
+    const int w = __builtin_amdgcn_readfirstlane(int(threadIdx.x) / kWave);
+    const int lane = threadIdx.x % kWave;
+    const int slot = C::EPI > 1 ? lane / C::LPR : 0;
+    const int sub = C::EPI > 1 ? lane % C::LPR : lane;
     const uint64_t item = uint64_t(blockIdx.x) * kWavesPerBlock + w;
-    const int hs = lane % C::K;
-    RowAcc<C> st;
+    Lane<C> st;
 #pragma unroll
     for (int x = 0; x < C::ACC; ++x) st.acc[x] = 0.0f;
-    st.dloc = 0.0f;
+#pragma unroll
+    for (int v = 0; v < C::VPL; ++v) {
+        st.h[v] = ((sub + kWave * v) * C::VEC) / C::DIM;
+        st.den[v] = 0.0f;
+    }
     if (item < a.sp.chunks) {
         // ---------------- chunk of a split row
         const uint64_t c = item;
@@ -296,25 +275,27 @@ __global__ void __launch_bounds__(kThreads) k_agg_vec(VArgs<ZT> a) {
         const uint32_t nch = uint32_t((rend - rbeg + a.sp.chunk_edges - 1) / a.sp.chunk_edges);
         const uint64_t beg = rbeg + uint64_t(c - first) * a.sp.chunk_edges;
         const uint64_t end = beg + a.sp.chunk_edges < rend ? beg + a.sp.chunk_edges : rend;
-        float m = -INFINITY;
-        for (uint32_t q = lane / C::K; q < nch; q += kWave / C::K) m = fmaxf(m, a.sp.mchunk[(first + q) * 8 + hs]);
-        for (int off = C::K; off < kWave; off <<= 1) m = fmaxf(m, __shfl_xor(m, off));
-        const float Lh = a.L[uint64_t(i) * C::K + hs];
-        float Mh = leaky(Lh + m);
-        accumulate<C, ZT>(beg, end, false, a.pcol, a.R, a.Z, Lh, Mh, pbuf[w], jbuf[w], st);
-        reduce_lanes<C>(st);
-        float* part = a.sp.part + c * (C::W + 8);
-        const int slot = C::EPI > 1 ? lane / C::LPR : 0;
-        const int sub = C::EPI > 1 ? lane % C::LPR : lane;
-        if (slot == 0)
 #pragma unroll
-            for (int v = 0; v < C::VPL; ++v)
+        for (int v = 0; v < C::VPL; ++v) {
+            float m = -INFINITY;
+            for (uint32_t q = 0; q < nch; ++q) m = fmaxf(m, a.sp.mchunk[(first + q) * 8 + st.h[v]]);
+            st.L[v] = a.L[uint64_t(i) * C::K + st.h[v]];
+            st.m[v] = leaky(st.L[v] + m);  // exact row max: no rescale happens in this chunk
+        }
+        aggregate<C, ZT>(beg, end, a.pcol, a.R, a.Z, slot, sub, st);
+        float* part = a.sp.part + c * (C::W + 8);
+        if (slot == 0) {
+#pragma unroll
+            for (int v = 0; v < C::VPL; ++v) {
+                const int f0 = (sub + kWave * v) * C::VEC;
 #pragma unroll
                 for (int x = 0; x < C::VEC; x += 4)
-                    *reinterpret_cast<float4*>(part + (sub + kWave * v) * C::VEC + x) =
+                    *reinterpret_cast<float4*>(part + f0 + x) =
                         make_float4(st.acc[v * C::VEC + x], st.acc[v * C::VEC + x + 1], st.acc[v * C::VEC + x + 2],
                                     st.acc[v * C::VEC + x + 3]);
-        if (lane < C::K) part[C::W + lane] = st.dloc;
+                if (f0 % C::DIM == 0) part[C::W + st.h[v]] = st.den[v];
+            }
+        }
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
         uint32_t old = 0;
         if (lane == 0)
@@ -324,32 +305,29 @@ __global__ void __launch_bounds__(kThreads) k_agg_vec(VArgs<ZT> a) {
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
         // Last arrival: add the partials of every chunk in chunk order.
         float tot[C::ACC];
+        float dtot[C::VPL];
 #pragma unroll
         for (int x = 0; x < C::ACC; ++x) tot[x] = 0.0f;
-        float dtot = 0.0f;
+#pragma unroll
+        for (int v = 0; v < C::VPL; ++v) dtot[v] = 0.0f;
         for (uint32_t q = 0; q < nch; ++q) {
             const float* pq = a.sp.part + uint64_t(first + q) * (C::W + 8);
-            if (slot == 0)
 #pragma unroll
-                for (int v = 0; v < C::VPL; ++v)
+            for (int v = 0; v < C::VPL; ++v) {
+                const int f0 = (sub + kWave * v) * C::VEC;
 #pragma unroll
-                    for (int x = 0; x < C::VEC; x += 4) {
-                        const float4 t = *reinterpret_cast<const float4*>(pq + (sub + kWave * v) * C::VEC + x);
-                        tot[v * C::VEC + x] += t.x;
-                        tot[v * C::VEC + x + 1] += t.y;
-                        tot[v * C::VEC + x + 2] += t.z;
-                        tot[v * C::VEC + x + 3] += t.w;
-                    }
-            if (lane < C::K) dtot += pq[C::W + lane];
-        }
-        if (lane < C::K) {
-            a.mx[uint64_t(i) * C::K + lane] = Mh;
-            a.den[uint64_t(i) * C::K + lane] = dtot;
-            dsh[w][lane] = dtot;
+                for (int x = 0; x < C::VEC; x += 4) {
+                    const float4 t = *reinterpret_cast<const float4*>(pq + f0 + x);
+                    tot[v * C::VEC + x] += t.x;
+                    tot[v * C::VEC + x + 1] += t.y;
+                    tot[v * C::VEC + x + 2] += t.z;
+                    tot[v * C::VEC + x + 3] += t.w;
+                }
+                dtot[v] += pq[C::W + st.h[v]];
+            }
         }
         if (lane == 0) a.sp.counter[first] = 0;  // ready for the next launch
-        wave_sync();
-        finish_row<C>(i, tot, dsh[w], a.hidden, a.out32, a.outbf);
+        finish_row<C>(i, tot, dtot, st.m, st.h, slot, sub, a.hidden, a.mx, a.den, a.out32, a.outbf);
         return;
     }
     // ---------------- whole row, heaviest first
@@ -359,20 +337,17 @@ __global__ void __launch_bounds__(kThreads) k_agg_vec(VArgs<ZT> a) {
     const uint32_t i = a.perm[k];
     const uint64_t beg = a.prow[k], end = a.prow[k + 1];
     if (i >= a.n || beg > end || end > a.e) return;
-    const float Lh = a.L[uint64_t(i) * C::K + hs];
-    const uint64_t deg = end - beg;
-    // Empty row: max 0, denominator 0, output 0 (baseline/src/ref_fp32.cpp:11).
-    float Mh = 0.0f;
-    if (deg > uint64_t(C::BE)) Mh = leaky(Lh + row_max<C>(beg, end, a.pcol, a.R));
-    if (deg) accumulate<C, ZT>(beg, end, deg <= uint64_t(C::BE), a.pcol, a.R, a.Z, Lh, Mh, pbuf[w], jbuf[w], st);
-    reduce_lanes<C>(st);
-    if (lane < C::K) {
-        a.mx[uint64_t(i) * C::K + lane] = Mh;
-        a.den[uint64_t(i) * C::K + lane] = st.dloc;
-        dsh[w][lane] = st.dloc;
+#pragma unroll
+    for (int v = 0; v < C::VPL; ++v) {
+        st.L[v] = a.L[uint64_t(i) * C::K + st.h[v]];
+        st.m[v] = -INFINITY;
     }
-    wave_sync();
-    finish_row<C>(i, st.acc, dsh[w], a.hidden, a.out32, a.outbf);
+    aggregate<C, ZT>(beg, end, a.pcol, a.R, a.Z, slot, sub, st);
+    // Empty row: max 0, denominator 0, output 0 (baseline/src/ref_fp32.cpp:11).
+    if (end == beg)
+#pragma unroll
+        for (int v = 0; v < C::VPL; ++v) st.m[v] = 0.0f;
+    finish_row<C>(i, st.acc, st.den, st.m, st.h, slot, sub, a.hidden, a.mx, a.den, a.out32, a.outbf);
 }
 
 template <class C, class ZT>
@@ -416,11 +391,11 @@ hipError_t launch_aggregate_vec(const AggArgs& g, const RowBins& bins, const Spl
     const int W = g.heads * g.dim;
     if (g.heads != 8) return hipErrorInvalidValue;
     if (g.feat_bf16) {
-        if (W == 256) return run<Cfg<uint16_t, 256, 8, 64>, uint16_t>(g, bins, t, s);
-        if (W == 512) return run<Cfg<uint16_t, 512, 8, 64>, uint16_t>(g, bins, t, s);
+        if (W == 256) return run<Cfg<uint16_t, 256, 8>, uint16_t>(g, bins, t, s);
+        if (W == 512) return run<Cfg<uint16_t, 512, 8>, uint16_t>(g, bins, t, s);
     } else {
-        if (W == 256) return run<Cfg<float, 256, 8, 64>, float>(g, bins, t, s);
-        if (W == 512) return run<Cfg<float, 512, 8, 64>, float>(g, bins, t, s);
+        if (W == 256) return run<Cfg<float, 256, 8>, float>(g, bins, t, s);
+        if (W == 512) return run<Cfg<float, 512, 8>, float>(g, bins, t, s);
     }
     return hipErrorInvalidValue;
 }

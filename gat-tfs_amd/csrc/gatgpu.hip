@@ -212,7 +212,8 @@ int build_schedule(gatgpu_ctx* c) {
                                      c->hist.as<uint32_t>(), n, passes, c->scan_tmp.p, c->stream,
                                      &c->sorted_deg, &c->perm));
     HIPCHECK(c, c->prow.ensure((n + 1) * 8));
-    HIPCHECK(c, c->pcol.ensure(c->e * 4));
+    HIPCHECK(c, c->pcol.ensure((c->e + kPcolPad) * 4));
+    HIPCHECK(c, hipMemsetAsync(c->pcol.as<uint32_t>() + c->e, 0, kPcolPad * 4, c->stream));
     HIPCHECK(c, exclusive_scan_u32_to_u64(c->sorted_deg, c->prow.as<uint64_t>(), n, c->scan_tmp.p,
                                           c->stream));
     HIPCHECK(c, hipMemcpyAsync(c->prow.as<uint64_t>() + n, &c->e, 8, hipMemcpyHostToDevice, c->stream));

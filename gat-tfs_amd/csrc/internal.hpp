@@ -122,6 +122,11 @@ struct AggArgs {
 };
 // Split rows (sorted positions [split_begin, n)) cut into chunks of
 // chunk_edges edges, heaviest rows first; built on the host from prow.
+// The permuted column array carries kPcolPad zero entries past its e
+// edges, so that kernels may load a whole batch of wave-uniform source ids
+// at the end of the last row without a bounds test.
+constexpr uint64_t kPcolPad = 64;
+
 struct SplitTable {
     uint64_t chunks = 0;
     const uint32_t* chunk_k = nullptr;      // [chunks] sorted position of the row

@@ -189,6 +189,71 @@ def test_layer2_micro_fp32(gpu_ctx):
     assert e["finite"] and e["max_abs"] < FP32_MAX_ABS, e
 
 
+# ---------------------------------------------------------------- single-head one-pass layer
+def exact_max_aggregate(row, col, z, L, R, hidden):
+    """FP64 restatement of max_prescan + standard_aggregate + finish
+    (baseline/src/baseline_standard.cpp:44-97) over given Z, L, R (one head)."""
+    n = row.size - 1
+    out = np.zeros(z.shape, np.float64)
+    mx = np.zeros(n, np.float32)
+    den = np.zeros(n, np.float64)
+    for i in range(n):
+        b, e = int(row[i]), int(row[i + 1])
+        if b == e:
+            continue
+        s = L[i, 0] + R[col[b:e], 0]
+        s = np.where(s >= 0, s, np.float32(0.2) * s).astype(np.float32)
+        mx[i] = s.max()
+        p = np.exp(s.astype(np.float64) - np.float64(mx[i]))
+        den[i] = p.sum()
+        out[i] = (p[:, None] * z[col[b:e]].astype(np.float64)).sum(0) / den[i]
+    if hidden:
+        out = np.where(out >= 0, out, np.expm1(out))
+    return mx, den, out
+
+
+@pytest.mark.parametrize("ramp", [False, True])
+def test_single_head_bf16_one_pass(gpu_ctx, ramp):
+    """bf16 single-head layers (C <= 60) read each source's Z line once, with R
+    in the line, and keep the softmax online.  The row max must still equal
+    leaky(L + max R) bit for bit, and den/out must match the exact-max formula
+    evaluated over the GPU's own Z, L, R.  With `ramp`, R rises with the source
+    id, so every batch of a row raises the running maximum (a rescale per
+    batch).  Rows up to 3000 edges run whole (split threshold lifted) and split
+    into chunks (default schedule)."""
+    n, d = 20000, 47
+    row, col = inputs.powerlaw_graph(n, 400000, 3000, 5)
+    if ramp:
+        rng = np.random.default_rng(3)
+        x = np.stack([np.arange(n, dtype=np.float32) * np.float32(6.0 / n), np.ones(n, np.float32)], 1)
+        p = {"in": 2, "heads": 1, "dim": d, "w": rng.standard_normal((2, d)).astype(np.float32),
+             "al": rng.standard_normal(d).astype(np.float32), "ar": rng.standard_normal(d).astype(np.float32)}
+        if float(p["w"][0] @ p["ar"]) < 0:
+            p["ar"] = -p["ar"]
+    else:
+        x = inputs.normal((n, 64), 8)
+        p = inputs.glorot_param(64, 1, d, 9)
+    for opts in ({}, {gatgpu.OPT_SPLIT_ROW_MIN_DEGREE: 1 << 30}):
+        for hidden in (False, True):
+            got = run_layer(gpu_ctx, row, col, x, p, hidden, gatgpu.BF16, opts)
+            z = gpu_ctx.stage(0, "z")
+            L, R = got["left"].reshape(n, 1), got["right"].reshape(n, 1)
+            if ramp:
+                assert np.mean(np.diff(R[:, 0]) >= 0) > 0.99
+            mx, den, out = exact_max_aggregate(row, col, z, L, R, hidden)
+            assert np.array_equal(got["max"].reshape(n), mx), opts
+            assert oracle.errors(den, got["den"].reshape(n))["relative_l2"] < 1e-5, opts
+            g_out = got["out"].reshape(n, d)
+            if hidden:
+                # hidden bf16 layers store their output in bf16: one rounding
+                assert np.all(np.abs(g_out - out) <= np.abs(out) * (2.0 ** -8 * 1.001) + 1e-6), opts
+            else:
+                e = oracle.errors(out, g_out)
+                assert e["finite"] and e["relative_l2"] < 1e-5, (opts, e)
+            r = oracle.ref_layer(row, col, x, p, hidden)
+            assert oracle.errors(r["out"], got["out"])["relative_l2"] < BF16_REL_L2
+
+
 # ---------------------------------------------------------------- error codes
 def test_error_codes(gpu_ctx):
     g = oracle.boundary_graph(17)
