@@ -2,6 +2,7 @@
 // orchestration, HIP-event stage timing.  Declarations: include/gatgpu.h.
 #include "gatgpu.h"
 
+#include <algorithm>
 #include <cmath>
 #include <cstdio>
 #include <cstring>
@@ -60,6 +61,9 @@ struct LayerState {
     DevBuf wlr;
     int lr_ksteps = 0;
     int dataflow = 0;  // dataflow of the last forward
+    // fixed-p fixture: p in degree-sorted edge order [e][heads], den [n][heads]
+    DevBuf fixp, fixden;
+    bool fixed_set = false;
     int width() const { return heads * dim; }
 };
 
@@ -339,7 +343,7 @@ int run_layer_af(gatgpu_ctx* c, int l, bool hidden, const float* src32, const ui
 // Runs layer l on the device.  ev_base: first of 4 events (start, after
 // convert, after projection, after aggregate) or -1 for no timing.
 int run_layer(gatgpu_ctx* c, int l, int precision, int dataflow, bool hidden, const float* host_input,
-              int ev_base) {
+              int ev_base, bool fixed = false) {
     LayerState& Ls = c->L[l];
     const uint64_t n = c->n;
     const int K = Ls.heads, dim = Ls.dim, W = Ls.width(), D = Ls.in;
@@ -370,7 +374,7 @@ int run_layer(gatgpu_ctx* c, int l, int precision, int dataflow, bool hidden, co
     HIPCHECK(c, Ls.mx.ensure(n * K * 4));
     HIPCHECK(c, Ls.den.ensure(n * K * 4));
     const bool bf16 = precision == GATGPU_BF16;
-    const bool want_outbf = bf16 && hidden;
+    const bool want_outbf = bf16 && hidden && !fixed;
     if (want_outbf) HIPCHECK(c, Ls.outbf.ensure(n * W * 2));
     else HIPCHECK(c, Ls.out32.ensure(n * W * 4));
     // bf16 path: X as [n][xs] bf16 (xs = ksteps*16, zero-padded), Z as [n][zs]
@@ -390,6 +394,8 @@ int run_layer(gatgpu_ctx* c, int l, int precision, int dataflow, bool hidden, co
     } else {
         HIPCHECK(c, Ls.z32.ensure(n * zs * 4));
     }
+    // The fixed-p operator has no row max (the reference leaves it unset).
+    if (fixed) HIPCHECK(c, hipMemsetAsync(Ls.mx.p, 0, n * K * 4, c->stream));
     if (ev_base >= 0) HIPCHECK(c, hipEventRecord(c->ev[ev_base], c->stream));
     // ---- convert (bf16 path, FP32 source only; a bf16 source was rounded in
     // the previous layer's epilogue, which equals convert() of that output)
@@ -445,7 +451,11 @@ int run_layer(gatgpu_ctx* c, int l, int precision, int dataflow, bool hidden, co
     a.outbf = want_outbf ? Ls.outbf.as<uint16_t>() : nullptr;
     a.n = c->n;
     a.e = c->e;
-    HIPCHECK(c, launch_aggregate_tf(a, c->bins, c->split, c->stream));
+    if (fixed)
+        HIPCHECK(c, launch_aggregate_fixed(a, Ls.fixp.as<float>(), Ls.fixden.as<float>(), c->bins, c->split,
+                                           c->stream));
+    else
+        HIPCHECK(c, launch_aggregate_tf(a, c->bins, c->split, c->stream));
     if (ev_base >= 0) HIPCHECK(c, hipEventRecord(c->ev[ev_base + 3], c->stream));
     Ls.ran = true;
     Ls.precision = precision;
@@ -531,7 +541,7 @@ int gatgpu_set_graph(gatgpu_ctx* c, uint64_t n, uint64_t e, const uint64_t* row,
         if (col[k] >= n) return fail(c, GATGPU_EINVAL, "source index out of bounds");
     if (c->input && c->n != n) c->input = false;
     c->graph = false;
-    for (auto& L : c->L) L.ran = false;
+    for (auto& L : c->L) L.ran = L.fixed_set = false;
     c->n = n;
     c->e = e;
     HIPCHECK(c, c->row.ensure((n + 1) * 8));
@@ -557,7 +567,7 @@ int gatgpu_set_layer(gatgpu_ctx* c, int layer, int in, int heads, int dim, const
     if (!all_finite(ar, W, &bad)) return fail(c, GATGPU_ENONFINITE, "nonfinite aR index=" + std::to_string(bad));
     LayerState& L = c->L[layer];
     L.set = false;
-    L.ran = false;
+    L.ran = L.fixed_set = false;
     L.in = in;
     L.heads = heads;
     L.dim = dim;
@@ -660,6 +670,71 @@ int gatgpu_layer_forward(gatgpu_ctx* c, int layer, int precision, int dataflow, 
     HIPCHECK(c, hipStreamSynchronize(c->stream));
     HIPCHECK(c, hipGetLastError());
     if (times) fill_times(c, 0, times, c->L[layer].dataflow);
+    return GATGPU_OK;
+}
+
+int gatgpu_set_fixed_p(gatgpu_ctx* c, int layer, const float* p, const float* den) {
+    if (int r = check_ctx(c)) return r;
+    if (layer < 0 || layer > 2) return fail(c, GATGPU_EINVAL, "layer must be 0, 1 or 2");
+    if (!c->graph) return fail(c, GATGPU_ESTATE, "graph not set");
+    LayerState& Ls = c->L[layer];
+    if (!Ls.set) return fail(c, GATGPU_ESTATE, "layer weights not set");
+    if ((c->e && !p) || !den) return fail(c, GATGPU_EINVAL, "null fixture pointer");
+    Ls.fixed_set = false;
+    const uint64_t n = c->n, e = c->e;
+    const int K = Ls.heads;
+    uint64_t bad = 0;
+    if (!all_finite(p, e * K, &bad)) return fail(c, GATGPU_ENONFINITE, "nonfinite fixture p index=" + std::to_string(bad));
+    if (!all_finite(den, n * K, &bad))
+        return fail(c, GATGPU_ENONFINITE, "nonfinite fixture denominator index=" + std::to_string(bad));
+    // load_fixture's checks (baseline/src/common.cpp:189-192): p in [0, 1], den
+    // equal to the row's sum of p in edge order, positive on a non-empty row.
+    std::vector<uint64_t> row(n + 1);
+    HIPCHECK(c, hipMemcpy(row.data(), c->row.p, (n + 1) * 8, hipMemcpyDeviceToHost));
+    for (uint64_t i = 0; i < n; ++i)
+        for (int h = 0; h < K; ++h) {
+            float sum = 0;
+            for (uint64_t q = row[i]; q < row[i + 1]; ++q) {
+                const float x = p[q * K + h];
+                if (x < 0 || x > 1) return fail(c, GATGPU_EINVAL, "fixture p outside [0,1] at edge " + std::to_string(q));
+                sum += x;
+            }
+            const float d = den[i * K + h];
+            if (std::abs(sum - d) > 1e-5f * std::max(1.f, sum) || (row[i] != row[i + 1] && d <= 0))
+                return fail(c, GATGPU_EINVAL, "fixture denominator mismatch at row " + std::to_string(i));
+        }
+    DevBuf tmp;
+    HIPCHECK(c, tmp.ensure(e * K * 4));
+    HIPCHECK(c, Ls.fixp.ensure(e * K * 4));
+    HIPCHECK(c, Ls.fixden.ensure(n * K * 4));
+    if (e) HIPCHECK(c, hipMemcpyAsync(tmp.p, p, e * K * 4, hipMemcpyHostToDevice, c->stream));
+    HIPCHECK(c, hipMemcpyAsync(Ls.fixden.p, den, n * K * 4, hipMemcpyHostToDevice, c->stream));
+    HIPCHECK(c, launch_permute_edge_values(c->row.as<uint64_t>(), c->perm, c->prow.as<uint64_t>(), tmp.as<float>(),
+                                           Ls.fixp.as<float>(), n, e, K, c->stream));
+    HIPCHECK(c, hipStreamSynchronize(c->stream));
+    Ls.fixed_set = true;
+    return GATGPU_OK;
+}
+
+int gatgpu_fixed_p_forward(gatgpu_ctx* c, int layer, int precision, int dataflow, const float* input,
+                           gatgpu_times* times) {
+    if (int r = check_ctx(c)) return r;
+    if (layer < 0 || layer > 2) return fail(c, GATGPU_EINVAL, "layer must be 0, 1 or 2");
+    if (precision != GATGPU_FP32 && precision != GATGPU_BF16) return fail(c, GATGPU_EINVAL, "bad precision");
+    if (dataflow != GATGPU_AUTO && dataflow != GATGPU_TRANSFORM_FIRST)
+        return fail(c, GATGPU_EINVAL, "the fixed-p operator is transform-first");
+    if (!c->graph) return fail(c, GATGPU_ESTATE, "graph not set");
+    if (!c->L[layer].set) return fail(c, GATGPU_ESTATE, "layer weights not set");
+    if (!c->L[layer].fixed_set) return fail(c, GATGPU_ESTATE, "fixture p/den not set for this layer");
+    if (input) {
+        uint64_t bad = 0;
+        if (!all_finite(input, c->n * uint64_t(c->L[layer].in), &bad))
+            return fail(c, GATGPU_ENONFINITE, "nonfinite layer input index=" + std::to_string(bad));
+    }
+    if (int r = run_layer(c, layer, precision, GATGPU_TRANSFORM_FIRST, false, input, times ? 0 : -1, true)) return r;
+    HIPCHECK(c, hipStreamSynchronize(c->stream));
+    HIPCHECK(c, hipGetLastError());
+    if (times) fill_times(c, 0, times, GATGPU_TRANSFORM_FIRST);
     return GATGPU_OK;
 }
 

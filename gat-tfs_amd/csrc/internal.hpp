@@ -51,6 +51,9 @@ hipError_t exclusive_scan_u32_to_u64(const uint32_t* in, uint64_t* out, uint64_t
 hipError_t launch_permute_cols(const uint64_t* row, const uint32_t* col, const uint32_t* perm,
                                const uint64_t* prow, uint32_t* pcol, uint64_t n, uint64_t e,
                                hipStream_t s);
+// Per-edge values ([e][K] floats) from original CSR order to degree-sorted order.
+hipError_t launch_permute_edge_values(const uint64_t* row, const uint32_t* perm, const uint64_t* prow,
+                                     const float* src, float* dst, uint64_t n, uint64_t e, int K, hipStream_t s);
 hipError_t launch_neighbor_steps(const uint32_t* sorted_deg, uint64_t n, uint64_t* steps,
                                  hipStream_t s);
 hipError_t launch_count_le(const uint32_t* sorted_deg, uint64_t n, const uint32_t* thresholds,
@@ -120,13 +123,13 @@ struct AggArgs {
     uint16_t* outbf; // [n][W] or null
     uint64_t n, e;           // nodes and CSR entries (bounds of perm/prow values)
 };
-// Split rows (sorted positions [split_begin, n)) cut into chunks of
-// chunk_edges edges, heaviest rows first; built on the host from prow.
 // The permuted column array carries kPcolPad zero entries past its e
 // edges, so that kernels may load a whole batch of wave-uniform source ids
 // at the end of the last row without a bounds test.
 constexpr uint64_t kPcolPad = 64;
 
+// Split rows (sorted positions [split_begin, n)) cut into chunks of
+// chunk_edges edges, heaviest rows first; built on the host from prow.
 struct SplitTable {
     uint64_t chunks = 0;
     const uint32_t* chunk_k = nullptr;      // [chunks] sorted position of the row
@@ -141,6 +144,10 @@ hipError_t launch_aggregate_tf(const AggArgs& a, const RowBins& bins, const Spli
 // Per-chunk maxima of R for split rows (heads 1, 2, 4 or 8).
 hipError_t launch_split_prescan(const uint64_t* prow, const uint32_t* pcol, const float* right, int heads,
                                 const SplitTable& t, uint64_t e, hipStream_t s);
+// aggregate_fixed.hip: aggregation with fixture weights p (degree-sorted
+// edge order, [e][K]) and fixture denominators ([n][K]); writes den and out32.
+hipError_t launch_aggregate_fixed(const AggArgs& a, const float* p_sorted, const float* den_fixture,
+                                  const RowBins& bins, const SplitTable& split, hipStream_t s);
 // aggregate_k1.hip: one head, rows of at most 64 features.
 bool aggregate_k1_supported(const AggArgs& a);
 hipError_t launch_aggregate_k1(const AggArgs& a, const RowBins& bins, const SplitTable& split,

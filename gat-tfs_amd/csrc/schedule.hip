@@ -210,6 +210,23 @@ k_permute_cols(const uint64_t* __restrict__ row, const uint32_t* __restrict__ co
     for (uint64_t q = lane; q < deg; q += kWave) pcol[dst + q] = col[src + q];
 }
 
+// The per-edge values of row perm[k] (K floats per edge, original CSR order)
+// to their degree-sorted position: dst[(prow[k] + q) K + h] = src[(row[r] + q) K + h].
+__global__ void __launch_bounds__(kThreads)
+k_permute_edge_values(const uint64_t* __restrict__ row, const uint32_t* __restrict__ perm,
+                      const uint64_t* __restrict__ prow, const float* __restrict__ src, float* __restrict__ dst,
+                      uint64_t n, uint64_t e, int K) {
+    const uint64_t k = (uint64_t(blockIdx.x) * kThreads + threadIdx.x) / kWave;
+    const int lane = threadIdx.x % kWave;
+    if (k >= n) return;
+    const uint32_t r = perm[k];
+    if (r >= n) return;
+    const uint64_t s0 = row[r], deg = row[r + 1] - s0, d0 = prow[k];
+    if (d0 > e || deg > e - d0 || s0 > e || deg > e - s0) return;
+    const uint64_t cnt = deg * uint64_t(K);
+    for (uint64_t q = lane; q < cnt; q += kWave) dst[d0 * K + q] = src[s0 * K + q];
+}
+
 // neighbor_steps = sum over 16-row tiles of the last (= largest) degree.
 __global__ void __launch_bounds__(kThreads)
 k_neighbor_steps(const uint32_t* __restrict__ sorted_deg, uint64_t n, uint64_t* __restrict__ steps) {
@@ -294,6 +311,14 @@ hipError_t launch_permute_cols(const uint64_t* row, const uint32_t* col, const u
     const uint64_t waves_per_block = kThreads / kWave;
     const uint64_t blocks = (n + waves_per_block - 1) / waves_per_block;
     k_permute_cols<<<dim3(uint32_t(blocks)), kThreads, 0, s>>>(row, col, perm, prow, pcol, n, e);
+    return hipGetLastError();
+}
+
+hipError_t launch_permute_edge_values(const uint64_t* row, const uint32_t* perm, const uint64_t* prow,
+                                     const float* src, float* dst, uint64_t n, uint64_t e, int K, hipStream_t s) {
+    const uint64_t waves_per_block = kThreads / kWave;
+    const uint64_t blocks = (n + waves_per_block - 1) / waves_per_block;
+    k_permute_edge_values<<<dim3(uint32_t(blocks)), kThreads, 0, s>>>(row, perm, prow, src, dst, n, e, K);
     return hipGetLastError();
 }
 

@@ -30,7 +30,7 @@ EXPORTS = (
     "gatgpu_create", "gatgpu_destroy", "gatgpu_last_error", "gatgpu_set_graph", "gatgpu_set_layer",
     "gatgpu_set_input", "gatgpu_degree_schedule", "gatgpu_permuted_csr", "gatgpu_choose_R",
     "gatgpu_layer_forward", "gatgpu_model_forward", "gatgpu_get_stage", "gatgpu_stage_size",
-    "gatgpu_set_option", "gatgpu_synchronize", "gatgpu_stream",
+    "gatgpu_set_option", "gatgpu_synchronize", "gatgpu_stream", "gatgpu_set_fixed_p", "gatgpu_fixed_p_forward",
 )
 
 
@@ -80,6 +80,8 @@ def load_library(path: os.PathLike | None = None):
     L.gatgpu_set_option.argtypes = [P, i32, i64]
     L.gatgpu_synchronize.argtypes = [P]
     L.gatgpu_stream.argtypes = [P]
+    L.gatgpu_set_fixed_p.argtypes = [P, i32, P, P]
+    L.gatgpu_fixed_p_forward.argtypes = [P, i32, i32, i32, P, P]
     L.gatgpu_stream.restype = P
     for name in EXPORTS:
         if name not in ("gatgpu_last_error", "gatgpu_stream"):
@@ -179,6 +181,19 @@ class Context:
         inp = None if input is None else np.ascontiguousarray(input, np.float32)
         self._check(self.lib.gatgpu_layer_forward(self.h, layer, precision, dataflow, int(hidden), _ptr(inp),
                                                   ctypes.byref(t)))
+        return t.as_dict()
+
+    def set_fixed_p(self, layer, p, den):
+        """Fixture weights for the fixed-p operator: p [e][heads] in CSR edge
+        order, den [n][heads] (GATFIX1 fields, baseline/src/common.cpp:171-194)."""
+        p = np.ascontiguousarray(p, np.float32)
+        den = np.ascontiguousarray(den, np.float32)
+        self._check(self.lib.gatgpu_set_fixed_p(self.h, layer, _ptr(p), _ptr(den)))
+
+    def fixed_p_forward(self, layer, precision=BF16, dataflow=TRANSFORM_FIRST, input=None):
+        t = Times()
+        inp = None if input is None else np.ascontiguousarray(input, np.float32)
+        self._check(self.lib.gatgpu_fixed_p_forward(self.h, layer, precision, dataflow, _ptr(inp), ctypes.byref(t)))
         return t.as_dict()
 
     def model_forward(self, precision=FP32, dataflow=AUTO, want_logits=True, timed=True):

@@ -3,7 +3,7 @@
 // Mirrors the reference harness baseline/bench/main.cpp: `--key value`
 // arguments against a whitelist with duplicates rejected (:9-16), a path
 // registry dispatched by name (run_path, :21-25), modes benchmark /
-// correctness / micro / export-fixture, and the same output lines (ENV,
+// correctness / micro / export-fixture / fixed-p, and the same output lines (ENV,
 // STATIC, CONFIG, ERROR, per-layer JSON, E2E, SUMMARY; :46-64, :182).
 // Registered paths: gpu_fp32 and gpu_bf16 (include/gatgpu.h through
 // gat_gpu_path.hpp).  Correctness compares against R0 stage dumps in the
@@ -37,7 +37,7 @@ struct Args {
                                         "--save-weights", "--save-graph", "--path", "--mode", "--layer",
                                         "--repeats", "--warmups", "--reference-prefix", "--dump-prefix",
                                         "--output", "--max-abs", "--rel-l2", "--fixture", "--dataflow",
-                                        "--device"};
+                                        "--device", "--reference"};
         for (int i = 1; i < argc; ++i) {
             const std::string k = argv[i];
             if (k.rfind("--", 0) != 0 || i + 1 == argc) throw std::runtime_error("arguments must be --key value");
@@ -160,7 +160,7 @@ int run(int argc, char** argv) {
     const std::string path = a.get("--path", "gpu_bf16"), mode = a.get("--mode", "benchmark");
     if (!PathRegistry::known(path)) throw std::runtime_error("bad path");
     if (mode != "benchmark" && mode != "correctness" && mode != "micro" && mode != "inspect" &&
-        mode != "export-fixture")
+        mode != "export-fixture" && mode != "fixed-p")
         throw std::runtime_error("bad mode");
     const int reps = a.num("--repeats", 5), warmups = a.num("--warmups", 2), layer = a.num("--layer", 0);
     if (reps < 1 || warmups < 0 || layer < 0 || layer > 3) throw std::runtime_error("invalid benchmark controls");
@@ -252,6 +252,36 @@ int run(int argc, char** argv) {
         std::cout << "CORRECTNESS finite=" << finite << " accuracy_gate="
                   << (have_abs ? (pass ? "PASS" : "FAIL") : "UNCONFIGURED_NOT_ACCEPTED") << "\n";
         return pass ? 0 : 1;
+    }
+
+    if (mode == "fixed-p") {  // main.cpp:103-150 with the GPU standard operator
+        const int l = layer ? layer : 2;
+        const Param& p = model[l - 1];
+        if (!a.has("--fixture")) throw std::runtime_error("--fixture (GATFIX1) is required");
+        const Fixture fixture = load_fixture(g, p, a.get("--fixture"));
+        Workspace w;
+        Times t;
+        gpu.fixed_p(g, p, l - 1, fixture, w, t, precision);
+        require_finite(w.out, "fixed-p GPU");
+        if (a.has("--reference")) {  // FP32 fixed-p master output (main.cpp:136-137), one f32 dump
+            const Error e = errors(read_dump(a.get("--reference"), checked(g.n, uint64_t(p.width()))), w.out);
+            print_error(path + "_fixed_p", l, "vs_master_fixed_p", e);
+        }
+        if (a.has("--output")) write_dump(a.get("--output"), w.out);
+        std::vector<double> tot, agg;
+        for (int r = -warmups; r < reps; ++r) {
+            Times s;
+            gpu.fixed_p(g, p, l - 1, fixture, w, s, precision);
+            if (r >= 0) {
+                tot.push_back(s.total);
+                agg.push_back(s.aggregate);
+                print_times(path, "fixed-p", l, r, g, p, s);
+            }
+        }
+        std::cout << "FIXED_P path=" << path << " layer=" << l << " median_ms=" << pct(tot, .5) * 1e3
+                  << " median_aggregate_ms=" << pct(agg, .5) * 1e3
+                  << " aggregate_gedge_per_s=" << double(g.e) / pct(agg, .5) / 1e9 << " conversion_included=true\n";
+        return 0;
     }
 
     if (mode == "micro") {

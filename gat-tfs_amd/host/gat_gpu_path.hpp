@@ -50,6 +50,7 @@ class GpuPath {
         check(ctx_, gatgpu_set_graph(ctx_, g.n, g.e, g.row.data(), g.col.data()), "gatgpu_set_graph");
         check(ctx_, gatgpu_set_input(ctx_, g.n, int(g.din), g.x.data()), "gatgpu_set_input");
         graph_ = &g;
+        fixture_ = nullptr;  // set_graph drops every fixture
         n_ = g.n;
         e_ = g.e;
     }
@@ -60,6 +61,7 @@ class GpuPath {
         check(ctx_, gatgpu_set_layer(ctx_, layer, p.in, p.heads, p.dim, p.w.data(), p.al.data(), p.ar.data()),
               "gatgpu_set_layer");
         layer_[layer] = &p;
+        if (fixture_layer_ == layer) fixture_ = nullptr;  // set_layer drops the layer's fixture
     }
 
     // The per-layer path: input -> w.out (plus the stage vectors the
@@ -89,6 +91,33 @@ class GpuPath {
         fetch(layer_index, GATGPU_STAGE_Z, w.z);
     }
 
+    // The fixed-p operator (baseline/bench/main.cpp:103-150, "standard_op"):
+    // uploads the fixture's p/den once per Fixture object, runs projection +
+    // fixed-weight aggregation + normalisation on fixture.input, fills w.z,
+    // w.den and w.out and the Times fields.
+    template <class Graph, class Param, class Fixture, class Workspace, class Times>
+    void fixed_p(const Graph& g, const Param& p, int layer_index, const Fixture& f, Workspace& w, Times& t,
+                 int precision) {
+        set_graph(g);
+        set_layer(layer_index, p);
+        if (fixture_ != static_cast<const void*>(&f) || fixture_layer_ != layer_index) {
+            check(ctx_, gatgpu_set_fixed_p(ctx_, layer_index, f.p.data(), f.den.data()), "gatgpu_set_fixed_p");
+            fixture_ = &f;
+            fixture_layer_ = layer_index;
+        }
+        gatgpu_times gt{};
+        check(ctx_,
+              gatgpu_fixed_p_forward(ctx_, layer_index, precision, GATGPU_TRANSFORM_FIRST, f.input.data(), &gt),
+              "gatgpu_fixed_p_forward");
+        t.convert = gt.convert_ms * 1e-3;
+        t.projection = gt.projection_ms * 1e-3;
+        t.aggregate = gt.aggregate_ms * 1e-3;
+        t.total = gt.total_ms * 1e-3;
+        fetch(layer_index, GATGPU_STAGE_OUT, w.out);
+        fetch(layer_index, GATGPU_STAGE_DEN, w.den);
+        fetch(layer_index, GATGPU_STAGE_Z, w.z);
+    }
+
     // Three layers chained on the device; returns the model time in seconds
     // (HIP events from layer 1's first kernel to layer 3's last).
     double model(int precision, std::vector<float>* logits, int dataflow = GATGPU_AUTO) {
@@ -114,6 +143,8 @@ class GpuPath {
     }
     gatgpu_ctx* ctx_ = nullptr;
     const void* graph_ = nullptr;
+    const void* fixture_ = nullptr;
+    int fixture_layer_ = -1;
     const void* layer_[3] = {nullptr, nullptr, nullptr};
     uint64_t n_ = 0, e_ = 0;
     int classes_hint_ = 0;

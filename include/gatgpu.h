@@ -150,6 +150,25 @@ int gatgpu_layer_forward(gatgpu_ctx* ctx, int layer, int precision, int dataflow
  * dataflow applies to every layer (AUTO decides per layer). */
 int gatgpu_model_forward(gatgpu_ctx* ctx, int precision, int dataflow, float* logits,
                          gatgpu_times* times, double* total_ms);
+/* ---- fixed-p operator ----------------------------------------------- */
+/* Uploads a fixture's attention weights for `layer`: p[e][heads] (the
+ * unnormalised exp weights, original CSR edge order) and den[n][heads].
+ * Checks them as load_fixture does (baseline/src/common.cpp:186-193): all
+ * finite, p in [0, 1], den equal to the row's sum of p within 1e-5 relative,
+ * den > 0 on a non-empty row.  p is permuted to degree-sorted order on the
+ * device.  set_graph and set_layer(layer) drop the fixture.  The GATFIX1 file
+ * (common.cpp:171-194) is read by the host harness. */
+int gatgpu_set_fixed_p(gatgpu_ctx* ctx, int layer, const float* p, const float* den);
+/* The fixed-p operator of the reference harness (baseline/bench/main.cpp:
+ * 103-150, "standard_op"): projection Z = XW in `precision`, then
+ * out = (sum_e p[e] Z[col[e]]) * (den > 0 ? 1/den : 0) with the fixture's p
+ * and den and no activation (standard_aggregate with fixed_p and finish,
+ * baseline/src/baseline_standard.cpp:52-97).  dataflow must be AUTO or
+ * TRANSFORM_FIRST.  input as in gatgpu_layer_forward.  Stages: Z, LEFT, RIGHT
+ * from the projection, DEN = the fixture's den, MAX zero, OUT FP32. */
+int gatgpu_fixed_p_forward(gatgpu_ctx* ctx, int layer, int precision, int dataflow, const float* input,
+                           gatgpu_times* times);
+
 /* Copies a stage of the last forward of `layer` as FP32 (bf16 stages are
  * widened exactly). */
 int gatgpu_get_stage(gatgpu_ctx* ctx, int layer, int which, float* host_out);

@@ -57,6 +57,7 @@ def lib():
         L.or_ref_layer.argtypes = [u64, P, P, P, i32, i32, i32, P, P, P, i32] + [P] * 9
         L.or_fp64_layer.argtypes = [u64, P, P, P, i32, i32, i32, P, P, P, i32] + [P] * 6
         L.or_standard_layer.argtypes = [u64, P, P, P, i32, i32, i32, P, P, P, i32, i32, i32] + [P] * 8
+        L.or_fixed_p_layer.argtypes = [u64, P, P, P, i32, i32, i32, P, P, P, i32, P, P]
         L.or_degree_schedule.argtypes = [u64, P, P, P]
         L.or_permute_csr.argtypes = [u64, P, P, P, P, P]
         L.or_choose_R.argtypes = [u64, u64, P]
@@ -254,6 +255,22 @@ def standard_layer(row, col, x, p, hidden, bf16, threads=0, wq=None, ws=None):
                             int(bf16), int(threads), _p(st["xq"]), _p(st["z"]), _p(st["left"]), _p(st["right"]),
                             _p(st["max"]), _p(st["den"]), _p(st["out"]), _p(t))
     return st, t
+
+
+def fixed_p_layer(row, col, x, p, P, den, bf16):
+    """Fixed-p operator (baseline/bench/main.cpp:103-150): Z = XW (bf16-rounded
+    X and W with FP32 Z when bf16, else FP32), out = sum_e P[e] Z[col[e]] / den.
+    P [e][heads] in CSR edge order, den [n][heads] -> dict(z, out)."""
+    row, col = _graph_args(row, col)
+    x = np.ascontiguousarray(x, np.float32)
+    P = np.ascontiguousarray(P, np.float32)
+    den = np.ascontiguousarray(den, np.float32)
+    n = row.size - 1
+    W = p["heads"] * p["dim"]
+    o = {k: np.empty((n, W), np.float32) for k in ("z", "out")}
+    lib().or_fixed_p_layer(n, _p(row), _p(col), _p(x), p["in"], p["heads"], p["dim"], _p(p["w"]), _p(P), _p(den),
+                           int(bool(bf16)), _p(o["z"]), _p(o["out"]))
+    return o
 
 
 def ref_model(row, col, x, model):

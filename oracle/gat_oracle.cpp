@@ -17,6 +17,8 @@
 //   or_ref_layer (R0)      FP64 oracle < 1e-4 on 64 shapes, NumPy FP64 chain < 2e-4,
 //                          smoke1024 checksum 221.971286 (+-1e-3), the logged errors
 //   or_fp64_layer          NumPy FP64 restatement of baseline/tests/oracle.py (1e-9)
+//   or_fixed_p_layer       fed R0's own p and den it reproduces R0's output (1e-6);
+//                          a hand-computed three-node case
 //   or_standard_layer (B0) the logged standard_bf16 stage errors and chain error
 //   or_degree_schedule,    numpy.lexsort on (degree, id); neighbor_steps definition;
 //   or_permute_csr         row-by-row copy check
@@ -214,6 +216,47 @@ void or_fp64_layer(uint64_t n, const uint64_t* row, const uint32_t* col, const f
                     out[i * W + h * dim + d] = o;
                 }
             }
+        }
+    }
+}
+
+// Fixed-p operator (baseline/bench/main.cpp:103-150): projection, then
+// standard_aggregate with the fixture's p and den (baseline/src/
+// baseline_standard.cpp:52-84) and finish without activation (:85-97).
+// bf16 != 0 rounds X and W to bf16 first and keeps Z in FP32, as the
+// reference's standard_bf16 projection does (cblas_gemm_bf16bf16f32); bf16 == 0
+// is the FP32 master of main.cpp:136-137.  p [e][heads], den [n][heads].
+void or_fixed_p_layer(uint64_t n, const uint64_t* row, const uint32_t* col, const float* x, int in,
+                      int heads, int dim, const float* w, const float* p, const float* den, int bf16,
+                      float* z, float* out) {
+    const int K = heads, W = heads * dim;
+    std::vector<float> wq(size_t(in) * W);
+    for (size_t q = 0; q < wq.size(); ++q) wq[q] = bf16 ? expand(rne(w[q])) : w[q];
+    #pragma omp parallel for schedule(static)
+    for (uint64_t i = 0; i < n; ++i) {
+        float* zi = z + i * W;
+        for (int c = 0; c < W; ++c) zi[c] = 0.0f;
+        for (int k = 0; k < in; ++k) {
+            const float a = bf16 ? expand(rne(x[i * in + k])) : x[i * in + k];
+            const float* wk = wq.data() + size_t(k) * W;
+            for (int c = 0; c < W; ++c) zi[c] += a * wk[c];
+        }
+    }
+    #pragma omp parallel for schedule(dynamic, 64)
+    for (uint64_t i = 0; i < n; ++i) {
+        float* oi = out + i * W;
+        for (int c = 0; c < W; ++c) oi[c] = 0.0f;
+        for (uint64_t e = row[i]; e < row[i + 1]; ++e) {
+            const float* zj = z + uint64_t(col[e]) * W;
+            for (int h = 0; h < K; ++h) {
+                const float pe = p[e * K + h];
+                for (int d = 0; d < dim; ++d) oi[h * dim + d] += pe * zj[h * dim + d];
+            }
+        }
+        for (int h = 0; h < K; ++h) {
+            const float d = den[i * K + h];
+            const float scale = d > 0 ? 1 / d : 0;
+            for (int c = 0; c < dim; ++c) oi[h * dim + c] *= scale;
         }
     }
 }

@@ -254,6 +254,75 @@ def test_single_head_bf16_one_pass(gpu_ctx, ramp):
             assert oracle.errors(r["out"], got["out"])["relative_l2"] < BF16_REL_L2
 
 
+# ---------------------------------------------------------------- fixed-p operator
+FIXED_SHAPES = [(128, 8, 32), (256, 8, 64), (256, 1, 47), (33, 4, 40), (17, 8, 7), (64, 2, 32)]
+
+
+@pytest.mark.parametrize("graph", ["boundary", "powerlaw"])
+@pytest.mark.parametrize("D,K,d", FIXED_SHAPES)
+def test_fixed_p_operator(gpu_ctx, graph, D, K, d):
+    """The fixed-p operator (baseline/bench/main.cpp:103-150) with R0's p/den
+    as the fixture: FP32 within 1e-4 of the oracle's FP32 master, bf16 within
+    rel-L2 1e-2 of the oracle's bf16-input operator, DEN equal to the fixture
+    bit for bit, on every schedule (whole rows, split chunks)."""
+    if graph == "boundary":
+        g = oracle.boundary_graph(D)
+        row, col, x = g["row"], g["col"], g["x"]
+        p = oracle.boundary_param(D, K, d)
+    else:
+        row, col = inputs.powerlaw_graph(4000, 90000, 1500, 3)
+        x = inputs.normal((row.size - 1, D), 4)
+        p = inputs.glorot_param(D, K, d, 5)
+    r = oracle.ref_layer(row, col, x, p, False, edge_stages=True)
+    m32 = oracle.fixed_p_layer(row, col, x, p, r["p"], r["den"], False)["out"]
+    m16 = oracle.fixed_p_layer(row, col, x, p, r["p"], r["den"], True)["out"]
+    gpu_ctx.set_graph(row, col)
+    gpu_ctx.set_layer(0, p)
+    gpu_ctx.set_fixed_p(0, r["p"], r["den"])
+    for opts in SCHEDULES:
+        for k, v in opts.items():
+            gpu_ctx.set_option(k, v)
+        gpu_ctx.fixed_p_forward(0, gatgpu.FP32, input=x)
+        e = oracle.errors(m32, gpu_ctx.stage(0, "out"))
+        assert e["finite"] and e["max_abs"] < FP32_MAX_ABS, (opts, e)
+        assert np.array_equal(gpu_ctx.stage(0, "den"), r["den"])
+        gpu_ctx.fixed_p_forward(0, gatgpu.BF16, input=x)
+        e = oracle.errors(m16, gpu_ctx.stage(0, "out"))
+        assert e["finite"] and e["relative_l2"] < BF16_REL_L2, (opts, e)
+        for k in opts:
+            gpu_ctx.set_option(k, DEFAULT_OPTIONS[k])
+
+
+def test_fixed_p_rejects_bad_fixtures(gpu_ctx):
+    """load_fixture's checks (baseline/src/common.cpp:189-192) and call order."""
+    g = oracle.boundary_graph(33)
+    p = oracle.boundary_param(33, 4, 8)
+    r = oracle.ref_layer(g["row"], g["col"], g["x"], p, False, edge_stages=True)
+    gpu_ctx.set_graph(g["row"], g["col"])
+    gpu_ctx.set_layer(0, p)
+    with pytest.raises(gatgpu.GatGpuError) as err:
+        gpu_ctx.fixed_p_forward(0, gatgpu.FP32, input=g["x"])
+    assert err.value.code == gatgpu.ESTATE
+    bad = r["p"].copy()
+    bad[3, 1] = 1.5
+    with pytest.raises(gatgpu.GatGpuError) as err:
+        gpu_ctx.set_fixed_p(0, bad, r["den"])
+    assert err.value.code == gatgpu.EINVAL and "outside [0,1]" in str(err.value)
+    bad_den = r["den"].copy()
+    bad_den[np.diff(g["row"]).argmax(), 0] *= 1.01
+    with pytest.raises(gatgpu.GatGpuError) as err:
+        gpu_ctx.set_fixed_p(0, r["p"], bad_den)
+    assert err.value.code == gatgpu.EINVAL and "denominator" in str(err.value)
+    gpu_ctx.set_fixed_p(0, r["p"], r["den"])
+    with pytest.raises(gatgpu.GatGpuError) as err:
+        gpu_ctx.fixed_p_forward(0, gatgpu.BF16, gatgpu.AGGREGATE_FIRST, input=g["x"])
+    assert err.value.code == gatgpu.EINVAL
+    gpu_ctx.set_layer(0, p)  # drops the fixture
+    with pytest.raises(gatgpu.GatGpuError) as err:
+        gpu_ctx.fixed_p_forward(0, gatgpu.FP32, input=g["x"])
+    assert err.value.code == gatgpu.ESTATE
+
+
 # ---------------------------------------------------------------- error codes
 def test_error_codes(gpu_ctx):
     g = oracle.boundary_graph(17)

@@ -135,3 +135,30 @@ def test_export_fixture_roundtrip(smoke_file, tmp_path):
         "--reference-prefix", tmp_path / "r0", "--fixture", tmp_path / "l2.fix", check_rc=0)
     b = (tmp_path / "l2.fix").read_bytes()
     assert b[:7] == b"GATFIX1"
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("path", ["gpu_fp32", "gpu_bf16"])
+def test_fixed_p_mode(smoke_file, tmp_path, path):
+    """export-fixture then fixed-p (baseline/bench/main.cpp:103-150): the GPU
+    standard operator against the FP32 fixed-p master computed by the oracle."""
+    g = smoke1024()
+    model = oracle.random_model(128, 40, 11)
+    write_r0_dumps(tmp_path / "r0", g, model)
+    run("--mode", "export-fixture", "--graph", smoke_file, "--seed", 11, "--layer", 2,
+        "--reference-prefix", tmp_path / "r0", "--fixture", tmp_path / "l2.fix", check_rc=0)
+    x1 = np.fromfile(f"{tmp_path / 'r0'}_layer1_output.f32", np.float32).reshape(1024, -1)
+    P = np.fromfile(f"{tmp_path / 'r0'}_layer2_p.f32", np.float32).reshape(-1, 8)
+    den = np.fromfile(f"{tmp_path / 'r0'}_layer2_den.f32", np.float32).reshape(1024, 8)
+    master = oracle.fixed_p_layer(g["row"], g["col"], x1, model[1], P, den, False)["out"]
+    master.astype("<f4").tofile(tmp_path / "master.f32")
+    p = run("--mode", "fixed-p", "--graph", smoke_file, "--seed", 11, "--layer", 2, "--path", path,
+            "--fixture", tmp_path / "l2.fix", "--reference", tmp_path / "master.f32", "--repeats", 3,
+            "--warmups", 1, check_rc=0)
+    line = next(l for l in p.stdout.splitlines() if "stage=vs_master_fixed_p" in l)
+    fields = dict(kv.split("=") for kv in line.split()[1:])
+    if path == "gpu_fp32":
+        assert float(fields["max_abs"]) < 1e-4, line
+    else:
+        assert float(fields["relative_l2"]) < 1e-2, line
+    assert f"FIXED_P path={path} layer=2 median_ms=" in p.stdout

@@ -259,3 +259,48 @@ def test_vector_exp_and_expm1_against_numpy():
     ours = np.array([oracle.lib().or_expm1_neg(float(v)) for v in ys], np.float64)
     ref = np.expm1(ys.astype(np.float64))
     assert np.max(np.abs(ours - ref) / np.abs(ref)) < 3e-7
+
+
+# ---------------------------------------------------------------- fixed-p operator
+def test_fixed_p_hand_computed_case():
+    """Two heads of one feature with W = I, so Z = X: every output is a
+    weighted mean written out by hand (baseline_standard.cpp:52-97 with
+    fixed_p / fixed_den)."""
+    row = np.array([0, 2, 3, 3], np.uint64)
+    col = np.array([1, 2, 0], np.uint32)
+    x = np.array([[1, 2], [3, 4], [5, 6]], np.float32)
+    p = {"in": 2, "heads": 2, "dim": 1, "w": np.eye(2, dtype=np.float32),
+         "al": np.zeros(2, np.float32), "ar": np.zeros(2, np.float32)}
+    P = np.array([[0.5, 1.0], [1.0, 0.25], [1.0, 1.0]], np.float32)
+    den = np.array([[1.5, 1.25], [1.0, 1.0], [0.0, 0.0]], np.float32)
+    o = oracle.fixed_p_layer(row, col, x, p, P, den, False)
+    expected = np.array([[(0.5 * 3 + 1.0 * 5) / 1.5, (1.0 * 4 + 0.25 * 6) / 1.25], [1.0, 2.0], [0.0, 0.0]])
+    np.testing.assert_allclose(o["out"], expected, rtol=1e-6, atol=0)
+    np.testing.assert_array_equal(o["z"], x)
+
+
+@pytest.mark.parametrize("D,K,d", [(17, 8, 7), (128, 8, 32), (256, 1, 47), (33, 4, 40)])
+def test_fixed_p_with_r0_weights_reproduces_r0(D, K, d):
+    """Fed R0's own p and den, the fixed-p operator is R0's layer
+    (alpha = p / den, out = sum alpha Z): equal up to rounding."""
+    g = oracle.boundary_graph(D)
+    p = oracle.boundary_param(D, K, d)
+    r = oracle.ref_layer(g["row"], g["col"], g["x"], p, False, edge_stages=True)
+    o = oracle.fixed_p_layer(g["row"], g["col"], g["x"], p, r["p"], r["den"], False)
+    assert oracle.errors(r["z"], o["z"])["max_abs"] == 0
+    e = oracle.errors(r["out"], o["out"])
+    assert e["finite"] and e["max_abs"] < 1e-5 * max(1.0, float(np.abs(r["out"]).max()))
+
+
+def test_fixed_p_bf16_rounds_only_the_inputs():
+    """bf16 mode = the FP32 operator on RNE-rounded X and W (Z stays FP32,
+    cblas_gemm_bf16bf16f32): bit-identical outputs."""
+    g = smoke1024()
+    m = oracle.random_model(128, 40, 11)
+    r = oracle.ref_layer(g["row"], g["col"], g["x"], m[0], False, edge_stages=True)
+    o16 = oracle.fixed_p_layer(g["row"], g["col"], g["x"], m[0], r["p"], r["den"], True)
+    pq = dict(m[0], w=oracle.quantize_bf16(m[0]["w"]))
+    o32 = oracle.fixed_p_layer(g["row"], g["col"], oracle.quantize_bf16(g["x"]), pq, r["p"], r["den"], False)
+    assert np.array_equal(o16["out"], o32["out"])
+    assert not np.array_equal(o16["out"], oracle.fixed_p_layer(g["row"], g["col"], g["x"], m[0], r["p"],
+                                                                r["den"], False)["out"])
