@@ -240,7 +240,12 @@ int run(int argc, char** argv) {
             std::vector<float> ref_out = read_dump(lp + "_output.f32", nw);
             check(l + 1, "layer", ref_out, w.out, true);
             print_times(path, "correctness", l + 1, 0, g, p, t);
-            if (a.has("--dump-prefix")) write_dump(a.get("--dump-prefix") + "_layer" + std::to_string(l + 1) + "_output.f32", w.out);
+            if (a.has("--dump-prefix")) {  // the path's stages in the reference's dump naming (main.cpp:74-77)
+                const std::string dp = a.get("--dump-prefix") + "_layer" + std::to_string(l + 1) + "_";
+                for (auto item : {std::make_pair("output", &w.out), {"z", &w.z}, {"left", &w.left}, {"right", &w.right},
+                                  {"max", &w.max}, {"den", &w.den}})
+                    if (!item.second->empty()) write_dump(dp + item.first + ".f32", *item.second);
+            }
             input = std::move(ref_out);
         }
         // The path's own three-layer chain against R0's (main.cpp:91-98).

@@ -1,0 +1,190 @@
+"""GATBIN1 / GATWGT1 / GATFIX1 readers and writers of the package
+(baseline/src/common.cpp:23-79, 171-194) and the node-classification
+evaluator (baseline/scripts/evaluate_task.py)."""
+import subprocess
+import sys
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+import oracle
+from gatgpu import evaluate, formats
+from make_smoke1024 import SMOKE1024_SHA256, smoke1024, smoke1024_bytes
+
+ROOT = Path(__file__).resolve().parent.parent
+BENCH = ROOT / "gat-tfs_amd" / "lib" / "gat_bench"
+
+
+# ---------------------------------------------------------------- GATBIN1
+def test_graph_reader_on_reference_fixture_and_writer_bytes(tmp_path):
+    f = tmp_path / "smoke1024.gatbin"
+    f.write_bytes(smoke1024_bytes())  # SHA-pinned to implementation/data/smoke1024.gatbin
+    g = formats.load_graph(f)
+    assert (g["n"], g["e"], g["din"], g["classes"]) == (1024, 41540, 128, 40)
+    formats.save_graph(tmp_path / "again.gatbin", g["row"], g["col"], g["x"], g["classes"])
+    assert (tmp_path / "again.gatbin").read_bytes() == smoke1024_bytes()
+    import hashlib
+    assert hashlib.sha256((tmp_path / "again.gatbin").read_bytes()).hexdigest() == SMOKE1024_SHA256
+
+
+@pytest.mark.parametrize("defect,msg", [("magic", "bad graph magic"), ("monotone", "nonmonotone CSR"),
+                                        ("col", "source index out of bounds"), ("x", "nonfinite graph input"),
+                                        ("truncated", "truncated file"), ("bounds", "bad CSR bounds")])
+def test_graph_reader_rejects(tmp_path, defect, msg):
+    g = smoke1024()
+    row, col, x = g["row"].copy(), g["col"].copy(), g["x"].copy()
+    if defect == "monotone":
+        row[5], row[6] = row[6], row[5]
+    elif defect == "col":
+        col[7] = 1024
+    elif defect == "x":
+        x[3, 4] = np.nan
+    elif defect == "bounds":
+        row[0] = 1
+    f = tmp_path / "g.gatbin"
+    oracle.save_graph(f, row, col, x, 40)  # the oracle's writer does not validate
+    b = f.read_bytes()
+    if defect == "magic":
+        b = b"GATBIX1\0" + b[8:]
+    elif defect == "truncated":
+        b = b[:-10]
+    f.write_bytes(b)
+    with pytest.raises(ValueError, match=msg):
+        formats.load_graph(f)
+
+
+# ---------------------------------------------------------------- GATWGT1
+def test_weights_bytes_match_oracle_writer_and_shape_checks(tmp_path):
+    m = oracle.random_model(128, 40, 11)
+    formats.save_model(tmp_path / "a.bin", m)
+    oracle.save_model(tmp_path / "b.bin", m)
+    assert (tmp_path / "a.bin").read_bytes() == (tmp_path / "b.bin").read_bytes()
+    back = formats.load_model(tmp_path / "a.bin", 128, 40)
+    for p, q in zip(m, back):
+        assert (p["in"], p["heads"], p["dim"]) == (q["in"], q["heads"], q["dim"])
+        for k in ("w", "al", "ar"):
+            assert np.array_equal(np.asarray(p[k]).reshape(-1), q[k].reshape(-1))
+    with pytest.raises(ValueError, match="checkpoint model shape mismatch"):
+        formats.load_model(tmp_path / "a.bin", 100, 40)
+    formats.save_model(tmp_path / "two.bin", m[:2])
+    with pytest.raises(ValueError, match="model must have 3 layers"):
+        formats.load_model(tmp_path / "two.bin", 128, 40)
+    bad = [dict(m[0], heads=9, w=np.zeros((128, 9 * 32), np.float32), al=np.zeros(288, np.float32),
+                ar=np.zeros(288, np.float32))]
+    with pytest.raises(ValueError, match="heads <=8"):
+        formats.save_model(tmp_path / "bad.bin", bad)
+
+
+# ---------------------------------------------------------------- GATFIX1
+def r0_fixture(layer=2):
+    g = smoke1024()
+    m = oracle.random_model(128, 40, 11)
+    x = g["x"]
+    for l in range(layer - 1):
+        x = oracle.ref_layer(g["row"], g["col"], x, m[l], True)["out"]
+    r = oracle.ref_layer(g["row"], g["col"], x, m[layer - 1], False, edge_stages=True)
+    return g, m[layer - 1], x, r["p"], r["den"]
+
+
+def test_fixture_bytes_match_harness_export(tmp_path):
+    """The harness's export-fixture (C++, no GPU) and formats.save_fixture write
+    the same GATFIX1 bytes; load_fixture reads them back."""
+    g, p, x, P, den = r0_fixture()
+    (tmp_path / "s.gatbin").write_bytes(smoke1024_bytes())
+    pre = tmp_path / "r0"
+    x.astype("<f4").tofile(f"{pre}_layer1_output.f32")
+    P.astype("<f4").tofile(f"{pre}_layer2_p.f32")
+    den.astype("<f4").tofile(f"{pre}_layer2_den.f32")
+    rc = subprocess.run([str(BENCH), "--mode", "export-fixture", "--graph", str(tmp_path / "s.gatbin"), "--seed",
+                         "11", "--layer", "2", "--reference-prefix", str(pre), "--fixture", str(tmp_path / "c.fix")],
+                        capture_output=True, text=True, timeout=120)
+    assert rc.returncode == 0, rc.stderr
+    formats.save_fixture(tmp_path / "py.fix", g["row"], g["col"], p, x, P, den)
+    assert (tmp_path / "py.fix").read_bytes() == (tmp_path / "c.fix").read_bytes()
+    q = formats.load_fixture(tmp_path / "c.fix", g["row"], g["col"], p)
+    assert np.array_equal(q["p"], P) and np.array_equal(q["den"], den) and np.array_equal(q["input"], x)
+
+
+@pytest.mark.parametrize("defect,msg", [("p", r"outside \[0,1\]"), ("den", "denominator mismatch"),
+                                        ("csr", "fixture CSR mismatch"), ("w", "fixture checkpoint mismatch")])
+def test_fixture_reader_rejects(tmp_path, defect, msg):
+    g, p, x, P, den = r0_fixture()
+    row, col = g["row"], g["col"]
+    if defect == "p":
+        P = P.copy()
+        P[10, 2] = 1.25
+    elif defect == "den":
+        den = den.copy()
+        den[3, 1] *= 1.001
+    formats.save_fixture(tmp_path / "f.fix", row, col, p, x, P, den)
+    if defect == "csr":
+        col = col.copy()
+        col[0] = (col[0] + 1) % 1024
+    elif defect == "w":
+        p = dict(p, w=np.asarray(p["w"]) * 2)
+    with pytest.raises(ValueError, match=msg):
+        formats.load_fixture(tmp_path / "f.fix", row, col, p)
+
+
+# ---------------------------------------------------------------- evaluator
+def write_case(tmp_path, nodes=50, classes=4, correct=(0, 1, 2, 3, 4, 5, 6)):
+    rng = np.random.default_rng(1)
+    labels = rng.integers(0, classes, nodes)
+    split = np.arange(10, 20)
+    logits = rng.standard_normal((nodes, classes)).astype(np.float32)
+    for k, i in enumerate(split):  # make the prediction right exactly for split[correct]
+        logits[i] = 0
+        logits[i, labels[i] if k in correct else (labels[i] + 1) % classes] = 1
+    logits.astype("<f4").tofile(tmp_path / "out.f32")
+    np.save(tmp_path / "labels.npy", labels)
+    np.savetxt(tmp_path / "split.csv", split, delimiter=",", fmt="%d")
+    return labels, split, logits
+
+
+def test_evaluator_accuracy_and_gate(tmp_path):
+    labels, split, logits = write_case(tmp_path)
+    r, passed = evaluate.evaluate(str(tmp_path / "out.f32"), 50, 4, str(tmp_path / "labels.npy"),
+                                  str(tmp_path / "split.csv"))
+    assert r == {"accuracy": 0.7, "split_nodes": 10, "gate": "UNCONFIGURED"} and passed is None
+    ref = logits.copy()
+    for i in split:
+        ref[i] = 0
+        ref[i, labels[i]] = 1
+    ref.astype("<f4").tofile(tmp_path / "ref.f32")
+    r, passed = evaluate.evaluate(str(tmp_path / "out.f32"), 50, 4, labels, split, str(tmp_path / "ref.f32"), 0.35)
+    assert passed and r["gate"] == "PASS" and r["reference_accuracy"] == 1.0
+    assert abs(r["accuracy_drop"] - 0.3) < 1e-12 and abs(r["prediction_agreement"] - 0.7) < 1e-12
+    r, passed = evaluate.evaluate(str(tmp_path / "out.f32"), 50, 4, labels, split, str(tmp_path / "ref.f32"), 0.25)
+    assert passed is False and r["gate"] == "FAIL"
+    cli = [sys.executable, "-m", "gatgpu.evaluate", "--output", str(tmp_path / "out.f32"), "--nodes", "50",
+           "--classes", "4", "--labels", str(tmp_path / "labels.npy"), "--split", str(tmp_path / "split.csv"),
+           "--reference", str(tmp_path / "ref.f32"), "--max-accuracy-drop", "0.25"]
+    p = subprocess.run(cli, capture_output=True, text=True, timeout=120,
+                       env={"PYTHONPATH": str(ROOT / "gat-tfs_amd"), "PATH": "/usr/bin:/bin"})
+    assert p.returncode == 1 and '"gate": "FAIL"' in p.stdout
+
+
+@pytest.mark.parametrize("defect,msg", [("dup", "duplicate split"), ("label", "split labels out of bounds"),
+                                        ("nan", "nonfinite logits"), ("frac", "must be integers"),
+                                        ("size", "label/split sizes"), ("gate", "needs reference")])
+def test_evaluator_rejects(tmp_path, defect, msg):
+    labels, split, logits = write_case(tmp_path)
+    kw = {}
+    if defect == "dup":
+        split = np.concatenate([split, split[:1]])
+    elif defect == "label":
+        labels = labels.copy()
+        labels[split[0]] = 7
+    elif defect == "nan":
+        logits[0, 0] = np.nan
+        logits.astype("<f4").tofile(tmp_path / "out.f32")
+    elif defect == "frac":
+        labels = labels.astype(np.float64)
+        labels[split[1]] += 0.5
+    elif defect == "size":
+        labels = labels[:-1]
+    elif defect == "gate":
+        kw = {"max_accuracy_drop": 0.1}
+    with pytest.raises(ValueError, match=msg):
+        evaluate.evaluate(str(tmp_path / "out.f32"), 50, 4, labels, split, **kw)
