@@ -89,6 +89,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--workload", default="large")
     ap.add_argument("--precision", default="bf16", choices=["bf16", "fp32"])
+    ap.add_argument("--dataflow", default="auto", choices=["auto", "transform_first", "aggregate_first"],
+                    help="per-layer dataflow; aggregate_first applies where the layer supports it")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-threads", type=int, default=int(os.environ.get("OMP_NUM_THREADS", "0") or 0))
     ap.add_argument("--calibrate-copy", action="store_true",
@@ -110,6 +112,8 @@ def main():
     gen_s = time.perf_counter() - t0
     n, e = w.n, int(row[-1])
     prec = gatgpu.BF16 if args.precision == "bf16" else gatgpu.FP32
+    flow = {"auto": gatgpu.AUTO, "transform_first": gatgpu.TRANSFORM_FIRST,
+            "aggregate_first": gatgpu.AGGREGATE_FIRST}[args.dataflow]
 
     ctx = gatgpu.Context(0)
     ctx.set_graph(row, col)
@@ -124,13 +128,13 @@ def main():
         torch.cuda.synchronize()
         del src, dst
     for _ in range(args.warmup):
-        ctx.model_forward(prec, gatgpu.AUTO, want_logits=False, timed=False)
+        ctx.model_forward(prec, flow, want_logits=False, timed=False)
     torch.cuda.synchronize()
     ctx.synchronize()
     step_ms, layer_times = [], []
     t0 = time.perf_counter()
     for _ in range(args.steps):
-        _, times, total = ctx.model_forward(prec, gatgpu.AUTO, want_logits=False, timed=True)
+        _, times, total = ctx.model_forward(prec, flow, want_logits=False, timed=True)
         step_ms.append(total)
         layer_times.append(times)
     ctx.synchronize()

@@ -1,31 +1,44 @@
-// Aggregate-first (TFS) GAT layer on bf16: gather the layer INPUT rows,
-// project afterwards.
+// Aggregate-first GAT layer on bf16: gather the layer's INPUT rows and
+// project each gathered row on the MFMA units, instead of gathering the
+// projected Z rows.
 //
-// Reference: tfs_online_fused (implementation/src/gat_tfs_online.cpp:200-283):
-// per head U^h_i = sum_j p^h_ij X_j, then U^h_i W^h, / l^h_i, ELU.  The
-// attention logits come from the reordered contraction L/R = X (W a)
-// (prepare_attention, :48-73).  The reference uses an online max with
-// rescaling; here the max is exact (the same M as the transform-first path),
-// so U needs no rescale, and the projection of U is done once per row.
+// Reference: tfs_online_fused (implementation/src/gat_tfs_online.cpp:200-283)
+// and the neighbour-step TFS of baseline/src/baseline_tfs.cpp:16-110: per
+// destination tile, step s takes the s-th neighbour of every row and
+// multiplies the gathered input rows by W_h with the output sums resident
+// (tile registers there, VGPRs here).  The attention logits come from the
+// reordered contraction L/R = X (W a) (prepare_attention, :48-73).
 //
-// Why: the gathered row is the input (D_in <= 128 bf16 = 256 bytes, two cache
-// lines) instead of Z (8 heads x 32 bf16 = 512 bytes); layer 1 of a
-// D_in=100/128 model moves half the bytes.
+//   out[i, h] = ELU?( sum_j p_ijh (X_j W_h) / den_ih ),
+//   p_ijh = exp(LeakyReLU(L_ih + R_jh) - M_ih),  M the row max
+//   (kept as a running max with rescaling; the final M is exact).
 //
-// Work split (tile kernel, 8 waves, one 32-row tile of degree-sorted rows at a
-// time, persistent over tiles):
-//   phase A  each wave runs 4 row groups of 16 lanes; a group owns one row and
-//            lane c of the group owns input features 8c..8c+7 for all K heads
-//            (64 FP32 accumulators).  Per batch of 16 edges the group scores
-//            (edge, head) pairs -- one exp each -- and gathers the 16 source
-//            rows with one 16-byte load per lane.  U is then split into bf16
-//            hi + lo and written to LDS in MFMA B-operand order.
-//   phase B  wave h multiplies U^h (32 rows x 128) by W^h on
-//            v_mfma_f32_32x32x16_bf16 (hi and lo products accumulated in
-//            FP32, ~16 mantissa bits of U), scales by 1/den, ELU, stores.
-// Rows at or above the split threshold go to k_af_split: one wave per chunk,
-// partial (U, den) to scratch, the last chunk to arrive adds the partials in
-// chunk order and projects the row on the VALU from the bf16 W.
+// X_j W_h is formed in FP32 by the MFMA from the bf16 row and the bf16 W,
+// i.e. the FP32 Z row of standard_bf16 (baseline_standard.cpp:3-6), and p is
+// applied to it in FP32.  Summed over j this equals (sum_j p X_j) W up to
+// rounding order, which is the aggregate-first identity.
+//
+// Why: the gathered row is the input (D_in <= 128 bf16, 256 bytes) instead of
+// Z (8 heads x 32 bf16 = 512 bytes), so layer 1 of a D_in = 100/128 model
+// moves about half the bytes; the per-edge projection costs 2 D W MACs per
+// edge, which the MFMA units absorb (about 1.5 ms of MFMA time for 64M edges
+// at 100 -> 256).
+//
+// Wave layout (v_mfma_f32_32x32x16_bf16, computed transposed as in
+// projection_mfma.hip): A = 32 output features x 16 k of W^T from LDS,
+// B = 16 k x 32 slots of X^T -- lane (half, slot) loads 8 consecutive input
+// features of its slot's current neighbour with one 16-byte load -- and
+// D = 32 features x 32 slots, so all 16 accumulators of a lane belong to one
+// slot and one head: p is one scalar per (lane, head).  A wave owns 32 slots
+// and up to 4 output blocks of 32 features (4 heads of 32); the other heads
+// of the same slots go to the next wave of the workgroup, which gathers the
+// same rows through the same L2.
+//
+// Slots: 32 consecutive degree-sorted rows (heaviest first), so the slots of
+// a wave have about the same number of steps; or 32 chunks of split rows,
+// whose partial sums a merge kernel adds in chunk order.  Whole rows keep an
+// online softmax per (slot, head); chunks start from their row's exact max
+// (per-chunk maxima of k_split_prescan), so their partials need no rescale.
 #include "internal.hpp"
 
 namespace gatgpu {
@@ -34,296 +47,310 @@ namespace {
 typedef __bf16 bf16x8 __attribute__((__vector_size__(8 * sizeof(__bf16))));
 typedef float f32x16 __attribute__((__vector_size__(16 * sizeof(float))));
 
-constexpr int kThreads = 512;
+constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / kWave;
-constexpr int kTile = 32;        // rows per tile
-constexpr int kXS = 128;         // input row stride (bf16), zero-padded
-constexpr int kGL = 16;          // lanes per row group = 16-byte vectors per input row
-constexpr int kGPW = kWave / kGL;  // row groups per wave
-constexpr int kBE = 16;          // edges per scoring batch
-constexpr int kUS = kXS / 8 + 1; // LDS row stride of U in 16-byte units (one pad unit: no bank conflicts)
+constexpr int kXS = 128;      // input row stride (bf16 elements), zero-padded
+constexpr int kSlots = 32;    // destination slots per wave (MFMA N)
+constexpr int kMB = 4;        // output blocks of 32 features per wave
+constexpr int kPart = 8 * 128 + 8;  // floats per chunk in the split scratch
+constexpr int kDenOff = 8 * 128;    // offset of the chunk's denominators
 
-__device__ inline void unpack8(const uint4& v, float (&f)[8]) {
-    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-        f[2 * q] = __builtin_bit_cast(float, w[q] << 16);
-        f[2 * q + 1] = __builtin_bit_cast(float, w[q] & 0xffff0000u);
+struct Items {
+    uint64_t chunk_groups;  // ceil(chunks / 32)
+    uint64_t tile_groups;   // ceil(rows / 32)
+    int waves_per_item;     // ceil(blocks / kMB)
+    int blocks;             // output blocks of 32 features (= heads at dim 32)
+};
+
+// Persistent workgroups: W^T fragments of every block in LDS once, then wave
+// items (slot group, head group) heaviest first.
+template <int KS>
+__global__ void __launch_bounds__(kThreads, 2) k_af_ns(AfArgs a, Items it) {
+    extern __shared__ uint4 wlds[];  // [block][ks][lane]
+    const int nb_all = it.blocks;
+    for (int q = threadIdx.x; q < nb_all * KS * kWave; q += kThreads) {
+        const int lane = q % kWave, ks = (q / kWave) % KS, mb = q / (kWave * KS);
+        wlds[q] = a.wpk[(size_t(ks) * a.nmb + mb) * kWave + lane];
     }
-}
-
-// Accumulates edges [beg, end) of one row into the group's U registers.
-// Lane c (= lane % 16) of the group owns features 8c..8c+7 of every head.
-// Max is exact: given (Mh of the scorer head) or, when the row fits one
-// batch, found from the scored R values.
-__device__ inline void group_rows(uint64_t beg, uint64_t end, bool find_max, const uint32_t* __restrict__ pcol,
-                                  const float* __restrict__ R, const uint16_t* __restrict__ X, int K, float Lh,
-                                  float& Mh, float* pb, uint32_t* jb, float (&acc)[8][8], float& dloc) {
-    const int c = threadIdx.x % kGL;
-    const int hs = c % 8;  // scorer head; pairs (t = c/8 + 2s, hs), s < 8
-    for (uint64_t base = beg; base < end; base += kBE) {
-        const uint64_t rem = end - base;
-        const int cnt = rem < uint64_t(kBE) ? int(rem) : kBE;
-        uint32_t jv[8];
-        float rv[8];
-#pragma unroll
-        for (int s = 0; s < 8; ++s) {
-            const int t = c / 8 + 2 * s;
-            const bool ok = t < cnt && hs < K;
-            jv[s] = t < cnt ? pcol[base + t] : 0u;
-            rv[s] = ok ? R[uint64_t(jv[s]) * K + hs] : -INFINITY;
-        }
-        if (find_max) {  // the whole row is this batch
-            float m = rv[0];
-#pragma unroll
-            for (int s = 1; s < 8; ++s) m = fmaxf(m, rv[s]);
-            m = fmaxf(m, __shfl_xor(m, 8));
-            Mh = cnt > 0 ? leaky(Lh + m) : 0.0f;
-        }
-#pragma unroll
-        for (int s = 0; s < 8; ++s) {
-            const int t = c / 8 + 2 * s;
-            const float p = (t < cnt && hs < K) ? expf(leaky(Lh + rv[s]) - Mh) : 0.0f;
-            dloc += p;
-            pb[t * 8 + hs] = p;
-            if (hs == 0) jb[t] = jv[s];
-        }
-        wave_sync();
-        uint4 raw[kBE];
-#pragma unroll
-        for (int t = 0; t < kBE; ++t)
-            raw[t] = t < cnt ? *reinterpret_cast<const uint4*>(X + uint64_t(jb[t]) * kXS + c * 8) : make_uint4(0, 0, 0, 0);
-#pragma unroll
-        for (int t = 0; t < kBE; ++t) {
-            const float4 p0 = *reinterpret_cast<const float4*>(pb + t * 8);
-            const float4 p1 = *reinterpret_cast<const float4*>(pb + t * 8 + 4);
-            const float p[8] = {p0.x, p0.y, p0.z, p0.w, p1.x, p1.y, p1.z, p1.w};
-            float f[8];
-            unpack8(raw[t], f);
-#pragma unroll
-            for (int h = 0; h < 8; ++h)
-#pragma unroll
-                for (int x = 0; x < 8; ++x) acc[h][x] += p[h] * f[x];
-        }
-        wave_sync();
-    }
-}
-
-// Exact max of R over [beg, end) for the scorer head, reduced within the group.
-__device__ inline float group_max(uint64_t beg, uint64_t end, const uint32_t* __restrict__ pcol,
-                                  const float* __restrict__ R, int K) {
-    const int c = threadIdx.x % kGL, hs = c % 8;
-    float m = -INFINITY;
-    if (hs < K)
-        for (uint64_t e = beg + c / 8; e < end; e += 2) m = fmaxf(m, R[uint64_t(pcol[e]) * K + hs]);
-    return fmaxf(m, __shfl_xor(m, 8));
-}
-
-__global__ void __launch_bounds__(kThreads) k_af_tiles(AfArgs a) {
-    __shared__ uint4 ut[2][8][kTile][kUS];          // U hi / lo, [head][row][k/8]
-    __shared__ float pbuf[kWaves][kGPW][kBE * 8];    // scores [edge][head]
-    __shared__ uint32_t jbuf[kWaves][kGPW][kBE];     // source ids
-    __shared__ float dsh[kTile][8];                  // denominators
-    const int w = threadIdx.x / kWave, lane = threadIdx.x % kWave;
-    const int g = lane / kGL, c = lane % kGL, hs = c % 8;
-    const int rs = w * kGPW + g;  // row slot of this group within the tile
+    __syncthreads();
+    const int w = __builtin_amdgcn_readfirstlane(int(threadIdx.x) / kWave);
+    const int l = threadIdx.x % kWave, half = l / 32, s = l % 32;
     const int K = a.heads;
-    for (uint64_t tile = blockIdx.x; tile < a.tiles; tile += gridDim.x) {
-        // ---------------- phase A: aggregate 32 rows (one per group)
-        const uint64_t idx = tile * kTile + rs;
-        float acc[8][8];
-#pragma unroll
-        for (int h = 0; h < 8; ++h)
-#pragma unroll
-            for (int x = 0; x < 8; ++x) acc[h][x] = 0.0f;
-        float dloc = 0.0f;
-        bool have = idx < a.rows;
-        uint32_t i = 0;
-        uint64_t beg = 0, end = 0;
-        if (have) {
-            const uint64_t k = a.rows - 1 - idx;  // heaviest first
-            i = a.perm[k];
-            beg = a.prow[k];
-            end = a.prow[k + 1];
-            if (i >= a.n || beg > end || end > a.e) have = false;
-        }
-        // Every group runs the batch loop (an empty range for a missing or
-        // shorter row): the wave-level LDS syncs inside stay uniform.
-        const float Lh = have && hs < K ? a.L[uint64_t(i) * K + hs] : 0.0f;
-        const uint64_t deg = have ? end - beg : 0;
-        uint64_t wmax = deg;  // longest row of the wave
-        for (int off = kGL; off < kWave; off <<= 1) {
-            const uint64_t o = __shfl_xor(wmax, off);
-            wmax = o > wmax ? o : wmax;
-        }
-        const bool single = wmax <= uint64_t(kBE);  // every row of the wave fits one batch
-        float Mh = 0.0f;                             // empty row: max 0 (ref_fp32.cpp:11)
-        if (!single && deg) Mh = leaky(Lh + group_max(beg, end, a.pcol, a.R, K));
-        const uint64_t span = (wmax + kBE - 1) / kBE * kBE;
-        for (uint64_t base = 0; base < span; base += kBE) {
-            const uint64_t b0 = beg + base < end ? beg + base : end;
-            const uint64_t b1 = beg + base + kBE < end ? beg + base + kBE : end;
-            group_rows(b0, b1, single, a.pcol, a.R, a.X, K, Lh, Mh, pbuf[w][g], jbuf[w][g], acc, dloc);
-        }
-        dloc += __shfl_xor(dloc, 8);
-        if (c < 8) dsh[rs][c] = (have && c < K) ? dloc : 0.0f;
-        if (have && c < K) {
-            a.mx[uint64_t(i) * K + c] = Mh;
-            a.den[uint64_t(i) * K + c] = dloc;
-        }
-#pragma unroll
-        for (int h = 0; h < 8; ++h) {
-            uint32_t hi[4], lo[4];
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                const float v0 = acc[h][2 * q], v1 = acc[h][2 * q + 1];
-                const uint16_t h0 = bf16_rne(v0), h1 = bf16_rne(v1);
-                hi[q] = uint32_t(h0) | (uint32_t(h1) << 16);
-                lo[q] = uint32_t(bf16_rne(v0 - bf16_widen(h0))) | (uint32_t(bf16_rne(v1 - bf16_widen(h1))) << 16);
+    const uint64_t total = (it.chunk_groups + it.tile_groups) * uint64_t(it.waves_per_item);
+    for (uint64_t gw = uint64_t(blockIdx.x) * kWaves + w; gw < total; gw += uint64_t(gridDim.x) * kWaves) {
+        const uint64_t item = gw / it.waves_per_item;
+        const int hg = int(gw % it.waves_per_item);
+        const int mb0 = hg * kMB;
+        const int nb = nb_all - mb0 < kMB ? nb_all - mb0 : kMB;
+        // ---- this lane's slot
+        const bool chunk_item = item < it.chunk_groups;
+        bool valid = false;
+        uint64_t beg = 0, end = 0, c = 0;
+        uint32_t i = 0, first = 0, nch = 0;
+        if (chunk_item) {
+            c = item * kSlots + s;
+            if (c < a.chunks) {
+                const uint32_t k = a.chunk_k[c];
+                first = a.chunk_first[c];
+                const uint64_t rbeg = a.prow[k], rend = a.prow[k + 1];
+                i = a.perm[k];
+                nch = uint32_t((rend - rbeg + a.chunk_edges - 1) / a.chunk_edges);
+                beg = rbeg + (c - first) * a.chunk_edges;
+                end = beg + a.chunk_edges < rend ? beg + a.chunk_edges : rend;
+                valid = i < a.n && rbeg <= rend && rend <= a.e && beg <= end;
             }
-            ut[0][h][rs][c] = make_uint4(hi[0], hi[1], hi[2], hi[3]);
-            ut[1][h][rs][c] = make_uint4(lo[0], lo[1], lo[2], lo[3]);
-        }
-        __syncthreads();
-        // ---------------- phase B: wave h projects head h of the 32 rows
-        if (w < K) {
-            const int h = w, half = lane / 32, col = lane % 32;
-            f32x16 o;
-#pragma unroll
-            for (int r = 0; r < 16; ++r) o[r] = 0.0f;
-            for (int ks = 0; ks < a.ksteps; ++ks) {
-                const bf16x8 av = __builtin_bit_cast(bf16x8, a.wpk[(size_t(ks) * a.nmb + h) * kWave + lane]);
-                const bf16x8 bh = __builtin_bit_cast(bf16x8, ut[0][h][col][2 * ks + half]);
-                const bf16x8 bl = __builtin_bit_cast(bf16x8, ut[1][h][col][2 * ks + half]);
-                o = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, bh, o, 0, 0, 0);
-                o = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, bl, o, 0, 0, 0);
+        } else {
+            const uint64_t t = (item - it.chunk_groups) * kSlots + s;
+            if (t < a.rows) {
+                const uint64_t k = a.rows - 1 - t;
+                i = a.perm[k];
+                beg = a.prow[k];
+                end = a.prow[k + 1];
+                valid = i < a.n && beg <= end && end <= a.e;
             }
-            const uint64_t ridx = tile * kTile + col;
-            if (ridx < a.rows) {
-                const uint32_t ri = a.perm[a.rows - 1 - ridx];
-                const float d = dsh[col][h];
-                const float scale = d > 0.0f ? 1.0f / d : 0.0f;
-                const int W = K * 32;
+        }
+        const uint64_t len = valid ? end - beg : 0;
+        uint64_t steps = len;
+        for (int off = 1; off < kWave; off <<= 1) {
+            const uint64_t o = __shfl_xor(steps, off);
+            steps = o > steps ? o : steps;
+        }
+        // ---- per head of this wave: L and the running softmax state.  A chunk
+        // starts from the exact row max of its split row (per-chunk maxima of
+        // k_split_prescan), so its m never moves and the partials add up
+        // directly; a whole row keeps the running-maximum form of
+        // tfs_online_fused (gat_tfs_online.cpp:86-117), rescaling its sums by
+        // exp(m_old - m_new) when a step raises m.  The final m is max
+        // leaky(L + R_j) = leaky(L + max R_j) bit for bit.
+        float L[kMB], m[kMB], den[kMB];
 #pragma unroll
-                for (int gq = 0; gq < 4; ++gq) {
-                    const int f0 = h * 32 + 8 * gq + 4 * half;
-                    float v[4];
+        for (int q = 0; q < kMB; ++q) {
+            L[q] = (valid && q < nb) ? a.L[uint64_t(i) * K + mb0 + q] : 0.0f;
+            den[q] = 0.0f;
+            m[q] = -INFINITY;
+        }
+        if (chunk_item) {
 #pragma unroll
-                    for (int q = 0; q < 4; ++q) {
-                        const float y = o[4 * gq + q] * scale;
-                        v[q] = a.hidden ? elu(y) : y;
+            for (int q = 0; q < kMB; ++q) {
+                float mc = -INFINITY;
+                if (valid && q < nb)
+                    for (uint32_t cq = 0; cq < nch; ++cq) mc = fmaxf(mc, a.mchunk[(first + cq) * 8 + mb0 + q]);
+                if (valid) m[q] = leaky(L[q] + mc);
+            }
+        }
+        // ---- neighbour steps: gather, project, weight, accumulate.
+        f32x16 acc[kMB];
+#pragma unroll
+        for (int q = 0; q < kMB; ++q)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[q][r] = 0.0f;
+        // Steps past a slot's last edge re-read that edge's row (weight 0), so
+        // every load is unconditional and no absent row is ever multiplied.
+        auto src = [&](uint64_t t) -> uint64_t { return a.pcol[len ? beg + (t < len ? t : len - 1) : 0]; };
+        auto fetch = [&](uint64_t j, uint4 (&xf)[KS], float (&rv)[kMB]) {
+            const uint16_t* xr = a.X + j * kXS + 8 * half;
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks) xf[ks] = *reinterpret_cast<const uint4*>(xr + 16 * ks);
+#pragma unroll
+            for (int q = 0; q < kMB; ++q) rv[q] = a.R[j * K + mb0 + (q < nb ? q : 0)];
+        };
+        auto frag = [&](int q, int ks) {
+            return __builtin_bit_cast(bf16x8, wlds[(size_t(mb0 + q) * KS + ks) * kWave + l]);
+        };
+        auto step = [&](uint64_t t, const uint4 (&x)[KS], const float (&rv)[kMB]) {
+            const bool ok = t < len;
+            float p[kMB], scale[kMB];
+#pragma unroll
+            for (int q = 0; q < kMB; ++q) {
+                const float sc_ = leaky(L[q] + rv[q]);
+                const float mn = ok ? fmaxf(m[q], sc_) : m[q];
+                scale[q] = mn > m[q] ? __expf(m[q] - mn) : 1.0f;  // exp(-inf) = 0 on the first edge
+                p[q] = ok ? __expf(sc_ - mn) : 0.0f;
+                m[q] = mn;
+                den[q] = den[q] * scale[q] + p[q];
+            }
+            // Two heads at a time: two independent MFMA chains, and the next
+            // k-step's W fragments read from LDS while this one multiplies.
+#pragma unroll
+            for (int q0 = 0; q0 < kMB; q0 += 2) {
+                if (q0 >= nb) continue;
+                const bool two = q0 + 1 < nb;
+                f32x16 T0, T1;
+#pragma unroll
+                for (int r = 0; r < 16; ++r) T0[r] = T1[r] = 0.0f;
+                bf16x8 a0 = frag(q0, 0), a1 = frag(two ? q0 + 1 : q0, 0);
+#pragma unroll
+                for (int ks = 0; ks < KS; ++ks) {
+                    bf16x8 n0 = a0, n1 = a1;
+                    if (ks + 1 < KS) {
+                        n0 = frag(q0, ks + 1);
+                        n1 = frag(two ? q0 + 1 : q0, ks + 1);
                     }
-                    const uint64_t off = uint64_t(ri) * W + f0;
-                    if (a.outbf)
-                        *reinterpret_cast<uint2*>(a.outbf + off) =
-                            make_uint2(uint32_t(bf16_rne(v[0])) | (uint32_t(bf16_rne(v[1])) << 16),
-                                       uint32_t(bf16_rne(v[2])) | (uint32_t(bf16_rne(v[3])) << 16));
-                    if (a.out32) *reinterpret_cast<float4*>(a.out32 + off) = make_float4(v[0], v[1], v[2], v[3]);
+                    const bf16x8 b = __builtin_bit_cast(bf16x8, x[ks]);
+                    T0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, b, T0, 0, 0, 0);
+                    if (two) T1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1, b, T1, 0, 0, 0);
+                    a0 = n0;
+                    a1 = n1;
+                }
+                // Rescale only when some slot of the wave raised its max.
+                if (__any(scale[q0] != 1.0f))
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) acc[q0][r] *= scale[q0];
+#pragma unroll
+                for (int r = 0; r < 16; ++r) acc[q0][r] += p[q0] * T0[r];
+                if (two) {
+                    if (__any(scale[q0 + 1] != 1.0f))
+#pragma unroll
+                        for (int r = 0; r < 16; ++r) acc[q0 + 1][r] *= scale[q0 + 1];
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) acc[q0 + 1][r] += p[q0 + 1] * T1[r];
                 }
             }
+        };
+        // Ping-pong: the rows of step t + 1 are requested before step t's
+        // MFMAs, and the source id of a step two steps before its rows, so a
+        // step waits on one memory round trip that overlaps the previous step.
+        uint4 xa[KS], xb[KS];
+        float ra[kMB], rb[kMB];
+        fetch(src(0), xa, ra);
+        uint64_t jb = src(1), ja = src(2);
+        for (uint64_t t = 0; t < steps; t += 2) {
+            fetch(jb, xb, rb);
+            jb = src(t + 3);
+            step(t, xa, ra);
+            if (t + 1 >= steps) break;
+            fetch(ja, xa, ra);
+            ja = src(t + 4);
+            step(t + 1, xb, rb);
         }
-        __syncthreads();
+        float M[kMB];
+#pragma unroll
+        for (int q = 0; q < kMB; ++q) M[q] = len ? m[q] : 0.0f;  // empty row: max 0 (ref_fp32.cpp:11)
+        if (!valid) continue;
+        // ---- epilogue.  Lane (half, slot) holds features 32 mb + 8 gq + 4 half + {0..3}.
+        const int W = it.blocks * 32;
+        if (chunk_item) {
+            float* part = a.part + c * kPart;
+#pragma unroll
+            for (int q = 0; q < kMB; ++q) {
+                if (q >= nb) continue;
+#pragma unroll
+                for (int gq = 0; gq < 4; ++gq) {
+                    const int f0 = (mb0 + q) * 32 + 8 * gq + 4 * half;
+                    *reinterpret_cast<float4*>(part + f0) =
+                        make_float4(acc[q][4 * gq], acc[q][4 * gq + 1], acc[q][4 * gq + 2], acc[q][4 * gq + 3]);
+                }
+                if (half == 0) part[kDenOff + mb0 + q] = den[q];
+            }
+            continue;
+        }
+#pragma unroll
+        for (int q = 0; q < kMB; ++q) {
+            if (q >= nb) continue;
+            const int h = mb0 + q;
+            const float scale = den[q] > 0.0f ? 1.0f / den[q] : 0.0f;
+            if (half == 0) {
+                a.mx[uint64_t(i) * K + h] = M[q];
+                a.den[uint64_t(i) * K + h] = den[q];
+            }
+#pragma unroll
+            for (int gq = 0; gq < 4; ++gq) {
+                const int f0 = h * 32 + 8 * gq + 4 * half;
+                float o[4];
+#pragma unroll
+                for (int x = 0; x < 4; ++x) {
+                    const float y = den[q] > 0.0f ? acc[q][4 * gq + x] * scale : 0.0f;  // empty row: exact 0
+                    o[x] = a.hidden ? elu(y) : y;
+                }
+                if (a.outbf)
+                    *reinterpret_cast<uint2*>(a.outbf + uint64_t(i) * W + f0) =
+                        make_uint2(uint32_t(bf16_rne(o[0])) | (uint32_t(bf16_rne(o[1])) << 16),
+                                   uint32_t(bf16_rne(o[2])) | (uint32_t(bf16_rne(o[3])) << 16));
+                if (a.out32)
+                    *reinterpret_cast<float4*>(a.out32 + uint64_t(i) * W + f0) = make_float4(o[0], o[1], o[2], o[3]);
+            }
+        }
     }
 }
 
-// One wave per chunk of a split row; 4 groups take quarters of the chunk.
-__global__ void __launch_bounds__(256) k_af_split(AfArgs a) {
-    __shared__ float pbuf[4][kGPW][kBE * 8];
-    __shared__ uint32_t jbuf[4][kGPW][kBE];
-    __shared__ float tot[4][8 * kXS + 8];
-    const int w = threadIdx.x / kWave, lane = threadIdx.x % kWave;
-    const int g = lane / kGL, c = lane % kGL, hs = c % 8;
-    const uint64_t ch = uint64_t(blockIdx.x) * 4 + w;
-    if (ch >= a.chunks) return;
-    const int K = a.heads, W = K * 32;
-    const uint32_t k = a.chunk_k[ch], first = a.chunk_first[ch];
+// One wave per split row (found at its first chunk): adds the chunks' partial
+// sums and denominators in chunk order, normalises, ELU, stores.
+__global__ void __launch_bounds__(kThreads) k_af_merge(AfArgs a, int blocks) {
+    const int w = threadIdx.x / kWave, l = threadIdx.x % kWave;
+    const uint64_t c = uint64_t(blockIdx.x) * kWaves + w;
+    if (c >= a.chunks || a.chunk_first[c] != c) return;
+    const uint32_t k = a.chunk_k[c];
     const uint64_t rbeg = a.prow[k], rend = a.prow[k + 1];
     const uint32_t i = a.perm[k];
     if (i >= a.n || rbeg > rend || rend > a.e) return;
     const uint32_t nch = uint32_t((rend - rbeg + a.chunk_edges - 1) / a.chunk_edges);
-    const uint64_t cbeg = rbeg + uint64_t(ch - first) * a.chunk_edges;
-    const uint64_t cend = cbeg + a.chunk_edges < rend ? cbeg + a.chunk_edges : rend;
-    float m = -INFINITY;
-    if (hs < K)
-        for (uint32_t q = lane / 8; q < nch; q += 8) m = fmaxf(m, a.mchunk[(first + q) * 8 + hs]);
-    for (int off = 8; off < kWave; off <<= 1) m = fmaxf(m, __shfl_xor(m, off));
-    const float Lh = hs < K ? a.L[uint64_t(i) * K + hs] : 0.0f;
-    float Mh = leaky(Lh + m);
-    // Quarter g of the chunk, padded to whole batches so the wave's syncs line up.
-    const uint64_t len = cend - cbeg, q0 = cbeg + len * g / kGPW, q1 = cbeg + len * (g + 1) / kGPW;
-    uint64_t span = q1 - q0;
-    for (int off = kGL; off < kWave; off <<= 1) {
-        const uint64_t o = __shfl_xor(span, off);
-        span = o > span ? o : span;
-    }
-    float acc[8][8];
-#pragma unroll
-    for (int h = 0; h < 8; ++h)
-#pragma unroll
-        for (int x = 0; x < 8; ++x) acc[h][x] = 0.0f;
-    float dloc = 0.0f;
-    for (uint64_t base = 0; base < span; base += kBE) {
-        const uint64_t b0 = q0 + base;
-        group_rows(b0 < q1 ? b0 : q1, b0 + kBE < q1 ? b0 + kBE : q1, false, a.pcol, a.R, a.X, K, Lh, Mh,
-                   pbuf[w][g], jbuf[w][g], acc, dloc);
-    }
-    // Sum the 4 groups (lanes c, c+16, c+32, c+48) and the scorer lanes of each head.
-#pragma unroll
-    for (int h = 0; h < 8; ++h)
-#pragma unroll
-        for (int x = 0; x < 8; ++x) {
-            acc[h][x] += __shfl_xor(acc[h][x], 16);
-            acc[h][x] += __shfl_xor(acc[h][x], 32);
+    if (c + nch > a.chunks) return;
+    const int K = a.heads, W = blocks * 32;
+    for (int f0 = 4 * l; f0 < W; f0 += 4 * kWave) {
+        const int h = f0 / 32;
+        float4 tot = make_float4(0.f, 0.f, 0.f, 0.f);
+        float d = 0.0f, m = -INFINITY;
+        for (uint32_t q = 0; q < nch; ++q) {
+            const float* pq = a.part + (c + q) * kPart;
+            const float4 v = *reinterpret_cast<const float4*>(pq + f0);
+            tot.x += v.x;
+            tot.y += v.y;
+            tot.z += v.z;
+            tot.w += v.w;
+            d += pq[kDenOff + h];
+            m = fmaxf(m, a.mchunk[(c + q) * 8 + h]);
         }
-    for (int off = 8; off < kWave; off <<= 1) dloc += __shfl_xor(dloc, off);
-    float* part = a.part + ch * (8 * kXS + 8);
-    if (g == 0)
+        const float M = leaky(a.L[uint64_t(i) * K + h] + m);
+        if (f0 % 32 == 0) {
+            a.mx[uint64_t(i) * K + h] = M;
+            a.den[uint64_t(i) * K + h] = d;
+        }
+        const float scale = d > 0.0f ? 1.0f / d : 0.0f;
+        float o[4] = {tot.x * scale, tot.y * scale, tot.z * scale, tot.w * scale};
+        if (!(d > 0.0f)) o[0] = o[1] = o[2] = o[3] = 0.0f;
+        if (a.hidden)
 #pragma unroll
-        for (int h = 0; h < 8; ++h)
-#pragma unroll
-            for (int x = 0; x < 8; x += 4)
-                *reinterpret_cast<float4*>(part + h * kXS + c * 8 + x) =
-                    make_float4(acc[h][x], acc[h][x + 1], acc[h][x + 2], acc[h][x + 3]);
-    if (lane < 8) part[8 * kXS + lane] = dloc;
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
-    uint32_t old = 0;
-    if (lane == 0) old = __hip_atomic_fetch_add(a.counter + first, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    old = __shfl(old, 0);
-    if (old + 1 != nch) return;
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-    // Last arrival: partials in chunk order into LDS, then out = U^h W^h / den.
-    float* t = tot[w];
-    for (int q = lane; q < 8 * kXS + 8; q += kWave) {
-        float s = 0.0f;
-        for (uint32_t cq = 0; cq < nch; ++cq) s += a.part[uint64_t(first + cq) * (8 * kXS + 8) + q];
-        t[q] = s;
+            for (int x = 0; x < 4; ++x) o[x] = elu(o[x]);
+        if (a.outbf)
+            *reinterpret_cast<uint2*>(a.outbf + uint64_t(i) * W + f0) =
+                make_uint2(uint32_t(bf16_rne(o[0])) | (uint32_t(bf16_rne(o[1])) << 16),
+                           uint32_t(bf16_rne(o[2])) | (uint32_t(bf16_rne(o[3])) << 16));
+        if (a.out32)
+            *reinterpret_cast<float4*>(a.out32 + uint64_t(i) * W + f0) = make_float4(o[0], o[1], o[2], o[3]);
     }
-    wave_sync();
-    if (lane < K) {  // lanes < 8 score head `lane`
-        a.mx[uint64_t(i) * K + lane] = Mh;
-        a.den[uint64_t(i) * K + lane] = t[8 * kXS + lane];
+}
+
+template <int KS>
+hipError_t launch_ns(const AfArgs& a, const Items& it, hipStream_t s, int cus) {
+    const size_t lds = size_t(it.blocks) * KS * kWave * sizeof(uint4);
+    if (lds > 64 * 1024) {
+        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_af_ns<KS>),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, int(lds));
+        if (e != hipSuccess) return e;
     }
-    if (lane == 0) a.counter[first] = 0;
-    for (int f = lane; f < W; f += kWave) {
-        const int h = f / 32;
-        float s = 0.0f;
-        for (int kk = 0; kk < a.in; ++kk) s += t[h * kXS + kk] * a.wq[size_t(kk) * W + f];
-        const float d = t[8 * kXS + h];
-        float y = s * (d > 0.0f ? 1.0f / d : 0.0f);
-        if (a.hidden) y = elu(y);
-        if (a.outbf) a.outbf[uint64_t(i) * W + f] = bf16_rne(y);
-        if (a.out32) a.out32[uint64_t(i) * W + f] = y;
-    }
+    const uint64_t waves = (it.chunk_groups + it.tile_groups) * uint64_t(it.waves_per_item);
+    uint64_t blocks = (waves + kWaves - 1) / kWaves;
+    if (blocks > uint64_t(cus) * 2) blocks = uint64_t(cus) * 2;
+    k_af_ns<KS><<<dim3(uint32_t(blocks)), kThreads, lds, s>>>(a, it);
+    return hipGetLastError();
 }
 
 }  // namespace
 
-bool aggregate_af_supported(int in, int heads, int dim) { return in <= kXS && heads <= 8 && dim == 32; }
+bool aggregate_af_supported(int in, int heads, int dim) {
+    return in <= kXS && (heads == 1 || heads == 2 || heads == 4 || heads == 8) && dim == 32;
+}
 
 int af_input_stride() { return kXS; }
 
 hipError_t launch_aggregate_af(const AfArgs& a, hipStream_t s, int cus) {
-    if (a.heads > 8 || a.in > kXS) return hipErrorInvalidValue;
+    if (!aggregate_af_supported(a.in, a.heads, 32) || a.ksteps < 1 || a.ksteps > kXS / 16 || a.nmb < a.heads)
+        return hipErrorInvalidValue;
+    Items it{};
+    it.blocks = a.heads;
+    it.waves_per_item = (it.blocks + kMB - 1) / kMB;
+    it.chunk_groups = (a.chunks + kSlots - 1) / kSlots;
+    it.tile_groups = (a.rows + kSlots - 1) / kSlots;
     if (a.chunks) {
         SplitTable t{};
         t.chunks = a.chunks;
@@ -333,13 +360,22 @@ hipError_t launch_aggregate_af(const AfArgs& a, hipStream_t s, int cus) {
         t.mchunk = const_cast<float*>(a.mchunk);
         hipError_t e = launch_split_prescan(a.prow, a.pcol, a.R, a.heads, t, a.e, s);
         if (e != hipSuccess) return e;
-        k_af_split<<<dim3(uint32_t((a.chunks + 3) / 4)), 256, 0, s>>>(a);
-        if ((e = hipGetLastError()) != hipSuccess) return e;
     }
-    if (a.tiles) {
-        uint64_t gx = a.tiles < uint64_t(cus) ? a.tiles : uint64_t(cus);
-        k_af_tiles<<<dim3(uint32_t(gx)), kThreads, 0, s>>>(a);
+    if (it.chunk_groups + it.tile_groups) {
+        hipError_t e = hipSuccess;
+        switch (a.ksteps) {
+            case 1: e = launch_ns<1>(a, it, s, cus); break;
+            case 2: e = launch_ns<2>(a, it, s, cus); break;
+            case 3: e = launch_ns<3>(a, it, s, cus); break;
+            case 4: e = launch_ns<4>(a, it, s, cus); break;
+            case 5: e = launch_ns<5>(a, it, s, cus); break;
+            case 6: e = launch_ns<6>(a, it, s, cus); break;
+            case 7: e = launch_ns<7>(a, it, s, cus); break;
+            default: e = launch_ns<8>(a, it, s, cus); break;
+        }
+        if (e != hipSuccess) return e;
     }
+    if (a.chunks) k_af_merge<<<dim3(uint32_t((a.chunks + kWaves - 1) / kWaves)), kThreads, 0, s>>>(a, it.blocks);
     return hipGetLastError();
 }
 

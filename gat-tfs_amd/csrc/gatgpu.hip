@@ -665,7 +665,7 @@ int gatgpu_layer_forward(gatgpu_ctx* c, int layer, int precision, int dataflow, 
             return fail(c, GATGPU_ENONFINITE, "nonfinite layer input index=" + std::to_string(bad));
     }
     const int flow = resolve_dataflow(c->L[layer], precision, dataflow);
-    if (flow < 0) return fail(c, GATGPU_EINVAL, "aggregate-first needs bf16, head_dim 32 and in <= 128");
+    if (flow < 0) return fail(c, GATGPU_EINVAL, "aggregate-first needs bf16, head_dim 32, 1/2/4/8 heads and in <= 128");
     if (int r = run_layer(c, layer, precision, flow, hidden != 0, input, times ? 0 : -1)) return r;
     HIPCHECK(c, hipStreamSynchronize(c->stream));
     HIPCHECK(c, hipGetLastError());
@@ -750,8 +750,9 @@ int gatgpu_model_forward(gatgpu_ctx* c, int precision, int dataflow, float* logi
         return fail(c, GATGPU_EINVAL, "layer widths do not chain");
     const bool timed = times || total_ms;
     for (int l = 0; l < 3; ++l) {
-        const int flow = resolve_dataflow(c->L[l], precision, dataflow);
-        if (flow < 0) return fail(c, GATGPU_EINVAL, "aggregate-first needs bf16, head_dim 32 and in <= 128");
+        // In the chained model, aggregate-first applies where the layer supports it.
+        int flow = resolve_dataflow(c->L[l], precision, dataflow);
+        if (flow < 0) flow = GATGPU_TRANSFORM_FIRST;
         if (int r = run_layer(c, l, precision, flow, l < 2, nullptr, timed ? 4 * l : -1)) return r;
     }
     HIPCHECK(c, hipStreamSynchronize(c->stream));

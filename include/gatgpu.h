@@ -54,10 +54,13 @@ enum { GATGPU_FP32 = 0, GATGPU_BF16 = 1 };
 
 /* Dataflow of one layer.  TRANSFORM_FIRST projects Z = X W then aggregates Z
  * rows (standard_layer, baseline/src/baseline_standard.cpp:98-108).
- * AGGREGATE_FIRST aggregates X rows per head and projects afterwards
- * (tfs_online_fused, implementation/src/gat_tfs_online.cpp:200-283), bf16
- * only, head_dim 32 and in <= 128.  AUTO selects the faster dataflow for the
- * layer shape on gfx950 (transform-first for every shape of this build). */
+ * AGGREGATE_FIRST gathers the layer's input rows instead of Z and projects
+ * each gathered row on the MFMA units, summing p (X_j W_h) (tfs_online_fused,
+ * implementation/src/gat_tfs_online.cpp:200-283, in the neighbour-step order
+ * of baseline/src/baseline_tfs.cpp:16-110); bf16 only, head_dim 32, 1, 2, 4
+ * or 8 heads and in <= 128.  AUTO selects the faster dataflow for the layer
+ * shape on gfx950.  gatgpu_model_forward with AGGREGATE_FIRST uses it on the
+ * layers that support it and transform-first on the others. */
 enum { GATGPU_AUTO = 0, GATGPU_TRANSFORM_FIRST = 1, GATGPU_AGGREGATE_FIRST = 2 };
 
 /* Stage selectors for gatgpu_get_stage (Workspace fields, gat.hpp:96-106). */
@@ -147,7 +150,8 @@ int gatgpu_layer_forward(gatgpu_ctx* ctx, int layer, int precision, int dataflow
  * timer of baseline/bench/main.cpp:171-174).  logits (NULL allowed) receives
  * layer 2's FP32 [n][dim] output after the timer stops.  times (NULL allowed)
  * points at 3 per-layer records; total_ms (NULL allowed) gets the model time.
- * dataflow applies to every layer (AUTO decides per layer). */
+ * dataflow applies to every layer (AUTO decides per layer; AGGREGATE_FIRST
+ * falls back to transform-first on layers it does not support). */
 int gatgpu_model_forward(gatgpu_ctx* ctx, int precision, int dataflow, float* logits,
                          gatgpu_times* times, double* total_ms);
 /* ---- fixed-p operator ----------------------------------------------- */

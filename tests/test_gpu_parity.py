@@ -449,6 +449,10 @@ def test_aggregate_first_matches_transform_first_on_arxiv(gpu_ctx):
         e = oracle.errors(ref, got)
         assert e["finite"] and e["relative_l2"] < BF16_REL_L2, e
     assert oracle.errors(tf, auto)["relative_l2"] < BF16_REL_L2
+    # The chained model runs aggregate-first where a layer supports it (layer 1
+    # here) and transform-first elsewhere: the same bits as the chain above.
+    af, _, _ = gpu_ctx.model_forward(gatgpu.BF16, gatgpu.AGGREGATE_FIRST)
+    assert np.array_equal(af, auto)
     with pytest.raises(gatgpu.GatGpuError) as err:
-        gpu_ctx.model_forward(gatgpu.FP32, gatgpu.AGGREGATE_FIRST)
+        gpu_ctx.layer_forward(1, gatgpu.BF16, gatgpu.AGGREGATE_FIRST, True)  # in = 256
     assert err.value.code == gatgpu.EINVAL
