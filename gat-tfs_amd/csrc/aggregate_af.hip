@@ -227,7 +227,8 @@ __global__ void __launch_bounds__(kThreads, 2) k_af_ns(AfArgs a, Items it) {
 #pragma unroll
         for (int q = 0; q < kMB; ++q) M[q] = len ? m[q] : 0.0f;  // empty row: max 0 (ref_fp32.cpp:11)
         if (!valid) continue;
-        // ---- epilogue.  Lane (half, slot) holds features 32 mb + 8 gq + 4 half + {0..3}.
+        // ---- epilogue.  Lane (half, slot) holds features 32 mb + 16 half + 4 gq + {0..3}
+        // (permuted packing of pack_projection_weights).
         const int W = it.blocks * 32;
         if (chunk_item) {
             float* part = a.part + c * kPart;
@@ -236,7 +237,7 @@ __global__ void __launch_bounds__(kThreads, 2) k_af_ns(AfArgs a, Items it) {
                 if (q >= nb) continue;
 #pragma unroll
                 for (int gq = 0; gq < 4; ++gq) {
-                    const int f0 = (mb0 + q) * 32 + 8 * gq + 4 * half;
+                    const int f0 = (mb0 + q) * 32 + 16 * half + 4 * gq;
                     *reinterpret_cast<float4*>(part + f0) =
                         make_float4(acc[q][4 * gq], acc[q][4 * gq + 1], acc[q][4 * gq + 2], acc[q][4 * gq + 3]);
                 }
@@ -255,7 +256,7 @@ __global__ void __launch_bounds__(kThreads, 2) k_af_ns(AfArgs a, Items it) {
             }
 #pragma unroll
             for (int gq = 0; gq < 4; ++gq) {
-                const int f0 = h * 32 + 8 * gq + 4 * half;
+                const int f0 = h * 32 + 16 * half + 4 * gq;
                 float o[4];
 #pragma unroll
                 for (int x = 0; x < 4; ++x) {

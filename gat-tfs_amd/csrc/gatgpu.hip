@@ -270,9 +270,9 @@ int run_layer_af(gatgpu_ctx* c, int l, bool hidden, const float* src32, const ui
     HIPCHECK(c, Ls.mx.ensure(n * K * 4));
     HIPCHECK(c, Ls.den.ensure(n * K * 4));
     if (hidden) HIPCHECK(c, Ls.outbf.ensure(n * W * 2));
-    else HIPCHECK(c, Ls.out32.ensure(n * W * 4));
+    else HIPCHECK(c, Ls.out32.ensure((n * W + kF32Pad) * 4));
     if (srcbf && D != xs) {  // chained bf16 input in another row layout
-        HIPCHECK(c, Ls.in32.ensure(n * D * 4));
+        HIPCHECK(c, Ls.in32.ensure((n * D + kF32Pad) * 4));
         HIPCHECK(c, launch_widen_bf16(srcbf, Ls.in32.as<float>(), n * D, c->stream));
         src32 = Ls.in32.as<float>();
         srcbf = nullptr;
@@ -351,7 +351,7 @@ int run_layer(gatgpu_ctx* c, int l, int precision, int dataflow, bool hidden, co
     const float* src32 = nullptr;
     const uint16_t* srcbf = nullptr;
     if (host_input) {
-        HIPCHECK(c, Ls.in32.ensure(n * D * 4));
+        HIPCHECK(c, Ls.in32.ensure((n * D + kF32Pad) * 4));
         HIPCHECK(c, hipMemcpyAsync(Ls.in32.p, host_input, n * D * 4, hipMemcpyHostToDevice, c->stream));
         src32 = Ls.in32.as<float>();
     } else if (l == 0) {
@@ -376,7 +376,7 @@ int run_layer(gatgpu_ctx* c, int l, int precision, int dataflow, bool hidden, co
     const bool bf16 = precision == GATGPU_BF16;
     const bool want_outbf = bf16 && hidden && !fixed;
     if (want_outbf) HIPCHECK(c, Ls.outbf.ensure(n * W * 2));
-    else HIPCHECK(c, Ls.out32.ensure(n * W * 4));
+    else HIPCHECK(c, Ls.out32.ensure((n * W + kF32Pad) * 4));
     // bf16 path: X as [n][xs] bf16 (xs = ksteps*16, zero-padded), Z as [n][zs]
     // bf16 (zs = W rounded up to 8 for aligned vector stores).
     const int xs = Ls.ksteps * 16;
@@ -385,7 +385,7 @@ int run_layer(gatgpu_ctx* c, int l, int precision, int dataflow, bool hidden, co
     if (bf16) {
         HIPCHECK(c, Ls.zbf.ensure(n * zs * 2));
         if (srcbf && D != xs) {  // chained bf16 input without the padded layout
-            HIPCHECK(c, Ls.in32.ensure(n * D * 4));
+            HIPCHECK(c, Ls.in32.ensure((n * D + kF32Pad) * 4));
             HIPCHECK(c, launch_widen_bf16(srcbf, Ls.in32.as<float>(), n * D, c->stream));
             src32 = Ls.in32.as<float>();
             srcbf = nullptr;
@@ -397,9 +397,28 @@ int run_layer(gatgpu_ctx* c, int l, int precision, int dataflow, bool hidden, co
     // The fixed-p operator has no row max (the reference leaves it unset).
     if (fixed) HIPCHECK(c, hipMemsetAsync(Ls.mx.p, 0, n * K * 4, c->stream));
     if (ev_base >= 0) HIPCHECK(c, hipEventRecord(c->ev[ev_base], c->stream));
+    // ---- projection arguments (bf16 path)
+    ProjArgs pa{};
+    pa.n = n;
+    pa.xs = xs;
+    pa.ksteps = Ls.ksteps;
+    pa.wpk = Ls.wpk.as<uint4>();
+    pa.groups = Ls.groups;
+    pa.head_blocks = (W + 31) / 32;
+    pa.nmb = Ls.nmb;
+    pa.width = W;
+    pa.heads = K;
+    pa.z = Ls.zbf.as<uint16_t>();
+    pa.zs = zs;
+    pa.left = Ls.left.as<float>();
+    pa.right = Ls.right.as<float>();
+    pa.tiles = (n + 31) / 32;
+    pa.r_in_z = r_in_z;
     // ---- convert (bf16 path, FP32 source only; a bf16 source was rounded in
-    // the previous layer's epilogue, which equals convert() of that output)
-    if (bf16 && src32) {
+    // the previous layer's epilogue, which equals convert() of that output).
+    // Where the fast projection applies, the rounding happens in its loads.
+    const bool fused_convert = bf16 && src32 && D % 4 == 0 && projection_fp32_input(pa);  // 16-byte aligned rows
+    if (bf16 && src32 && !fused_convert) {
         HIPCHECK(c, launch_to_bf16_pad(src32, Ls.inbf.as<uint16_t>(), n, D, xs, c->stream));
         srcbf = Ls.inbf.as<uint16_t>();
         src32 = nullptr;
@@ -407,23 +426,13 @@ int run_layer(gatgpu_ctx* c, int l, int precision, int dataflow, bool hidden, co
     if (ev_base >= 0) HIPCHECK(c, hipEventRecord(c->ev[ev_base + 1], c->stream));
     // ---- projection + L/R
     if (bf16) {
-        ProjArgs pa{};
-        pa.x = srcbf;
-        pa.n = n;
-        pa.xs = xs;
-        pa.ksteps = Ls.ksteps;
-        pa.wpk = Ls.wpk.as<uint4>();
-        pa.groups = Ls.groups;
-        pa.head_blocks = (W + 31) / 32;
-        pa.nmb = Ls.nmb;
-        pa.width = W;
-        pa.heads = K;
-        pa.z = Ls.zbf.as<uint16_t>();
-        pa.zs = zs;
-        pa.left = Ls.left.as<float>();
-        pa.right = Ls.right.as<float>();
-        pa.tiles = (n + 31) / 32;
-        pa.r_in_z = r_in_z;
+        if (fused_convert) {
+            pa.x32 = src32;  // FP32 buffers of the context carry 16 floats of padding
+            pa.xs = D;
+            pa.in = D;
+        } else {
+            pa.x = srcbf;
+        }
         HIPCHECK(c, launch_projection_mfma(pa, c->stream, c->cus));
     } else {
         HIPCHECK(c, launch_projection(src32, nullptr, Ls.w32.as<float>(), n, D, K, dim, Ls.al.as<float>(),
@@ -617,7 +626,7 @@ int gatgpu_set_input(gatgpu_ctx* c, uint64_t n, int din, const float* x) {
     if (mul_overflows(n, uint64_t(din) * 4)) return fail(c, GATGPU_EOVERFLOW, "size overflow");
     uint64_t bad = 0;
     if (!all_finite(x, n * din, &bad)) return fail(c, GATGPU_ENONFINITE, "nonfinite graph input index=" + std::to_string(bad));
-    HIPCHECK(c, c->x32.ensure(n * din * 4));
+    HIPCHECK(c, c->x32.ensure((n * din + kF32Pad) * 4));
     HIPCHECK(c, hipMemcpyAsync(c->x32.p, x, n * din * 4, hipMemcpyHostToDevice, c->stream));
     HIPCHECK(c, hipStreamSynchronize(c->stream));
     c->din = din;

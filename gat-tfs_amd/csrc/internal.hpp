@@ -79,8 +79,11 @@ hipError_t launch_lr_reordered(const float* x32, const uint16_t* xbf, const floa
 // projection_mfma.hip: bf16 MFMA projection with the fused L/R block.
 struct ProjArgs {
     const uint16_t* x;   // [n][xs] bf16 input, zero-padded to ksteps*16 columns
+    const float* x32;    // or FP32 input [n][xs] (in valid columns, 16 floats of
+                         // padding after the last row), rounded to bf16 in the kernel
+    int in;              // valid input features (FP32 input)
     uint64_t n;
-    int xs;              // row stride of x (elements, multiple of 8)
+    int xs;              // row stride of x / x32 (elements)
     int ksteps;          // ceil(in / 16)
     const uint4* wpk;    // packed weights, pack_projection_weights() order
     int groups, head_blocks, nmb, width, heads;
@@ -92,6 +95,12 @@ struct ProjArgs {
     bool r_in_z;         // one head: also store R as FP32 in z[row][zs-2..zs-1]
 };
 int proj_blocks_per_group(int width);
+// True when launch_projection_mfma takes the fast path for these arguments
+// (one output group, 1..8 or 16 k steps, 0/1/2/8 head blocks); the FP32-input
+// form requires it.
+bool projection_fast_path(const ProjArgs& a);
+// True when the fast path also takes FP32 input rows (rounding them itself).
+bool projection_fp32_input(const ProjArgs& a);
 void pack_projection_weights(const float* wq, const float* al, const float* ar, int in, int heads, int dim,
                              std::vector<uint16_t>& out, int& ksteps, int& groups, int& nmb);
 hipError_t launch_projection_mfma(const ProjArgs& a, hipStream_t s, int cus);
@@ -127,6 +136,9 @@ struct AggArgs {
 // edges, so that kernels may load a whole batch of wave-uniform source ids
 // at the end of the last row without a bounds test.
 constexpr uint64_t kPcolPad = 64;
+// FP32 feature buffers carry kF32Pad floats past their last row, so that the
+// fused-convert projection may read a row's 16-feature tail unmasked.
+constexpr uint64_t kF32Pad = 16;
 
 // Split rows (sorted positions [split_begin, n)) cut into chunks of
 // chunk_edges edges, heaviest rows first; built on the host from prow.

@@ -80,14 +80,15 @@ __global__ void __launch_bounds__(kThreads) k_proj_mfma(ProjArgs a) {
             }
         }
         if (!row_ok) continue;
-        // Z: lane (half, col) holds features 32*gb + 8*gq + 4*half + {0..3} of row.
+        // Z: lane (half, col) holds features 32*gb + 16*half + 4*gq + {0..3} of row
+        // (permuted packing).
 #pragma unroll
         for (int mb = 0; mb < NMB; ++mb) {
             if (mb >= head_blocks) continue;
             const int gb = 8 * g + mb;
 #pragma unroll
             for (int gq = 0; gq < 4; ++gq) {
-                const int f0 = gb * 32 + 8 * gq + 4 * half;
+                const int f0 = gb * 32 + 16 * half + 4 * gq;
                 if (f0 >= a.width) continue;
                 const uint32_t w0 = uint32_t(bf16_rne(acc[mb][4 * gq])) | (uint32_t(bf16_rne(acc[mb][4 * gq + 1])) << 16);
                 const uint32_t w1 = uint32_t(bf16_rne(acc[mb][4 * gq + 2])) | (uint32_t(bf16_rne(acc[mb][4 * gq + 3])) << 16);
@@ -114,6 +115,190 @@ __global__ void __launch_bounds__(kThreads) k_proj_mfma(ProjArgs a) {
             }
         }
     }
+}
+
+// Fast path for one output group (head blocks HB <= 8 plus the L/R block)
+// and KS <= 16 k steps, both compile-time: the W^T fragments of the group
+// sit in LDS in [ks][block] order, each k step reads the HB + 1 fragments and
+// issues HB + 1 independent MFMAs (no dependent chain between consecutive
+// MFMAs, no branches between them), and the tile's X fragments are loaded
+// unconditionally (rows past n re-read row n - 1 and are not stored).
+// Head blocks use the permuted packing (pack_projection_weights): lane
+// (half, col) ends with features 32 mb + 16 half + {0..15} of row col, so
+// Z leaves as two 16-byte stores per block.
+template <int KS, int HB, bool F32IN, bool FULL>
+__global__ void __launch_bounds__(kThreads) k_proj_fast(ProjArgs a) {
+    constexpr int NB = HB + 1;
+    extern __shared__ uint4 wlds[];
+    for (int q = threadIdx.x; q < KS * NB * kWave; q += kThreads) {
+        const int lane = q % kWave, b = (q / kWave) % NB, ks = q / (kWave * NB);
+        wlds[q] = a.wpk[(size_t(ks) * a.nmb + b) * kWave + lane];
+    }
+    __syncthreads();
+    const int w = threadIdx.x / kWave, l = threadIdx.x % kWave;
+    const int half = l / 32, col = l % 32;
+    // Raw input fragments of the tile: 16 bytes of bf16 per k step, or 32
+    // bytes of FP32 (rounded to bf16 when used, so a load is never waited on
+    // at issue).  Rolling two-part pipeline over the wave's tiles: each part
+    // (k steps 0..KA-1, KA..KS-1) of tile t+1 is requested as soon as tile t
+    // has multiplied that part, in the same registers.
+    constexpr int KA = (KS + 1) / 2;
+    constexpr int RW = F32IN ? 2 : 1;  // 16-byte loads per k step
+    uint4 raw[KS][RW];
+    auto load_ks = [&](uint64_t tile, int ks) {
+        const uint64_t r = tile * 32 + col;
+        const uint64_t rc = r < a.n ? r : a.n - 1;
+        if constexpr (F32IN) {
+            const float* p = a.x32 + rc * a.xs + 16 * ks + 8 * half;
+            raw[ks][0] = *reinterpret_cast<const uint4*>(p);
+            raw[ks][RW - 1] = *reinterpret_cast<const uint4*>(p + 4);
+        } else {
+            raw[ks][0] = *reinterpret_cast<const uint4*>(a.x + rc * a.xs + 16 * ks + 8 * half);
+        }
+    };
+    // B operand of k step ks.  FP32 input (stride xs floats, `in` valid
+    // features): rounded to bf16 here -- the convert stage, common.cpp:80-93,
+    // fused; features >= in are zeroed.  The buffer carries 16 floats of
+    // padding, so the last row's tail loads stay inside it.
+    auto operand = [&](int ks) -> bf16x8 {
+        if constexpr (F32IN) {
+            const int f0 = 16 * ks + 8 * half;
+            const float e[8] = {__builtin_bit_cast(float, raw[ks][0].x), __builtin_bit_cast(float, raw[ks][0].y),
+                                __builtin_bit_cast(float, raw[ks][0].z), __builtin_bit_cast(float, raw[ks][0].w),
+                                __builtin_bit_cast(float, raw[ks][RW - 1].x), __builtin_bit_cast(float, raw[ks][RW - 1].y),
+                                __builtin_bit_cast(float, raw[ks][RW - 1].z), __builtin_bit_cast(float, raw[ks][RW - 1].w)};
+            uint32_t w4[4];
+#pragma unroll
+            for (int x = 0; x < 4; ++x) {
+                const uint32_t lo = f0 + 2 * x < a.in ? bf16_rne(e[2 * x]) : 0u;
+                const uint32_t hi = f0 + 2 * x + 1 < a.in ? bf16_rne(e[2 * x + 1]) : 0u;
+                w4[x] = lo | (hi << 16);
+            }
+            return __builtin_bit_cast(bf16x8, make_uint4(w4[0], w4[1], w4[2], w4[3]));
+        } else {
+            return __builtin_bit_cast(bf16x8, raw[ks][0]);
+        }
+    };
+    const uint64_t stride = uint64_t(gridDim.x) * kWaves;
+    uint64_t tile = uint64_t(blockIdx.x) * kWaves + w;
+    const uint64_t last = a.tiles - 1;
+    {
+        const uint64_t t0 = tile < a.tiles ? tile : last;
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) load_ks(t0, ks);
+    }
+    for (; tile < a.tiles; tile += stride) {
+        const uint64_t row = tile * 32 + col;
+        const uint64_t next = tile + stride < a.tiles ? tile + stride : last;
+        f32x16 acc[NB];
+#pragma unroll
+        for (int mb = 0; mb < NB; ++mb)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[mb][r] = 0.0f;
+        auto kstep = [&](int ks) {
+            const bf16x8 b = operand(ks);
+            const uint4* wk = wlds + size_t(ks) * NB * kWave + l;
+#pragma unroll
+            for (int mb = 0; mb < NB; ++mb)
+                acc[mb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, wk[mb * kWave]), b,
+                                                                  acc[mb], 0, 0, 0);
+            // Keep each k step's fragment reads inside the step: hoisting all of
+            // them ahead of the MFMAs would need KS * NB * 4 registers.
+            __builtin_amdgcn_sched_barrier(0);
+        };
+        // Part A of this tile, then part A of the next tile requested into the
+        // freed registers; part B of this tile, the stores, then part B of the
+        // next tile.  Every load is unconditional, so each wait is exact.
+#pragma unroll
+        for (int ks = 0; ks < KA; ++ks) kstep(ks);
+#pragma unroll
+        for (int ks = 0; ks < KA; ++ks) load_ks(next, ks);
+#pragma unroll
+        for (int ks = KA; ks < KS; ++ks) kstep(ks);
+        // A lane past n computed row n - 1 from the same input, so it stores
+        // that row's own values to it: no branch around the stores, which
+        // keeps the wait counts of the next tile's loads exact.
+        const uint64_t rs = row < a.n ? row : a.n - 1;
+        // FULL: all 8 heads and 32 HB features present (8 x 32): no per-store
+        // bounds tests either.
+        const bool full = FULL;
+#pragma unroll
+        for (int mb = 0; mb < HB; ++mb)
+#pragma unroll
+            for (int q8 = 0; q8 < 2; ++q8) {
+                const int f0 = 32 * mb + 16 * half + 8 * q8;
+                if (!full && f0 >= a.width) continue;
+                uint32_t w4[4];
+#pragma unroll
+                for (int x = 0; x < 4; ++x)
+                    w4[x] = uint32_t(bf16_rne(acc[mb][8 * q8 + 2 * x])) |
+                            (uint32_t(bf16_rne(acc[mb][8 * q8 + 2 * x + 1])) << 16);
+                *reinterpret_cast<uint4*>(a.z + rs * a.zs + f0) = make_uint4(w4[0], w4[1], w4[2], w4[3]);
+            }
+        // L/R block: lane half h4 holds heads 4 h4 + {0..3} of each quarter
+        // (L hi, R hi, L lo, R lo) in registers {0..3}, {4..7}, {8..11}, {12..15}.
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const int h = 4 * half + q;
+            if (full || h < a.heads) {
+                const float rv = acc[HB][4 + q] + acc[HB][12 + q];
+                a.left[rs * a.heads + h] = acc[HB][q] + acc[HB][8 + q];
+                a.right[rs * a.heads + h] = rv;
+                if (!full && a.r_in_z) *reinterpret_cast<float*>(a.z + rs * a.zs + a.zs - 2) = rv;
+            }
+        }
+#pragma unroll
+        for (int ks = KA; ks < KS; ++ks) load_ks(next, ks);
+    }
+}
+
+template <int KS, int HB, bool F32IN, bool FULL>
+hipError_t launch_fast_io(const ProjArgs& a, hipStream_t s, int cus) {
+    const size_t lds = size_t(KS) * (HB + 1) * kWave * sizeof(uint4);
+    if (lds > 64 * 1024) {
+        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_proj_fast<KS, HB, F32IN, FULL>),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, int(lds));
+        if (e != hipSuccess) return e;
+    }
+    const int per_cu = lds <= 80 * 1024 ? 2 : 1;
+    uint64_t gx = uint64_t(cus) * per_cu;
+    const uint64_t wg_needed = (a.tiles + kWaves - 1) / kWaves;
+    if (gx > wg_needed) gx = wg_needed;
+    if (gx < 1) gx = 1;
+    k_proj_fast<KS, HB, F32IN, FULL><<<dim3(uint32_t(gx)), kThreads, lds, s>>>(a);
+    return hipGetLastError();
+}
+
+template <int KS, int HB>
+hipError_t launch_fast(const ProjArgs& a, hipStream_t s, int cus) {
+    if constexpr (HB == 8) {
+        if (a.width == 256 && a.heads == 8 && !a.r_in_z)
+            return a.x32 ? launch_fast_io<KS, HB, true, true>(a, s, cus)
+                         : launch_fast_io<KS, HB, false, true>(a, s, cus);
+    }
+    return a.x32 ? launch_fast_io<KS, HB, true, false>(a, s, cus) : launch_fast_io<KS, HB, false, false>(a, s, cus);
+}
+
+template <int HB>
+hipError_t launch_fast_ks(const ProjArgs& a, hipStream_t s, int cus) {
+    switch (a.ksteps) {
+        case 1: return launch_fast<1, HB>(a, s, cus);
+        case 2: return launch_fast<2, HB>(a, s, cus);
+        case 3: return launch_fast<3, HB>(a, s, cus);
+        case 4: return launch_fast<4, HB>(a, s, cus);
+        case 5: return launch_fast<5, HB>(a, s, cus);
+        case 6: return launch_fast<6, HB>(a, s, cus);
+        case 7: return launch_fast<7, HB>(a, s, cus);
+        case 8: return launch_fast<8, HB>(a, s, cus);
+        case 16: return launch_fast<16, HB>(a, s, cus);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+bool fast_supported_impl(const ProjArgs& a) {
+    const bool ks_ok = (a.ksteps >= 1 && a.ksteps <= 8) || a.ksteps == 16;
+    const bool hb_ok = a.head_blocks == 0 || a.head_blocks == 1 || a.head_blocks == 2 || a.head_blocks == 8;
+    return a.groups == 1 && ks_ok && hb_ok && a.n > 0;
 }
 
 template <int NMB>
@@ -148,7 +333,24 @@ int proj_blocks_per_group(int width) {
     return need <= 2 ? 2 : need <= 3 ? 3 : need <= 5 ? 5 : 9;
 }
 
+bool projection_fast_path(const ProjArgs& a) { return fast_supported_impl(a); }
+
+// The FP32-input form holds 32 bytes per k step; at 16 k steps and 8 head
+// blocks that no longer fits the registers.
+bool projection_fp32_input(const ProjArgs& a) {
+    return fast_supported_impl(a) && (a.ksteps <= 8 || a.head_blocks <= 2);
+}
+
 hipError_t launch_projection_mfma(const ProjArgs& a, hipStream_t s, int cus) {
+    if (a.x32 && !fast_supported_impl(a)) return hipErrorInvalidValue;  // FP32 input needs the fast path
+    if (fast_supported_impl(a)) {
+        switch (a.head_blocks) {
+            case 0: return launch_fast_ks<0>(a, s, cus);
+            case 1: return launch_fast_ks<1>(a, s, cus);
+            case 2: return launch_fast_ks<2>(a, s, cus);
+            default: return launch_fast_ks<8>(a, s, cus);
+        }
+    }
     switch (a.nmb) {
         case 2: return launch_nmb<2>(a, s, cus);
         case 3: return launch_nmb<3>(a, s, cus);
@@ -159,8 +361,10 @@ hipError_t launch_projection_mfma(const ProjArgs& a, hipStream_t s, int cus) {
 }
 
 // Packs W (bf16-rounded, [in][width]) and B_LR = W_bf16 a (hi/lo) into the
-// A-fragment order [group][kstep][block][lane][8]: lane l of block b at k step
-// ks holds W^T[32 b + l % 32][16 ks + 8 (l / 32) + j], j = 0..7.
+// A-fragment order [group][kstep][block][lane][8]: lane l of head block b at
+// k step ks holds W^T[32 b + phi(l % 32)][16 ks + 8 (l / 32) + j], j = 0..7,
+// with phi(c) = 16 ((c % 8) / 4) + 4 (c / 8) + c % 4; the L/R block is not
+// permuted.
 void pack_projection_weights(const float* wq, const float* al, const float* ar, int in, int heads, int dim,
                              std::vector<uint16_t>& out, int& ksteps, int& groups, int& nmb) {
     const int width = heads * dim;
@@ -195,10 +399,15 @@ void pack_projection_weights(const float* wq, const float* al, const float* ar, 
                 for (int l = 0; l < kWave; ++l)
                     for (int j = 0; j < 8; ++j) {
                         const int k = 16 * ks + 8 * (l / 32) + j, c = l % 32;
+                        // Head blocks: A row c (= D row c) carries feature phi(c), so that the
+                        // D rows a lane holds, 8 (r / 4) + 4 half + r % 4, are features
+                        // 16 half + r -- 16 consecutive features per lane.
+                        const int phi = 16 * ((c % 8) / 4) + 4 * (c / 8) + c % 4;
                         float v = 0.0f;
                         if (k < in) {
                             if (lr) v = lrcol[size_t(k) * 32 + c];
-                            else if (32 * (8 * g + b) + c < width) v = wq[size_t(k) * width + 32 * (8 * g + b) + c];
+                            else if (32 * (8 * g + b) + phi < width)
+                                v = wq[size_t(k) * width + 32 * (8 * g + b) + phi];
                         }
                         out[((((size_t(g) * ksteps + ks) * nmb + b) * kWave + l) * 8) + j] = bf16_rne(v);
                     }
