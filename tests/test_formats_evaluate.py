@@ -188,3 +188,42 @@ def test_evaluator_rejects(tmp_path, defect, msg):
         kw = {"max_accuracy_drop": 0.1}
     with pytest.raises(ValueError, match=msg):
         evaluate.evaluate(str(tmp_path / "out.f32"), 50, 4, labels, split, **kw)
+
+
+# ---------------------------------------------------------------- OGB converter
+def write_ogb_raw(root, x, edges, labels):
+    import gzip
+    raw = root / "raw"
+    raw.mkdir(parents=True)
+    for name, arr, fmt in (("node-feat", x, "%.9g"), ("edge", edges, "%d"), ("node-label", labels, "%d")):
+        with gzip.open(raw / f"{name}.csv.gz", "wt") as f:
+            np.savetxt(f, arr, delimiter=",", fmt=fmt)
+
+
+def test_ogb_converter_symmetrises_deduplicates_and_self_loops(tmp_path):
+    """implementation/tools/prepare_arxiv.py:26-36 on a hand-built edge list:
+    duplicates and both directions of one edge collapse, node 4 has no edge
+    and keeps only its self-loop; checked against scipy's COO -> CSR."""
+    from scipy import sparse
+    from gatgpu import ogb
+
+    rng = np.random.default_rng(0)
+    x = rng.standard_normal((6, 3)).astype(np.float32)
+    edges = np.array([[0, 1], [1, 0], [0, 1], [2, 3], [3, 3], [5, 0], [2, 5]])
+    labels = np.array([0, 2, 1, 1, 0, 2])
+    write_ogb_raw(tmp_path / "ds", x, edges, labels)
+    meta = ogb.convert(tmp_path / "ds", tmp_path / "out" / "g.gatbin", "tiny")
+    g = formats.load_graph(tmp_path / "out" / "g.gatbin")
+    n = 6
+    r = np.concatenate((edges[:, 1], edges[:, 0], np.arange(n)))
+    c = np.concatenate((edges[:, 0], edges[:, 1], np.arange(n)))
+    m = sparse.coo_matrix((np.ones(r.size), (r, c)), shape=(n, n)).tocsr()
+    m.sum_duplicates()
+    m.sort_indices()
+    assert np.array_equal(g["row"], m.indptr.astype(np.uint64))
+    assert np.array_equal(g["col"], m.indices.astype(np.uint32))
+    assert list(g["col"][g["row"][4]:g["row"][5]]) == [4]
+    assert np.array_equal(g["x"], x) and g["classes"] == 3
+    assert meta["edges"] == g["e"] == 2 * 4 + 6  # {0-1, 2-3, 0-5, 2-5} both ways + 6 loops (3-3 is a loop)
+    import json
+    assert json.loads((tmp_path / "out" / "g.json").read_text())["nodes"] == 6
