@@ -62,9 +62,17 @@ struct Items {
     int blocks;             // output blocks of 32 features (= heads at dim 32)
 };
 
+// Softmax modes: the online running max (aggregate-first), the exact row
+// max precomputed by k_af_rowmax (B1), or fixture weights (fixed-p).
+enum { kOnline = 0, kExact = 1, kFixed = 2 };
+
 // Persistent workgroups: W^T fragments of every block in LDS once, then wave
-// items (slot group, head group) heaviest first.
-template <int KS>
+// items (slot group, head group) heaviest first.  B1: the faithful
+// neighbour-step TFS of baseline/src/baseline_tfs.cpp:16-110 -- the weighted
+// row p X_j is rounded to bf16 (cvtneps_pbh there, v_cvt_pk_bf16_f32 here)
+// and multiplied by W_h with the sums resident in the MFMA accumulators;
+// otherwise the FP32 product X_j W_h is weighted by p afterwards.
+template <int KS, int SM, bool B1>
 __global__ void __launch_bounds__(kThreads, 2) k_af_ns(AfArgs a, Items it) {
     extern __shared__ uint4 wlds[];  // [block][ks][lane]
     const int nb_all = it.blocks;
@@ -115,21 +123,23 @@ __global__ void __launch_bounds__(kThreads, 2) k_af_ns(AfArgs a, Items it) {
             const uint64_t o = __shfl_xor(steps, off);
             steps = o > steps ? o : steps;
         }
-        // ---- per head of this wave: L and the running softmax state.  A chunk
-        // starts from the exact row max of its split row (per-chunk maxima of
-        // k_split_prescan), so its m never moves and the partials add up
-        // directly; a whole row keeps the running-maximum form of
+        // ---- per head of this wave: L and the softmax state.  Online mode: a
+        // chunk starts from the exact row max of its split row (per-chunk
+        // maxima of k_split_prescan), so its m never moves and the partials
+        // add up directly; a whole row keeps the running-maximum form of
         // tfs_online_fused (gat_tfs_online.cpp:86-117), rescaling its sums by
         // exp(m_old - m_new) when a step raises m.  The final m is max
-        // leaky(L + R_j) = leaky(L + max R_j) bit for bit.
+        // leaky(L + R_j) = leaky(L + max R_j) bit for bit.  Exact mode reads
+        // that max from a.mx (max_prescan, baseline_standard.cpp:44-51).
         float L[kMB], m[kMB], den[kMB];
 #pragma unroll
         for (int q = 0; q < kMB; ++q) {
-            L[q] = (valid && q < nb) ? a.L[uint64_t(i) * K + mb0 + q] : 0.0f;
+            L[q] = (SM != kFixed && valid && q < nb) ? a.L[uint64_t(i) * K + mb0 + q] : 0.0f;
             den[q] = 0.0f;
             m[q] = -INFINITY;
+            if (SM == kExact && valid && q < nb) m[q] = a.mx[uint64_t(i) * K + mb0 + q];
         }
-        if (chunk_item) {
+        if (SM == kOnline && chunk_item) {
 #pragma unroll
             for (int q = 0; q < kMB; ++q) {
                 float mc = -INFINITY;
@@ -147,12 +157,15 @@ __global__ void __launch_bounds__(kThreads, 2) k_af_ns(AfArgs a, Items it) {
         // Steps past a slot's last edge re-read that edge's row (weight 0), so
         // every load is unconditional and no absent row is ever multiplied.
         auto src = [&](uint64_t t) -> uint64_t { return a.pcol[len ? beg + (t < len ? t : len - 1) : 0]; };
-        auto fetch = [&](uint64_t j, uint4 (&xf)[KS], float (&rv)[kMB]) {
+        // rv: R of the source (softmax modes) or the fixture weight of the edge.
+        auto fetch = [&](uint64_t j, uint64_t t, uint4 (&xf)[KS], float (&rv)[kMB]) {
             const uint16_t* xr = a.X + j * kXS + 8 * half;
 #pragma unroll
             for (int ks = 0; ks < KS; ++ks) xf[ks] = *reinterpret_cast<const uint4*>(xr + 16 * ks);
+            const uint64_t e = len ? beg + (t < len ? t : len - 1) : 0;
 #pragma unroll
-            for (int q = 0; q < kMB; ++q) rv[q] = a.R[j * K + mb0 + (q < nb ? q : 0)];
+            for (int q = 0; q < kMB; ++q)
+                rv[q] = SM == kFixed ? a.fixp[e * K + mb0 + (q < nb ? q : 0)] : a.R[j * K + mb0 + (q < nb ? q : 0)];
         };
         auto frag = [&](int q, int ks) {
             return __builtin_bit_cast(bf16x8, wlds[(size_t(mb0 + q) * KS + ks) * kWave + l]);
@@ -162,12 +175,43 @@ __global__ void __launch_bounds__(kThreads, 2) k_af_ns(AfArgs a, Items it) {
             float p[kMB], scale[kMB];
 #pragma unroll
             for (int q = 0; q < kMB; ++q) {
-                const float sc_ = leaky(L[q] + rv[q]);
-                const float mn = ok ? fmaxf(m[q], sc_) : m[q];
-                scale[q] = mn > m[q] ? __expf(m[q] - mn) : 1.0f;  // exp(-inf) = 0 on the first edge
-                p[q] = ok ? __expf(sc_ - mn) : 0.0f;
-                m[q] = mn;
-                den[q] = den[q] * scale[q] + p[q];
+                scale[q] = 1.0f;
+                if constexpr (SM == kFixed) {
+                    p[q] = ok ? rv[q] : 0.0f;
+                } else if constexpr (SM == kExact) {
+                    p[q] = ok ? expf(leaky(L[q] + rv[q]) - m[q]) : 0.0f;
+                    den[q] += p[q];
+                } else {
+                    const float sc_ = leaky(L[q] + rv[q]);
+                    const float mn = ok ? fmaxf(m[q], sc_) : m[q];
+                    scale[q] = mn > m[q] ? __expf(m[q] - mn) : 1.0f;  // exp(-inf) = 0 on the first edge
+                    p[q] = ok ? __expf(sc_ - mn) : 0.0f;
+                    m[q] = mn;
+                    den[q] = den[q] * scale[q] + p[q];
+                }
+            }
+            if constexpr (B1) {
+                // bf16(p X_j) W_h accumulated in the MFMA: k step outer, heads
+                // inner (independent accumulation chains).
+#pragma unroll
+                for (int ks = 0; ks < KS; ++ks) {
+                    const uint32_t wv[4] = {x[ks].x, x[ks].y, x[ks].z, x[ks].w};
+                    float f[8];
+#pragma unroll
+                    for (int v = 0; v < 4; ++v) {
+                        f[2 * v] = __builtin_bit_cast(float, wv[v] << 16);
+                        f[2 * v + 1] = __builtin_bit_cast(float, wv[v] & 0xffff0000u);
+                    }
+#pragma unroll
+                    for (int q = 0; q < kMB; ++q) {
+                        if (q >= nb) continue;
+                        bf16x8 b;
+#pragma unroll
+                        for (int v = 0; v < 8; ++v) b[v] = (__bf16)(p[q] * f[v]);
+                        acc[q] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(frag(q, ks), b, acc[q], 0, 0, 0);
+                    }
+                }
+                return;
             }
             // Two heads at a time: two independent MFMA chains, and the next
             // k-step's W fragments read from LDS while this one multiplies.
@@ -193,13 +237,13 @@ __global__ void __launch_bounds__(kThreads, 2) k_af_ns(AfArgs a, Items it) {
                     a1 = n1;
                 }
                 // Rescale only when some slot of the wave raised its max.
-                if (__any(scale[q0] != 1.0f))
+                if (SM == kOnline && __any(scale[q0] != 1.0f))
 #pragma unroll
                     for (int r = 0; r < 16; ++r) acc[q0][r] *= scale[q0];
 #pragma unroll
                 for (int r = 0; r < 16; ++r) acc[q0][r] += p[q0] * T0[r];
                 if (two) {
-                    if (__any(scale[q0 + 1] != 1.0f))
+                    if (SM == kOnline && __any(scale[q0 + 1] != 1.0f))
 #pragma unroll
                         for (int r = 0; r < 16; ++r) acc[q0 + 1][r] *= scale[q0 + 1];
 #pragma unroll
@@ -212,14 +256,14 @@ __global__ void __launch_bounds__(kThreads, 2) k_af_ns(AfArgs a, Items it) {
         // step waits on one memory round trip that overlaps the previous step.
         uint4 xa[KS], xb[KS];
         float ra[kMB], rb[kMB];
-        fetch(src(0), xa, ra);
+        fetch(src(0), 0, xa, ra);
         uint64_t jb = src(1), ja = src(2);
         for (uint64_t t = 0; t < steps; t += 2) {
-            fetch(jb, xb, rb);
+            fetch(jb, t + 1, xb, rb);
             jb = src(t + 3);
             step(t, xa, ra);
             if (t + 1 >= steps) break;
-            fetch(ja, xa, ra);
+            fetch(ja, t + 2, xa, ra);
             ja = src(t + 4);
             step(t + 1, xb, rb);
         }
@@ -249,9 +293,10 @@ __global__ void __launch_bounds__(kThreads, 2) k_af_ns(AfArgs a, Items it) {
         for (int q = 0; q < kMB; ++q) {
             if (q >= nb) continue;
             const int h = mb0 + q;
+            if (SM == kFixed) den[q] = a.fixden[uint64_t(i) * K + h];  // the fixture's denominator
             const float scale = den[q] > 0.0f ? 1.0f / den[q] : 0.0f;
             if (half == 0) {
-                a.mx[uint64_t(i) * K + h] = M[q];
+                if (SM == kOnline) a.mx[uint64_t(i) * K + h] = M[q];
                 a.den[uint64_t(i) * K + h] = den[q];
             }
 #pragma unroll
@@ -276,6 +321,7 @@ __global__ void __launch_bounds__(kThreads, 2) k_af_ns(AfArgs a, Items it) {
 
 // One wave per split row (found at its first chunk): adds the chunks' partial
 // sums and denominators in chunk order, normalises, ELU, stores.
+template <int SM>
 __global__ void __launch_bounds__(kThreads) k_af_merge(AfArgs a, int blocks) {
     const int w = threadIdx.x / kWave, l = threadIdx.x % kWave;
     const uint64_t c = uint64_t(blockIdx.x) * kWaves + w;
@@ -299,11 +345,11 @@ __global__ void __launch_bounds__(kThreads) k_af_merge(AfArgs a, int blocks) {
             tot.z += v.z;
             tot.w += v.w;
             d += pq[kDenOff + h];
-            m = fmaxf(m, a.mchunk[(c + q) * 8 + h]);
+            if (SM == kOnline) m = fmaxf(m, a.mchunk[(c + q) * 8 + h]);
         }
-        const float M = leaky(a.L[uint64_t(i) * K + h] + m);
+        if (SM == kFixed) d = a.fixden[uint64_t(i) * K + h];
         if (f0 % 32 == 0) {
-            a.mx[uint64_t(i) * K + h] = M;
+            if (SM == kOnline) a.mx[uint64_t(i) * K + h] = leaky(a.L[uint64_t(i) * K + h] + m);
             a.den[uint64_t(i) * K + h] = d;
         }
         const float scale = d > 0.0f ? 1.0f / d : 0.0f;
@@ -321,18 +367,61 @@ __global__ void __launch_bounds__(kThreads) k_af_merge(AfArgs a, int blocks) {
     }
 }
 
-template <int KS>
+template <int KS, int SM, bool B1>
 hipError_t launch_ns(const AfArgs& a, const Items& it, hipStream_t s, int cus) {
     const size_t lds = size_t(it.blocks) * KS * kWave * sizeof(uint4);
     if (lds > 64 * 1024) {
-        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_af_ns<KS>),
+        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_af_ns<KS, SM, B1>),
                                            hipFuncAttributeMaxDynamicSharedMemorySize, int(lds));
         if (e != hipSuccess) return e;
     }
     const uint64_t waves = (it.chunk_groups + it.tile_groups) * uint64_t(it.waves_per_item);
     uint64_t blocks = (waves + kWaves - 1) / kWaves;
     if (blocks > uint64_t(cus) * 2) blocks = uint64_t(cus) * 2;
-    k_af_ns<KS><<<dim3(uint32_t(blocks)), kThreads, lds, s>>>(a, it);
+    k_af_ns<KS, SM, B1><<<dim3(uint32_t(blocks)), kThreads, lds, s>>>(a, it);
+    return hipGetLastError();
+}
+
+template <int SM, bool B1>
+hipError_t launch_ns_ks(const AfArgs& a, const Items& it, hipStream_t s, int cus) {
+    switch (a.ksteps) {
+        case 1: return launch_ns<1, SM, B1>(a, it, s, cus);
+        case 2: return launch_ns<2, SM, B1>(a, it, s, cus);
+        case 3: return launch_ns<3, SM, B1>(a, it, s, cus);
+        case 4: return launch_ns<4, SM, B1>(a, it, s, cus);
+        case 5: return launch_ns<5, SM, B1>(a, it, s, cus);
+        case 6: return launch_ns<6, SM, B1>(a, it, s, cus);
+        case 7: return launch_ns<7, SM, B1>(a, it, s, cus);
+        default: return launch_ns<8, SM, B1>(a, it, s, cus);
+    }
+}
+
+// Exact row max for the B1 path (max_prescan, baseline_standard.cpp:44-51):
+// M[i, h] = LeakyReLU(L[i, h] + max_j R[j, h]), 0 for an empty row.  One wave
+// per degree-sorted row; lane l covers edges l / K + (64 / K) q of head l % K.
+template <int K>
+__global__ void __launch_bounds__(kThreads) k_af_rowmax(AfArgs a) {
+    const int w = threadIdx.x / kWave, l = threadIdx.x % kWave;
+    const uint64_t k = uint64_t(blockIdx.x) * kWaves + w;
+    if (k >= a.n) return;
+    const uint32_t i = a.perm[k];
+    const uint64_t beg = a.prow[k], end = a.prow[k + 1];
+    if (i >= a.n || beg > end || end > a.e) return;
+    const int h = l % K;
+    float m = -INFINITY;
+    for (uint64_t e = beg + l / K; e < end; e += kWave / K) m = fmaxf(m, a.R[uint64_t(a.pcol[e]) * K + h]);
+    for (int off = K; off < kWave; off <<= 1) m = fmaxf(m, __shfl_xor(m, off));
+    if (l < K) a.mx[uint64_t(i) * K + l] = end > beg ? leaky(a.L[uint64_t(i) * K + l] + m) : 0.0f;
+}
+
+hipError_t launch_rowmax(const AfArgs& a, hipStream_t s) {
+    const dim3 grid(uint32_t((a.n + kWaves - 1) / kWaves));
+    switch (a.heads) {
+        case 1: k_af_rowmax<1><<<grid, kThreads, 0, s>>>(a); break;
+        case 2: k_af_rowmax<2><<<grid, kThreads, 0, s>>>(a); break;
+        case 4: k_af_rowmax<4><<<grid, kThreads, 0, s>>>(a); break;
+        default: k_af_rowmax<8><<<grid, kThreads, 0, s>>>(a); break;
+    }
     return hipGetLastError();
 }
 
@@ -352,7 +441,7 @@ hipError_t launch_aggregate_af(const AfArgs& a, hipStream_t s, int cus) {
     it.waves_per_item = (it.blocks + kMB - 1) / kMB;
     it.chunk_groups = (a.chunks + kSlots - 1) / kSlots;
     it.tile_groups = (a.rows + kSlots - 1) / kSlots;
-    if (a.chunks) {
+    if (a.chunks && !a.fixp && !a.b1) {
         SplitTable t{};
         t.chunks = a.chunks;
         t.chunk_k = a.chunk_k;
@@ -362,21 +451,25 @@ hipError_t launch_aggregate_af(const AfArgs& a, hipStream_t s, int cus) {
         hipError_t e = launch_split_prescan(a.prow, a.pcol, a.R, a.heads, t, a.e, s);
         if (e != hipSuccess) return e;
     }
-    if (it.chunk_groups + it.tile_groups) {
-        hipError_t e = hipSuccess;
-        switch (a.ksteps) {
-            case 1: e = launch_ns<1>(a, it, s, cus); break;
-            case 2: e = launch_ns<2>(a, it, s, cus); break;
-            case 3: e = launch_ns<3>(a, it, s, cus); break;
-            case 4: e = launch_ns<4>(a, it, s, cus); break;
-            case 5: e = launch_ns<5>(a, it, s, cus); break;
-            case 6: e = launch_ns<6>(a, it, s, cus); break;
-            case 7: e = launch_ns<7>(a, it, s, cus); break;
-            default: e = launch_ns<8>(a, it, s, cus); break;
-        }
+    const int sm = a.fixp ? kFixed : a.b1 ? kExact : kOnline;
+    if (sm == kExact) {
+        hipError_t e = launch_rowmax(a, s);
         if (e != hipSuccess) return e;
     }
-    if (a.chunks) k_af_merge<<<dim3(uint32_t((a.chunks + kWaves - 1) / kWaves)), kThreads, 0, s>>>(a, it.blocks);
+    if (it.chunk_groups + it.tile_groups) {
+        hipError_t e = hipSuccess;
+        if (sm == kOnline) e = launch_ns_ks<kOnline, false>(a, it, s, cus);
+        else if (sm == kExact) e = launch_ns_ks<kExact, true>(a, it, s, cus);
+        else if (a.b1) e = launch_ns_ks<kFixed, true>(a, it, s, cus);
+        else e = launch_ns_ks<kFixed, false>(a, it, s, cus);
+        if (e != hipSuccess) return e;
+    }
+    if (a.chunks) {
+        const dim3 grid(uint32_t((a.chunks + kWaves - 1) / kWaves));
+        if (sm == kOnline) k_af_merge<kOnline><<<grid, kThreads, 0, s>>>(a, it.blocks);
+        else if (sm == kExact) k_af_merge<kExact><<<grid, kThreads, 0, s>>>(a, it.blocks);
+        else k_af_merge<kFixed><<<grid, kThreads, 0, s>>>(a, it.blocks);
+    }
     return hipGetLastError();
 }
 

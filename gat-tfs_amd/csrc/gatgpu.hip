@@ -248,7 +248,7 @@ int z_stride(int precision, int heads, int width, bool* r_in_z) {
 int resolve_dataflow(const LayerState& L, int precision, int dataflow) {
     const bool af_ok = precision == GATGPU_BF16 && aggregate_af_supported(L.in, L.heads, L.dim);
     if (dataflow == GATGPU_AUTO) return GATGPU_TRANSFORM_FIRST;
-    if (dataflow == GATGPU_AGGREGATE_FIRST && !af_ok) return -1;
+    if ((dataflow == GATGPU_AGGREGATE_FIRST || dataflow == GATGPU_TFS_B1) && !af_ok) return -1;
     return dataflow;
 }
 
@@ -261,8 +261,10 @@ float ms_between(hipEvent_t a, hipEvent_t b) {
 // Aggregate-first bf16 layer: convert the input to bf16 rows of 128, the
 // L/R-only MFMA front end (reordered contraction), then the aggregate-first
 // kernels (tiles of 32 rows + split-row chunks).
-int run_layer_af(gatgpu_ctx* c, int l, bool hidden, const float* src32, const uint16_t* srcbf, int ev_base) {
+int run_layer_af(gatgpu_ctx* c, int l, bool hidden, const float* src32, const uint16_t* srcbf, int ev_base,
+                 int dataflow, bool fixed) {
     LayerState& Ls = c->L[l];
+    if (fixed) hidden = false;
     const uint64_t n = c->n;
     const int K = Ls.heads, W = Ls.width(), D = Ls.in, xs = af_input_stride();
     HIPCHECK(c, Ls.left.ensure(n * K * 4));
@@ -278,6 +280,8 @@ int run_layer_af(gatgpu_ctx* c, int l, bool hidden, const float* src32, const ui
         srcbf = nullptr;
     }
     if (src32) HIPCHECK(c, Ls.inbf.ensure(n * xs * 2));
+    // The fixed-p operator has no row max (the reference leaves it unset).
+    if (fixed) HIPCHECK(c, hipMemsetAsync(Ls.mx.p, 0, n * K * 4, c->stream));
     if (ev_base >= 0) HIPCHECK(c, hipEventRecord(c->ev[ev_base], c->stream));
     if (src32) {
         HIPCHECK(c, launch_to_bf16_pad(src32, Ls.inbf.as<uint16_t>(), n, D, xs, c->stream));
@@ -329,11 +333,14 @@ int run_layer_af(gatgpu_ctx* c, int l, bool hidden, const float* src32, const ui
     a.mchunk = c->split.mchunk;
     a.part = c->split.part;
     a.counter = c->split.counter;
+    a.b1 = dataflow == GATGPU_TFS_B1;
+    a.fixp = fixed ? Ls.fixp.as<float>() : nullptr;
+    a.fixden = fixed ? Ls.fixden.as<float>() : nullptr;
     HIPCHECK(c, launch_aggregate_af(a, c->stream, c->cus));
     if (ev_base >= 0) HIPCHECK(c, hipEventRecord(c->ev[ev_base + 3], c->stream));
     Ls.ran = true;
     Ls.precision = GATGPU_BF16;
-    Ls.dataflow = GATGPU_AGGREGATE_FIRST;
+    Ls.dataflow = dataflow;
     Ls.z_valid = false;
     Ls.out32_valid = !hidden;
     Ls.outbf_valid = hidden;
@@ -367,7 +374,8 @@ int run_layer(gatgpu_ctx* c, int l, int precision, int dataflow, bool hidden, co
         else if (P.out32_valid) src32 = P.out32.as<float>();
         else return fail(c, GATGPU_ESTATE, "previous layer output missing");
     }
-    if (dataflow == GATGPU_AGGREGATE_FIRST) return run_layer_af(c, l, hidden, src32, srcbf, ev_base);
+    if (dataflow == GATGPU_AGGREGATE_FIRST || dataflow == GATGPU_TFS_B1)
+        return run_layer_af(c, l, hidden, src32, srcbf, ev_base, dataflow, fixed);
     // ---- outputs
     HIPCHECK(c, Ls.left.ensure(n * K * 4));
     HIPCHECK(c, Ls.right.ensure(n * K * 4));
@@ -481,7 +489,8 @@ void fill_times(gatgpu_ctx* c, int ev_base, gatgpu_times* t, int dataflow) {
     // Transform-first: the MFMA projection with its fused L/R block.
     // Aggregate-first: the L/R front end only; the projection runs inside the
     // aggregation kernel and is counted in aggregate_ms.
-    if (dataflow == GATGPU_AGGREGATE_FIRST) t->lr_ms = ms_between(c->ev[ev_base + 1], c->ev[ev_base + 2]);
+    if (dataflow == GATGPU_AGGREGATE_FIRST || dataflow == GATGPU_TFS_B1)
+        t->lr_ms = ms_between(c->ev[ev_base + 1], c->ev[ev_base + 2]);
     else t->projection_ms = ms_between(c->ev[ev_base + 1], c->ev[ev_base + 2]);
     t->aggregate_ms = ms_between(c->ev[ev_base + 2], c->ev[ev_base + 3]);
     t->total_ms = ms_between(c->ev[ev_base], c->ev[ev_base + 3]);
@@ -665,7 +674,7 @@ int gatgpu_layer_forward(gatgpu_ctx* c, int layer, int precision, int dataflow, 
     if (int r = check_ctx(c)) return r;
     if (layer < 0 || layer > 2) return fail(c, GATGPU_EINVAL, "layer must be 0, 1 or 2");
     if (precision != GATGPU_FP32 && precision != GATGPU_BF16) return fail(c, GATGPU_EINVAL, "bad precision");
-    if (dataflow < GATGPU_AUTO || dataflow > GATGPU_AGGREGATE_FIRST) return fail(c, GATGPU_EINVAL, "bad dataflow");
+    if (dataflow < GATGPU_AUTO || dataflow > GATGPU_TFS_B1) return fail(c, GATGPU_EINVAL, "bad dataflow");
     if (!c->graph) return fail(c, GATGPU_ESTATE, "graph not set");
     if (!c->L[layer].set) return fail(c, GATGPU_ESTATE, "layer weights not set");
     if (input) {
@@ -730,8 +739,7 @@ int gatgpu_fixed_p_forward(gatgpu_ctx* c, int layer, int precision, int dataflow
     if (int r = check_ctx(c)) return r;
     if (layer < 0 || layer > 2) return fail(c, GATGPU_EINVAL, "layer must be 0, 1 or 2");
     if (precision != GATGPU_FP32 && precision != GATGPU_BF16) return fail(c, GATGPU_EINVAL, "bad precision");
-    if (dataflow != GATGPU_AUTO && dataflow != GATGPU_TRANSFORM_FIRST)
-        return fail(c, GATGPU_EINVAL, "the fixed-p operator is transform-first");
+    if (dataflow < GATGPU_AUTO || dataflow > GATGPU_TFS_B1) return fail(c, GATGPU_EINVAL, "bad dataflow");
     if (!c->graph) return fail(c, GATGPU_ESTATE, "graph not set");
     if (!c->L[layer].set) return fail(c, GATGPU_ESTATE, "layer weights not set");
     if (!c->L[layer].fixed_set) return fail(c, GATGPU_ESTATE, "fixture p/den not set for this layer");
@@ -740,10 +748,16 @@ int gatgpu_fixed_p_forward(gatgpu_ctx* c, int layer, int precision, int dataflow
         if (!all_finite(input, c->n * uint64_t(c->L[layer].in), &bad))
             return fail(c, GATGPU_ENONFINITE, "nonfinite layer input index=" + std::to_string(bad));
     }
-    if (int r = run_layer(c, layer, precision, GATGPU_TRANSFORM_FIRST, false, input, times ? 0 : -1, true)) return r;
+    int flow = dataflow == GATGPU_AUTO ? GATGPU_TRANSFORM_FIRST : dataflow;
+    if (flow != GATGPU_TRANSFORM_FIRST) {
+        flow = resolve_dataflow(c->L[layer], precision, flow);
+        if (flow < 0)
+            return fail(c, GATGPU_EINVAL, "aggregate-first needs bf16, head_dim 32, 1/2/4/8 heads and in <= 128");
+    }
+    if (int r = run_layer(c, layer, precision, flow, false, input, times ? 0 : -1, true)) return r;
     HIPCHECK(c, hipStreamSynchronize(c->stream));
     HIPCHECK(c, hipGetLastError());
-    if (times) fill_times(c, 0, times, GATGPU_TRANSFORM_FIRST);
+    if (times) fill_times(c, 0, times, flow);
     return GATGPU_OK;
 }
 
@@ -751,7 +765,7 @@ int gatgpu_model_forward(gatgpu_ctx* c, int precision, int dataflow, float* logi
                          double* total_ms) {
     if (int r = check_ctx(c)) return r;
     if (precision != GATGPU_FP32 && precision != GATGPU_BF16) return fail(c, GATGPU_EINVAL, "bad precision");
-    if (dataflow < GATGPU_AUTO || dataflow > GATGPU_AGGREGATE_FIRST) return fail(c, GATGPU_EINVAL, "bad dataflow");
+    if (dataflow < GATGPU_AUTO || dataflow > GATGPU_TFS_B1) return fail(c, GATGPU_EINVAL, "bad dataflow");
     if (!c->graph || !c->input) return fail(c, GATGPU_ESTATE, "graph or features not set");
     for (int l = 0; l < 3; ++l)
         if (!c->L[l].set) return fail(c, GATGPU_ESTATE, "layer weights not set");

@@ -191,6 +191,9 @@ struct AfArgs {
     const float* mchunk;
     float* part;         // [chunks][8*128 + 8]
     uint32_t* counter;
+    bool b1;             // bf16(p X_j) W_h, exact max (faithful neighbour-step TFS)
+    const float* fixp;   // fixed-p: fixture p in degree-sorted edge order [e][heads], else null
+    const float* fixden; // fixed-p: fixture denominators [n][heads]
 };
 bool aggregate_af_supported(int in, int heads, int dim);
 int af_input_stride();

@@ -18,7 +18,7 @@ LIB_PATH = PKG_ROOT / "lib" / "libgatgpu.so"
 
 OK, EINVAL, ESTATE, ENODEV, ENOMEM, EDEVICE, ENONFINITE, EOVERFLOW = 0, -1, -2, -3, -4, -5, -6, -7
 FP32, BF16 = 0, 1
-AUTO, TRANSFORM_FIRST, AGGREGATE_FIRST = 0, 1, 2
+AUTO, TRANSFORM_FIRST, AGGREGATE_FIRST, TFS_B1 = 0, 1, 2, 3
 STAGE_Z, STAGE_LEFT, STAGE_RIGHT, STAGE_MAX, STAGE_DEN, STAGE_OUT = range(6)
 OPT_BLOCK_ROW_MIN_DEGREE, OPT_SPLIT_ROW_MIN_DEGREE, OPT_SPLIT_CHUNK_EDGES, OPT_SMALL_ROW_MAX_DEGREE = 1, 2, 3, 4
 

@@ -61,7 +61,12 @@ enum { GATGPU_FP32 = 0, GATGPU_BF16 = 1 };
  * or 8 heads and in <= 128.  AUTO selects the faster dataflow for the layer
  * shape on gfx950.  gatgpu_model_forward with AGGREGATE_FIRST uses it on the
  * layers that support it and transform-first on the others. */
-enum { GATGPU_AUTO = 0, GATGPU_TRANSFORM_FIRST = 1, GATGPU_AGGREGATE_FIRST = 2 };
+/* TFS_B1 is the faithful neighbour-step TFS ("tfs_bf16",
+ * baseline/src/baseline_tfs.cpp:16-110, max_prescan first): per step the
+ * weighted source row p X_j is rounded to bf16 and multiplied by W_h with FP32
+ * sums, the exact row max taken before any exponent.  Same shape limits as
+ * AGGREGATE_FIRST; used for dataflow comparisons, not selected by AUTO. */
+enum { GATGPU_AUTO = 0, GATGPU_TRANSFORM_FIRST = 1, GATGPU_AGGREGATE_FIRST = 2, GATGPU_TFS_B1 = 3 };
 
 /* Stage selectors for gatgpu_get_stage (Workspace fields, gat.hpp:96-106). */
 enum {
@@ -167,9 +172,11 @@ int gatgpu_set_fixed_p(gatgpu_ctx* ctx, int layer, const float* p, const float* 
  * 103-150, "standard_op"): projection Z = XW in `precision`, then
  * out = (sum_e p[e] Z[col[e]]) * (den > 0 ? 1/den : 0) with the fixture's p
  * and den and no activation (standard_aggregate with fixed_p and finish,
- * baseline/src/baseline_standard.cpp:52-97).  dataflow must be AUTO or
- * TRANSFORM_FIRST.  input as in gatgpu_layer_forward.  Stages: Z, LEFT, RIGHT
- * from the projection, DEN = the fixture's den, MAX zero, OUT FP32. */
+ * baseline/src/baseline_standard.cpp:52-97).  dataflow TFS_B1 is the
+ * reference's "tfs_op" of the same mode (tfs_aggregate with fixed_p,
+ * baseline_tfs.cpp:16-110), AGGREGATE_FIRST the FP32-product variant; both
+ * bf16 only.  input as in gatgpu_layer_forward.  Stages: Z (transform-first),
+ * LEFT, RIGHT from the projection, DEN = the fixture's den, MAX zero, OUT FP32. */
 int gatgpu_fixed_p_forward(gatgpu_ctx* ctx, int layer, int precision, int dataflow, const float* input,
                            gatgpu_times* times);
 

@@ -58,6 +58,7 @@ def lib():
         L.or_fp64_layer.argtypes = [u64, P, P, P, i32, i32, i32, P, P, P, i32] + [P] * 6
         L.or_standard_layer.argtypes = [u64, P, P, P, i32, i32, i32, P, P, P, i32, i32, i32] + [P] * 8
         L.or_fixed_p_layer.argtypes = [u64, P, P, P, i32, i32, i32, P, P, P, i32, P, P]
+        L.or_b1_layer.argtypes = [u64, P, P, P, i32, i32, i32, P, P, P, i32, P]
         L.or_degree_schedule.argtypes = [u64, P, P, P]
         L.or_permute_csr.argtypes = [u64, P, P, P, P, P]
         L.or_choose_R.argtypes = [u64, u64, P]
@@ -271,6 +272,22 @@ def fixed_p_layer(row, col, x, p, P, den, bf16):
     lib().or_fixed_p_layer(n, _p(row), _p(col), _p(x), p["in"], p["heads"], p["dim"], _p(p["w"]), _p(P), _p(den),
                            int(bool(bf16)), _p(o["z"]), _p(o["out"]))
     return o
+
+
+def b1_layer(row, col, xq, p, wq, P, den, hidden):
+    """Neighbour-step TFS with bf16-rounded p x (baseline/src/baseline_tfs.cpp:16-110;
+    emulation of baseline/bench/main.cpp:139-143).  xq, wq: bf16-rounded FP32;
+    P [e][heads], den [n][heads] -> out [n][heads*dim]."""
+    row, col = _graph_args(row, col)
+    xq = np.ascontiguousarray(xq, np.float32)
+    wq = np.ascontiguousarray(wq, np.float32)
+    P = np.ascontiguousarray(P, np.float32)
+    den = np.ascontiguousarray(den, np.float32)
+    n = row.size - 1
+    out = np.empty((n, p["heads"] * p["dim"]), np.float32)
+    lib().or_b1_layer(n, _p(row), _p(col), _p(xq), p["in"], p["heads"], p["dim"], _p(wq), _p(P), _p(den),
+                      int(bool(hidden)), _p(out))
+    return out
 
 
 def ref_model(row, col, x, model):

@@ -19,6 +19,9 @@
 //   or_fp64_layer          NumPy FP64 restatement of baseline/tests/oracle.py (1e-9)
 //   or_fixed_p_layer       fed R0's own p and den it reproduces R0's output (1e-6);
 //                          a hand-computed three-node case
+//   or_b1_layer            with weights p whose products p x round exactly in bf16 it
+//                          equals or_fixed_p_layer on bf16 inputs bit for bit; a
+//                          hand-computed case where the bf16 rounding of p x shows
 //   or_standard_layer (B0) the logged standard_bf16 stage errors and chain error
 //   or_degree_schedule,    numpy.lexsort on (degree, id); neighbor_steps definition;
 //   or_permute_csr         row-by-row copy check
@@ -257,6 +260,41 @@ void or_fixed_p_layer(uint64_t n, const uint64_t* row, const uint32_t* col, cons
             const float d = den[i * K + h];
             const float scale = d > 0 ? 1 / d : 0;
             for (int c = 0; c < dim; ++c) oi[h * dim + c] *= scale;
+        }
+    }
+}
+
+// Neighbour-step TFS with bf16 weighted rows (B1, baseline/src/baseline_tfs.cpp:
+// 16-110, and the explicit emulation of baseline/bench/main.cpp:139-143):
+// out[i, h, :] = sum_e sum_k expand(rne(p[e, h] * xq[col[e], k])) * wq[k, h, :],
+// then / den (0 if den == 0) and ELU when hidden.  xq and wq are bf16-rounded
+// values held in FP32; p [e][heads] and den [n][heads] are given (computed
+// from L/R and the exact max, or a fixture's).
+void or_b1_layer(uint64_t n, const uint64_t* row, const uint32_t* col, const float* xq, int in, int heads,
+                 int dim, const float* wq, const float* p, const float* den, int hidden, float* out) {
+    const int K = heads, W = heads * dim;
+    #pragma omp parallel for schedule(dynamic, 64)
+    for (uint64_t i = 0; i < n; ++i) {
+        float* oi = out + i * W;
+        for (int c = 0; c < W; ++c) oi[c] = 0.0f;
+        for (uint64_t e = row[i]; e < row[i + 1]; ++e) {
+            const float* xj = xq + uint64_t(col[e]) * in;
+            for (int h = 0; h < K; ++h) {
+                const float pe = p[e * K + h];
+                for (int k = 0; k < in; ++k) {
+                    const float v = expand(rne(pe * xj[k]));
+                    const float* wk = wq + size_t(k) * W + h * dim;
+                    for (int d = 0; d < dim; ++d) oi[h * dim + d] += v * wk[d];
+                }
+            }
+        }
+        for (int h = 0; h < K; ++h) {
+            const float d_ = den[i * K + h];
+            const float scale = d_ > 0 ? 1 / d_ : 0;
+            for (int c = 0; c < dim; ++c) {
+                const float y = d_ > 0 ? oi[h * dim + c] * scale : 0.0f;
+                oi[h * dim + c] = hidden ? elu(y) : y;
+            }
         }
     }
 }

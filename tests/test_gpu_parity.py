@@ -276,6 +276,7 @@ def test_fixed_p_operator(gpu_ctx, graph, D, K, d):
     r = oracle.ref_layer(row, col, x, p, False, edge_stages=True)
     m32 = oracle.fixed_p_layer(row, col, x, p, r["p"], r["den"], False)["out"]
     m16 = oracle.fixed_p_layer(row, col, x, p, r["p"], r["den"], True)["out"]
+    b1 = oracle.b1_layer(row, col, oracle.quantize_bf16(x), p, oracle.quantize_bf16(p["w"]), r["p"], r["den"], False)
     gpu_ctx.set_graph(row, col)
     gpu_ctx.set_layer(0, p)
     gpu_ctx.set_fixed_p(0, r["p"], r["den"])
@@ -289,6 +290,17 @@ def test_fixed_p_operator(gpu_ctx, graph, D, K, d):
         gpu_ctx.fixed_p_forward(0, gatgpu.BF16, input=x)
         e = oracle.errors(m16, gpu_ctx.stage(0, "out"))
         assert e["finite"] and e["relative_l2"] < BF16_REL_L2, (opts, e)
+        if d == 32 and D <= 128 and K in (1, 2, 4, 8):
+            # The reference's tfs_op of the same mode (baseline_tfs.cpp with fixed_p):
+            # bf16(p x) W summed in FP32, against the oracle's emulation; and the
+            # FP32-product aggregate-first form against the bf16-input master.
+            gpu_ctx.fixed_p_forward(0, gatgpu.BF16, gatgpu.TFS_B1, input=x)
+            e = oracle.errors(b1, gpu_ctx.stage(0, "out"))
+            assert e["finite"] and e["relative_l2"] < 1e-5, (opts, e)
+            assert np.array_equal(gpu_ctx.stage(0, "den"), r["den"])
+            gpu_ctx.fixed_p_forward(0, gatgpu.BF16, gatgpu.AGGREGATE_FIRST, input=x)
+            e = oracle.errors(m16, gpu_ctx.stage(0, "out"))
+            assert e["finite"] and e["relative_l2"] < 1e-5, (opts, e)
         for k in opts:
             gpu_ctx.set_option(k, DEFAULT_OPTIONS[k])
 
@@ -428,6 +440,47 @@ def test_aggregate_first_layer(gpu_ctx, D, K, d):
             assert oracle.errors(r32["out"], out)["relative_l2"] < BF16_REL_L2
             for k_ in ("max", "den"):
                 assert oracle.errors(r[k_], gpu_ctx.stage(0, k_))["relative_l2"] < 1e-4, (k_, opts)
+
+
+@pytest.mark.parametrize("D,K,d", AF_SHAPES)
+def test_tfs_b1_layer(gpu_ctx, D, K, d):
+    """Faithful neighbour-step TFS (baseline/src/baseline_tfs.cpp:16-110): the
+    row max is exact (equal bit for bit to the scalar max of LeakyReLU(L + R)
+    over the GPU's own L/R), and the output equals the oracle's emulation
+    sum_e sum_k bf16(p x) W / den with p from the same L/R and max."""
+    w = inputs.WORKLOADS["smoke"]
+    row, col = w.graph()
+    x = inputs.normal((w.n, D), 23)
+    p = inputs.glorot_param(D, K, d, 24)
+    xq, wq = oracle.quantize_bf16(x), oracle.quantize_bf16(p["w"])
+    deg = np.diff(row).astype(np.int64)
+    dst = np.repeat(np.arange(w.n), deg)
+    for hidden in (False, True):
+        r32 = oracle.ref_layer(row, col, x, p, hidden)
+        for opts in SCHEDULES:
+            gpu_ctx.set_graph(row, col)
+            for k_, v_ in opts.items():
+                gpu_ctx.set_option(k_, v_)
+            gpu_ctx.set_layer(0, p)
+            gpu_ctx.set_input(x)
+            gpu_ctx.layer_forward(0, gatgpu.BF16, gatgpu.TFS_B1, hidden)
+            for k_ in opts:
+                gpu_ctx.set_option(k_, DEFAULT_OPTIONS[k_])
+            L, R, M = gpu_ctx.stage(0, "left"), gpu_ctx.stage(0, "right"), gpu_ctx.stage(0, "max")
+            s = L[dst] + R[col]
+            s = np.where(s >= 0, s, np.float32(0.2) * s).astype(np.float32)
+            mfull = np.full((w.n, K), -np.inf, np.float32)
+            np.maximum.at(mfull, dst, s)
+            mref = np.where(deg[:, None] > 0, mfull, 0).astype(np.float32)
+            assert np.array_equal(M, mref), opts
+            P = np.exp(s - M[dst]).astype(np.float32)
+            den = np.zeros((w.n, K), np.float32)
+            np.add.at(den, dst, P)
+            want = oracle.b1_layer(row, col, xq, p, wq, P, den, hidden)
+            got = gpu_ctx.stage(0, "out")
+            e = oracle.errors(oracle.quantize_bf16(want) if hidden else want, got)
+            assert e["finite"] and e["relative_l2"] < (4e-3 if hidden else 1e-4), (hidden, opts, e)
+            assert oracle.errors(r32["out"], got)["relative_l2"] < BF16_REL_L2
 
 
 def test_aggregate_first_matches_transform_first_on_arxiv(gpu_ctx):

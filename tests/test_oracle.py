@@ -304,3 +304,34 @@ def test_fixed_p_bf16_rounds_only_the_inputs():
     assert np.array_equal(o16["out"], o32["out"])
     assert not np.array_equal(o16["out"], oracle.fixed_p_layer(g["row"], g["col"], g["x"], m[0], r["p"],
                                                                 r["den"], False)["out"])
+
+
+# ---------------------------------------------------------------- neighbour-step TFS (B1)
+def test_b1_rounds_each_weighted_row_to_bf16():
+    """One edge, x = 1 + 2^-7 (exact in bf16), p = 0.7: p x = 0.70546875
+    rounds to the bf16 value 0.70703125, which is what B1 multiplies by W."""
+    row = np.array([0, 1], np.uint64)
+    col = np.array([0], np.uint32)
+    x = np.array([[1.0078125]], np.float32)
+    p = {"in": 1, "heads": 1, "dim": 1}
+    out = oracle.b1_layer(row, col, x, p, np.ones((1, 1), np.float32), np.array([[0.7]], np.float32),
+                          np.ones((1, 1), np.float32), False)
+    assert out[0, 0] == np.float32(0.70703125)
+
+
+def test_b1_equals_fixed_p_when_products_are_exact():
+    """With weights that are powers of two, every p x is exact in bf16, so B1 is
+    the fixed-p operator on bf16 inputs up to summation order."""
+    g = smoke1024()
+    m = oracle.random_model(128, 40, 11)
+    p = dict(m[0])
+    rng = np.random.default_rng(4)
+    E, K = g["col"].size, p["heads"]
+    P = (2.0 ** -rng.integers(0, 4, (E, K))).astype(np.float32)
+    den = np.zeros((g["n"], K), np.float32)
+    np.add.at(den, np.repeat(np.arange(g["n"]), np.diff(g["row"]).astype(np.int64)), P)
+    xq, wq = oracle.quantize_bf16(g["x"]), oracle.quantize_bf16(p["w"])
+    b1 = oracle.b1_layer(g["row"], g["col"], xq, p, wq, P, den, False)
+    fx = oracle.fixed_p_layer(g["row"], g["col"], g["x"], p, P, den, True)["out"]
+    e = oracle.errors(fx, b1)
+    assert e["finite"] and e["relative_l2"] < 1e-6, e
