@@ -152,7 +152,8 @@ int dataflow_of(const std::string& s) {
     if (s == "auto") return GATGPU_AUTO;
     if (s == "transform_first") return GATGPU_TRANSFORM_FIRST;
     if (s == "aggregate_first") return GATGPU_AGGREGATE_FIRST;
-    throw std::runtime_error("bad --dataflow (auto | transform_first | aggregate_first)");
+    if (s == "tfs_b1") return GATGPU_TFS_B1;
+    throw std::runtime_error("bad --dataflow (auto | transform_first | aggregate_first | tfs_b1)");
 }
 
 int run(int argc, char** argv) {
@@ -259,33 +260,52 @@ int run(int argc, char** argv) {
         return pass ? 0 : 1;
     }
 
-    if (mode == "fixed-p") {  // main.cpp:103-150 with the GPU standard operator
+    if (mode == "fixed-p") {  // main.cpp:103-150: standard_op and, where it applies, tfs_op
         const int l = layer ? layer : 2;
         const Param& p = model[l - 1];
         if (!a.has("--fixture")) throw std::runtime_error("--fixture (GATFIX1) is required");
         const Fixture fixture = load_fixture(g, p, a.get("--fixture"));
-        Workspace w;
+        const bool tfs = precision == GATGPU_BF16 && p.dim == 32 && p.in <= 128 &&
+                         (p.heads == 1 || p.heads == 2 || p.heads == 4 || p.heads == 8);
+        Workspace sw, tw;
         Times t;
-        gpu.fixed_p(g, p, l - 1, fixture, w, t, precision);
-        require_finite(w.out, "fixed-p GPU");
-        if (a.has("--reference")) {  // FP32 fixed-p master output (main.cpp:136-137), one f32 dump
-            const Error e = errors(read_dump(a.get("--reference"), checked(g.n, uint64_t(p.width()))), w.out);
-            print_error(path + "_fixed_p", l, "vs_master_fixed_p", e);
+        gpu.fixed_p(g, p, l - 1, fixture, sw, t, precision);
+        require_finite(sw.out, "fixed-p standard");
+        if (tfs) {
+            gpu.fixed_p(g, p, l - 1, fixture, tw, t, precision, GATGPU_TFS_B1);
+            require_finite(tw.out, "fixed-p TFS");
+            print_error("tfs_b1_fixed_p", l, "vs_standard_extra_pX_quantization_and_reduction", errors(sw.out, tw.out));
         }
-        if (a.has("--output")) write_dump(a.get("--output"), w.out);
-        std::vector<double> tot, agg;
+        if (a.has("--reference")) {  // FP32 fixed-p master output (main.cpp:136-137), one f32 dump
+            const std::vector<float> master = read_dump(a.get("--reference"), checked(g.n, uint64_t(p.width())));
+            print_error(path + "_fixed_p", l, "vs_master_fixed_p", errors(master, sw.out));
+            if (tfs) print_error("tfs_b1_fixed_p", l, "vs_master_fixed_p", errors(master, tw.out));
+        }
+        if (a.has("--output")) write_dump(a.get("--output"), sw.out);
+        // Alternate the two operators each repetition (the reference's AB/BA policy).
+        std::vector<double> st, tt, agg;
         for (int r = -warmups; r < reps; ++r) {
-            Times s;
-            gpu.fixed_p(g, p, l - 1, fixture, w, s, precision);
+            Times s, u;
+            const bool ab = (r & 1) == 0;
+            if (ab) gpu.fixed_p(g, p, l - 1, fixture, sw, s, precision);
+            if (tfs) gpu.fixed_p(g, p, l - 1, fixture, tw, u, precision, GATGPU_TFS_B1);
+            if (!ab) gpu.fixed_p(g, p, l - 1, fixture, sw, s, precision);
             if (r >= 0) {
-                tot.push_back(s.total);
+                st.push_back(s.total);
                 agg.push_back(s.aggregate);
                 print_times(path, "fixed-p", l, r, g, p, s);
+                if (tfs) {
+                    tt.push_back(u.total);
+                    print_times("tfs_b1", "fixed-p", l, r, g, p, u);
+                }
             }
         }
-        std::cout << "FIXED_P path=" << path << " layer=" << l << " median_ms=" << pct(tot, .5) * 1e3
+        std::cout << "FIXED_P path=" << path << " layer=" << l << " median_ms=" << pct(st, .5) * 1e3
                   << " median_aggregate_ms=" << pct(agg, .5) * 1e3
-                  << " aggregate_gedge_per_s=" << double(g.e) / pct(agg, .5) / 1e9 << " conversion_included=true\n";
+                  << " aggregate_gedge_per_s=" << double(g.e) / pct(agg, .5) / 1e9;
+        if (tfs)
+            std::cout << " median_tfs_ms=" << pct(tt, .5) * 1e3 << " speedup=" << pct(st, .5) / pct(tt, .5);
+        std::cout << " conversion_included=true policy=AB_BA\n";
         return 0;
     }
 

@@ -91,13 +91,13 @@ class GpuPath {
         fetch(layer_index, GATGPU_STAGE_Z, w.z);
     }
 
-    // The fixed-p operator (baseline/bench/main.cpp:103-150, "standard_op"):
-    // uploads the fixture's p/den once per Fixture object, runs projection +
-    // fixed-weight aggregation + normalisation on fixture.input, fills w.z,
-    // w.den and w.out and the Times fields.
+    // The fixed-p operator (baseline/bench/main.cpp:103-150): uploads the
+    // fixture's p/den once per Fixture object, runs it on fixture.input --
+    // "standard_op" with TRANSFORM_FIRST, "tfs_op" with GATGPU_TFS_B1 -- and
+    // fills w.z (transform-first only), w.den, w.out and the Times fields.
     template <class Graph, class Param, class Fixture, class Workspace, class Times>
     void fixed_p(const Graph& g, const Param& p, int layer_index, const Fixture& f, Workspace& w, Times& t,
-                 int precision) {
+                 int precision, int dataflow = GATGPU_TRANSFORM_FIRST) {
         set_graph(g);
         set_layer(layer_index, p);
         if (fixture_ != static_cast<const void*>(&f) || fixture_layer_ != layer_index) {
@@ -107,7 +107,7 @@ class GpuPath {
         }
         gatgpu_times gt{};
         check(ctx_,
-              gatgpu_fixed_p_forward(ctx_, layer_index, precision, GATGPU_TRANSFORM_FIRST, f.input.data(), &gt),
+              gatgpu_fixed_p_forward(ctx_, layer_index, precision, dataflow, f.input.data(), &gt),
               "gatgpu_fixed_p_forward");
         t.convert = gt.convert_ms * 1e-3;
         t.projection = gt.projection_ms * 1e-3;

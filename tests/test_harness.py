@@ -162,3 +162,28 @@ def test_fixed_p_mode(smoke_file, tmp_path, path):
     else:
         assert float(fields["relative_l2"]) < 1e-2, line
     assert f"FIXED_P path={path} layer=2 median_ms=" in p.stdout
+    if path == "gpu_bf16":  # layer 2 is 256 -> 8x32: in > 128, so no tfs_op
+        assert "median_tfs_ms" not in p.stdout
+
+
+@pytest.mark.gpu
+def test_fixed_p_mode_runs_tfs_operator_on_layer1(smoke_file, tmp_path):
+    """Layer 1 of the smoke model (128 -> 8x32) takes both operators of the
+    reference's fixed-p mode: standard_op and the neighbour-step tfs_op."""
+    g = smoke1024()
+    model = oracle.random_model(128, 40, 11)
+    write_r0_dumps(tmp_path / "r0", g, model)
+    run("--mode", "export-fixture", "--graph", smoke_file, "--seed", 11, "--layer", 1,
+        "--reference-prefix", tmp_path / "r0", "--fixture", tmp_path / "l1.fix", check_rc=0)
+    P = np.fromfile(f"{tmp_path / 'r0'}_layer1_p.f32", np.float32).reshape(-1, 8)
+    den = np.fromfile(f"{tmp_path / 'r0'}_layer1_den.f32", np.float32).reshape(1024, 8)
+    master = oracle.fixed_p_layer(g["row"], g["col"], g["x"], model[0], P, den, False)["out"]
+    master.astype("<f4").tofile(tmp_path / "master.f32")
+    p = run("--mode", "fixed-p", "--graph", smoke_file, "--seed", 11, "--layer", 1, "--path", "gpu_bf16",
+            "--fixture", tmp_path / "l1.fix", "--reference", tmp_path / "master.f32", "--repeats", 2,
+            "--warmups", 1, check_rc=0)
+    lines = {l.split()[1] + " " + l.split()[3]: dict(kv.split("=") for kv in l.split()[1:])
+             for l in p.stdout.splitlines() if l.startswith("ERROR")}
+    for key in ("path=gpu_bf16_fixed_p stage=vs_master_fixed_p", "path=tfs_b1_fixed_p stage=vs_master_fixed_p"):
+        assert float(lines[key]["relative_l2"]) < 1e-2, (key, lines[key])
+    assert "median_tfs_ms=" in p.stdout and "speedup=" in p.stdout
