@@ -28,11 +28,13 @@ HBM_PEAK_GBS = 8000.0
 MFMA_BF16_PEAK_TFLOPS = 2500.0
 
 
-def agg_bytes(n, e, heads, dim, s_z, s_out):
+def agg_bytes(n, e, heads, dim, s_z, s_out, r_gather=True):
     """Algorithmic bytes of one transform-first aggregation launch: rowptr,
     col, R gathers (K floats per edge), L/M/den per node, the gathered Z rows
-    and the output rows."""
-    return 8 * (n + 1) + 4 * e + 4 * heads * e + 4 * heads * n + e * heads * dim * s_z + n * heads * dim * s_out
+    and the output rows.  bf16 layers of 8 heads x 32 features form R from the
+    gathered bf16 Z row itself, so their launches have no R gathers."""
+    r = 4 * heads * e if r_gather else 0
+    return 8 * (n + 1) + 4 * e + r + 4 * heads * n + e * heads * dim * s_z + n * heads * dim * s_out
 
 
 def pmc_traffic(workload, precision):
@@ -147,7 +149,8 @@ def main():
     s_z = 2 if prec == gatgpu.BF16 else 4
     L2 = model[1]
     agg_ms = float(np.mean([t[1]["aggregate_ms"] for t in layer_times]))
-    b2 = agg_bytes(n, e, L2["heads"], L2["dim"], s_z, s_z)
+    rz = prec == gatgpu.BF16 and (L2["heads"], L2["dim"]) == (8, 32)
+    b2 = agg_bytes(n, e, L2["heads"], L2["dim"], s_z, s_z, r_gather=not rz)
     achieved = b2 / (agg_ms * 1e-3) / 1e9
     pmc = pmc_traffic(w.name, args.precision)
     per_layer = [{k: round(float(np.mean([t[l][k] for t in layer_times])), 4)

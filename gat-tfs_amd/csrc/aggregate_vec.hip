@@ -82,6 +82,7 @@ struct VArgs {
     uint64_t n, e;
     uint64_t rows;  // non-split rows: sorted positions [0, rows)
     SplitArgs sp;
+    const float* ar;  // aR [W] when R is recomputed from the gathered rows
 };
 
 __device__ inline void unpack(const uint4& v, float (&f)[8]) {
@@ -108,10 +109,15 @@ struct Lane {
     float m[C::VPL];
     float L[C::VPL];
     int h[C::VPL];
+    float ar[C::VEC];  // aR of the lane's features (R from the gathered row)
 };
 
-// One batch of edges [base, base + BATCH) clipped to end.
-template <class C, class ZT>
+// One batch of edges [base, base + BATCH) clipped to end.  RZ (bf16 8 x 32):
+// R of the source is recomputed from the gathered row, R = Z_bf16 . aR, as an
+// FMA chain over the lane's 8 features and (s0 + s1) + (s2 + s3) over the 4
+// lanes of the head -- the summation the projection used to store R -- so no
+// R line is fetched.
+template <class C, class ZT, bool RZ>
 __device__ inline void batch(uint64_t base, uint64_t end, const uint32_t* __restrict__ pcol,
                              const float* __restrict__ R, const ZT* __restrict__ Z, int slot, int sub,
                              Lane<C>& st) {
@@ -132,9 +138,42 @@ __device__ inline void batch(uint64_t base, uint64_t end, const uint32_t* __rest
         for (int v = 0; v < C::VPL; ++v) {
             z[u][v] = ok[u] ? *reinterpret_cast<const uint4*>(row + (sub + kWave * v) * C::VEC)
                             : make_uint4(0, 0, 0, 0);
-            const float r = ok[u] ? R[uint64_t(j) * C::K + st.h[v]] : 0.0f;
-            s[u][v] = leaky(st.L[v] + r);
+            if constexpr (!RZ) {
+                const float r = ok[u] ? R[uint64_t(j) * C::K + st.h[v]] : 0.0f;
+                s[u][v] = leaky(st.L[v] + r);
+            }
         }
+    }
+    if constexpr (RZ) {
+        // Score, weigh and accumulate each edge as soon as its row is here
+        // (the unpacked row is used twice, so it is not kept for a batch):
+        // online per edge, the accumulators rescaled only when some lane of
+        // the wave raised its max.
+        static_assert(C::VEC == 8 && C::DIM == 32 && C::VPL == 1, "R from Z: bf16 8 x 32 rows");
+#pragma unroll
+        for (int u = 0; u < C::U; ++u) {
+            float f[C::VEC];
+            unpack(z[u][0], f);
+            float t = 0.0f;
+#pragma unroll
+            for (int x = 0; x < C::VEC; ++x) t = __builtin_fmaf(f[x], st.ar[x], t);
+            t += __shfl_xor(t, 1);
+            t += __shfl_xor(t, 2);
+            const float sc_ = leaky(st.L[0] + t);
+            const float mn = ok[u] ? fmaxf(st.m[0], sc_) : st.m[0];
+            const float scale = mn > st.m[0] ? expf(st.m[0] - mn) : 1.0f;  // exp(-inf) = 0 on a slot's first edge
+            if (__any(scale != 1.0f)) {
+                st.den[0] *= scale;
+#pragma unroll
+                for (int x = 0; x < C::VEC; ++x) st.acc[x] *= scale;
+            }
+            st.m[0] = mn;
+            const float p = ok[u] ? expf(sc_ - mn) : 0.0f;
+            st.den[0] += p;
+#pragma unroll
+            for (int x = 0; x < C::VEC; ++x) st.acc[x] += p * f[x];
+        }
+        return;
     }
 #pragma unroll
     for (int v = 0; v < C::VPL; ++v) {
@@ -164,11 +203,11 @@ __device__ inline void batch(uint64_t base, uint64_t end, const uint32_t* __rest
 
 // Edges [beg, end) of a row or chunk, then the edge slots merged: afterwards
 // every lane holds its heads' totals and m is the max over all the edges.
-template <class C, class ZT>
+template <class C, class ZT, bool RZ>
 __device__ inline void aggregate(uint64_t beg, uint64_t end, const uint32_t* __restrict__ pcol,
                                  const float* __restrict__ R, const ZT* __restrict__ Z, int slot, int sub,
                                  Lane<C>& st) {
-    for (uint64_t base = beg; base < end; base += C::BATCH) batch<C, ZT>(base, end, pcol, R, Z, slot, sub, st);
+    for (uint64_t base = beg; base < end; base += C::BATCH) batch<C, ZT, RZ>(base, end, pcol, R, Z, slot, sub, st);
     if constexpr (C::EPI > 1) {
         for (int off = C::LPR; off < kWave; off <<= 1) {
 #pragma unroll
@@ -248,7 +287,7 @@ k_split_prescan(const uint64_t* __restrict__ prow, const uint32_t* __restrict__ 
     if (lane < K) sp.mchunk[c * 8 + lane] = m;
 }
 
-template <class C, class ZT>
+template <class C, class ZT, bool RZ>
 __global__ void __launch_bounds__(kThreads) k_agg_vec(VArgs<ZT> a) {
     // The wave index is made wave-uniform so that row bounds and source ids
     // come in through scalar loads.
@@ -265,6 +304,8 @@ __global__ void __launch_bounds__(kThreads) k_agg_vec(VArgs<ZT> a) {
         st.h[v] = ((sub + kWave * v) * C::VEC) / C::DIM;
         st.den[v] = 0.0f;
     }
+#pragma unroll
+    for (int x = 0; x < C::VEC; ++x) st.ar[x] = RZ ? a.ar[sub * C::VEC + x] : 0.0f;
     if (item < a.sp.chunks) {
         // ---------------- chunk of a split row
         const uint64_t c = item;
@@ -282,7 +323,7 @@ __global__ void __launch_bounds__(kThreads) k_agg_vec(VArgs<ZT> a) {
             st.L[v] = a.L[uint64_t(i) * C::K + st.h[v]];
             st.m[v] = leaky(st.L[v] + m);  // exact row max: no rescale happens in this chunk
         }
-        aggregate<C, ZT>(beg, end, a.pcol, a.R, a.Z, slot, sub, st);
+        aggregate<C, ZT, RZ>(beg, end, a.pcol, a.R, a.Z, slot, sub, st);
         float* part = a.sp.part + c * (C::W + 8);
         if (slot == 0) {
 #pragma unroll
@@ -342,7 +383,7 @@ __global__ void __launch_bounds__(kThreads) k_agg_vec(VArgs<ZT> a) {
         st.L[v] = a.L[uint64_t(i) * C::K + st.h[v]];
         st.m[v] = -INFINITY;
     }
-    aggregate<C, ZT>(beg, end, a.pcol, a.R, a.Z, slot, sub, st);
+    aggregate<C, ZT, RZ>(beg, end, a.pcol, a.R, a.Z, slot, sub, st);
     // Empty row: max 0, denominator 0, output 0 (baseline/src/ref_fp32.cpp:11).
     if (end == beg)
 #pragma unroll
@@ -354,14 +395,22 @@ template <class C, class ZT>
 hipError_t run(const AggArgs& g, const RowBins& bins, const SplitTable& t, hipStream_t s) {
     VArgs<ZT> a{g.prow, g.pcol, g.perm, g.left, g.right, static_cast<const ZT*>(g.feat), g.hidden, g.mx, g.den,
                 g.out32, g.outbf, g.n, g.e, bins.split_begin,
-                SplitArgs{t.chunks, t.chunk_k, t.chunk_first, t.chunk_edges, t.mchunk, t.part, t.counter}};
+                SplitArgs{t.chunks, t.chunk_k, t.chunk_first, t.chunk_edges, t.mchunk, t.part, t.counter}, g.ar};
     if (t.chunks) {
         hipError_t e = launch_split_prescan(g.prow, g.pcol, g.right, C::K, t, g.e, s);
         if (e != hipSuccess) return e;
     }
     const uint64_t items = t.chunks + bins.split_begin;
-    if (items)
-        k_agg_vec<C, ZT><<<dim3(uint32_t((items + kWavesPerBlock - 1) / kWavesPerBlock)), kThreads, 0, s>>>(a);
+    if (!items) return hipSuccess;
+    const dim3 grid(uint32_t((items + kWavesPerBlock - 1) / kWavesPerBlock));
+    if constexpr (sizeof(ZT) == 2 && C::W == 256) {
+        if (g.r_from_z) {
+            if (!g.ar) return hipErrorInvalidValue;
+            k_agg_vec<C, ZT, true><<<grid, kThreads, 0, s>>>(a);
+            return hipGetLastError();
+        }
+    }
+    k_agg_vec<C, ZT, false><<<grid, kThreads, 0, s>>>(a);
     return hipGetLastError();
 }
 

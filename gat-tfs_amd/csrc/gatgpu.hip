@@ -422,6 +422,8 @@ int run_layer(gatgpu_ctx* c, int l, int precision, int dataflow, bool hidden, co
     pa.right = Ls.right.as<float>();
     pa.tiles = (n + 31) / 32;
     pa.r_in_z = r_in_z;
+    pa.ar = Ls.ar.as<float>();
+    pa.r_from_z = bf16 && !fixed && r_from_z_supported(pa);
     // ---- convert (bf16 path, FP32 source only; a bf16 source was rounded in
     // the previous layer's epilogue, which equals convert() of that output).
     // Where the fast projection applies, the rounding happens in its loads.
@@ -468,6 +470,8 @@ int run_layer(gatgpu_ctx* c, int l, int precision, int dataflow, bool hidden, co
     a.outbf = want_outbf ? Ls.outbf.as<uint16_t>() : nullptr;
     a.n = c->n;
     a.e = c->e;
+    a.r_from_z = pa.r_from_z;
+    a.ar = Ls.ar.as<float>();
     if (fixed)
         HIPCHECK(c, launch_aggregate_fixed(a, Ls.fixp.as<float>(), Ls.fixden.as<float>(), c->bins, c->split,
                                            c->stream));

@@ -93,7 +93,13 @@ struct ProjArgs {
     float* right;        // [n][heads]
     uint64_t tiles;      // ceil(n / 32)
     bool r_in_z;         // one head: also store R as FP32 in z[row][zs-2..zs-1]
+    bool r_from_z;       // 8 x 32 bf16: R = Z_bf16 . aR (the aggregation recomputes it)
+    const float* ar;     // aR [256] when r_from_z
 };
+// R from the stored bf16 Z: the fast projection writes R = Z_bf16 . aR and
+// the 8-head aggregation recomputes it from each gathered row instead of
+// loading it (same FMA order, so both give the same bits).
+bool r_from_z_supported(const ProjArgs& a);
 int proj_blocks_per_group(int width);
 // True when launch_projection_mfma takes the fast path for these arguments
 // (one output group, 1..8 or 16 k steps, 0/1/2/8 head blocks); the FP32-input
@@ -131,6 +137,8 @@ struct AggArgs {
     float* out32;    // [n][W] or null
     uint16_t* outbf; // [n][W] or null
     uint64_t n, e;           // nodes and CSR entries (bounds of perm/prow values)
+    bool r_from_z = false;   // bf16 8 x 32: recompute R = Z_bf16 . aR from the gathered rows
+    const float* ar = nullptr;
 };
 // The permuted column array carries kPcolPad zero entries past its e
 // edges, so that kernels may load a whole batch of wave-uniform source ids

@@ -134,6 +134,10 @@ __global__ void __launch_bounds__(kThreads) k_proj_fast(ProjArgs a) {
         const int lane = q % kWave, b = (q / kWave) % NB, ks = q / (kWave * NB);
         wlds[q] = a.wpk[(size_t(ks) * a.nmb + b) * kWave + lane];
     }
+    // FULL layers keep aR (256 floats) after the fragments for R from the stored Z.
+    float* arl = reinterpret_cast<float*>(wlds + KS * NB * kWave);
+    if (FULL)
+        for (int q = threadIdx.x; q < 256; q += kThreads) arl[q] = a.ar ? a.ar[q] : 0.0f;
     __syncthreads();
     const int w = threadIdx.x / kWave, l = threadIdx.x % kWave;
     const int half = l / 32, col = l % 32;
@@ -222,8 +226,12 @@ __global__ void __launch_bounds__(kThreads) k_proj_fast(ProjArgs a) {
         // FULL: all 8 heads and 32 HB features present (8 x 32): no per-store
         // bounds tests either.
         const bool full = FULL;
+        float rz[HB > 0 ? HB : 1];  // R from the stored (bf16) Z, per head
 #pragma unroll
-        for (int mb = 0; mb < HB; ++mb)
+        for (int mb = 0; mb < HB; ++mb) {
+            float zr[16];
+#pragma unroll
+            for (int r = 0; r < 16; ++r) zr[r] = bf16_widen(bf16_rne(acc[mb][r]));
 #pragma unroll
             for (int q8 = 0; q8 < 2; ++q8) {
                 const int f0 = 32 * mb + 16 * half + 8 * q8;
@@ -235,6 +243,22 @@ __global__ void __launch_bounds__(kThreads) k_proj_fast(ProjArgs a) {
                             (uint32_t(bf16_rne(acc[mb][8 * q8 + 2 * x + 1])) << 16);
                 *reinterpret_cast<uint4*>(a.z + rs * a.zs + f0) = make_uint4(w4[0], w4[1], w4[2], w4[3]);
             }
+            if (FULL && a.r_from_z) {
+                // R = Z_bf16 . aR with the summation the aggregation kernel uses:
+                // an FMA chain over each 8 features, then (s0 + s1) + (s2 + s3).
+                float s8[2];
+#pragma unroll
+                for (int q8 = 0; q8 < 2; ++q8) {
+                    float t = 0.0f;
+#pragma unroll
+                    for (int x = 0; x < 8; ++x)
+                        t = __builtin_fmaf(zr[8 * q8 + x], arl[32 * mb + 16 * half + 8 * q8 + x], t);
+                    s8[q8] = t;
+                }
+                const float part = s8[0] + s8[1];
+                rz[mb] = part + __shfl_xor(part, 32);
+            }
+        }
         // L/R block: lane half h4 holds heads 4 h4 + {0..3} of each quarter
         // (L hi, R hi, L lo, R lo) in registers {0..3}, {4..7}, {8..11}, {12..15}.
 #pragma unroll
@@ -243,10 +267,13 @@ __global__ void __launch_bounds__(kThreads) k_proj_fast(ProjArgs a) {
             if (full || h < a.heads) {
                 const float rv = acc[HB][4 + q] + acc[HB][12 + q];
                 a.left[rs * a.heads + h] = acc[HB][q] + acc[HB][8 + q];
-                a.right[rs * a.heads + h] = rv;
+                if (!(FULL && a.r_from_z)) a.right[rs * a.heads + h] = rv;
                 if (!full && a.r_in_z) *reinterpret_cast<float*>(a.z + rs * a.zs + a.zs - 2) = rv;
             }
         }
+        if (FULL && a.r_from_z && half == 0)
+#pragma unroll
+            for (int mb = 0; mb < HB; ++mb) a.right[rs * a.heads + mb] = rz[mb];
 #pragma unroll
         for (int ks = KA; ks < KS; ++ks) load_ks(next, ks);
     }
@@ -254,7 +281,7 @@ __global__ void __launch_bounds__(kThreads) k_proj_fast(ProjArgs a) {
 
 template <int KS, int HB, bool F32IN, bool FULL>
 hipError_t launch_fast_io(const ProjArgs& a, hipStream_t s, int cus) {
-    const size_t lds = size_t(KS) * (HB + 1) * kWave * sizeof(uint4);
+    const size_t lds = size_t(KS) * (HB + 1) * kWave * sizeof(uint4) + (FULL ? 256 * sizeof(float) : 0);
     if (lds > 64 * 1024) {
         hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_proj_fast<KS, HB, F32IN, FULL>),
                                            hipFuncAttributeMaxDynamicSharedMemorySize, int(lds));
@@ -265,6 +292,7 @@ hipError_t launch_fast_io(const ProjArgs& a, hipStream_t s, int cus) {
     const uint64_t wg_needed = (a.tiles + kWaves - 1) / kWaves;
     if (gx > wg_needed) gx = wg_needed;
     if (gx < 1) gx = 1;
+    if (FULL && a.r_from_z && !a.ar) return hipErrorInvalidValue;
     k_proj_fast<KS, HB, F32IN, FULL><<<dim3(uint32_t(gx)), kThreads, lds, s>>>(a);
     return hipGetLastError();
 }
@@ -334,6 +362,10 @@ int proj_blocks_per_group(int width) {
 }
 
 bool projection_fast_path(const ProjArgs& a) { return fast_supported_impl(a); }
+
+bool r_from_z_supported(const ProjArgs& a) {
+    return fast_supported_impl(a) && a.head_blocks == 8 && a.width == 256 && a.heads == 8 && !a.r_in_z;
+}
 
 // The FP32-input form holds 32 bytes per k step; at 16 k steps and 8 head
 // blocks that no longer fits the registers.

@@ -49,7 +49,11 @@ enum {
  * reference's ref_fp32 / standard_fp32).  BF16: RNE-rounded bf16 X and W,
  * FP32 MFMA accumulation, L/R from the FP32 accumulators, Z stored bf16,
  * FP32 score/max/exp/denominator/output accumulation (standard_bf16 with a
- * bf16 copy of Z; baseline/IMPLEMENTATION_CONTRACT.md sections 3.2-3.3). */
+ * bf16 copy of Z; baseline/IMPLEMENTATION_CONTRACT.md sections 3.2-3.3).
+ * On transform-first layers of 8 heads x 32 features R is instead the FP32
+ * dot of the stored bf16 Z row with a_r, formed both in the projection and,
+ * per edge, in the aggregation from the Z row it gathers anyway, so no R
+ * values are gathered; the row max stays exact over those R values. */
 enum { GATGPU_FP32 = 0, GATGPU_BF16 = 1 };
 
 /* Dataflow of one layer.  TRANSFORM_FIRST projects Z = X W then aggregates Z
