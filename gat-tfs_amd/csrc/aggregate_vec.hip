@@ -40,7 +40,7 @@ namespace {
 constexpr int kThreads = 256;
 constexpr int kWavesPerBlock = kThreads / kWave;
 
-template <class ZT, int W_, int K_>
+template <class ZT, int W_, int K_, int U_ = 0>
 struct Cfg {
     static constexpr int W = W_, K = K_;
     static constexpr int VEC = 16 / int(sizeof(ZT));  // features per 16-byte load
@@ -48,12 +48,12 @@ struct Cfg {
     static constexpr int LPR = W / VEC;               // 16-byte vectors per row
     static constexpr int EPI = LPR >= kWave ? 1 : kWave / LPR;  // edges per load instruction
     static constexpr int VPL = LPR <= kWave ? 1 : LPR / kWave;  // vectors per lane per edge
-    static constexpr int U = VPL == 1 ? 8 : 4;        // load instructions per vector per batch
+    static constexpr int U = U_ ? U_ : VPL == 1 ? 8 : 4;  // load instructions per vector per batch
     static constexpr int BATCH = U * EPI;             // edges per batch
     static constexpr int ACC = VPL * VEC;
     static_assert(W % K == 0 && DIM % VEC == 0, "a vector must not straddle two heads");
     static_assert(LPR * EPI == kWave || LPR % kWave == 0, "lanes per row must divide or fill the wave");
-    static_assert(BATCH <= int(kPcolPad), "a batch may read at most kPcolPad entries past the row");
+    static_assert(2 * BATCH <= int(kPcolPad), "the id prefetch may read 2 BATCH - 1 entries past the row");
 };
 
 struct SplitArgs {
@@ -117,13 +117,19 @@ struct Lane {
 // FMA chain over the lane's 8 features and (s0 + s1) + (s2 + s3) over the 4
 // lanes of the head -- the summation the projection used to store R -- so no
 // R line is fetched.
+// Source ids of edges [base, base + BATCH): wave-uniform scalar loads, which
+// may run up to 2 BATCH - 1 entries past the last edge (pcol is padded).
+template <class C>
+__device__ inline void load_ids(const uint32_t* __restrict__ pcol, uint64_t base, uint32_t (&js)[C::BATCH]) {
+    const auto* pc = read_only(pcol);
+#pragma unroll
+    for (int t = 0; t < C::BATCH; ++t) js[t] = pc[base + t];
+}
+
 template <class C, class ZT, bool RZ>
-__device__ inline void batch(uint64_t base, uint64_t end, const uint32_t* __restrict__ pcol,
+__device__ inline void batch(uint64_t base, uint64_t end, const uint32_t (&js)[C::BATCH],
                              const float* __restrict__ R, const ZT* __restrict__ Z, int slot, int sub,
                              Lane<C>& st) {
-    uint32_t js[C::BATCH];
-#pragma unroll
-    for (int t = 0; t < C::BATCH; ++t) js[t] = pcol[base + t];  // wave-uniform, padded past e
     uint4 z[C::U][C::VPL];
     float s[C::U][C::VPL];
     bool ok[C::U];
@@ -157,18 +163,18 @@ __device__ inline void batch(uint64_t base, uint64_t end, const uint32_t* __rest
             float t = 0.0f;
 #pragma unroll
             for (int x = 0; x < C::VEC; ++x) t = __builtin_fmaf(f[x], st.ar[x], t);
-            t += __shfl_xor(t, 1);
-            t += __shfl_xor(t, 2);
+            t += quad_xor1(t);
+            t += quad_xor2(t);
             const float sc_ = leaky(st.L[0] + t);
             const float mn = ok[u] ? fmaxf(st.m[0], sc_) : st.m[0];
-            const float scale = mn > st.m[0] ? expf(st.m[0] - mn) : 1.0f;  // exp(-inf) = 0 on a slot's first edge
+            const float scale = mn > st.m[0] ? exp_w(st.m[0] - mn) : 1.0f;  // exp(-inf) = 0 on a slot's first edge
             if (__any(scale != 1.0f)) {
                 st.den[0] *= scale;
 #pragma unroll
                 for (int x = 0; x < C::VEC; ++x) st.acc[x] *= scale;
             }
             st.m[0] = mn;
-            const float p = ok[u] ? expf(sc_ - mn) : 0.0f;
+            const float p = ok[u] ? exp_w(sc_ - mn) : 0.0f;
             st.den[0] += p;
 #pragma unroll
             for (int x = 0; x < C::VEC; ++x) st.acc[x] += p * f[x];
@@ -207,7 +213,16 @@ template <class C, class ZT, bool RZ>
 __device__ inline void aggregate(uint64_t beg, uint64_t end, const uint32_t* __restrict__ pcol,
                                  const float* __restrict__ R, const ZT* __restrict__ Z, int slot, int sub,
                                  Lane<C>& st) {
-    for (uint64_t base = beg; base < end; base += C::BATCH) batch<C, ZT, RZ>(base, end, pcol, R, Z, slot, sub, st);
+    uint32_t js[C::BATCH];
+    load_ids<C>(pcol, beg, js);
+    for (uint64_t base = beg; base < end; base += C::BATCH) {
+        // The next batch's ids are requested before this batch's rows arrive.
+        uint32_t jn[C::BATCH];
+        load_ids<C>(pcol, base + C::BATCH, jn);
+        batch<C, ZT, RZ>(base, end, js, R, Z, slot, sub, st);
+#pragma unroll
+        for (int t = 0; t < C::BATCH; ++t) js[t] = jn[t];
+    }
     if constexpr (C::EPI > 1) {
         for (int off = C::LPR; off < kWave; off <<= 1) {
 #pragma unroll
@@ -391,6 +406,9 @@ __global__ void __launch_bounds__(kThreads) k_agg_vec(VArgs<ZT> a) {
     finish_row<C>(i, st.acc, st.den, st.m, st.h, slot, sub, a.hidden, a.mx, a.den, a.out32, a.outbf);
 }
 
+// Edge loads per lane and batch of the R-from-Z form.
+constexpr int kURz = 4;
+
 template <class C, class ZT>
 hipError_t run(const AggArgs& g, const RowBins& bins, const SplitTable& t, hipStream_t s) {
     VArgs<ZT> a{g.prow, g.pcol, g.perm, g.left, g.right, static_cast<const ZT*>(g.feat), g.hidden, g.mx, g.den,
@@ -406,7 +424,7 @@ hipError_t run(const AggArgs& g, const RowBins& bins, const SplitTable& t, hipSt
     if constexpr (sizeof(ZT) == 2 && C::W == 256) {
         if (g.r_from_z) {
             if (!g.ar) return hipErrorInvalidValue;
-            k_agg_vec<C, ZT, true><<<grid, kThreads, 0, s>>>(a);
+            k_agg_vec<Cfg<ZT, C::W, C::K, kURz>, ZT, true><<<grid, kThreads, 0, s>>>(a);
             return hipGetLastError();
         }
     }

@@ -26,6 +26,30 @@ __host__ __device__ inline float bf16_widen(uint16_t b) {
 __device__ inline float leaky(float x) { return x >= 0.0f ? x : 0.2f * x; }
 __device__ inline float elu(float x) { return x >= 0.0f ? x : expm1f(x); }
 
+// Softmax weight e^x for x <= 0 as 2^(x log2 e) on the hardware base-2
+// exponential (v_exp_f32): two instructions instead of the range-reduced
+// expf.  exp_w(0) = 1 and exp_w(-inf) = 0 exactly; otherwise the relative
+// error is about |x| 2^-24 (the rounded product) plus one ulp, below 2e-6
+// wherever e^x is above 2^-30.
+__device__ inline float exp_w(float x) { return __builtin_amdgcn_exp2f(x * 1.44269504088896341f); }
+
+// A buffer that no thread of the launch writes, seen through the constant
+// address space: loads from it at wave-uniform addresses become scalar loads
+// whatever stores the kernel makes elsewhere.
+template <class T>
+__device__ inline const __attribute__((address_space(4))) T* read_only(const T* p) {
+    return (const __attribute__((address_space(4))) T*)(p);
+}
+
+// x from lane (lane ^ 1) and (lane ^ 2) within each group of four lanes (DPP
+// quad permutations, no LDS round trip).
+__device__ inline float quad_xor1(float x) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0xB1, 0xF, 0xF, false));
+}
+__device__ inline float quad_xor2(float x) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0x4E, 0xF, 0xF, false));
+}
+
 // Wave-local ordering of LDS traffic between lanes of one wavefront.
 __device__ inline void wave_sync() {
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
