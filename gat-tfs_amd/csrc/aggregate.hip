@@ -69,7 +69,7 @@ __device__ inline void range_accumulate(uint64_t beg, uint64_t end, const uint32
         const bool ev = e < end;
         const uint32_t j = ev ? pcol[e] : 0u;
         float p = 0.0f;
-        if (ev && ln.hvalid) p = expf(leaky(Lh + R[uint64_t(j) * K + ln.hh]) - Mh);
+        if (ev && ln.hvalid) p = exp_w(leaky(Lh + R[uint64_t(j) * K + ln.hh]) - Mh);
         dloc += p;
         pbuf[ln.hh * ln.eb_count + ln.eb] = p;
         if (ln.hh == 0) jbuf[ln.eb] = j;

@@ -179,13 +179,13 @@ __global__ void __launch_bounds__(kThreads, 2) k_af_ns(AfArgs a, Items it) {
                 if constexpr (SM == kFixed) {
                     p[q] = ok ? rv[q] : 0.0f;
                 } else if constexpr (SM == kExact) {
-                    p[q] = ok ? expf(leaky(L[q] + rv[q]) - m[q]) : 0.0f;
+                    p[q] = ok ? exp_w(leaky(L[q] + rv[q]) - m[q]) : 0.0f;
                     den[q] += p[q];
                 } else {
                     const float sc_ = leaky(L[q] + rv[q]);
                     const float mn = ok ? fmaxf(m[q], sc_) : m[q];
-                    scale[q] = mn > m[q] ? __expf(m[q] - mn) : 1.0f;  // exp(-inf) = 0 on the first edge
-                    p[q] = ok ? __expf(sc_ - mn) : 0.0f;
+                    scale[q] = mn > m[q] ? exp_w(m[q] - mn) : 1.0f;  // exp(-inf) = 0 on the first edge
+                    p[q] = ok ? exp_w(sc_ - mn) : 0.0f;
                     m[q] = mn;
                     den[q] = den[q] * scale[q] + p[q];
                 }

@@ -88,7 +88,7 @@ __device__ inline void group_accumulate(uint64_t beg, uint64_t end, const uint32
         const uint64_t e = base + sub;
         const bool ev = e < end;
         const uint32_t j = ev ? pcol[e] : 0u;
-        const float p = ev ? expf(leaky(Li + R[uint64_t(j) * rs]) - Mi) : 0.0f;
+        const float p = ev ? exp_w(leaky(Li + R[uint64_t(j) * rs]) - Mi) : 0.0f;
         dloc += p;
         const uint64_t rem = end - base;
         const int cnt = rem < uint64_t(C::G) ? int(rem) : C::G;
@@ -148,14 +148,14 @@ __device__ inline void group_online(uint64_t beg, uint64_t end, const uint32_t* 
             mb = fmaxf(mb, s[t]);
         }
         const float mn = fmaxf(m, mb);
-        const float sc = expf(m - mn);  // 0 on the first batch (m = -inf)
+        const float sc = exp_w(m - mn);  // 0 on the first batch (m = -inf)
         m = mn;
         dsum *= sc;
 #pragma unroll
         for (int x = 0; x < C::VEC; ++x) acc[x] *= sc;
 #pragma unroll
         for (int t = 0; t < C::G; ++t) {
-            const float p = t < cnt ? expf(s[t] - mn) : 0.0f;
+            const float p = t < cnt ? exp_w(s[t] - mn) : 0.0f;
             dsum += p;
             float f[C::VEC];
             unpack(raw[t], f);

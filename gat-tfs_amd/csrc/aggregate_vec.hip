@@ -187,7 +187,7 @@ __device__ inline void batch(uint64_t base, uint64_t end, const uint32_t (&js)[C
 #pragma unroll
         for (int u = 0; u < C::U; ++u) mb = ok[u] ? fmaxf(mb, s[u][v]) : mb;
         const float mn = fmaxf(st.m[v], mb);
-        const float sc = mn > st.m[v] ? expf(st.m[v] - mn) : 1.0f;  // exp(-inf) = 0 on a slot's first edge
+        const float sc = mn > st.m[v] ? exp_w(st.m[v] - mn) : 1.0f;  // exp(-inf) = 0 on a slot's first edge
         st.m[v] = mn;
         st.den[v] *= sc;
 #pragma unroll
@@ -197,7 +197,7 @@ __device__ inline void batch(uint64_t base, uint64_t end, const uint32_t (&js)[C
     for (int u = 0; u < C::U; ++u) {
 #pragma unroll
         for (int v = 0; v < C::VPL; ++v) {
-            const float p = ok[u] ? expf(s[u][v] - st.m[v]) : 0.0f;
+            const float p = ok[u] ? exp_w(s[u][v] - st.m[v]) : 0.0f;
             st.den[v] += p;
             float f[C::VEC];
             unpack(z[u][v], f);
@@ -229,7 +229,7 @@ __device__ inline void aggregate(uint64_t beg, uint64_t end, const uint32_t* __r
             for (int v = 0; v < C::VPL; ++v) {
                 const float mo = __shfl_xor(st.m[v], off);
                 const float M = fmaxf(st.m[v], mo);
-                const float f = st.m[v] == M ? 1.0f : expf(st.m[v] - M);
+                const float f = st.m[v] == M ? 1.0f : exp_w(st.m[v] - M);
                 st.m[v] = M;
                 st.den[v] *= f;
                 st.den[v] += __shfl_xor(st.den[v], off);
