@@ -100,7 +100,7 @@ __device__ inline void store_row(float* out32, uint16_t* outbf, uint64_t i, int 
         float v = acc[q] * (d > 0.0f ? 1.0f / d : 0.0f);
         if (hidden) v = elu(v);
         if (out32) out32[i * W + f] = v;
-        if (outbf) outbf[i * W + f] = bf16_rne(v);
+        if (outbf) outbf[i * W + f] = bf16_hw(v);
     }
 }
 

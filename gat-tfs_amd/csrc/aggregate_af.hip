@@ -310,8 +310,7 @@ __global__ void __launch_bounds__(kThreads, 2) k_af_ns(AfArgs a, Items it) {
                 }
                 if (a.outbf)
                     *reinterpret_cast<uint2*>(a.outbf + uint64_t(i) * W + f0) =
-                        make_uint2(uint32_t(bf16_rne(o[0])) | (uint32_t(bf16_rne(o[1])) << 16),
-                                   uint32_t(bf16_rne(o[2])) | (uint32_t(bf16_rne(o[3])) << 16));
+                        make_uint2(bf16x2(o[0], o[1]), bf16x2(o[2], o[3]));
                 if (a.out32)
                     *reinterpret_cast<float4*>(a.out32 + uint64_t(i) * W + f0) = make_float4(o[0], o[1], o[2], o[3]);
             }
@@ -360,8 +359,7 @@ __global__ void __launch_bounds__(kThreads) k_af_merge(AfArgs a, int blocks) {
             for (int x = 0; x < 4; ++x) o[x] = elu(o[x]);
         if (a.outbf)
             *reinterpret_cast<uint2*>(a.outbf + uint64_t(i) * W + f0) =
-                make_uint2(uint32_t(bf16_rne(o[0])) | (uint32_t(bf16_rne(o[1])) << 16),
-                           uint32_t(bf16_rne(o[2])) | (uint32_t(bf16_rne(o[3])) << 16));
+                make_uint2(bf16x2(o[0], o[1]), bf16x2(o[2], o[3]));
         if (a.out32)
             *reinterpret_cast<float4*>(a.out32 + uint64_t(i) * W + f0) = make_float4(o[0], o[1], o[2], o[3]);
     }

@@ -1,0 +1,491 @@
+// Aggregate-first layer in its sum form, for D_in <= 112 inputs and 8 heads of
+// 32: first U_ih = sum_j p_ijh X_j over the row's edges, then the projection
+// U_ih W_h / den_ih.  This is the order of tfs_online_fused
+// (implementation/src/gat_tfs_online.cpp:200-283), where a row tile's U panel
+// is multiplied by W_h once its rows are summed.
+//
+//   out[i, h] = ELU?( (sum_j p_ijh X_j) W_h / den_ih ),
+//   p_ijh = exp(LeakyReLU(L_ih + R_jh) - M_ih),  M the row max
+//   (kept as a running max with rescaling; the final M is exact).
+//
+// Why: the gathered row is the bf16 input row with the source's R values in
+// its tail, 256 bytes, where transform-first gathers the 512-byte Z row of
+// 8 x 32 bf16 features.  A 100 -> 8 x 32 layer so moves about half the bytes.
+//
+// Gather table XR [n][128] bf16 (256-byte rows, 64 words of 4 bytes): X_j at
+// [0, D_in), zeros up to 112, R_jh as FP32 in word 56 + h.
+//
+// The per-edge sums run on the matrix cores.  Per batch of 32 edges,
+// v_mfma_f32_16x16x32_bf16 forms D[row][feature] += P[row][edge] X[edge][feature]
+// with the edge as the contraction index.  Lane l = 16 g + n (k group g takes
+// edges 8g .. 8g + 7 of the batch) loads word 16 sb + n of each of its 8
+// edges' rows, sb = 0..3 (features 2(16 sb + n) and 2(16 sb + n) + 1): the low
+// halves of those 8 words are the B operand of an even-feature block, the
+// high halves that of an odd-feature block.  Word 56 + h of a row is R_jh, so
+// lane n = 8 + h of super-block 3 holds R of its 8 edges for head h: it scores
+// them, keeps the running max m_h and the denominator, and splits p into
+// hi + lo bf16 (p enters to about 2^-17): A row h holds the hi parts, row
+// 8 + h the lo parts.  A batch that raises some m_h first rescales the sums
+// by exp(m_old - m_new) (the running-maximum form of
+// gat_tfs_online.cpp:86-117); the final m_h is leaky(L_h + max_j R_jh) bit
+// for bit, as leaky and the addition are monotone.  Lane (g, n), register r
+// of block (sb, par) holds the hi (g = 0, 1) or lo (g = 2, 3) sum of head
+// 4 (g % 2) + r, feature 2(16 sb + n) + par; U is their sum.
+//
+// Blocks of 8 waves take tiles of 16 consecutive degree-sorted rows, two per
+// wave.  A row's normalised sums S_h = U_h / den_h go to LDS as a hi + lo pair
+// of bf16 (S = hi + lo to about 2^-17 relative), in the B-operand layout of
+// v_mfma_f32_32x32x16_bf16.  After a barrier, wave h multiplies the tile's S_h
+// by W_h (A fragments packed as for the projection, read from L2; hi and
+// lo in two MFMA chains) and stores the 16 output rows; a second barrier
+// frees the tile buffer.  Split rows: one wave per chunk sums its edges from
+// the exact row max (per-chunk maxima of k_split_prescan) into scratch, and
+// one wave per row adds the chunks in chunk order and projects the row on
+// the VALU with the FP32 W.
+#include "internal.hpp"
+
+namespace gatgpu {
+namespace {
+
+typedef __bf16 bf16x8 __attribute__((__vector_size__(8 * sizeof(__bf16))));
+typedef float f32x4 __attribute__((__vector_size__(4 * sizeof(float))));
+typedef float f32x16 __attribute__((__vector_size__(16 * sizeof(float))));
+
+constexpr int kThreads = 512;
+constexpr int kWaves = kThreads / kWave;   // 8 = heads
+constexpr int kTile = 2 * kWaves;          // rows per block tile
+constexpr int kMaxKS = 7;                  // k steps of 16 features: D_in <= 112
+constexpr int kRowWords = kXRStride / 2;   // 64 words of 4 bytes per XR row
+constexpr int kB = 32;                     // edges per batch (MFMA contraction)
+constexpr int kSB = 4;                     // super-blocks of 16 words per row
+constexpr int kBlk = kTile * 32 + 16;      // bytes per (head, k step, hi|lo) block of S, padded
+constexpr int kSBytes = 8 * kMaxKS * 2 * kBlk;
+constexpr int kPart = 8 * 128 + 8;         // floats per chunk partial (U_h rows of 128, then den)
+constexpr int kDenOff = 8 * 128;
+constexpr int kChunkThreads = 256;
+
+static_assert(2 * kB <= int(kPcolPad), "the id prefetch may read 2 kB - 1 entries past the row");
+static_assert(kRowWords == 16 * kSB && kXRFeat == 112, "XR row: 4 super-blocks, R in words 56..63");
+
+__device__ inline int sblk(int h, int ks, int hl) { return ((h * kMaxKS + ks) * 2 + hl) * kBlk; }
+
+__device__ inline float lane_f(float x, int lane) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), lane));
+}
+
+// Running sums of one row or chunk.  d[2 sb + par] are the D accumulators of
+// the feature blocks; m, den and L live in the head lanes (n >= 8, head n - 8;
+// den of the lane's own k group until combined).
+struct Sums {
+    f32x4 d[2 * kSB];
+    float m, den, L;
+};
+
+// Edges [beg, end).  EXACT: s.m holds the exact row max already (a chunk) and
+// never moves.
+template <bool EXACT>
+__device__ inline void gather_sums(const uint32_t* __restrict__ pcol, const uint32_t* __restrict__ xr,
+                                   uint64_t beg, uint64_t end, int l, Sums& s) {
+    if (beg >= end) return;
+    const int g = l / 16, n = l % 16;
+    const bool head = n >= 8;
+    const auto* pc = read_only(pcol);
+    uint32_t js[kB];
+#pragma unroll
+    for (int t = 0; t < kB; ++t) js[t] = pc[beg + t];
+    for (uint64_t base = beg; base < end; base += kB) {
+        uint32_t jn[kB];
+#pragma unroll
+        for (int t = 0; t < kB; ++t) jn[t] = pc[base + kB + t];  // padded past e
+        const uint64_t rem = end - base;
+        const int cnt = rem < uint64_t(kB) ? int(rem) : kB;
+        // This lane's 8 edges; edges past the end re-read the batch's first row
+        // (weight 0).
+        uint32_t jl[8];
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+            uint32_t j = js[t];
+#pragma unroll
+            for (int q = 1; q < 4; ++q) j = g == q ? js[8 * q + t] : j;
+            jl[t] = 8 * g + t < cnt ? j : js[0];
+        }
+        // 32-bit byte offsets (n * 256 < 2^32 is checked at launch).
+        const unsigned char* xb = reinterpret_cast<const unsigned char*>(xr);
+        uint32_t raw[kSB][8];
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+            const uint32_t off = jl[t] * uint32_t(4 * kRowWords) + 4u * uint32_t(n);
+#pragma unroll
+            for (int sb = 0; sb < kSB; ++sb) raw[sb][t] = *reinterpret_cast<const uint32_t*>(xb + off + 64 * sb);
+        }
+        // ---- head lanes: scores of their 8 edges, batch max over the 4 k groups
+        float sc[8];
+        float mb = -INFINITY;
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+            sc[t] = (head && 8 * g + t < cnt) ? leaky(s.L + __builtin_bit_cast(float, raw[3][t])) : -INFINITY;
+            mb = fmaxf(mb, sc[t]);
+        }
+        mb = fmaxf(mb, __shfl_xor(mb, 16));
+        mb = fmaxf(mb, __shfl_xor(mb, 32));
+        float scale = 1.0f;
+        if constexpr (!EXACT) {
+            const float mn = fmaxf(s.m, mb);
+            scale = mn > s.m ? exp_w(s.m - mn) : 1.0f;  // exp(-inf) = 0 on the first batch
+            s.m = mn;
+        }
+        // ---- A operand: row h = hi part of p_h for edges 8g + t, row 8 + h = lo
+        // part (S = hi + lo to about 2^-17); the head lanes form both and the
+        // lanes n < 8 take the hi words from lane n + 8 (DPP rotate by 8).
+        uint32_t ah[4], al[4];
+        float ps = 0.0f;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const float p0 = head ? exp_w(sc[2 * q] - s.m) : 0.0f;  // -inf past the end: 0
+            const float p1 = head ? exp_w(sc[2 * q + 1] - s.m) : 0.0f;
+            ps += p0 + p1;
+            ah[q] = bf16x2(p0, p1);
+            al[q] = bf16x2(p0 - __builtin_bit_cast(float, ah[q] << 16), p1 - __builtin_bit_cast(float, ah[q] & 0xffff0000u));
+        }
+        uint32_t av[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const uint32_t hi_from_head = uint32_t(__builtin_amdgcn_mov_dpp(int(ah[q]), 0x128, 0xF, 0xF, false));
+            av[q] = head ? al[q] : hi_from_head;
+        }
+        s.den = s.den * scale + ps;
+        if (!EXACT && __any(head && scale != 1.0f)) {
+            // D register r of lane group g belongs to head 4 (g % 2) + r.
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const float f = __shfl(scale, 8 + 4 * (g & 1) + r);
+#pragma unroll
+                for (int b = 0; b < 2 * kSB; ++b) s.d[b][r] *= f;
+            }
+        }
+        const bf16x8 A = __builtin_bit_cast(bf16x8, make_uint4(av[0], av[1], av[2], av[3]));
+        // ---- B operands from the low / high halves of the 8 words, and the MFMAs
+#pragma unroll
+        for (int sb = 0; sb < kSB; ++sb) {
+            uint32_t ev[4], od[4];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const uint32_t w0 = raw[sb][2 * q], w1 = raw[sb][2 * q + 1];
+                ev[q] = (w0 & 0xffffu) | (w1 << 16);
+                od[q] = (w0 >> 16) | (w1 & 0xffff0000u);
+            }
+            const bf16x8 Be = __builtin_bit_cast(bf16x8, make_uint4(ev[0], ev[1], ev[2], ev[3]));
+            const bf16x8 Bo = __builtin_bit_cast(bf16x8, make_uint4(od[0], od[1], od[2], od[3]));
+            s.d[2 * sb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A, Be, s.d[2 * sb], 0, 0, 0);
+            s.d[2 * sb + 1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A, Bo, s.d[2 * sb + 1], 0, 0, 0);
+        }
+#pragma unroll
+        for (int t = 0; t < kB; ++t) js[t] = jn[t];
+    }
+}
+
+__device__ inline void zero_sums(Sums& s) {
+#pragma unroll
+    for (int b = 0; b < 2 * kSB; ++b)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) s.d[b][r] = 0.0f;
+    s.den = 0.0f;
+}
+
+// Denominator of head lane (n = 8 + h) over the 4 k groups.
+__device__ inline float total_den(float den) {
+    den += __shfl_xor(den, 16);
+    return den + __shfl_xor(den, 32);
+}
+
+// hi + lo sums: afterwards lanes g = 2, 3 hold U of head 4 (g - 2) + r.
+__device__ inline void combine_hilo(Sums& s) {
+#pragma unroll
+    for (int b = 0; b < 2 * kSB; ++b)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) s.d[b][r] += __shfl_xor(s.d[b][r], 32);
+}
+
+template <int KS>
+__global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) k_afs_tiles(AfsArgs a) {
+    extern __shared__ __attribute__((aligned(16))) unsigned char slds[];
+    const int w = __builtin_amdgcn_readfirstlane(int(threadIdx.x) / kWave);
+    const int l = threadIdx.x % kWave;
+    const int g = l / 16, n = l % 16;
+    const bool head = n >= 8;
+    const uint64_t tiles = (a.rows + kTile - 1) / kTile;
+    for (uint64_t tile = blockIdx.x; tile < tiles; tile += gridDim.x) {
+        // ---- two rows per wave: sums, softmax state, S into LDS
+#pragma unroll 1
+        for (int rr = 0; rr < 2; ++rr) {
+            const int r = w + kWaves * rr;
+            const uint64_t tpos = tile * kTile + r;
+            if (tpos >= a.rows) continue;
+            const uint64_t k = a.rows - 1 - tpos;
+            const uint32_t i = a.perm[k];
+            const uint64_t beg = a.prow[k], end = a.prow[k + 1];
+            if (i >= a.n || beg > end || end > a.e) continue;
+            Sums s;
+            zero_sums(s);
+            s.L = head ? a.L[uint64_t(i) * 8 + (n - 8)] : 0.0f;
+            s.m = -INFINITY;
+            gather_sums<false>(a.pcol, a.xr, beg, end, l, s);
+            combine_hilo(s);
+            const float den = total_den(s.den);
+            if (head && g == 0) {
+                a.mx[uint64_t(i) * 8 + (n - 8)] = end > beg ? s.m : 0.0f;  // empty row: max 0 (ref_fp32.cpp:11)
+                a.den[uint64_t(i) * 8 + (n - 8)] = den;
+            }
+            const float inv = den > 0.0f ? 1.0f / den : 0.0f;
+            // 1 / den of head 4 (g - 2) + q for the lanes g = 2, 3, gathered before
+            // any lane is masked off
+            float iq[4];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) iq[q] = __shfl(inv, 8 + 4 * (g & 1) + q);
+            if (g >= 2) {
+                // Element (head h, feature pair P = 16 sb + n) of tile row r sits at
+                // sblk(h, P / 8, hl) + 32 r + 4 (P % 8): a per-lane base plus a
+                // compile-time offset for each (q, sb, hl).
+                unsigned char* base = slds + (56 * (g - 2) + 2 * (n / 8)) * kBlk + 32 * r + 4 * (n % 8);
+#pragma unroll
+                for (int sb = 0; sb < kSB; ++sb) {
+                    const int ks = 2 * sb + n / 8;
+                    if (16 * sb + n >= kXRFeat / 2 || ks >= KS) continue;
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        const float s0 = s.d[2 * sb][q] * iq[q], s1 = s.d[2 * sb + 1][q] * iq[q];
+                        const uint32_t hw = bf16x2(s0, s1);
+                        const uint32_t lw = bf16x2(s0 - __builtin_bit_cast(float, hw << 16),
+                                                   s1 - __builtin_bit_cast(float, hw & 0xffff0000u));
+                        unsigned char* e = base + (14 * q + 4 * sb) * kBlk;
+                        *reinterpret_cast<uint32_t*>(e) = hw;
+                        *reinterpret_cast<uint32_t*>(e + kBlk) = lw;
+                    }
+                }
+            }
+        }
+        // W_h^T fragments of this wave's head (h = w; 1 KB per k step, L2
+        // resident), requested before the barrier.  A wave-uniform base plus a
+        // 32-bit lane offset, made opaque so that the addresses are formed here
+        // instead of being held across the gather.
+        bf16x8 wf[KS];
+        {
+            uint32_t lo = uint32_t(l) * uint32_t(sizeof(uint4));
+            asm volatile("" : "+v"(lo));
+            const unsigned char* wb = reinterpret_cast<const unsigned char*>(a.wpk) + uint64_t(w) * kWave * sizeof(uint4);
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks)
+                wf[ks] = __builtin_bit_cast(
+                    bf16x8, *reinterpret_cast<const uint4*>(wb + uint64_t(ks) * a.nmb * kWave * sizeof(uint4) + lo));
+        }
+        __syncthreads();
+        // ---- wave h: the tile's S_h W_h.  B lane l reads tile row l % 16 (lanes
+        // with l % 32 >= 16 repeat rows 0..15; their output columns are dropped).
+        {
+            const int h = w;
+            f32x16 dh, dl;
+#pragma unroll
+            for (int x = 0; x < 16; ++x) dh[x] = dl[x] = 0.0f;
+            const int boff = (l % 16) * 32 + 16 * (l / 32);
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks) {
+                const bf16x8 bh = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(slds + sblk(h, ks, 0) + boff));
+                const bf16x8 bl = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(slds + sblk(h, ks, 1) + boff));
+                dh = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wf[ks], bh, dh, 0, 0, 0);
+                dl = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wf[ks], bl, dl, 0, 0, 0);
+            }
+            const int r = l % 32, half = l / 32;
+            const uint64_t tpos = tile * kTile + r;
+            if (r < kTile && tpos < a.rows) {
+                const uint64_t k = a.rows - 1 - tpos;
+                const uint32_t i = a.perm[k];
+                const uint64_t beg = a.prow[k], end = a.prow[k + 1];
+                if (i < a.n && beg <= end && end <= a.e) {
+                    // Lane (half, r) holds features 32 h + 16 half + {0..15} (permuted packing).
+                    float o[16];
+#pragma unroll
+                    for (int x = 0; x < 16; ++x) {
+                        const float y = dh[x] + dl[x];
+                        o[x] = a.hidden ? elu(y) : y;
+                    }
+                    const uint64_t off = uint64_t(i) * 256 + 32 * h + 16 * half;
+                    if (a.outbf) {
+#pragma unroll
+                        for (int q = 0; q < 2; ++q) {
+                            uint32_t v[4];
+#pragma unroll
+                            for (int x = 0; x < 4; ++x)
+                                v[x] = bf16x2(o[8 * q + 2 * x], o[8 * q + 2 * x + 1]);
+                            *reinterpret_cast<uint4*>(a.outbf + off + 8 * q) = make_uint4(v[0], v[1], v[2], v[3]);
+                        }
+                    }
+                    if (a.out32) {
+#pragma unroll
+                        for (int q = 0; q < 4; ++q)
+                            *reinterpret_cast<float4*>(a.out32 + off + 4 * q) =
+                                make_float4(o[4 * q], o[4 * q + 1], o[4 * q + 2], o[4 * q + 3]);
+                    }
+                }
+            }
+        }
+        __syncthreads();
+    }
+}
+
+// One wave per chunk of a split row: sums from the exact row max into
+// part[c][h * 128 + f] and the denominators into part[c][1024 + h].
+__global__ void __launch_bounds__(kChunkThreads) k_afs_chunks(AfsArgs a) {
+    const int w = __builtin_amdgcn_readfirstlane(int(threadIdx.x) / kWave);
+    const int l = threadIdx.x % kWave;
+    const int g = l / 16, n = l % 16;
+    const bool head = n >= 8;
+    const uint64_t c = uint64_t(blockIdx.x) * (kChunkThreads / kWave) + w;
+    if (c >= a.chunks) return;
+    const uint32_t k = a.chunk_k[c], first = a.chunk_first[c];
+    const uint64_t rbeg = a.prow[k], rend = a.prow[k + 1];
+    const uint32_t i = a.perm[k];
+    if (i >= a.n || rbeg > rend || rend > a.e) return;
+    const uint32_t nch = uint32_t((rend - rbeg + a.chunk_edges - 1) / a.chunk_edges);
+    const uint64_t beg = rbeg + uint64_t(c - first) * a.chunk_edges;
+    const uint64_t end = beg + a.chunk_edges < rend ? beg + a.chunk_edges : rend;
+    Sums s;
+    zero_sums(s);
+    s.L = 0.0f;
+    s.m = 0.0f;
+    if (head) {
+        const int h = n - 8;
+        s.L = a.L[uint64_t(i) * 8 + h];
+        float mc = -INFINITY;
+        for (uint32_t q = 0; q < nch; ++q) mc = fmaxf(mc, a.mchunk[(first + q) * 8 + h]);
+        s.m = leaky(s.L + mc);
+    }
+    gather_sums<true>(a.pcol, a.xr, beg, end, l, s);
+    combine_hilo(s);
+    const float den = total_den(s.den);
+    float* part = a.part + c * kPart;
+    if (g >= 2) {
+#pragma unroll
+        for (int sb = 0; sb < kSB; ++sb) {
+            const int P = 16 * sb + n;
+            if (P >= kXRFeat / 2) continue;
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+                *reinterpret_cast<float2*>(part + (4 * (g - 2) + q) * 128 + 2 * P) =
+                    make_float2(s.d[2 * sb][q], s.d[2 * sb + 1][q]);
+        }
+    }
+    if (head && g == 0) part[kDenOff + (n - 8)] = den;
+}
+
+// One wave per split row (found at its first chunk): adds the chunks' sums
+// and denominators in chunk order, then out_h = (U_h / den_h) W_h on the VALU
+// with the FP32 (bf16-rounded) W; lane l computes columns 4 (l % 8) .. + 3 of
+// head l / 8.
+__global__ void __launch_bounds__(kChunkThreads) k_afs_merge(AfsArgs a) {
+    __shared__ float s[kChunkThreads / kWave][8 * kXRFeat];
+    const int w = threadIdx.x / kWave, l = threadIdx.x % kWave;
+    const uint64_t c = uint64_t(blockIdx.x) * (kChunkThreads / kWave) + w;
+    if (c >= a.chunks || a.chunk_first[c] != c) return;
+    const uint32_t k = a.chunk_k[c];
+    const uint64_t rbeg = a.prow[k], rend = a.prow[k + 1];
+    const uint32_t i = a.perm[k];
+    if (i >= a.n || rbeg > rend || rend > a.e) return;
+    const uint32_t nch = uint32_t((rend - rbeg + a.chunk_edges - 1) / a.chunk_edges);
+    if (c + nch > a.chunks) return;
+    // denominators and the exact max (lanes 0..7)
+    float d = 0.0f;
+    if (l < 8) {
+        float mc = -INFINITY;
+        for (uint32_t q = 0; q < nch; ++q) {
+            d += a.part[(c + q) * kPart + kDenOff + l];
+            mc = fmaxf(mc, a.mchunk[(c + q) * 8 + l]);
+        }
+        a.mx[uint64_t(i) * 8 + l] = leaky(a.L[uint64_t(i) * 8 + l] + mc);
+        a.den[uint64_t(i) * 8 + l] = d;
+    }
+    // S_h[f] = U_h[f] / den_h into LDS; lane l adds features 2l, 2l + 1.
+    float dall[8];  // read before any lane is masked off
+#pragma unroll
+    for (int h = 0; h < 8; ++h) dall[h] = lane_f(d, h);
+    if (l < kXRFeat / 2) {
+        for (int h = 0; h < 8; ++h) {
+            const float inv = dall[h] > 0.0f ? 1.0f / dall[h] : 0.0f;
+            float t0 = 0.0f, t1 = 0.0f;
+            for (uint32_t q = 0; q < nch; ++q) {
+                const float2 v = *reinterpret_cast<const float2*>(a.part + (c + q) * kPart + h * 128 + 2 * l);
+                t0 += v.x;
+                t1 += v.y;
+            }
+            s[w][h * kXRFeat + 2 * l] = t0 * inv;
+            s[w][h * kXRFeat + 2 * l + 1] = t1 * inv;
+        }
+    }
+    wave_sync();
+    const int h = l / 8, c0 = 4 * (l % 8);
+    float o[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int f = 0; f < a.in; ++f) {
+        const float sv = s[w][h * kXRFeat + f];
+        const float4 wv = *reinterpret_cast<const float4*>(a.wq + uint64_t(f) * 256 + 32 * h + c0);
+        o[0] = __builtin_fmaf(sv, wv.x, o[0]);
+        o[1] = __builtin_fmaf(sv, wv.y, o[1]);
+        o[2] = __builtin_fmaf(sv, wv.z, o[2]);
+        o[3] = __builtin_fmaf(sv, wv.w, o[3]);
+    }
+    if (a.hidden)
+#pragma unroll
+        for (int x = 0; x < 4; ++x) o[x] = elu(o[x]);
+    const uint64_t off = uint64_t(i) * 256 + 32 * h + c0;
+    if (a.outbf)
+        *reinterpret_cast<uint2*>(a.outbf + off) =
+            make_uint2(bf16x2(o[0], o[1]), bf16x2(o[2], o[3]));
+    if (a.out32) *reinterpret_cast<float4*>(a.out32 + off) = make_float4(o[0], o[1], o[2], o[3]);
+}
+
+template <int KS>
+hipError_t launch_tiles(const AfsArgs& a, hipStream_t s, int cus) {
+    const uint64_t tiles = (a.rows + kTile - 1) / kTile;
+    if (!tiles) return hipSuccess;
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_afs_tiles<KS>),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, kSBytes);
+    if (e != hipSuccess) return e;
+    uint64_t blocks = uint64_t(cus) * 2;
+    if (blocks > tiles) blocks = tiles;
+    k_afs_tiles<KS><<<dim3(uint32_t(blocks)), kThreads, kSBytes, s>>>(a);
+    return hipGetLastError();
+}
+
+}  // namespace
+
+bool aggregate_afsum_supported(int in, int heads, int dim, uint64_t n) {
+    return in >= 1 && in <= kXRFeat && heads == 8 && dim == 32 && n <= (uint64_t(1) << 32) / (4 * kRowWords);
+}
+
+hipError_t launch_aggregate_afsum(const AfsArgs& a, const SplitTable& t, hipStream_t s, int cus) {
+    if (!aggregate_afsum_supported(a.in, 8, 32, a.n) || a.nmb < 8 || a.ksteps != (a.in + 15) / 16 || !a.xr || !a.wq)
+        return hipErrorInvalidValue;
+    if (a.chunks) {
+        hipError_t e = launch_split_prescan(a.prow, a.pcol, a.R, 8, t, a.e, s);
+        if (e != hipSuccess) return e;
+        const dim3 grid(uint32_t((a.chunks + kChunkThreads / kWave - 1) / (kChunkThreads / kWave)));
+        k_afs_chunks<<<grid, kChunkThreads, 0, s>>>(a);
+        if ((e = hipGetLastError()) != hipSuccess) return e;
+    }
+    hipError_t e = hipSuccess;
+    switch (a.ksteps) {
+        case 1: e = launch_tiles<1>(a, s, cus); break;
+        case 2: e = launch_tiles<2>(a, s, cus); break;
+        case 3: e = launch_tiles<3>(a, s, cus); break;
+        case 4: e = launch_tiles<4>(a, s, cus); break;
+        case 5: e = launch_tiles<5>(a, s, cus); break;
+        case 6: e = launch_tiles<6>(a, s, cus); break;
+        default: e = launch_tiles<7>(a, s, cus); break;
+    }
+    if (e != hipSuccess) return e;
+    if (a.chunks) {
+        const dim3 grid(uint32_t((a.chunks + kChunkThreads / kWave - 1) / (kChunkThreads / kWave)));
+        k_afs_merge<<<grid, kChunkThreads, 0, s>>>(a);
+    }
+    return hipGetLastError();
+}
+
+}  // namespace gatgpu

@@ -176,7 +176,7 @@ __device__ inline void store_row(uint32_t i, int W, int sub, const float (&acc)[
         float y = acc[x] * scale;
         if (hidden) y = elu(y);
         if (out32) out32[uint64_t(i) * W + f] = y;
-        if (outbf) outbf[uint64_t(i) * W + f] = bf16_rne(y);
+        if (outbf) outbf[uint64_t(i) * W + f] = bf16_hw(y);
     }
 }
 

@@ -270,7 +270,7 @@ __device__ inline void finish_row(uint32_t i, const float (&acc)[C::ACC], const 
             uint32_t w[C::VEC / 2];
 #pragma unroll
             for (int x = 0; x < C::VEC / 2; ++x)
-                w[x] = uint32_t(bf16_rne(o[2 * x])) | (uint32_t(bf16_rne(o[2 * x + 1])) << 16);
+                w[x] = bf16x2(o[2 * x], o[2 * x + 1]);
             if constexpr (C::VEC == 8) *reinterpret_cast<uint4*>(outbf + off) = make_uint4(w[0], w[1], w[2], w[3]);
             else *reinterpret_cast<uint2*>(outbf + off) = make_uint2(w[0], w[1]);
         }

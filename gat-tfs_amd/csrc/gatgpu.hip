@@ -302,8 +302,45 @@ int run_layer_af(gatgpu_ctx* c, int l, bool hidden, const float* src32, const ui
     pa.left = Ls.left.as<float>();
     pa.right = Ls.right.as<float>();
     pa.tiles = (n + 31) / 32;
+    // Sum form: R also goes into the tail of each input row (the gather table).
+    const bool sum_form = !fixed && dataflow == GATGPU_AGGREGATE_FIRST && aggregate_afsum_supported(D, K, Ls.dim, n);
+    if (sum_form) {
+        pa.z = Ls.inbf.as<uint16_t>();
+        pa.zs = kXRStride;
+        pa.r_in_z = true;
+        pa.r_off = kXRFeat;
+    }
     HIPCHECK(c, launch_projection_mfma(pa, c->stream, c->cus));
     if (ev_base >= 0) HIPCHECK(c, hipEventRecord(c->ev[ev_base + 2], c->stream));
+    if (sum_form) {
+        AfsArgs a{};
+        a.prow = c->prow.as<uint64_t>();
+        a.pcol = c->pcol.as<uint32_t>();
+        a.perm = c->perm;
+        a.L = Ls.left.as<float>();
+        a.R = Ls.right.as<float>();
+        a.xr = reinterpret_cast<const uint32_t*>(Ls.inbf.as<uint16_t>());
+        a.wpk = Ls.wpk.as<uint4>();
+        a.nmb = Ls.nmb;
+        a.ksteps = Ls.ksteps;
+        a.wq = Ls.wq32.as<float>();
+        a.in = D;
+        a.hidden = hidden;
+        a.mx = Ls.mx.as<float>();
+        a.den = Ls.den.as<float>();
+        a.out32 = hidden ? nullptr : Ls.out32.as<float>();
+        a.outbf = hidden ? Ls.outbf.as<uint16_t>() : nullptr;
+        a.n = n;
+        a.e = c->e;
+        a.rows = c->bins.split_begin;
+        a.chunks = c->split.chunks;
+        a.chunk_k = c->split.chunk_k;
+        a.chunk_first = c->split.chunk_first;
+        a.chunk_edges = c->split.chunk_edges;
+        a.mchunk = c->split.mchunk;
+        a.part = c->split.part;
+        HIPCHECK(c, launch_aggregate_afsum(a, c->split, c->stream, c->cus));
+    } else {
     AfArgs a{};
     a.prow = c->prow.as<uint64_t>();
     a.pcol = c->pcol.as<uint32_t>();
@@ -337,6 +374,7 @@ int run_layer_af(gatgpu_ctx* c, int l, bool hidden, const float* src32, const ui
     a.fixp = fixed ? Ls.fixp.as<float>() : nullptr;
     a.fixden = fixed ? Ls.fixden.as<float>() : nullptr;
     HIPCHECK(c, launch_aggregate_af(a, c->stream, c->cus));
+    }
     if (ev_base >= 0) HIPCHECK(c, hipEventRecord(c->ev[ev_base + 3], c->stream));
     Ls.ran = true;
     Ls.precision = GATGPU_BF16;
@@ -422,6 +460,7 @@ int run_layer(gatgpu_ctx* c, int l, int precision, int dataflow, bool hidden, co
     pa.right = Ls.right.as<float>();
     pa.tiles = (n + 31) / 32;
     pa.r_in_z = r_in_z;
+    pa.r_off = zs - 2;
     pa.ar = Ls.ar.as<float>();
     pa.r_from_z = bf16 && !fixed && r_from_z_supported(pa);
     // ---- convert (bf16 path, FP32 source only; a bf16 source was rounded in

@@ -23,6 +23,17 @@ __host__ __device__ inline uint16_t bf16_rne(float x) {
 __host__ __device__ inline float bf16_widen(uint16_t b) {
     return __builtin_bit_cast(float, uint32_t(b) << 16);
 }
+// Device FP32 -> bf16 on the hardware converter (v_cvt_pk_bf16_f32, round to
+// nearest even): the bits of bf16_rne for every non-NaN input.  Used where
+// the values are finite by construction (sums and products of checked
+// inputs); the input conversion kernels keep bf16_rne.
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+__device__ inline uint32_t bf16x2(float lo, float hi) {
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t){lo, hi}, bf16x2_t));
+}
+__device__ inline uint16_t bf16_hw(float x) { return __builtin_bit_cast(uint16_t, static_cast<__bf16>(x)); }
+
 __device__ inline float leaky(float x) { return x >= 0.0f ? x : 0.2f * x; }
 __device__ inline float elu(float x) { return x >= 0.0f ? x : expm1f(x); }
 
@@ -116,7 +127,8 @@ struct ProjArgs {
     float* left;         // [n][heads]
     float* right;        // [n][heads]
     uint64_t tiles;      // ceil(n / 32)
-    bool r_in_z;         // one head: also store R as FP32 in z[row][zs-2..zs-1]
+    bool r_in_z;         // also store R of head h as FP32 in z[row][r_off + 2h ..]
+    int r_off;           // bf16 offset of R in the z row when r_in_z (one head: zs - 2)
     bool r_from_z;       // 8 x 32 bf16: R = Z_bf16 . aR (the aggregation recomputes it)
     const float* ar;     // aR [256] when r_from_z
 };
@@ -227,6 +239,38 @@ struct AfArgs {
     const float* fixp;   // fixed-p: fixture p in degree-sorted edge order [e][heads], else null
     const float* fixden; // fixed-p: fixture denominators [n][heads]
 };
+// aggregate_afsum.hip: aggregate-first in its sum form (U = sum p X, then U W),
+// 8 heads x 32, D_in <= 112, over the XR gather table.
+constexpr int kXRStride = 128;  // XR row: bf16 elements (256 bytes)
+constexpr int kXRFeat = 112;    // feature slots; R_h as FP32 at bf16 offset kXRFeat + 2h
+struct AfsArgs {
+    const uint64_t* prow;
+    const uint32_t* pcol;
+    const uint32_t* perm;
+    const float* L;      // [n][8]
+    const float* R;      // [n][8] (per-chunk maxima of split rows)
+    const uint32_t* xr;  // XR as 4-byte words [n][64]
+    const uint4* wpk;    // projection weights in pack_projection_weights() order (one group)
+    int nmb, ksteps;     // blocks per group and k steps of wpk
+    const float* wq;     // [in][256] bf16-rounded W as FP32 (split rows)
+    int in;
+    bool hidden;
+    float* mx;
+    float* den;
+    float* out32;
+    uint16_t* outbf;
+    uint64_t n, e;
+    uint64_t rows;       // non-split rows: sorted positions [0, rows)
+    uint64_t chunks;
+    const uint32_t* chunk_k;
+    const uint32_t* chunk_first;
+    uint32_t chunk_edges;
+    float* mchunk;
+    float* part;         // [chunks][8*128 + 8]
+};
+// (n * 256 bytes must stay below 4 GiB: the gather uses 32-bit row offsets)
+bool aggregate_afsum_supported(int in, int heads, int dim, uint64_t n);
+hipError_t launch_aggregate_afsum(const AfsArgs& a, const SplitTable& t, hipStream_t s, int cus);
 bool aggregate_af_supported(int in, int heads, int dim);
 int af_input_stride();
 hipError_t launch_aggregate_af(const AfArgs& a, hipStream_t s, int cus);

@@ -90,8 +90,8 @@ __global__ void __launch_bounds__(kThreads) k_proj_mfma(ProjArgs a) {
             for (int gq = 0; gq < 4; ++gq) {
                 const int f0 = gb * 32 + 16 * half + 4 * gq;
                 if (f0 >= a.width) continue;
-                const uint32_t w0 = uint32_t(bf16_rne(acc[mb][4 * gq])) | (uint32_t(bf16_rne(acc[mb][4 * gq + 1])) << 16);
-                const uint32_t w1 = uint32_t(bf16_rne(acc[mb][4 * gq + 2])) | (uint32_t(bf16_rne(acc[mb][4 * gq + 3])) << 16);
+                const uint32_t w0 = bf16x2(acc[mb][4 * gq], acc[mb][4 * gq + 1]);
+                const uint32_t w1 = bf16x2(acc[mb][4 * gq + 2], acc[mb][4 * gq + 3]);
                 *reinterpret_cast<uint2*>(a.z + row * a.zs + f0) = make_uint2(w0, w1);
             }
         }
@@ -109,7 +109,7 @@ __global__ void __launch_bounds__(kThreads) k_proj_mfma(ProjArgs a) {
                         const float rv = acc[mb][4 + q] + acc[mb][12 + q];
                         a.left[row * a.heads + h] = acc[mb][q] + acc[mb][8 + q];
                         a.right[row * a.heads + h] = rv;
-                        if (a.r_in_z) *reinterpret_cast<float*>(a.z + row * a.zs + a.zs - 2) = rv;
+                        if (a.r_in_z) *reinterpret_cast<float*>(a.z + row * a.zs + a.r_off + 2 * h) = rv;
                     }
                 }
             }
@@ -173,11 +173,8 @@ __global__ void __launch_bounds__(kThreads) k_proj_fast(ProjArgs a) {
                                 __builtin_bit_cast(float, raw[ks][RW - 1].z), __builtin_bit_cast(float, raw[ks][RW - 1].w)};
             uint32_t w4[4];
 #pragma unroll
-            for (int x = 0; x < 4; ++x) {
-                const uint32_t lo = f0 + 2 * x < a.in ? bf16_rne(e[2 * x]) : 0u;
-                const uint32_t hi = f0 + 2 * x + 1 < a.in ? bf16_rne(e[2 * x + 1]) : 0u;
-                w4[x] = lo | (hi << 16);
-            }
+            for (int x = 0; x < 4; ++x)
+                w4[x] = bf16x2(f0 + 2 * x < a.in ? e[2 * x] : 0.0f, f0 + 2 * x + 1 < a.in ? e[2 * x + 1] : 0.0f);
             return __builtin_bit_cast(bf16x8, make_uint4(w4[0], w4[1], w4[2], w4[3]));
         } else {
             return __builtin_bit_cast(bf16x8, raw[ks][0]);
@@ -230,17 +227,21 @@ __global__ void __launch_bounds__(kThreads) k_proj_fast(ProjArgs a) {
 #pragma unroll
         for (int mb = 0; mb < HB; ++mb) {
             float zr[16];
+            uint32_t zp[8];  // the stored bf16 pairs
 #pragma unroll
-            for (int r = 0; r < 16; ++r) zr[r] = bf16_widen(bf16_rne(acc[mb][r]));
+            for (int x = 0; x < 8; ++x) zp[x] = bf16x2(acc[mb][2 * x], acc[mb][2 * x + 1]);
+#pragma unroll
+            for (int x = 0; x < 8; ++x) {
+                zr[2 * x] = __builtin_bit_cast(float, zp[x] << 16);
+                zr[2 * x + 1] = __builtin_bit_cast(float, zp[x] & 0xffff0000u);
+            }
 #pragma unroll
             for (int q8 = 0; q8 < 2; ++q8) {
                 const int f0 = 32 * mb + 16 * half + 8 * q8;
                 if (!full && f0 >= a.width) continue;
                 uint32_t w4[4];
 #pragma unroll
-                for (int x = 0; x < 4; ++x)
-                    w4[x] = uint32_t(bf16_rne(acc[mb][8 * q8 + 2 * x])) |
-                            (uint32_t(bf16_rne(acc[mb][8 * q8 + 2 * x + 1])) << 16);
+                for (int x = 0; x < 4; ++x) w4[x] = zp[4 * q8 + x];
                 *reinterpret_cast<uint4*>(a.z + rs * a.zs + f0) = make_uint4(w4[0], w4[1], w4[2], w4[3]);
             }
             if (FULL && a.r_from_z) {
@@ -268,7 +269,7 @@ __global__ void __launch_bounds__(kThreads) k_proj_fast(ProjArgs a) {
                 const float rv = acc[HB][4 + q] + acc[HB][12 + q];
                 a.left[rs * a.heads + h] = acc[HB][q] + acc[HB][8 + q];
                 if (!(FULL && a.r_from_z)) a.right[rs * a.heads + h] = rv;
-                if (!full && a.r_in_z) *reinterpret_cast<float*>(a.z + rs * a.zs + a.zs - 2) = rv;
+                if (!full && a.r_in_z) *reinterpret_cast<float*>(a.z + rs * a.zs + a.r_off + 2 * h) = rv;
             }
         }
         if (FULL && a.r_from_z && half == 0)
