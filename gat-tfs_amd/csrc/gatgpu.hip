@@ -241,13 +241,15 @@ int z_stride(int precision, int heads, int width, bool* r_in_z) {
     return precision == GATGPU_BF16 ? (width + 7) / 8 * 8 : (width + 3) / 4 * 4;
 }
 
-// AUTO selects transform-first: on gfx950 its aggregation plus MFMA
-// projection is faster than the aggregate-first kernel even where the input
-// row is narrower (measured: 100 -> 8x32 on the 64.3M-edge graph, 9.2 ms TF
-// against 10.7 ms AF).  Aggregate-first stays selectable per call.
-int resolve_dataflow(const LayerState& L, int precision, int dataflow) {
+// AUTO selects aggregate-first where its sum form applies (bf16, 8 x 32,
+// D_in <= 112: it gathers 256-byte input rows instead of 512-byte Z rows;
+// measured on the 64.3M-edge graph, 100 -> 8 x 32: 5.9 ms against 6.8 ms
+// for transform-first) and transform-first everywhere else.
+int resolve_dataflow(const LayerState& L, int precision, int dataflow, uint64_t n) {
     const bool af_ok = precision == GATGPU_BF16 && aggregate_af_supported(L.in, L.heads, L.dim);
-    if (dataflow == GATGPU_AUTO) return GATGPU_TRANSFORM_FIRST;
+    if (dataflow == GATGPU_AUTO)
+        return precision == GATGPU_BF16 && aggregate_afsum_supported(L.in, L.heads, L.dim, n) ? GATGPU_AGGREGATE_FIRST
+                                                                                              : GATGPU_TRANSFORM_FIRST;
     if ((dataflow == GATGPU_AGGREGATE_FIRST || dataflow == GATGPU_TFS_B1) && !af_ok) return -1;
     return dataflow;
 }
@@ -282,29 +284,42 @@ int run_layer_af(gatgpu_ctx* c, int l, bool hidden, const float* src32, const ui
     if (src32) HIPCHECK(c, Ls.inbf.ensure(n * xs * 2));
     // The fixed-p operator has no row max (the reference leaves it unset).
     if (fixed) HIPCHECK(c, hipMemsetAsync(Ls.mx.p, 0, n * K * 4, c->stream));
-    if (ev_base >= 0) HIPCHECK(c, hipEventRecord(c->ev[ev_base], c->stream));
-    if (src32) {
-        HIPCHECK(c, launch_to_bf16_pad(src32, Ls.inbf.as<uint16_t>(), n, D, xs, c->stream));
-        srcbf = Ls.inbf.as<uint16_t>();
-    }
-    if (ev_base >= 0) HIPCHECK(c, hipEventRecord(c->ev[ev_base + 1], c->stream));
+    // Sum form: the gather table is the bf16 input rows with R in their tail.
+    const bool sum_form = !fixed && dataflow == GATGPU_AGGREGATE_FIRST && aggregate_afsum_supported(D, K, Ls.dim, n);
     ProjArgs pa{};
-    pa.x = srcbf;
     pa.n = n;
-    pa.xs = xs;
     pa.ksteps = Ls.lr_ksteps;
     pa.wpk = Ls.wlr.as<uint4>();
     pa.groups = 1;
     pa.head_blocks = 0;
     pa.nmb = 2;
+    // FP32 input, sum form: the L/R projection rounds the rows itself and
+    // writes them into the gather table (the convert stage fused); with 7 k
+    // steps it writes all 112 feature slots, zero past D.
+    const bool fused_convert =
+        sum_form && src32 && D % 4 == 0 && Ls.lr_ksteps * 16 == kXRFeat && projection_fp32_input(pa);
+    if (ev_base >= 0) HIPCHECK(c, hipEventRecord(c->ev[ev_base], c->stream));
+    if (src32 && !fused_convert) {
+        HIPCHECK(c, launch_to_bf16_pad(src32, Ls.inbf.as<uint16_t>(), n, D, xs, c->stream));
+        srcbf = Ls.inbf.as<uint16_t>();
+    }
+    if (ev_base >= 0) HIPCHECK(c, hipEventRecord(c->ev[ev_base + 1], c->stream));
+    if (fused_convert) {
+        pa.x32 = src32;
+        pa.in = D;
+        pa.xs = D;
+        pa.xout = Ls.inbf.as<uint16_t>();
+        pa.xouts = xs;
+    } else {
+        pa.x = srcbf;
+        pa.xs = xs;
+    }
     pa.width = 0;
     pa.heads = K;
     pa.left = Ls.left.as<float>();
     pa.right = Ls.right.as<float>();
     pa.tiles = (n + 31) / 32;
-    // Sum form: R also goes into the tail of each input row (the gather table).
-    const bool sum_form = !fixed && dataflow == GATGPU_AGGREGATE_FIRST && aggregate_afsum_supported(D, K, Ls.dim, n);
-    if (sum_form) {
+    if (sum_form) {  // R also goes into the tail of each input row
         pa.z = Ls.inbf.as<uint16_t>();
         pa.zs = kXRStride;
         pa.r_in_z = true;
@@ -725,7 +740,7 @@ int gatgpu_layer_forward(gatgpu_ctx* c, int layer, int precision, int dataflow, 
         if (!all_finite(input, c->n * uint64_t(c->L[layer].in), &bad))
             return fail(c, GATGPU_ENONFINITE, "nonfinite layer input index=" + std::to_string(bad));
     }
-    const int flow = resolve_dataflow(c->L[layer], precision, dataflow);
+    const int flow = resolve_dataflow(c->L[layer], precision, dataflow, c->n);
     if (flow < 0) return fail(c, GATGPU_EINVAL, "aggregate-first needs bf16, head_dim 32, 1/2/4/8 heads and in <= 128");
     if (int r = run_layer(c, layer, precision, flow, hidden != 0, input, times ? 0 : -1)) return r;
     HIPCHECK(c, hipStreamSynchronize(c->stream));
@@ -793,7 +808,7 @@ int gatgpu_fixed_p_forward(gatgpu_ctx* c, int layer, int precision, int dataflow
     }
     int flow = dataflow == GATGPU_AUTO ? GATGPU_TRANSFORM_FIRST : dataflow;
     if (flow != GATGPU_TRANSFORM_FIRST) {
-        flow = resolve_dataflow(c->L[layer], precision, flow);
+        flow = resolve_dataflow(c->L[layer], precision, flow, c->n);
         if (flow < 0)
             return fail(c, GATGPU_EINVAL, "aggregate-first needs bf16, head_dim 32, 1/2/4/8 heads and in <= 128");
     }
@@ -817,7 +832,7 @@ int gatgpu_model_forward(gatgpu_ctx* c, int precision, int dataflow, float* logi
     const bool timed = times || total_ms;
     for (int l = 0; l < 3; ++l) {
         // In the chained model, aggregate-first applies where the layer supports it.
-        int flow = resolve_dataflow(c->L[l], precision, dataflow);
+        int flow = resolve_dataflow(c->L[l], precision, dataflow, c->n);
         if (flow < 0) flow = GATGPU_TRANSFORM_FIRST;
         if (int r = run_layer(c, l, precision, flow, l < 2, nullptr, timed ? 4 * l : -1)) return r;
     }

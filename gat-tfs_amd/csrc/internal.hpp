@@ -129,6 +129,8 @@ struct ProjArgs {
     uint64_t tiles;      // ceil(n / 32)
     bool r_in_z;         // also store R of head h as FP32 in z[row][r_off + 2h ..]
     int r_off;           // bf16 offset of R in the z row when r_in_z (one head: zs - 2)
+    uint16_t* xout;      // FP32 input, L/R only (head_blocks 0): also store the rounded
+    int xouts;           // bf16 input rows, features [0, 16 ksteps), at xout[row * xouts]
     bool r_from_z;       // 8 x 32 bf16: R = Z_bf16 . aR (the aggregation recomputes it)
     const float* ar;     // aR [256] when r_from_z
 };

@@ -196,8 +196,13 @@ __global__ void __launch_bounds__(kThreads) k_proj_fast(ProjArgs a) {
         for (int mb = 0; mb < NB; ++mb)
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[mb][r] = 0.0f;
+        const uint64_t rs = row < a.n ? row : a.n - 1;  // lanes past n repeat row n - 1
         auto kstep = [&](int ks) {
             const bf16x8 b = operand(ks);
+            if constexpr (F32IN && HB == 0) {
+                if (a.xout)
+                    *reinterpret_cast<uint4*>(a.xout + rs * a.xouts + 16 * ks + 8 * half) = __builtin_bit_cast(uint4, b);
+            }
             const uint4* wk = wlds + size_t(ks) * NB * kWave + l;
 #pragma unroll
             for (int mb = 0; mb < NB; ++mb)
@@ -217,9 +222,8 @@ __global__ void __launch_bounds__(kThreads) k_proj_fast(ProjArgs a) {
 #pragma unroll
         for (int ks = KA; ks < KS; ++ks) kstep(ks);
         // A lane past n computed row n - 1 from the same input, so it stores
-        // that row's own values to it: no branch around the stores, which
+        // that row's own values to it (rs): no branch around the stores, which
         // keeps the wait counts of the next tile's loads exact.
-        const uint64_t rs = row < a.n ? row : a.n - 1;
         // FULL: all 8 heads and 32 HB features present (8 x 32): no per-store
         // bounds tests either.
         const bool full = FULL;

@@ -58,13 +58,17 @@ enum { GATGPU_FP32 = 0, GATGPU_BF16 = 1 };
 
 /* Dataflow of one layer.  TRANSFORM_FIRST projects Z = X W then aggregates Z
  * rows (standard_layer, baseline/src/baseline_standard.cpp:98-108).
- * AGGREGATE_FIRST gathers the layer's input rows instead of Z and projects
- * each gathered row on the MFMA units, summing p (X_j W_h) (tfs_online_fused,
- * implementation/src/gat_tfs_online.cpp:200-283, in the neighbour-step order
- * of baseline/src/baseline_tfs.cpp:16-110); bf16 only, head_dim 32, 1, 2, 4
- * or 8 heads and in <= 128.  AUTO selects the faster dataflow for the layer
- * shape on gfx950.  gatgpu_model_forward with AGGREGATE_FIRST uses it on the
- * layers that support it and transform-first on the others. */
+ * AGGREGATE_FIRST gathers the layer's input rows instead of Z
+ * (tfs_online_fused, implementation/src/gat_tfs_online.cpp:200-283); bf16
+ * only, head_dim 32, 1, 2, 4 or 8 heads and in <= 128.  For 8 heads and
+ * in <= 112 it runs in the sum form of tfs_online_fused: U_h = sum_j p_jh X_j
+ * per row (FP32 sums of the bf16 rows, p entering as hi + lo bf16), then
+ * U_h W_h / den_h on the MFMA units; otherwise each gathered row is projected
+ * and p (X_j W_h) summed, in the neighbour-step order of
+ * baseline/src/baseline_tfs.cpp:16-110.  AUTO selects the sum form where it
+ * applies (bf16) and transform-first elsewhere.  gatgpu_model_forward with
+ * AGGREGATE_FIRST uses it on the layers that support it and transform-first
+ * on the others. */
 /* TFS_B1 is the faithful neighbour-step TFS ("tfs_bf16",
  * baseline/src/baseline_tfs.cpp:16-110, max_prescan first): per step the
  * weighted source row p X_j is rounded to bf16 and multiplied by W_h with FP32

@@ -524,3 +524,48 @@ def test_aggregate_first_matches_transform_first_on_arxiv(gpu_ctx):
     with pytest.raises(gatgpu.GatGpuError) as err:
         gpu_ctx.layer_forward(1, gatgpu.BF16, gatgpu.AGGREGATE_FIRST, True)  # in = 256
     assert err.value.code == gatgpu.EINVAL
+
+
+def test_large_model_auto_sum_form(gpu_ctx):
+    """Full-size check of the 100 -> 8x32 layer on the 64.3M-edge graph, where
+    AUTO takes the aggregate-first sum form (U_h = sum p X_j, then U_h W_h):
+    on 2000 sampled rows plus the 64 heaviest (split into chunks), the row max
+    equals the scalar max of LeakyReLU(L + R) over the GPU's own L/R bit for
+    bit, the denominator and the bf16 output equal a float64 recomputation from
+    the bf16-rounded X and W (to FP32 summation order and one bf16 rounding),
+    and the logits stay within the bf16 tolerance of the transform-first model."""
+    w = inputs.WORKLOADS["large"]
+    row, col = w.graph()
+    x = w.features()
+    m = w.model()
+    gpu_ctx.set_graph(row, col)
+    gpu_ctx.set_model(m)
+    gpu_ctx.set_input(x)
+    auto, _, _ = gpu_ctx.model_forward(gatgpu.BF16, gatgpu.AUTO)
+    assert gpu_ctx.stage(0, "z") is None  # layer 1 ran aggregate-first
+    L, R = gpu_ctx.stage(0, "left"), gpu_ctx.stage(0, "right")
+    M, den, out = gpu_ctx.stage(0, "max"), gpu_ctx.stage(0, "den"), gpu_ctx.stage(0, "out")
+    p0 = m[0]
+    K, d = p0["heads"], p0["dim"]
+    wq = oracle.quantize_bf16(p0["w"]).astype(np.float64)
+    deg = np.diff(row.astype(np.int64))
+    rng = np.random.default_rng(5)
+    rows = np.concatenate((rng.choice(w.n, 2000, replace=False), np.argsort(deg)[-64:]))
+    for i in rows:
+        b, e = int(row[i]), int(row[i + 1])
+        js = col[b:e].astype(np.int64)
+        s = L[i][None, :] + R[js]
+        s = np.where(s >= 0, s, np.float32(0.2) * s).astype(np.float32)
+        assert np.array_equal(M[i], s.max(axis=0)), i
+        p = np.exp(s.astype(np.float64) - M[i].astype(np.float64))
+        dsum = p.sum(axis=0)
+        assert np.all(np.abs(den[i] - dsum) <= 1e-5 * dsum), i
+        xq = oracle.quantize_bf16(x[js]).astype(np.float64)
+        u = p.T @ xq / dsum[:, None]  # [K][D]
+        y = np.concatenate([u[h] @ wq[:, h * d:(h + 1) * d] for h in range(K)])
+        y = np.where(y >= 0, y, np.expm1(y))
+        tol = np.abs(y) * 2.0 ** -8 + 1e-5
+        assert np.all(np.abs(out[i] - y) <= tol), (i, np.max(np.abs(out[i] - y) - tol))
+    tf, _, _ = gpu_ctx.model_forward(gatgpu.BF16, gatgpu.TRANSFORM_FIRST)
+    e = oracle.errors(tf, auto)
+    assert e["finite"] and e["relative_l2"] < BF16_REL_L2, e
