@@ -60,6 +60,8 @@ constexpr int kB = 32;                     // edges per batch (MFMA contraction)
 constexpr int kSB = 4;                     // super-blocks of 16 words per row
 constexpr int kBlk = kTile * 32 + 16;      // bytes per (head, k step, hi|lo) block of S, padded
 constexpr int kSBytes = 8 * kMaxKS * 2 * kBlk;
+constexpr int kLdsBytes = kSBytes + kTile * 4;  // S, then the tile's node ids
+constexpr uint32_t kNoRow = 0xffffffffu;
 constexpr int kPart = 8 * 128 + 8;         // floats per chunk partial (U_h rows of 128, then den)
 constexpr int kDenOff = 8 * 128;
 constexpr int kChunkThreads = 256;
@@ -209,6 +211,8 @@ __device__ inline void combine_hilo(Sums& s) {
 template <int KS>
 __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) k_afs_tiles(AfsArgs a) {
     extern __shared__ __attribute__((aligned(16))) unsigned char slds[];
+    // Destination node of each tile row (kNoRow: none), for the projection stores.
+    uint32_t* trow = reinterpret_cast<uint32_t*>(slds + kSBytes);
     const int w = __builtin_amdgcn_readfirstlane(int(threadIdx.x) / kWave);
     const int l = threadIdx.x % kWave;
     const int g = l / 16, n = l % 16;
@@ -220,11 +224,17 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4
         for (int rr = 0; rr < 2; ++rr) {
             const int r = w + kWaves * rr;
             const uint64_t tpos = tile * kTile + r;
-            if (tpos >= a.rows) continue;
-            const uint64_t k = a.rows - 1 - tpos;
-            const uint32_t i = a.perm[k];
-            const uint64_t beg = a.prow[k], end = a.prow[k + 1];
-            if (i >= a.n || beg > end || end > a.e) continue;
+            uint32_t i = kNoRow;
+            uint64_t beg = 0, end = 0;
+            if (tpos < a.rows) {
+                const uint64_t k = a.rows - 1 - tpos;
+                i = a.perm[k];
+                beg = a.prow[k];
+                end = a.prow[k + 1];
+                if (i >= a.n || beg > end || end > a.e) i = kNoRow;
+            }
+            if (l == 0) trow[r] = i;
+            if (i == kNoRow) continue;
             Sums s;
             zero_sums(s);
             s.L = head ? a.L[uint64_t(i) * 8 + (n - 8)] : 0.0f;
@@ -295,12 +305,9 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4
                 dl = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wf[ks], bl, dl, 0, 0, 0);
             }
             const int r = l % 32, half = l / 32;
-            const uint64_t tpos = tile * kTile + r;
-            if (r < kTile && tpos < a.rows) {
-                const uint64_t k = a.rows - 1 - tpos;
-                const uint32_t i = a.perm[k];
-                const uint64_t beg = a.prow[k], end = a.prow[k + 1];
-                if (i < a.n && beg <= end && end <= a.e) {
+            const uint32_t i = trow[r % kTile];
+            if (r < kTile) {
+                if (i != kNoRow) {
                     // Lane (half, r) holds features 32 h + 16 half + {0..15} (permuted packing).
                     float o[16];
 #pragma unroll
@@ -446,11 +453,11 @@ hipError_t launch_tiles(const AfsArgs& a, hipStream_t s, int cus) {
     const uint64_t tiles = (a.rows + kTile - 1) / kTile;
     if (!tiles) return hipSuccess;
     hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_afs_tiles<KS>),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, kSBytes);
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, kLdsBytes);
     if (e != hipSuccess) return e;
     uint64_t blocks = uint64_t(cus) * 2;
     if (blocks > tiles) blocks = tiles;
-    k_afs_tiles<KS><<<dim3(uint32_t(blocks)), kThreads, kSBytes, s>>>(a);
+    k_afs_tiles<KS><<<dim3(uint32_t(blocks)), kThreads, kLdsBytes, s>>>(a);
     return hipGetLastError();
 }
 
