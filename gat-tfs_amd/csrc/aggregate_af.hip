@@ -306,7 +306,7 @@ __global__ void __launch_bounds__(kThreads, 2) k_af_ns(AfArgs a, Items it) {
 #pragma unroll
                 for (int x = 0; x < 4; ++x) {
                     const float y = den[q] > 0.0f ? acc[q][4 * gq + x] * scale : 0.0f;  // empty row: exact 0
-                    o[x] = a.hidden ? elu(y) : y;
+                    o[x] = a.hidden ? elu_bf16(y) : y;
                 }
                 if (a.outbf)
                     *reinterpret_cast<uint2*>(a.outbf + uint64_t(i) * W + f0) =
@@ -356,7 +356,7 @@ __global__ void __launch_bounds__(kThreads) k_af_merge(AfArgs a, int blocks) {
         if (!(d > 0.0f)) o[0] = o[1] = o[2] = o[3] = 0.0f;
         if (a.hidden)
 #pragma unroll
-            for (int x = 0; x < 4; ++x) o[x] = elu(o[x]);
+            for (int x = 0; x < 4; ++x) o[x] = elu_bf16(o[x]);
         if (a.outbf)
             *reinterpret_cast<uint2*>(a.outbf + uint64_t(i) * W + f0) =
                 make_uint2(bf16x2(o[0], o[1]), bf16x2(o[2], o[3]));

@@ -313,7 +313,7 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4
 #pragma unroll
                     for (int x = 0; x < 16; ++x) {
                         const float y = dh[x] + dl[x];
-                        o[x] = a.hidden ? elu(y) : y;
+                        o[x] = a.hidden ? elu_bf16(y) : y;
                     }
                     const uint64_t off = uint64_t(i) * 256 + 32 * h + 16 * half;
                     if (a.outbf) {
@@ -440,7 +440,7 @@ __global__ void __launch_bounds__(kChunkThreads) k_afs_merge(AfsArgs a) {
     }
     if (a.hidden)
 #pragma unroll
-        for (int x = 0; x < 4; ++x) o[x] = elu(o[x]);
+        for (int x = 0; x < 4; ++x) o[x] = elu_bf16(o[x]);
     const uint64_t off = uint64_t(i) * 256 + 32 * h + c0;
     if (a.outbf)
         *reinterpret_cast<uint2*>(a.outbf + off) =

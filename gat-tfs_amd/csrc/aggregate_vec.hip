@@ -261,9 +261,13 @@ __device__ inline void finish_row(uint32_t i, const float (&acc)[C::ACC], const 
         const float scale = den[v] > 0.0f ? 1.0f / den[v] : 0.0f;
         float o[C::VEC];
 #pragma unroll
-        for (int x = 0; x < C::VEC; ++x) {
-            const float y = acc[v * C::VEC + x] * scale;
-            o[x] = hidden ? elu(y) : y;
+        for (int x = 0; x < C::VEC; ++x) o[x] = acc[v * C::VEC + x] * scale;
+        if (hidden && out32) {
+#pragma unroll
+            for (int x = 0; x < C::VEC; ++x) o[x] = elu(o[x]);
+        } else if (hidden) {  // stored as bf16 only
+#pragma unroll
+            for (int x = 0; x < C::VEC; ++x) o[x] = elu_bf16(o[x]);
         }
         const uint64_t off = uint64_t(i) * C::W + f0;
         if (outbf) {

@@ -37,12 +37,24 @@ __device__ inline uint16_t bf16_hw(float x) { return __builtin_bit_cast(uint16_t
 __device__ inline float leaky(float x) { return x >= 0.0f ? x : 0.2f * x; }
 __device__ inline float elu(float x) { return x >= 0.0f ? x : expm1f(x); }
 
+
 // Softmax weight e^x for x <= 0 as 2^(x log2 e) on the hardware base-2
 // exponential (v_exp_f32): two instructions instead of the range-reduced
 // expf.  exp_w(0) = 1 and exp_w(-inf) = 0 exactly; otherwise the relative
 // error is about |x| 2^-24 (the rounded product) plus one ulp, below 2e-6
 // wherever e^x is above 2^-30.
 __device__ inline float exp_w(float x) { return __builtin_amdgcn_exp2f(x * 1.44269504088896341f); }
+
+// ELU for outputs that are stored as bf16: e^x - 1 from the hardware exp2
+// (exp_w) where x < -1/4 (there |e^x - 1| > 0.22, so the exp2 error stays
+// below 1e-6 of the result), and from the Taylor polynomial of e^x - 1 to
+// x^6 / 720 above (remainder below |x|^7 / 5040 < 2e-8 |x|).  The relative
+// error is under 1e-6, against 2^-9 for the bf16 rounding that follows.
+__device__ inline float elu_bf16(float x) {
+    if (x >= 0.0f) return x;
+    const float t = x * (1.0f + x * (0.5f + x * (1.0f / 6 + x * (1.0f / 24 + x * (1.0f / 120 + x * (1.0f / 720))))));
+    return x < -0.25f ? exp_w(x) - 1.0f : t;
+}
 
 // A buffer that no thread of the launch writes, seen through the constant
 // address space: loads from it at wave-uniform addresses become scalar loads
