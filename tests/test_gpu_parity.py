@@ -569,3 +569,47 @@ def test_large_model_auto_sum_form(gpu_ctx):
     tf, _, _ = gpu_ctx.model_forward(gatgpu.BF16, gatgpu.TRANSFORM_FIRST)
     e = oracle.errors(tf, auto)
     assert e["finite"] and e["relative_l2"] < BF16_REL_L2, e
+
+
+def test_skew_model_properties(gpu_ctx):
+    """Full-size check on the R-MAT graph (2^22 nodes, 100.6M edges, max
+    in-degree 132 270, 9 109 split rows; 128 -> 8x64 -> 8x64 -> 1x64, bf16):
+    on 1000 sampled rows plus the 32 heaviest, for layer 2 (8 x 64) and layer 3
+    (one head of 64), the row max equals the scalar max of LeakyReLU(L + R)
+    over the GPU's own L/R bit for bit, the denominator equals a float64 sum of
+    p, and the output equals the float64 sum_j p Z_j / den over the GPU's own
+    bf16 Z rows (to FP32 summation error and one bf16 rounding of hidden
+    outputs)."""
+    w = inputs.WORKLOADS["skew"]
+    row, col = w.graph()
+    x = w.features()
+    m = w.model()
+    gpu_ctx.set_graph(row, col)
+    gpu_ctx.set_model(m)
+    gpu_ctx.set_input(x)
+    logits, _, _ = gpu_ctx.model_forward(gatgpu.BF16, gatgpu.AUTO)
+    assert np.isfinite(logits).all()
+    deg = np.diff(row.astype(np.int64))
+    rng = np.random.default_rng(7)
+    rows = np.concatenate((rng.choice(w.n, 1000, replace=False), np.argsort(deg)[-32:]))
+    for layer, hidden in ((1, True), (2, False)):
+        K, d = m[layer]["heads"], m[layer]["dim"]
+        Z = gpu_ctx.stage(layer, "z").astype(np.float64)
+        L, R = gpu_ctx.stage(layer, "left"), gpu_ctx.stage(layer, "right")
+        M, den, out = gpu_ctx.stage(layer, "max"), gpu_ctx.stage(layer, "den"), gpu_ctx.stage(layer, "out")
+        for i in rows:
+            js = col[int(row[i]):int(row[i + 1])].astype(np.int64)
+            s = L[i][None, :] + R[js]
+            s = np.where(s >= 0, s, np.float32(0.2) * s).astype(np.float32)
+            assert np.array_equal(M[i], s.max(axis=0)), (layer, i)
+            p = np.exp(s.astype(np.float64) - M[i].astype(np.float64))
+            dsum = p.sum(axis=0)
+            assert np.all(np.abs(den[i] - dsum) <= 1e-5 * dsum), (layer, i)
+            zj = Z[js][:, :K * d].reshape(len(js), K, d)
+            y = (np.einsum("jh,jhc->hc", p, zj) / dsum[:, None]).reshape(-1)
+            mag = (np.einsum("jh,jhc->hc", p, np.abs(zj)) / dsum[:, None]).reshape(-1)
+            if hidden:
+                y = np.where(y >= 0, y, np.expm1(y))
+            # FP32 sums over up to 132K edges (256-edge chunks added in order)
+            tol = (np.abs(y) * 2.0 ** -8 if hidden else 0.0) + 1e-4 * mag + 1e-6
+            assert np.all(np.abs(out[i] - y) <= tol), (layer, i, np.max(np.abs(out[i] - y) - tol))
