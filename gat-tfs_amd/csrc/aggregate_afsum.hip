@@ -60,7 +60,7 @@ constexpr int kB = 32;                     // edges per batch (MFMA contraction)
 constexpr int kSB = 4;                     // super-blocks of 16 words per row
 constexpr int kBlk = kTile * 32 + 16;      // bytes per (head, k step, hi|lo) block of S, padded
 constexpr int kSBytes = 8 * kMaxKS * 2 * kBlk;
-constexpr int kLdsBytes = kSBytes + kTile * 4;  // S, then the tile's node ids
+constexpr int kLdsBytes = kSBytes + 2 * kTile * 4;  // S, then the tile's node ids (two buffers)
 constexpr uint32_t kNoRow = 0xffffffffu;
 constexpr int kPart = 8 * 128 + 8;         // floats per chunk partial (U_h rows of 128, then den)
 constexpr int kDenOff = 8 * 128;
@@ -208,17 +208,25 @@ __device__ inline void combine_hilo(Sums& s) {
         for (int r = 0; r < 4; ++r) s.d[b][r] += __shfl_xor(s.d[b][r], 32);
 }
 
-template <int KS>
+// HL: S staged as hi + lo bf16 (FP32 outputs), one buffer, a barrier before and
+// after the projection.  Otherwise (bf16-stored hidden outputs) S is staged
+// as one bf16 (its rounding is that of a bf16 projection input, 2^-9
+// relative) in two alternating buffers, with one barrier per tile: a wave
+// writes buffer t % 2 only after the barrier of tile t - 1, which every wave
+// reaches after projecting tile t - 2 from the same buffer.
+template <int KS, bool HL>
 __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) k_afs_tiles(AfsArgs a) {
     extern __shared__ __attribute__((aligned(16))) unsigned char slds[];
     // Destination node of each tile row (kNoRow: none), for the projection stores.
-    uint32_t* trow = reinterpret_cast<uint32_t*>(slds + kSBytes);
+    uint32_t* const trow_all = reinterpret_cast<uint32_t*>(slds + kSBytes);
+    int buf = 0;
     const int w = __builtin_amdgcn_readfirstlane(int(threadIdx.x) / kWave);
     const int l = threadIdx.x % kWave;
     const int g = l / 16, n = l % 16;
     const bool head = n >= 8;
     const uint64_t tiles = (a.rows + kTile - 1) / kTile;
-    for (uint64_t tile = blockIdx.x; tile < tiles; tile += gridDim.x) {
+    for (uint64_t tile = blockIdx.x; tile < tiles; tile += gridDim.x, buf ^= HL ? 0 : 1) {
+        uint32_t* const trow = trow_all + buf * kTile;
         // ---- two rows per wave: sums, softmax state, S into LDS
 #pragma unroll 1
         for (int rr = 0; rr < 2; ++rr) {
@@ -255,8 +263,10 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4
             if (g >= 2) {
                 // Element (head h, feature pair P = 16 sb + n) of tile row r sits at
                 // sblk(h, P / 8, hl) + 32 r + 4 (P % 8): a per-lane base plus a
-                // compile-time offset for each (q, sb, hl).
-                unsigned char* base = slds + (56 * (g - 2) + 2 * (n / 8)) * kBlk + 32 * r + 4 * (n % 8);
+                // compile-time offset for each (q, sb, hl); block index
+                // ((h * 7 + ks) * 2 + hl) with hi + lo, (buf * 8 + h) * 7 + ks without.
+                unsigned char* base = slds + 32 * r + 4 * (n % 8) +
+                                      (HL ? 56 * (g - 2) + 2 * (n / 8) : buf * 56 + 28 * (g - 2) + n / 8) * kBlk;
 #pragma unroll
                 for (int sb = 0; sb < kSB; ++sb) {
                     const int ks = 2 * sb + n / 8;
@@ -265,11 +275,15 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4
                     for (int q = 0; q < 4; ++q) {
                         const float s0 = s.d[2 * sb][q] * iq[q], s1 = s.d[2 * sb + 1][q] * iq[q];
                         const uint32_t hw = bf16x2(s0, s1);
-                        const uint32_t lw = bf16x2(s0 - __builtin_bit_cast(float, hw << 16),
-                                                   s1 - __builtin_bit_cast(float, hw & 0xffff0000u));
-                        unsigned char* e = base + (14 * q + 4 * sb) * kBlk;
-                        *reinterpret_cast<uint32_t*>(e) = hw;
-                        *reinterpret_cast<uint32_t*>(e + kBlk) = lw;
+                        if constexpr (HL) {
+                            const uint32_t lw = bf16x2(s0 - __builtin_bit_cast(float, hw << 16),
+                                                       s1 - __builtin_bit_cast(float, hw & 0xffff0000u));
+                            unsigned char* e = base + (14 * q + 4 * sb) * kBlk;
+                            *reinterpret_cast<uint32_t*>(e) = hw;
+                            *reinterpret_cast<uint32_t*>(e + kBlk) = lw;
+                        } else {
+                            *reinterpret_cast<uint32_t*>(base + (7 * q + 2 * sb) * kBlk) = hw;
+                        }
                     }
                 }
             }
@@ -299,10 +313,18 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4
             const int boff = (l % 16) * 32 + 16 * (l / 32);
 #pragma unroll
             for (int ks = 0; ks < KS; ++ks) {
-                const bf16x8 bh = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(slds + sblk(h, ks, 0) + boff));
-                const bf16x8 bl = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(slds + sblk(h, ks, 1) + boff));
-                dh = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wf[ks], bh, dh, 0, 0, 0);
-                dl = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wf[ks], bl, dl, 0, 0, 0);
+                if constexpr (HL) {
+                    const bf16x8 bh = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(slds + sblk(h, ks, 0) + boff));
+                    const bf16x8 bl = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(slds + sblk(h, ks, 1) + boff));
+                    dh = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wf[ks], bh, dh, 0, 0, 0);
+                    dl = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wf[ks], bl, dl, 0, 0, 0);
+                } else {
+                    // even / odd k steps in two chains
+                    const bf16x8 b = __builtin_bit_cast(
+                        bf16x8, *reinterpret_cast<const uint4*>(slds + ((buf * 8 + h) * kMaxKS + ks) * kBlk + boff));
+                    if (ks % 2 == 0) dh = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wf[ks], b, dh, 0, 0, 0);
+                    else dl = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wf[ks], b, dl, 0, 0, 0);
+                }
             }
             const int r = l % 32, half = l / 32;
             const uint32_t i = trow[r % kTile];
@@ -335,7 +357,7 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4
                 }
             }
         }
-        __syncthreads();
+        if constexpr (HL) __syncthreads();
     }
 }
 
@@ -448,17 +470,23 @@ __global__ void __launch_bounds__(kChunkThreads) k_afs_merge(AfsArgs a) {
     if (a.out32) *reinterpret_cast<float4*>(a.out32 + off) = make_float4(o[0], o[1], o[2], o[3]);
 }
 
-template <int KS>
-hipError_t launch_tiles(const AfsArgs& a, hipStream_t s, int cus) {
+template <int KS, bool HL>
+hipError_t launch_tiles_hl(const AfsArgs& a, hipStream_t s, int cus) {
     const uint64_t tiles = (a.rows + kTile - 1) / kTile;
     if (!tiles) return hipSuccess;
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_afs_tiles<KS>),
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_afs_tiles<KS, HL>),
                                        hipFuncAttributeMaxDynamicSharedMemorySize, kLdsBytes);
     if (e != hipSuccess) return e;
     uint64_t blocks = uint64_t(cus) * 2;
     if (blocks > tiles) blocks = tiles;
-    k_afs_tiles<KS><<<dim3(uint32_t(blocks)), kThreads, kLdsBytes, s>>>(a);
+    k_afs_tiles<KS, HL><<<dim3(uint32_t(blocks)), kThreads, kLdsBytes, s>>>(a);
     return hipGetLastError();
+}
+
+// FP32 outputs keep S as hi + lo; bf16-stored outputs stage one bf16.
+template <int KS>
+hipError_t launch_tiles(const AfsArgs& a, hipStream_t s, int cus) {
+    return a.out32 ? launch_tiles_hl<KS, true>(a, s, cus) : launch_tiles_hl<KS, false>(a, s, cus);
 }
 
 }  // namespace

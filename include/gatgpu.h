@@ -63,7 +63,9 @@ enum { GATGPU_FP32 = 0, GATGPU_BF16 = 1 };
  * only, head_dim 32, 1, 2, 4 or 8 heads and in <= 128.  For 8 heads and
  * in <= 112 it runs in the sum form of tfs_online_fused: U_h = sum_j p_jh X_j
  * per row (FP32 sums of the bf16 rows, p entering as hi + lo bf16), then
- * U_h W_h / den_h on the MFMA units; otherwise each gathered row is projected
+ * (U_h / den_h) W_h on the MFMA units, with U_h / den_h entering as hi + lo
+ * bf16 for FP32 outputs and as one bf16 for bf16-stored hidden outputs (the
+ * rounding of a bf16 projection input); otherwise each gathered row is projected
  * and p (X_j W_h) summed, in the neighbour-step order of
  * baseline/src/baseline_tfs.cpp:16-110.  AUTO selects the sum form where it
  * applies (bf16) and transform-first elsewhere.  gatgpu_model_forward with

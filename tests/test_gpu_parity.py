@@ -532,7 +532,8 @@ def test_large_model_auto_sum_form(gpu_ctx):
     on 2000 sampled rows plus the 64 heaviest (split into chunks), the row max
     equals the scalar max of LeakyReLU(L + R) over the GPU's own L/R bit for
     bit, the denominator and the bf16 output equal a float64 recomputation from
-    the bf16-rounded X and W (to FP32 summation order and one bf16 rounding),
+    the bf16-rounded X and W (to one bf16 rounding of the staged sums and of
+    the output),
     and the logits stay within the bf16 tolerance of the transform-first model."""
     w = inputs.WORKLOADS["large"]
     row, col = w.graph()
@@ -563,8 +564,10 @@ def test_large_model_auto_sum_form(gpu_ctx):
         xq = oracle.quantize_bf16(x[js]).astype(np.float64)
         u = p.T @ xq / dsum[:, None]  # [K][D]
         y = np.concatenate([u[h] @ wq[:, h * d:(h + 1) * d] for h in range(K)])
+        mag = np.concatenate([np.abs(u[h]) @ np.abs(wq[:, h * d:(h + 1) * d]) for h in range(K)])
         y = np.where(y >= 0, y, np.expm1(y))
-        tol = np.abs(y) * 2.0 ** -8 + 1e-5
+        # one bf16 rounding of the output and of the staged sums U / den
+        tol = np.abs(y) * 2.0 ** -8 + mag * 2.0 ** -8 + 1e-6
         assert np.all(np.abs(out[i] - y) <= tol), (i, np.max(np.abs(out[i] - y) - tol))
     tf, _, _ = gpu_ctx.model_forward(gatgpu.BF16, gatgpu.TRANSFORM_FIRST)
     e = oracle.errors(tf, auto)
