@@ -21,16 +21,17 @@
 // edges 8g .. 8g + 7 of the batch) loads word 16 sb + n of each of its 8
 // edges' rows, sb = 0..3 (features 2(16 sb + n) and 2(16 sb + n) + 1): the low
 // halves of those 8 words are the B operand of an even-feature block, the
-// high halves that of an odd-feature block.  Word 56 + h of a row is R_jh, so
-// lane n = 8 + h of super-block 3 holds R of its 8 edges for head h: it scores
-// them, keeps the running max m_h and the denominator, and splits p into
-// hi + lo bf16 (p enters to about 2^-17): A row h holds the hi parts, row
-// 8 + h the lo parts.  A batch that raises some m_h first rescales the sums
-// by exp(m_old - m_new) (the running-maximum form of
-// gat_tfs_online.cpp:86-117); the final m_h is leaky(L_h + max_j R_jh) bit
-// for bit, as leaky and the addition are monotone.  Lane (g, n), register r
-// of block (sb, par) holds the hi (g = 0, 1) or lo (g = 2, 3) sum of head
-// 4 (g % 2) + r, feature 2(16 sb + n) + par; U is their sum.
+// high halves that of an odd-feature block.  Word 56 + h of a row is R_jh; a
+// DPP rotation by 8 hands it from lane 8 + h of super-block 3 to lane h, which
+// scores head h for its 8 edges, keeps the running max m_h and the
+// denominator, and splits p into hi + lo bf16 (p enters to about 2^-17): A
+// row h holds the hi parts in one MFMA and the lo parts in a second one into
+// the same accumulators (rows 8..15 of A are zero).  A batch that raises some
+// m_h first rescales the sums by exp(m_old - m_new) (the running-maximum form
+// of gat_tfs_online.cpp:86-117); the final m_h is leaky(L_h + max_j R_jh) bit
+// for bit, as leaky and the addition are monotone.  Lane (g, n), g = 0, 1,
+// register r of block (sb, par) holds U of head 4g + r, feature
+// 2(16 sb + n) + par.
 //
 // Blocks of 8 waves take tiles of 16 consecutive degree-sorted rows, two per
 // wave.  A row's normalised sums S_h = U_h / den_h go to LDS as a hi + lo pair
@@ -76,7 +77,7 @@ __device__ inline float lane_f(float x, int lane) {
 }
 
 // Running sums of one row or chunk.  d[2 sb + par] are the D accumulators of
-// the feature blocks; m, den and L live in the head lanes (n >= 8, head n - 8;
+// the feature blocks; m, den and L live in the head lanes (n < 8, head n;
 // den of the lane's own k group until combined).
 struct Sums {
     f32x4 d[2 * kSB];
@@ -90,7 +91,7 @@ __device__ inline void gather_sums(const uint32_t* __restrict__ pcol, const uint
                                    uint64_t beg, uint64_t end, int l, Sums& s) {
     if (beg >= end) return;
     const int g = l / 16, n = l % 16;
-    const bool head = n >= 8;
+    const bool head = n < 8;
     const auto* pc = read_only(pcol);
     uint32_t js[kB];
 #pragma unroll
@@ -125,7 +126,8 @@ __device__ inline void gather_sums(const uint32_t* __restrict__ pcol, const uint
         float mb = -INFINITY;
 #pragma unroll
         for (int t = 0; t < 8; ++t) {
-            sc[t] = (head && 8 * g + t < cnt) ? leaky(s.L + __builtin_bit_cast(float, raw[3][t])) : -INFINITY;
+            const float r = __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(int(raw[3][t]), 0x128, 0xF, 0xF, false));
+            sc[t] = (head && 8 * g + t < cnt) ? leaky(s.L + r) : -INFINITY;
             mb = fmaxf(mb, sc[t]);
         }
         mb = fmaxf(mb, __shfl_xor(mb, 16));
@@ -136,9 +138,7 @@ __device__ inline void gather_sums(const uint32_t* __restrict__ pcol, const uint
             scale = mn > s.m ? exp_w(s.m - mn) : 1.0f;  // exp(-inf) = 0 on the first batch
             s.m = mn;
         }
-        // ---- A operand: row h = hi part of p_h for edges 8g + t, row 8 + h = lo
-        // part (S = hi + lo to about 2^-17); the head lanes form both and the
-        // lanes n < 8 take the hi words from lane n + 8 (DPP rotate by 8).
+        // ---- A operands: row h = hi (then lo) part of p_h for edges 8g + t
         uint32_t ah[4], al[4];
         float ps = 0.0f;
 #pragma unroll
@@ -149,23 +149,18 @@ __device__ inline void gather_sums(const uint32_t* __restrict__ pcol, const uint
             ah[q] = bf16x2(p0, p1);
             al[q] = bf16x2(p0 - __builtin_bit_cast(float, ah[q] << 16), p1 - __builtin_bit_cast(float, ah[q] & 0xffff0000u));
         }
-        uint32_t av[4];
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            const uint32_t hi_from_head = uint32_t(__builtin_amdgcn_mov_dpp(int(ah[q]), 0x128, 0xF, 0xF, false));
-            av[q] = head ? al[q] : hi_from_head;
-        }
         s.den = s.den * scale + ps;
         if (!EXACT && __any(head && scale != 1.0f)) {
             // D register r of lane group g belongs to head 4 (g % 2) + r.
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                const float f = __shfl(scale, 8 + 4 * (g & 1) + r);
+                const float f = __shfl(scale, 4 * (g & 1) + r);
 #pragma unroll
                 for (int b = 0; b < 2 * kSB; ++b) s.d[b][r] *= f;
             }
         }
-        const bf16x8 A = __builtin_bit_cast(bf16x8, make_uint4(av[0], av[1], av[2], av[3]));
+        const bf16x8 Ah = __builtin_bit_cast(bf16x8, make_uint4(ah[0], ah[1], ah[2], ah[3]));
+        const bf16x8 Al = __builtin_bit_cast(bf16x8, make_uint4(al[0], al[1], al[2], al[3]));
         // ---- B operands from the low / high halves of the 8 words, and the MFMAs
 #pragma unroll
         for (int sb = 0; sb < kSB; ++sb) {
@@ -178,8 +173,10 @@ __device__ inline void gather_sums(const uint32_t* __restrict__ pcol, const uint
             }
             const bf16x8 Be = __builtin_bit_cast(bf16x8, make_uint4(ev[0], ev[1], ev[2], ev[3]));
             const bf16x8 Bo = __builtin_bit_cast(bf16x8, make_uint4(od[0], od[1], od[2], od[3]));
-            s.d[2 * sb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A, Be, s.d[2 * sb], 0, 0, 0);
-            s.d[2 * sb + 1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A, Bo, s.d[2 * sb + 1], 0, 0, 0);
+            s.d[2 * sb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(Ah, Be, s.d[2 * sb], 0, 0, 0);
+            s.d[2 * sb + 1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(Ah, Bo, s.d[2 * sb + 1], 0, 0, 0);
+            s.d[2 * sb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(Al, Be, s.d[2 * sb], 0, 0, 0);
+            s.d[2 * sb + 1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(Al, Bo, s.d[2 * sb + 1], 0, 0, 0);
         }
 #pragma unroll
         for (int t = 0; t < kB; ++t) js[t] = jn[t];
@@ -194,19 +191,12 @@ __device__ inline void zero_sums(Sums& s) {
     s.den = 0.0f;
 }
 
-// Denominator of head lane (n = 8 + h) over the 4 k groups.
+// Denominator of head lane (n = h) over the 4 k groups.
 __device__ inline float total_den(float den) {
     den += __shfl_xor(den, 16);
     return den + __shfl_xor(den, 32);
 }
 
-// hi + lo sums: afterwards lanes g = 2, 3 hold U of head 4 (g - 2) + r.
-__device__ inline void combine_hilo(Sums& s) {
-#pragma unroll
-    for (int b = 0; b < 2 * kSB; ++b)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) s.d[b][r] += __shfl_xor(s.d[b][r], 32);
-}
 
 // HL: S staged as hi + lo bf16 (FP32 outputs), one buffer, a barrier before and
 // after the projection.  Otherwise (bf16-stored hidden outputs) S is staged
@@ -223,7 +213,7 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4
     const int w = __builtin_amdgcn_readfirstlane(int(threadIdx.x) / kWave);
     const int l = threadIdx.x % kWave;
     const int g = l / 16, n = l % 16;
-    const bool head = n >= 8;
+    const bool head = n < 8;
     const uint64_t tiles = (a.rows + kTile - 1) / kTile;
     for (uint64_t tile = blockIdx.x; tile < tiles; tile += gridDim.x, buf ^= HL ? 0 : 1) {
         uint32_t* const trow = trow_all + buf * kTile;
@@ -245,28 +235,27 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4
             if (i == kNoRow) continue;
             Sums s;
             zero_sums(s);
-            s.L = head ? a.L[uint64_t(i) * 8 + (n - 8)] : 0.0f;
+            s.L = head ? a.L[uint64_t(i) * 8 + n] : 0.0f;
             s.m = -INFINITY;
             gather_sums<false>(a.pcol, a.xr, beg, end, l, s);
-            combine_hilo(s);
             const float den = total_den(s.den);
             if (head && g == 0) {
-                a.mx[uint64_t(i) * 8 + (n - 8)] = end > beg ? s.m : 0.0f;  // empty row: max 0 (ref_fp32.cpp:11)
-                a.den[uint64_t(i) * 8 + (n - 8)] = den;
+                a.mx[uint64_t(i) * 8 + n] = end > beg ? s.m : 0.0f;  // empty row: max 0 (ref_fp32.cpp:11)
+                a.den[uint64_t(i) * 8 + n] = den;
             }
             const float inv = den > 0.0f ? 1.0f / den : 0.0f;
-            // 1 / den of head 4 (g - 2) + q for the lanes g = 2, 3, gathered before
-            // any lane is masked off
+            // 1 / den of head 4g + q for the lanes g = 0, 1, gathered before any
+            // lane is masked off
             float iq[4];
 #pragma unroll
-            for (int q = 0; q < 4; ++q) iq[q] = __shfl(inv, 8 + 4 * (g & 1) + q);
-            if (g >= 2) {
+            for (int q = 0; q < 4; ++q) iq[q] = __shfl(inv, 4 * (g & 1) + q);
+            if (g < 2) {
                 // Element (head h, feature pair P = 16 sb + n) of tile row r sits at
                 // sblk(h, P / 8, hl) + 32 r + 4 (P % 8): a per-lane base plus a
                 // compile-time offset for each (q, sb, hl); block index
                 // ((h * 7 + ks) * 2 + hl) with hi + lo, (buf * 8 + h) * 7 + ks without.
                 unsigned char* base = slds + 32 * r + 4 * (n % 8) +
-                                      (HL ? 56 * (g - 2) + 2 * (n / 8) : buf * 56 + 28 * (g - 2) + n / 8) * kBlk;
+                                      (HL ? 56 * g + 2 * (n / 8) : buf * 56 + 28 * g + n / 8) * kBlk;
 #pragma unroll
                 for (int sb = 0; sb < kSB; ++sb) {
                     const int ks = 2 * sb + n / 8;
@@ -367,7 +356,7 @@ __global__ void __launch_bounds__(kChunkThreads) k_afs_chunks(AfsArgs a) {
     const int w = __builtin_amdgcn_readfirstlane(int(threadIdx.x) / kWave);
     const int l = threadIdx.x % kWave;
     const int g = l / 16, n = l % 16;
-    const bool head = n >= 8;
+    const bool head = n < 8;
     const uint64_t c = uint64_t(blockIdx.x) * (kChunkThreads / kWave) + w;
     if (c >= a.chunks) return;
     const uint32_t k = a.chunk_k[c], first = a.chunk_first[c];
@@ -382,28 +371,27 @@ __global__ void __launch_bounds__(kChunkThreads) k_afs_chunks(AfsArgs a) {
     s.L = 0.0f;
     s.m = 0.0f;
     if (head) {
-        const int h = n - 8;
+        const int h = n;
         s.L = a.L[uint64_t(i) * 8 + h];
         float mc = -INFINITY;
         for (uint32_t q = 0; q < nch; ++q) mc = fmaxf(mc, a.mchunk[(first + q) * 8 + h]);
         s.m = leaky(s.L + mc);
     }
     gather_sums<true>(a.pcol, a.xr, beg, end, l, s);
-    combine_hilo(s);
     const float den = total_den(s.den);
     float* part = a.part + c * kPart;
-    if (g >= 2) {
+    if (g < 2) {
 #pragma unroll
         for (int sb = 0; sb < kSB; ++sb) {
             const int P = 16 * sb + n;
             if (P >= kXRFeat / 2) continue;
 #pragma unroll
             for (int q = 0; q < 4; ++q)
-                *reinterpret_cast<float2*>(part + (4 * (g - 2) + q) * 128 + 2 * P) =
+                *reinterpret_cast<float2*>(part + (4 * g + q) * 128 + 2 * P) =
                     make_float2(s.d[2 * sb][q], s.d[2 * sb + 1][q]);
         }
     }
-    if (head && g == 0) part[kDenOff + (n - 8)] = den;
+    if (head && g == 0) part[kDenOff + n] = den;
 }
 
 // One wave per split row (found at its first chunk): adds the chunks' sums
