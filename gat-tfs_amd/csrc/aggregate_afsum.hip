@@ -413,6 +413,7 @@ __global__ void __launch_bounds__(kChunkThreads) k_afs_merge(AfsArgs a) {
     float d = 0.0f;
     if (l < 8) {
         float mc = -INFINITY;
+#pragma unroll 4
         for (uint32_t q = 0; q < nch; ++q) {
             d += a.part[(c + q) * kPart + kDenOff + l];
             mc = fmaxf(mc, a.mchunk[(c + q) * 8 + l]);
@@ -425,29 +426,50 @@ __global__ void __launch_bounds__(kChunkThreads) k_afs_merge(AfsArgs a) {
 #pragma unroll
     for (int h = 0; h < 8; ++h) dall[h] = lane_f(d, h);
     if (l < kXRFeat / 2) {
+        // Chunk by chunk (the order of the sums), the 8 heads' loads of a chunk
+        // independent of each other.
+        float t[8][2];
+#pragma unroll
+        for (int h = 0; h < 8; ++h) t[h][0] = t[h][1] = 0.0f;
+#pragma unroll 2
+        for (uint32_t q = 0; q < nch; ++q) {
+            const float* pq = a.part + (c + q) * kPart + 2 * l;
+            float2 v[8];
+#pragma unroll
+            for (int h = 0; h < 8; ++h) v[h] = *reinterpret_cast<const float2*>(pq + h * 128);
+#pragma unroll
+            for (int h = 0; h < 8; ++h) {
+                t[h][0] += v[h].x;
+                t[h][1] += v[h].y;
+            }
+        }
+#pragma unroll
         for (int h = 0; h < 8; ++h) {
             const float inv = dall[h] > 0.0f ? 1.0f / dall[h] : 0.0f;
-            float t0 = 0.0f, t1 = 0.0f;
-            for (uint32_t q = 0; q < nch; ++q) {
-                const float2 v = *reinterpret_cast<const float2*>(a.part + (c + q) * kPart + h * 128 + 2 * l);
-                t0 += v.x;
-                t1 += v.y;
-            }
-            s[w][h * kXRFeat + 2 * l] = t0 * inv;
-            s[w][h * kXRFeat + 2 * l + 1] = t1 * inv;
+            s[w][h * kXRFeat + 2 * l] = t[h][0] * inv;
+            s[w][h * kXRFeat + 2 * l + 1] = t[h][1] * inv;
         }
     }
     wave_sync();
     const int h = l / 8, c0 = 4 * (l % 8);
     float o[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-    for (int f = 0; f < a.in; ++f) {
-        const float sv = s[w][h * kXRFeat + f];
-        const float4 wv = *reinterpret_cast<const float4*>(a.wq + uint64_t(f) * 256 + 32 * h + c0);
+    const float* wcol = a.wq + 32 * h + c0;
+    auto fma4 = [&](float sv, const float4& wv) {
         o[0] = __builtin_fmaf(sv, wv.x, o[0]);
         o[1] = __builtin_fmaf(sv, wv.y, o[1]);
         o[2] = __builtin_fmaf(sv, wv.z, o[2]);
         o[3] = __builtin_fmaf(sv, wv.w, o[3]);
+    };
+    // 16 rows of W requested at a time (L2-resident), then their FMAs in order.
+    int f = 0;
+    for (; f + 16 <= a.in; f += 16) {
+        float4 wv[16];
+#pragma unroll
+        for (int x = 0; x < 16; ++x) wv[x] = *reinterpret_cast<const float4*>(wcol + uint64_t(f + x) * 256);
+#pragma unroll
+        for (int x = 0; x < 16; ++x) fma4(s[w][h * kXRFeat + f + x], wv[x]);
     }
+    for (; f < a.in; ++f) fma4(s[w][h * kXRFeat + f], *reinterpret_cast<const float4*>(wcol + uint64_t(f) * 256));
     if (a.hidden)
 #pragma unroll
         for (int x = 0; x < 4; ++x) o[x] = elu_bf16(o[x]);
