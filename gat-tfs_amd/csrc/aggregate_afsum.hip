@@ -324,7 +324,7 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4
 #pragma unroll
                     for (int x = 0; x < 16; ++x) {
                         const float y = dh[x] + dl[x];
-                        o[x] = a.hidden ? elu_bf16(y) : y;
+                        o[x] = HL ? y : elu_bf16(y);  // FP32 outputs: the last layer; bf16: hidden
                     }
                     const uint64_t off = uint64_t(i) * 256 + 32 * h + 16 * half;
                     if (a.outbf) {
@@ -493,9 +493,11 @@ hipError_t launch_tiles_hl(const AfsArgs& a, hipStream_t s, int cus) {
     return hipGetLastError();
 }
 
-// FP32 outputs keep S as hi + lo; bf16-stored outputs stage one bf16.
+// FP32 outputs (the last layer, no ELU) keep S as hi + lo; bf16-stored hidden
+// outputs stage one bf16.
 template <int KS>
 hipError_t launch_tiles(const AfsArgs& a, hipStream_t s, int cus) {
+    if (a.hidden != (a.out32 == nullptr) || (a.out32 == nullptr) == (a.outbf == nullptr)) return hipErrorInvalidValue;
     return a.out32 ? launch_tiles_hl<KS, true>(a, s, cus) : launch_tiles_hl<KS, false>(a, s, cus);
 }
 

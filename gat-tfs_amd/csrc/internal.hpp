@@ -50,10 +50,12 @@ __device__ inline float exp_w(float x) { return __builtin_amdgcn_exp2f(x * 1.442
 // below 1e-6 of the result), and from the Taylor polynomial of e^x - 1 to
 // x^6 / 720 above (remainder below |x|^7 / 5040 < 2e-8 |x|).  The relative
 // error is under 1e-6, against 2^-9 for the bf16 rounding that follows.
+// Both pieces are evaluated and selected, with no branch per element.
 __device__ inline float elu_bf16(float x) {
-    if (x >= 0.0f) return x;
     const float t = x * (1.0f + x * (0.5f + x * (1.0f / 6 + x * (1.0f / 24 + x * (1.0f / 120 + x * (1.0f / 720))))));
-    return x < -0.25f ? exp_w(x) - 1.0f : t;
+    const float e = exp_w(fminf(x, 0.0f)) - 1.0f;
+    const float neg = x < -0.25f ? e : t;
+    return x >= 0.0f ? x : neg;
 }
 
 // A buffer that no thread of the launch writes, seen through the constant
