@@ -33,13 +33,13 @@
 // register r of block (sb, par) holds U of head 4g + r, feature
 // 2(16 sb + n) + par.
 //
-// Blocks of 8 waves take tiles of 16 consecutive degree-sorted rows, two per
-// wave.  A row's normalised sums S_h = U_h / den_h go to LDS as a hi + lo pair
-// of bf16 (S = hi + lo to about 2^-17 relative), in the B-operand layout of
-// v_mfma_f32_32x32x16_bf16.  After a barrier, wave h multiplies the tile's S_h
-// by W_h (A fragments packed as for the projection, read from L2; hi and
-// lo in two MFMA chains) and stores the 16 output rows; a second barrier
-// frees the tile buffer.  Split rows: one wave per chunk sums its edges from
+// Blocks of 8 waves take tiles of consecutive degree-sorted rows (16 or 32,
+// see k_afs_tiles).  A row's normalised sums S_h = U_h / den_h go to LDS in
+// the B-operand layout of v_mfma_f32_32x32x16_bf16, as a hi + lo pair of bf16
+// (S = hi + lo to about 2^-17 relative) for FP32 outputs and as one bf16 for
+// bf16-stored hidden outputs.  After a barrier, wave h multiplies the tile's
+// S_h by W_h (A fragments packed as for the projection, read from L2; two
+// MFMA chains) and stores the tile's output rows.  Split rows: one wave per chunk sums its edges from
 // the exact row max (per-chunk maxima of k_split_prescan) into scratch, and
 // one wave per row adds the chunks in chunk order and projects the row on
 // the VALU with the FP32 W.
@@ -54,14 +54,15 @@ typedef float f32x16 __attribute__((__vector_size__(16 * sizeof(float))));
 
 constexpr int kThreads = 512;
 constexpr int kWaves = kThreads / kWave;   // 8 = heads
-constexpr int kTile = 2 * kWaves;          // rows per block tile
+constexpr int kTile = 2 * kWaves;          // rows per block tile (hi + lo S)
+constexpr int kTileBf16 = 32;              // rows per block tile with one bf16 S
 constexpr int kMaxKS = 7;                  // k steps of 16 features: D_in <= 112
 constexpr int kRowWords = kXRStride / 2;   // 64 words of 4 bytes per XR row
 constexpr int kB = 32;                     // edges per batch (MFMA contraction)
 constexpr int kSB = 4;                     // super-blocks of 16 words per row
 constexpr int kBlk = kTile * 32 + 16;      // bytes per (head, k step, hi|lo) block of S, padded
 constexpr int kSBytes = 8 * kMaxKS * 2 * kBlk;
-constexpr int kLdsBytes = kSBytes + 2 * kTile * 4;  // S, then the tile's node ids (two buffers)
+constexpr int kLdsBytes = kSBytes + 2 * 2 * kTile * 4;  // S, then the tile's node ids (up to 2 x 32)
 constexpr uint32_t kNoRow = 0xffffffffu;
 constexpr int kPart = 8 * 128 + 8;         // floats per chunk partial (U_h rows of 128, then den)
 constexpr int kDenOff = 8 * 128;
@@ -69,8 +70,6 @@ constexpr int kChunkThreads = 256;
 
 static_assert(2 * kB <= int(kPcolPad), "the id prefetch may read 2 kB - 1 entries past the row");
 static_assert(kRowWords == 16 * kSB && kXRFeat == 112, "XR row: 4 super-blocks, R in words 56..63");
-
-__device__ inline int sblk(int h, int ks, int hl) { return ((h * kMaxKS + ks) * 2 + hl) * kBlk; }
 
 __device__ inline float lane_f(float x, int lane) {
     return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), lane));
@@ -198,14 +197,21 @@ __device__ inline float total_den(float den) {
 }
 
 
-// HL: S staged as hi + lo bf16 (FP32 outputs), one buffer, a barrier before and
-// after the projection.  Otherwise (bf16-stored hidden outputs) S is staged
-// as one bf16 (its rounding is that of a bf16 projection input, 2^-9
-// relative) in two alternating buffers, with one barrier per tile: a wave
-// writes buffer t % 2 only after the barrier of tile t - 1, which every wave
-// reaches after projecting tile t - 2 from the same buffer.
-template <int KS, bool HL>
+// HL: S staged as hi + lo bf16 (FP32 outputs) for 16-row tiles.  Otherwise
+// (bf16-stored hidden outputs) S is staged as one bf16 (its rounding is that
+// of a bf16 projection input, 2^-9 relative): 32-row tiles (4 rows per wave,
+// the MFMA's 32 columns all used), or 16-row tiles in two alternating buffers
+// with one barrier per tile (a wave writes buffer t % 2 only after the
+// barrier of tile t - 1, which every wave reaches after projecting tile t - 2
+// from the same buffer).  Single-buffered tiles take a barrier before and
+// after the projection.
+template <int KS, bool HL, int TR>
 __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) k_afs_tiles(AfsArgs a) {
+    static_assert(TR == 16 || (TR == 32 && !HL), "16-row tiles, or 32-row tiles of one bf16");
+    constexpr int RPW = TR / kWaves;          // rows per wave and tile
+    constexpr bool DB = !HL && TR == 16;      // two alternating S buffers
+    constexpr int BLK = TR * 32 + 16;         // bytes per (head, k step[, hi|lo]) block of S
+    static_assert(8 * kMaxKS * (HL ? 2 : DB ? 2 : 1) * BLK <= kSBytes, "S fits");
     extern __shared__ __attribute__((aligned(16))) unsigned char slds[];
     // Destination node of each tile row (kNoRow: none), for the projection stores.
     uint32_t* const trow_all = reinterpret_cast<uint32_t*>(slds + kSBytes);
@@ -214,14 +220,14 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4
     const int l = threadIdx.x % kWave;
     const int g = l / 16, n = l % 16;
     const bool head = n < 8;
-    const uint64_t tiles = (a.rows + kTile - 1) / kTile;
-    for (uint64_t tile = blockIdx.x; tile < tiles; tile += gridDim.x, buf ^= HL ? 0 : 1) {
-        uint32_t* const trow = trow_all + buf * kTile;
-        // ---- two rows per wave: sums, softmax state, S into LDS
+    const uint64_t tiles = (a.rows + TR - 1) / TR;
+    for (uint64_t tile = blockIdx.x; tile < tiles; tile += gridDim.x, buf ^= DB ? 1 : 0) {
+        uint32_t* const trow = trow_all + buf * TR;
+        // ---- RPW rows per wave: sums, softmax state, S into LDS
 #pragma unroll 1
-        for (int rr = 0; rr < 2; ++rr) {
+        for (int rr = 0; rr < RPW; ++rr) {
             const int r = w + kWaves * rr;
-            const uint64_t tpos = tile * kTile + r;
+            const uint64_t tpos = tile * TR + r;
             uint32_t i = kNoRow;
             uint64_t beg = 0, end = 0;
             if (tpos < a.rows) {
@@ -251,11 +257,11 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4
             for (int q = 0; q < 4; ++q) iq[q] = __shfl(inv, 4 * (g & 1) + q);
             if (g < 2) {
                 // Element (head h, feature pair P = 16 sb + n) of tile row r sits at
-                // sblk(h, P / 8, hl) + 32 r + 4 (P % 8): a per-lane base plus a
+                // block (h, P / 8[, hl]) + 32 r + 4 (P % 8): a per-lane base plus a
                 // compile-time offset for each (q, sb, hl); block index
                 // ((h * 7 + ks) * 2 + hl) with hi + lo, (buf * 8 + h) * 7 + ks without.
                 unsigned char* base = slds + 32 * r + 4 * (n % 8) +
-                                      (HL ? 56 * g + 2 * (n / 8) : buf * 56 + 28 * g + n / 8) * kBlk;
+                                      (HL ? 56 * g + 2 * (n / 8) : buf * 56 + 28 * g + n / 8) * BLK;
 #pragma unroll
                 for (int sb = 0; sb < kSB; ++sb) {
                     const int ks = 2 * sb + n / 8;
@@ -267,11 +273,11 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4
                         if constexpr (HL) {
                             const uint32_t lw = bf16x2(s0 - __builtin_bit_cast(float, hw << 16),
                                                        s1 - __builtin_bit_cast(float, hw & 0xffff0000u));
-                            unsigned char* e = base + (14 * q + 4 * sb) * kBlk;
+                            unsigned char* e = base + (14 * q + 4 * sb) * BLK;
                             *reinterpret_cast<uint32_t*>(e) = hw;
-                            *reinterpret_cast<uint32_t*>(e + kBlk) = lw;
+                            *reinterpret_cast<uint32_t*>(e + BLK) = lw;
                         } else {
-                            *reinterpret_cast<uint32_t*>(base + (7 * q + 2 * sb) * kBlk) = hw;
+                            *reinterpret_cast<uint32_t*>(base + (7 * q + 2 * sb) * BLK) = hw;
                         }
                     }
                 }
@@ -299,25 +305,27 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4
             f32x16 dh, dl;
 #pragma unroll
             for (int x = 0; x < 16; ++x) dh[x] = dl[x] = 0.0f;
-            const int boff = (l % 16) * 32 + 16 * (l / 32);
+            const int boff = (l % TR) * 32 + 16 * (l / 32);
 #pragma unroll
             for (int ks = 0; ks < KS; ++ks) {
                 if constexpr (HL) {
-                    const bf16x8 bh = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(slds + sblk(h, ks, 0) + boff));
-                    const bf16x8 bl = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(slds + sblk(h, ks, 1) + boff));
+                    const bf16x8 bh = __builtin_bit_cast(
+                        bf16x8, *reinterpret_cast<const uint4*>(slds + ((h * kMaxKS + ks) * 2) * BLK + boff));
+                    const bf16x8 bl = __builtin_bit_cast(
+                        bf16x8, *reinterpret_cast<const uint4*>(slds + ((h * kMaxKS + ks) * 2 + 1) * BLK + boff));
                     dh = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wf[ks], bh, dh, 0, 0, 0);
                     dl = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wf[ks], bl, dl, 0, 0, 0);
                 } else {
                     // even / odd k steps in two chains
                     const bf16x8 b = __builtin_bit_cast(
-                        bf16x8, *reinterpret_cast<const uint4*>(slds + ((buf * 8 + h) * kMaxKS + ks) * kBlk + boff));
+                        bf16x8, *reinterpret_cast<const uint4*>(slds + ((buf * 8 + h) * kMaxKS + ks) * BLK + boff));
                     if (ks % 2 == 0) dh = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wf[ks], b, dh, 0, 0, 0);
                     else dl = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wf[ks], b, dl, 0, 0, 0);
                 }
             }
             const int r = l % 32, half = l / 32;
-            const uint32_t i = trow[r % kTile];
-            if (r < kTile) {
+            const uint32_t i = trow[r % TR];
+            if (r < TR) {
                 if (i != kNoRow) {
                     // Lane (half, r) holds features 32 h + 16 half + {0..15} (permuted packing).
                     float o[16];
@@ -346,7 +354,7 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4
                 }
             }
         }
-        if constexpr (HL) __syncthreads();
+        if constexpr (!DB) __syncthreads();
     }
 }
 
@@ -480,16 +488,16 @@ __global__ void __launch_bounds__(kChunkThreads) k_afs_merge(AfsArgs a) {
     if (a.out32) *reinterpret_cast<float4*>(a.out32 + off) = make_float4(o[0], o[1], o[2], o[3]);
 }
 
-template <int KS, bool HL>
+template <int KS, bool HL, int TR>
 hipError_t launch_tiles_hl(const AfsArgs& a, hipStream_t s, int cus) {
-    const uint64_t tiles = (a.rows + kTile - 1) / kTile;
+    const uint64_t tiles = (a.rows + TR - 1) / TR;
     if (!tiles) return hipSuccess;
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_afs_tiles<KS, HL>),
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_afs_tiles<KS, HL, TR>),
                                        hipFuncAttributeMaxDynamicSharedMemorySize, kLdsBytes);
     if (e != hipSuccess) return e;
     uint64_t blocks = uint64_t(cus) * 2;
     if (blocks > tiles) blocks = tiles;
-    k_afs_tiles<KS, HL><<<dim3(uint32_t(blocks)), kThreads, kLdsBytes, s>>>(a);
+    k_afs_tiles<KS, HL, TR><<<dim3(uint32_t(blocks)), kThreads, kLdsBytes, s>>>(a);
     return hipGetLastError();
 }
 
@@ -498,7 +506,7 @@ hipError_t launch_tiles_hl(const AfsArgs& a, hipStream_t s, int cus) {
 template <int KS>
 hipError_t launch_tiles(const AfsArgs& a, hipStream_t s, int cus) {
     if (a.hidden != (a.out32 == nullptr) || (a.out32 == nullptr) == (a.outbf == nullptr)) return hipErrorInvalidValue;
-    return a.out32 ? launch_tiles_hl<KS, true>(a, s, cus) : launch_tiles_hl<KS, false>(a, s, cus);
+    return a.out32 ? launch_tiles_hl<KS, true, 16>(a, s, cus) : launch_tiles_hl<KS, false, kTileBf16>(a, s, cus);
 }
 
 }  // namespace
