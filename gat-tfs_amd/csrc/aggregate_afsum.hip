@@ -68,7 +68,7 @@ constexpr int kPart = 8 * 128 + 8;         // floats per chunk partial (U_h rows
 constexpr int kDenOff = 8 * 128;
 constexpr int kChunkThreads = 256;
 
-static_assert(2 * kB <= int(kPcolPad), "the id prefetch may read 2 kB - 1 entries past the row");
+static_assert(kB <= int(kPcolPad), "an id request may read kB - 1 entries past the row");
 static_assert(kRowWords == 16 * kSB && kXRFeat == 112, "XR row: 4 super-blocks, R in words 56..63");
 
 __device__ inline float lane_f(float x, int lane) {
@@ -83,34 +83,25 @@ struct Sums {
     float m, den, L;
 };
 
-// Edges [beg, end).  EXACT: s.m holds the exact row max already (a chunk) and
-// never moves.
+// Edges [beg, end).  ids: lane id0 + t holds pcol[beg + t], t < 32 (requested
+// by the caller ahead of time); each batch requests the next batch's ids the
+// same way (pcol is padded past e).  EXACT: s.m holds the exact row max
+// already (a chunk) and never moves.
 template <bool EXACT>
 __device__ inline void gather_sums(const uint32_t* __restrict__ pcol, const uint32_t* __restrict__ xr,
-                                   uint64_t beg, uint64_t end, int l, Sums& s) {
+                                   uint64_t beg, uint64_t end, int l, Sums& s, uint32_t ids, int id0) {
     if (beg >= end) return;
     const int g = l / 16, n = l % 16;
     const bool head = n < 8;
-    const auto* pc = read_only(pcol);
-    uint32_t js[kB];
-#pragma unroll
-    for (int t = 0; t < kB; ++t) js[t] = pc[beg + t];
     for (uint64_t base = beg; base < end; base += kB) {
-        uint32_t jn[kB];
-#pragma unroll
-        for (int t = 0; t < kB; ++t) jn[t] = pc[base + kB + t];  // padded past e
+        const uint32_t nids = pcol[(base + kB < end ? base + kB : end) + uint32_t(l % 32)];
         const uint64_t rem = end - base;
         const int cnt = rem < uint64_t(kB) ? int(rem) : kB;
         // This lane's 8 edges; edges past the end re-read the batch's first row
         // (weight 0).
         uint32_t jl[8];
 #pragma unroll
-        for (int t = 0; t < 8; ++t) {
-            uint32_t j = js[t];
-#pragma unroll
-            for (int q = 1; q < 4; ++q) j = g == q ? js[8 * q + t] : j;
-            jl[t] = 8 * g + t < cnt ? j : js[0];
-        }
+        for (int t = 0; t < 8; ++t) jl[t] = __shfl(ids, id0 + (8 * g + t < cnt ? 8 * g + t : 0));
         // 32-bit byte offsets (n * 256 < 2^32 is checked at launch).
         const unsigned char* xb = reinterpret_cast<const unsigned char*>(xr);
         uint32_t raw[kSB][8];
@@ -177,8 +168,8 @@ __device__ inline void gather_sums(const uint32_t* __restrict__ pcol, const uint
             s.d[2 * sb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(Al, Be, s.d[2 * sb], 0, 0, 0);
             s.d[2 * sb + 1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(Al, Bo, s.d[2 * sb + 1], 0, 0, 0);
         }
-#pragma unroll
-        for (int t = 0; t < kB; ++t) js[t] = jn[t];
+        ids = nids;
+        id0 = 0;
     }
 }
 
@@ -223,27 +214,52 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4
     const uint64_t tiles = (a.rows + TR - 1) / TR;
     for (uint64_t tile = blockIdx.x; tile < tiles; tile += gridDim.x, buf ^= DB ? 1 : 0) {
         uint32_t* const trow = trow_all + buf * TR;
-        // ---- RPW rows per wave: sums, softmax state, S into LDS
+        // ---- RPW rows per wave (tile rows w + 8 q).  Their bounds (lane q), L
+        // (lane 8 q + h) and first ids (lane 32 (q % 2) + t of ids[q / 2]) are
+        // requested together at the start of the tile, so a row waits only on
+        // its own source rows.
+        uint32_t mi = kNoRow;
+        uint64_t mb = 0, me = 0;
+        if (l < RPW) {
+            const uint64_t tpos = tile * TR + w + kWaves * l;
+            if (tpos < a.rows) {
+                const uint64_t k = a.rows - 1 - tpos;
+                mi = a.perm[k];
+                mb = a.prow[k];
+                me = a.prow[k + 1];
+                if (mi >= a.n || mb > me || me > a.e) mi = kNoRow;
+            }
+        }
+        uint32_t idr[(RPW + 1) / 2];
+#pragma unroll
+        for (int c = 0; c < (RPW + 1) / 2; ++c) {
+            const int q = 2 * c + l / 32;
+            const uint32_t qi = __shfl(mi, q);
+            const uint64_t qb = (uint64_t(__shfl(uint32_t(mb >> 32), q)) << 32) | __shfl(uint32_t(mb), q);
+            idr[c] = a.pcol[(q < RPW && qi != kNoRow ? qb : 0) + uint32_t(l % 32)];
+        }
+        float Lall = 0.0f;
+        {
+            const uint32_t qi = __shfl(mi, l / 8);
+            if (l / 8 < RPW && qi != kNoRow) Lall = a.L[uint64_t(qi) * 8 + l % 8];
+        }
 #pragma unroll 1
         for (int rr = 0; rr < RPW; ++rr) {
             const int r = w + kWaves * rr;
-            const uint64_t tpos = tile * TR + r;
-            uint32_t i = kNoRow;
-            uint64_t beg = 0, end = 0;
-            if (tpos < a.rows) {
-                const uint64_t k = a.rows - 1 - tpos;
-                i = a.perm[k];
-                beg = a.prow[k];
-                end = a.prow[k + 1];
-                if (i >= a.n || beg > end || end > a.e) i = kNoRow;
-            }
+            const uint32_t i = uint32_t(__builtin_amdgcn_readlane(int(mi), rr));
+            const uint64_t beg = (uint64_t(uint32_t(__builtin_amdgcn_readlane(int(mb >> 32), rr))) << 32) |
+                                 uint32_t(__builtin_amdgcn_readlane(int(uint32_t(mb)), rr));
+            const uint64_t end = (uint64_t(uint32_t(__builtin_amdgcn_readlane(int(me >> 32), rr))) << 32) |
+                                 uint32_t(__builtin_amdgcn_readlane(int(uint32_t(me)), rr));
+            const uint32_t ids = rr / 2 == 0 ? idr[0] : idr[(RPW + 1) / 2 - 1];
+            const float Lr = __shfl(Lall, 8 * rr + n % 8);
             if (l == 0) trow[r] = i;
             if (i == kNoRow) continue;
             Sums s;
             zero_sums(s);
-            s.L = head ? a.L[uint64_t(i) * 8 + n] : 0.0f;
+            s.L = head ? Lr : 0.0f;
             s.m = -INFINITY;
-            gather_sums<false>(a.pcol, a.xr, beg, end, l, s);
+            gather_sums<false>(a.pcol, a.xr, beg, end, l, s, ids, 32 * (rr % 2));
             const float den = total_den(s.den);
             if (head && g == 0) {
                 a.mx[uint64_t(i) * 8 + n] = end > beg ? s.m : 0.0f;  // empty row: max 0 (ref_fp32.cpp:11)
@@ -385,7 +401,7 @@ __global__ void __launch_bounds__(kChunkThreads) k_afs_chunks(AfsArgs a) {
         for (uint32_t q = 0; q < nch; ++q) mc = fmaxf(mc, a.mchunk[(first + q) * 8 + h]);
         s.m = leaky(s.L + mc);
     }
-    gather_sums<true>(a.pcol, a.xr, beg, end, l, s);
+    gather_sums<true>(a.pcol, a.xr, beg, end, l, s, a.pcol[beg + uint32_t(l % 32)], 0);
     const float den = total_den(s.den);
     float* part = a.part + c * kPart;
     if (g < 2) {
