@@ -212,24 +212,29 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4
     const int g = l / 16, n = l % 16;
     const bool head = n < 8;
     const uint64_t tiles = (a.rows + TR - 1) / TR;
+    // Bounds of the wave's rows of tile t (lane q < RPW: tile row w + 8 q),
+    // requested one tile ahead (during the previous tile's projection).
+    auto fetch_bounds = [&](uint64_t t, uint32_t& fi, uint64_t& fb, uint64_t& fe) {
+        fi = kNoRow;
+        fb = fe = 0;
+        const uint64_t tpos = t * TR + w + kWaves * l;
+        if (l < RPW && t < tiles && tpos < a.rows) {
+            const uint64_t k = a.rows - 1 - tpos;
+            fi = a.perm[k];
+            fb = a.prow[k];
+            fe = a.prow[k + 1];
+        }
+    };
+    uint32_t mi;
+    uint64_t mb, me;
+    fetch_bounds(blockIdx.x, mi, mb, me);
     for (uint64_t tile = blockIdx.x; tile < tiles; tile += gridDim.x, buf ^= DB ? 1 : 0) {
         uint32_t* const trow = trow_all + buf * TR;
         // ---- RPW rows per wave (tile rows w + 8 q).  Their bounds (lane q), L
         // (lane 8 q + h) and first ids (lane 32 (q % 2) + t of ids[q / 2]) are
         // requested together at the start of the tile, so a row waits only on
         // its own source rows.
-        uint32_t mi = kNoRow;
-        uint64_t mb = 0, me = 0;
-        if (l < RPW) {
-            const uint64_t tpos = tile * TR + w + kWaves * l;
-            if (tpos < a.rows) {
-                const uint64_t k = a.rows - 1 - tpos;
-                mi = a.perm[k];
-                mb = a.prow[k];
-                me = a.prow[k + 1];
-                if (mi >= a.n || mb > me || me > a.e) mi = kNoRow;
-            }
-        }
+        if (mi != kNoRow && (mi >= a.n || mb > me || me > a.e)) mi = kNoRow;
         uint32_t idr[(RPW + 1) / 2];
 #pragma unroll
         for (int c = 0; c < (RPW + 1) / 2; ++c) {
@@ -303,6 +308,9 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4
         // resident), requested before the barrier.  A wave-uniform base plus a
         // 32-bit lane offset, made opaque so that the addresses are formed here
         // instead of being held across the gather.
+        uint32_t nmi;
+        uint64_t nmb, nme;
+        fetch_bounds(tile + gridDim.x, nmi, nmb, nme);
         bf16x8 wf[KS];
         {
             uint32_t lo = uint32_t(l) * uint32_t(sizeof(uint4));
@@ -371,6 +379,9 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4
             }
         }
         if constexpr (!DB) __syncthreads();
+        mi = nmi;
+        mb = nmb;
+        me = nme;
     }
 }
 
