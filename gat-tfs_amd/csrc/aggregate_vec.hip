@@ -207,22 +207,10 @@ __device__ inline void batch(uint64_t base, uint64_t end, const uint32_t (&js)[C
     }
 }
 
-// Edges [beg, end) of a row or chunk, then the edge slots merged: afterwards
-// every lane holds its heads' totals and m is the max over all the edges.
-template <class C, class ZT, bool RZ>
-__device__ inline void aggregate(uint64_t beg, uint64_t end, const uint32_t* __restrict__ pcol,
-                                 const float* __restrict__ R, const ZT* __restrict__ Z, int slot, int sub,
-                                 Lane<C>& st) {
-    uint32_t js[C::BATCH];
-    load_ids<C>(pcol, beg, js);
-    for (uint64_t base = beg; base < end; base += C::BATCH) {
-        // The next batch's ids are requested before this batch's rows arrive.
-        uint32_t jn[C::BATCH];
-        load_ids<C>(pcol, base + C::BATCH, jn);
-        batch<C, ZT, RZ>(base, end, js, R, Z, slot, sub, st);
-#pragma unroll
-        for (int t = 0; t < C::BATCH; ++t) js[t] = jn[t];
-    }
+// The edge slots' states merged: afterwards every lane holds its heads'
+// totals and m is the max over all the edges.
+template <class C>
+__device__ inline void merge_slots(Lane<C>& st) {
     if constexpr (C::EPI > 1) {
         for (int off = C::LPR; off < kWave; off <<= 1) {
 #pragma unroll
@@ -241,6 +229,24 @@ __device__ inline void aggregate(uint64_t beg, uint64_t end, const uint32_t* __r
             }
         }
     }
+}
+
+// Edges [beg, end) of a row or chunk, then the edge slots merged.
+template <class C, class ZT, bool RZ>
+__device__ inline void aggregate(uint64_t beg, uint64_t end, const uint32_t* __restrict__ pcol,
+                                 const float* __restrict__ R, const ZT* __restrict__ Z, int slot, int sub,
+                                 Lane<C>& st) {
+    uint32_t js[C::BATCH];
+    load_ids<C>(pcol, beg, js);
+    for (uint64_t base = beg; base < end; base += C::BATCH) {
+        // The next batch's ids are requested before this batch's rows arrive.
+        uint32_t jn[C::BATCH];
+        load_ids<C>(pcol, base + C::BATCH, jn);
+        batch<C, ZT, RZ>(base, end, js, R, Z, slot, sub, st);
+#pragma unroll
+        for (int t = 0; t < C::BATCH; ++t) js[t] = jn[t];
+    }
+    merge_slots<C>(st);
 }
 
 // Normalise, ELU and store one output row from the slot-0 lanes; the first
@@ -306,16 +312,9 @@ k_split_prescan(const uint64_t* __restrict__ prow, const uint32_t* __restrict__ 
     if (lane < K) sp.mchunk[c * 8 + lane] = m;
 }
 
+// Lane state at the start of a row or chunk: zero sums, the lane's head and aR.
 template <class C, class ZT, bool RZ>
-__global__ void __launch_bounds__(kThreads) k_agg_vec(VArgs<ZT> a) {
-    // The wave index is made wave-uniform so that row bounds and source ids
-    // come in through scalar loads.
-    const int w = __builtin_amdgcn_readfirstlane(int(threadIdx.x) / kWave);
-    const int lane = threadIdx.x % kWave;
-    const int slot = C::EPI > 1 ? lane / C::LPR : 0;
-    const int sub = C::EPI > 1 ? lane % C::LPR : lane;
-    const uint64_t item = uint64_t(blockIdx.x) * kWavesPerBlock + w;
-    Lane<C> st;
+__device__ inline void init_lane(const VArgs<ZT>& a, int sub, Lane<C>& st) {
 #pragma unroll
     for (int x = 0; x < C::ACC; ++x) st.acc[x] = 0.0f;
 #pragma unroll
@@ -325,69 +324,88 @@ __global__ void __launch_bounds__(kThreads) k_agg_vec(VArgs<ZT> a) {
     }
 #pragma unroll
     for (int x = 0; x < C::VEC; ++x) st.ar[x] = RZ ? a.ar[sub * C::VEC + x] : 0.0f;
-    if (item < a.sp.chunks) {
-        // ---------------- chunk of a split row
-        const uint64_t c = item;
-        const uint32_t k = a.sp.chunk_k[c], first = a.sp.chunk_first[c];
-        const uint64_t rbeg = a.prow[k], rend = a.prow[k + 1];
-        const uint32_t i = a.perm[k];
-        if (i >= a.n || rbeg > rend || rend > a.e) return;
-        const uint32_t nch = uint32_t((rend - rbeg + a.sp.chunk_edges - 1) / a.sp.chunk_edges);
-        const uint64_t beg = rbeg + uint64_t(c - first) * a.sp.chunk_edges;
-        const uint64_t end = beg + a.sp.chunk_edges < rend ? beg + a.sp.chunk_edges : rend;
+}
+
+// Chunk c of a split row: its edges from the exact row max, the partial sums
+// to scratch; the last chunk of the row to arrive adds the partials in chunk
+// order and finishes the row.
+template <class C, class ZT, bool RZ>
+__device__ inline void run_chunk(const VArgs<ZT>& a, uint64_t c, int lane, int slot, int sub) {
+    Lane<C> st;
+    init_lane<C, ZT, RZ>(a, sub, st);
+    const uint32_t k = a.sp.chunk_k[c], first = a.sp.chunk_first[c];
+    const uint64_t rbeg = a.prow[k], rend = a.prow[k + 1];
+    const uint32_t i = a.perm[k];
+    if (i >= a.n || rbeg > rend || rend > a.e) return;
+    const uint32_t nch = uint32_t((rend - rbeg + a.sp.chunk_edges - 1) / a.sp.chunk_edges);
+    const uint64_t beg = rbeg + uint64_t(c - first) * a.sp.chunk_edges;
+    const uint64_t end = beg + a.sp.chunk_edges < rend ? beg + a.sp.chunk_edges : rend;
+#pragma unroll
+    for (int v = 0; v < C::VPL; ++v) {
+        float m = -INFINITY;
+        for (uint32_t q = 0; q < nch; ++q) m = fmaxf(m, a.sp.mchunk[(first + q) * 8 + st.h[v]]);
+        st.L[v] = a.L[uint64_t(i) * C::K + st.h[v]];
+        st.m[v] = leaky(st.L[v] + m);  // exact row max: no rescale happens in this chunk
+    }
+    aggregate<C, ZT, RZ>(beg, end, a.pcol, a.R, a.Z, slot, sub, st);
+    float* part = a.sp.part + c * (C::W + 8);
+    if (slot == 0) {
 #pragma unroll
         for (int v = 0; v < C::VPL; ++v) {
-            float m = -INFINITY;
-            for (uint32_t q = 0; q < nch; ++q) m = fmaxf(m, a.sp.mchunk[(first + q) * 8 + st.h[v]]);
-            st.L[v] = a.L[uint64_t(i) * C::K + st.h[v]];
-            st.m[v] = leaky(st.L[v] + m);  // exact row max: no rescale happens in this chunk
+            const int f0 = (sub + kWave * v) * C::VEC;
+#pragma unroll
+            for (int x = 0; x < C::VEC; x += 4)
+                *reinterpret_cast<float4*>(part + f0 + x) =
+                    make_float4(st.acc[v * C::VEC + x], st.acc[v * C::VEC + x + 1], st.acc[v * C::VEC + x + 2],
+                                st.acc[v * C::VEC + x + 3]);
+            if (f0 % C::DIM == 0) part[C::W + st.h[v]] = st.den[v];
         }
-        aggregate<C, ZT, RZ>(beg, end, a.pcol, a.R, a.Z, slot, sub, st);
-        float* part = a.sp.part + c * (C::W + 8);
-        if (slot == 0) {
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+    uint32_t old = 0;
+    if (lane == 0)
+        old = __hip_atomic_fetch_add(a.sp.counter + first, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    old = __shfl(old, 0);
+    if (old + 1 != nch) return;  // not the last chunk of this row
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    // Last arrival: add the partials of every chunk in chunk order.
+    float tot[C::ACC];
+    float dtot[C::VPL];
 #pragma unroll
-            for (int v = 0; v < C::VPL; ++v) {
-                const int f0 = (sub + kWave * v) * C::VEC;
+    for (int x = 0; x < C::ACC; ++x) tot[x] = 0.0f;
 #pragma unroll
-                for (int x = 0; x < C::VEC; x += 4)
-                    *reinterpret_cast<float4*>(part + f0 + x) =
-                        make_float4(st.acc[v * C::VEC + x], st.acc[v * C::VEC + x + 1], st.acc[v * C::VEC + x + 2],
-                                    st.acc[v * C::VEC + x + 3]);
-                if (f0 % C::DIM == 0) part[C::W + st.h[v]] = st.den[v];
+    for (int v = 0; v < C::VPL; ++v) dtot[v] = 0.0f;
+    for (uint32_t q = 0; q < nch; ++q) {
+        const float* pq = a.sp.part + uint64_t(first + q) * (C::W + 8);
+#pragma unroll
+        for (int v = 0; v < C::VPL; ++v) {
+            const int f0 = (sub + kWave * v) * C::VEC;
+#pragma unroll
+            for (int x = 0; x < C::VEC; x += 4) {
+                const float4 t = *reinterpret_cast<const float4*>(pq + f0 + x);
+                tot[v * C::VEC + x] += t.x;
+                tot[v * C::VEC + x + 1] += t.y;
+                tot[v * C::VEC + x + 2] += t.z;
+                tot[v * C::VEC + x + 3] += t.w;
             }
+            dtot[v] += pq[C::W + st.h[v]];
         }
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
-        uint32_t old = 0;
-        if (lane == 0)
-            old = __hip_atomic_fetch_add(a.sp.counter + first, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        old = __shfl(old, 0);
-        if (old + 1 != nch) return;  // not the last chunk of this row
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-        // Last arrival: add the partials of every chunk in chunk order.
-        float tot[C::ACC];
-        float dtot[C::VPL];
-#pragma unroll
-        for (int x = 0; x < C::ACC; ++x) tot[x] = 0.0f;
-#pragma unroll
-        for (int v = 0; v < C::VPL; ++v) dtot[v] = 0.0f;
-        for (uint32_t q = 0; q < nch; ++q) {
-            const float* pq = a.sp.part + uint64_t(first + q) * (C::W + 8);
-#pragma unroll
-            for (int v = 0; v < C::VPL; ++v) {
-                const int f0 = (sub + kWave * v) * C::VEC;
-#pragma unroll
-                for (int x = 0; x < C::VEC; x += 4) {
-                    const float4 t = *reinterpret_cast<const float4*>(pq + f0 + x);
-                    tot[v * C::VEC + x] += t.x;
-                    tot[v * C::VEC + x + 1] += t.y;
-                    tot[v * C::VEC + x + 2] += t.z;
-                    tot[v * C::VEC + x + 3] += t.w;
-                }
-                dtot[v] += pq[C::W + st.h[v]];
-            }
-        }
-        if (lane == 0) a.sp.counter[first] = 0;  // ready for the next launch
-        finish_row<C>(i, tot, dtot, st.m, st.h, slot, sub, a.hidden, a.mx, a.den, a.out32, a.outbf);
+    }
+    if (lane == 0) a.sp.counter[first] = 0;  // ready for the next launch
+    finish_row<C>(i, tot, dtot, st.m, st.h, slot, sub, a.hidden, a.mx, a.den, a.out32, a.outbf);
+}
+
+template <class C, class ZT, bool RZ>
+__global__ void __launch_bounds__(kThreads) k_agg_vec(VArgs<ZT> a) {
+    // The wave index is made wave-uniform so that row bounds and source ids
+    // come in through scalar loads.
+    const int w = __builtin_amdgcn_readfirstlane(int(threadIdx.x) / kWave);
+    const int lane = threadIdx.x % kWave;
+    const int slot = C::EPI > 1 ? lane / C::LPR : 0;
+    const int sub = C::EPI > 1 ? lane % C::LPR : lane;
+    const uint64_t item = uint64_t(blockIdx.x) * kWavesPerBlock + w;
+    if (item < a.sp.chunks) {
+        run_chunk<C, ZT, RZ>(a, item, lane, slot, sub);
         return;
     }
     // ---------------- whole row, heaviest first
@@ -397,6 +415,8 @@ __global__ void __launch_bounds__(kThreads) k_agg_vec(VArgs<ZT> a) {
     const uint32_t i = a.perm[k];
     const uint64_t beg = a.prow[k], end = a.prow[k + 1];
     if (i >= a.n || beg > end || end > a.e) return;
+    Lane<C> st;
+    init_lane<C, ZT, RZ>(a, sub, st);
 #pragma unroll
     for (int v = 0; v < C::VPL; ++v) {
         st.L[v] = a.L[uint64_t(i) * C::K + st.h[v]];

@@ -78,7 +78,14 @@ struct gatgpu_ctx {
     uint64_t n = 0, e = 0;
     DevBuf row, col, keys_a, keys_b, vals_a, vals_b, hist, scan_tmp, prow, pcol, small;
     uint32_t* sorted_deg = nullptr;
-    uint32_t* perm = nullptr;
+    uint32_t* perm = nullptr;     // sorted position -> original node
+    // Node-indexed device state (features, Z, L, R, max, den, outputs) is kept
+    // in sorted node order: node k is original node perm[k], rcol holds the
+    // sorted CSR's sources as sorted positions, and the kernels get the
+    // identity as their row permutation.  Inputs are gathered into this order
+    // when they are uploaded and outputs are put back in original order.
+    DevBuf invperm, ident, rcol, logits;
+    std::vector<uint32_t> perm_h;
     uint64_t neighbor_steps = 0;
     uint32_t max_degree = 0;
     RowBins bins;
@@ -86,6 +93,7 @@ struct gatgpu_ctx {
     bool input = false;
     int din = 0;
     DevBuf x32, xbf;
+    DevBuf xorig;  // the features in original node order (x32 is their sorted-order copy)
     LayerState L[3];
     // options (in-degree thresholds)
     uint32_t small_max = 0;          // rows <= this share a wave (0: off)
@@ -223,6 +231,14 @@ int build_schedule(gatgpu_ctx* c) {
     HIPCHECK(c, hipMemcpyAsync(c->prow.as<uint64_t>() + n, &c->e, 8, hipMemcpyHostToDevice, c->stream));
     HIPCHECK(c, launch_permute_cols(c->row.as<uint64_t>(), c->col.as<uint32_t>(), c->perm,
                                     c->prow.as<uint64_t>(), c->pcol.as<uint32_t>(), n, c->e, c->stream));
+    HIPCHECK(c, c->invperm.ensure(n * 4));
+    HIPCHECK(c, c->ident.ensure(n * 4));
+    HIPCHECK(c, c->rcol.ensure((c->e + kPcolPad) * 4));
+    HIPCHECK(c, hipMemsetAsync(c->rcol.as<uint32_t>() + c->e, 0, kPcolPad * 4, c->stream));
+    HIPCHECK(c, launch_relabel(c->perm, c->pcol.as<uint32_t>(), c->invperm.as<uint32_t>(), c->ident.as<uint32_t>(),
+                               c->rcol.as<uint32_t>(), n, c->e, c->stream));
+    c->perm_h.resize(n);
+    HIPCHECK(c, hipMemcpyAsync(c->perm_h.data(), c->perm, n * 4, hipMemcpyDeviceToHost, c->stream));
     uint64_t* dsteps = reinterpret_cast<uint64_t*>(c->small.as<char>() + 8);
     HIPCHECK(c, hipMemsetAsync(dsteps, 0, 8, c->stream));
     HIPCHECK(c, launch_neighbor_steps(c->sorted_deg, n, dsteps, c->stream));
@@ -330,8 +346,8 @@ int run_layer_af(gatgpu_ctx* c, int l, bool hidden, const float* src32, const ui
     if (sum_form) {
         AfsArgs a{};
         a.prow = c->prow.as<uint64_t>();
-        a.pcol = c->pcol.as<uint32_t>();
-        a.perm = c->perm;
+        a.pcol = c->rcol.as<uint32_t>();
+        a.perm = c->ident.as<uint32_t>();
         a.L = Ls.left.as<float>();
         a.R = Ls.right.as<float>();
         a.xr = reinterpret_cast<const uint32_t*>(Ls.inbf.as<uint16_t>());
@@ -358,8 +374,8 @@ int run_layer_af(gatgpu_ctx* c, int l, bool hidden, const float* src32, const ui
     } else {
     AfArgs a{};
     a.prow = c->prow.as<uint64_t>();
-    a.pcol = c->pcol.as<uint32_t>();
-    a.perm = c->perm;
+    a.pcol = c->rcol.as<uint32_t>();
+    a.perm = c->ident.as<uint32_t>();
     a.L = Ls.left.as<float>();
     a.R = Ls.right.as<float>();
     a.X = srcbf;
@@ -400,6 +416,49 @@ int run_layer_af(gatgpu_ctx* c, int l, bool hidden, const float* src32, const ui
     return GATGPU_OK;
 }
 
+// Host rows [n][width] FP32 in original node order to device rows in sorted
+// node order (dst row k = host row perm[k]).  Staged through a device buffer;
+// returns after the copy is enqueued and the staging buffer is released by a
+// stream synchronisation.
+hipError_t upload_rows_sorted(gatgpu_ctx* c, const float* host, int width, void* dst) {
+    const uint64_t n = c->n;
+    DevBuf tmp;
+    hipError_t e = tmp.ensure(n * uint64_t(width) * 4);
+    if (e != hipSuccess) return e;
+    if ((e = hipMemcpyAsync(tmp.p, host, n * uint64_t(width) * 4, hipMemcpyHostToDevice, c->stream)) != hipSuccess)
+        return e;
+    if ((e = launch_gather_rows(tmp.p, uint64_t(width), dst, uint64_t(width), c->perm, n, n, uint32_t(width),
+                                c->stream)) != hipSuccess)
+        return e;
+    return hipStreamSynchronize(c->stream);
+}
+
+// Device rows [n][stride] in sorted node order, `width` elements of `esize`
+// bytes each, to host rows [n][width] in original order.
+template <class T>
+int download_rows_original(gatgpu_ctx* c, const void* src, uint64_t stride, int width, std::vector<T>& out) {
+    const uint64_t n = c->n;
+    std::vector<T> tmp(n * stride);
+    HIPCHECK(c, hipMemcpy(tmp.data(), src, tmp.size() * sizeof(T), hipMemcpyDeviceToHost));
+    out.resize(n * uint64_t(width));
+    for (uint64_t k = 0; k < n; ++k)
+        std::memcpy(&out[uint64_t(c->perm_h[k]) * width], &tmp[k * stride], size_t(width) * sizeof(T));
+    return GATGPU_OK;
+}
+
+// x32 = the features in sorted node order (row k = original row perm[k]),
+// with kF32Pad floats of zero padding.
+int sort_features(gatgpu_ctx* c) {
+    const uint64_t n = c->n;
+    const int din = c->din;
+    HIPCHECK(c, c->x32.ensure((n * din + kF32Pad) * 4));
+    HIPCHECK(c, launch_gather_rows(c->xorig.p, uint64_t(din), c->x32.p, uint64_t(din), c->perm, n, n, uint32_t(din),
+                                   c->stream));
+    HIPCHECK(c, hipMemsetAsync(c->x32.as<float>() + n * din, 0, kF32Pad * 4, c->stream));
+    HIPCHECK(c, hipStreamSynchronize(c->stream));
+    return GATGPU_OK;
+}
+
 // Runs layer l on the device.  ev_base: first of 4 events (start, after
 // convert, after projection, after aggregate) or -1 for no timing.
 int run_layer(gatgpu_ctx* c, int l, int precision, int dataflow, bool hidden, const float* host_input,
@@ -412,7 +471,8 @@ int run_layer(gatgpu_ctx* c, int l, int precision, int dataflow, bool hidden, co
     const uint16_t* srcbf = nullptr;
     if (host_input) {
         HIPCHECK(c, Ls.in32.ensure((n * D + kF32Pad) * 4));
-        HIPCHECK(c, hipMemcpyAsync(Ls.in32.p, host_input, n * D * 4, hipMemcpyHostToDevice, c->stream));
+        HIPCHECK(c, upload_rows_sorted(c, host_input, D, Ls.in32.p));
+        HIPCHECK(c, hipMemsetAsync(Ls.in32.as<float>() + n * D, 0, kF32Pad * 4, c->stream));
         src32 = Ls.in32.as<float>();
     } else if (l == 0) {
         if (!c->input) return fail(c, GATGPU_ESTATE, "node features not set");
@@ -507,8 +567,8 @@ int run_layer(gatgpu_ctx* c, int l, int precision, int dataflow, bool hidden, co
     // ---- fused prescan + softmax + aggregation + normalise + ELU
     AggArgs a{};
     a.prow = c->prow.as<uint64_t>();
-    a.pcol = c->pcol.as<uint32_t>();
-    a.perm = c->perm;
+    a.pcol = c->rcol.as<uint32_t>();
+    a.perm = c->ident.as<uint32_t>();
     a.left = Ls.left.as<float>();
     a.right = Ls.right.as<float>();
     a.feat = bf16 ? static_cast<const void*>(Ls.zbf.p) : Ls.z32.p;
@@ -626,6 +686,8 @@ int gatgpu_set_graph(gatgpu_ctx* c, uint64_t n, uint64_t e, const uint64_t* row,
     if (e) HIPCHECK(c, hipMemcpyAsync(c->col.p, col, e * 4, hipMemcpyHostToDevice, c->stream));
     if (int r = build_schedule(c)) return r;
     c->graph = true;
+    if (c->input)  // the features follow the new node order
+        if (int r = sort_features(c)) return r;
     return GATGPU_OK;
 }
 
@@ -693,10 +755,10 @@ int gatgpu_set_input(gatgpu_ctx* c, uint64_t n, int din, const float* x) {
     if (mul_overflows(n, uint64_t(din) * 4)) return fail(c, GATGPU_EOVERFLOW, "size overflow");
     uint64_t bad = 0;
     if (!all_finite(x, n * din, &bad)) return fail(c, GATGPU_ENONFINITE, "nonfinite graph input index=" + std::to_string(bad));
-    HIPCHECK(c, c->x32.ensure((n * din + kF32Pad) * 4));
-    HIPCHECK(c, hipMemcpyAsync(c->x32.p, x, n * din * 4, hipMemcpyHostToDevice, c->stream));
-    HIPCHECK(c, hipStreamSynchronize(c->stream));
+    HIPCHECK(c, c->xorig.ensure(n * din * 4));
+    HIPCHECK(c, hipMemcpyAsync(c->xorig.p, x, n * din * 4, hipMemcpyHostToDevice, c->stream));
     c->din = din;
+    if (int r = sort_features(c)) return r;
     c->input = true;
     c->L[0].ran = false;
     return GATGPU_OK;
@@ -784,7 +846,7 @@ int gatgpu_set_fixed_p(gatgpu_ctx* c, int layer, const float* p, const float* de
     HIPCHECK(c, Ls.fixp.ensure(e * K * 4));
     HIPCHECK(c, Ls.fixden.ensure(n * K * 4));
     if (e) HIPCHECK(c, hipMemcpyAsync(tmp.p, p, e * K * 4, hipMemcpyHostToDevice, c->stream));
-    HIPCHECK(c, hipMemcpyAsync(Ls.fixden.p, den, n * K * 4, hipMemcpyHostToDevice, c->stream));
+    HIPCHECK(c, upload_rows_sorted(c, den, K, Ls.fixden.p));
     HIPCHECK(c, launch_permute_edge_values(c->row.as<uint64_t>(), c->perm, c->prow.as<uint64_t>(), tmp.as<float>(),
                                            Ls.fixp.as<float>(), n, e, K, c->stream));
     HIPCHECK(c, hipStreamSynchronize(c->stream));
@@ -836,15 +898,19 @@ int gatgpu_model_forward(gatgpu_ctx* c, int precision, int dataflow, float* logi
         if (flow < 0) flow = GATGPU_TRANSFORM_FIRST;
         if (int r = run_layer(c, l, precision, flow, l < 2, nullptr, timed ? 4 * l : -1)) return r;
     }
+    // Logits back to original node order (row i = sorted row invperm[i]),
+    // inside the timed forward.
+    const LayerState& L2 = c->L[2];
+    const uint32_t C = uint32_t(L2.width());
+    HIPCHECK(c, c->logits.ensure(c->n * C * 4));
+    HIPCHECK(c, launch_gather_rows(L2.out32.p, C, c->logits.p, C, c->invperm.as<uint32_t>(), c->n, c->n, C, c->stream));
+    if (timed) HIPCHECK(c, hipEventRecord(c->ev[12], c->stream));
     HIPCHECK(c, hipStreamSynchronize(c->stream));
     HIPCHECK(c, hipGetLastError());
     if (times)
         for (int l = 0; l < 3; ++l) fill_times(c, 4 * l, &times[l], c->L[l].dataflow);
-    if (total_ms) *total_ms = ms_between(c->ev[0], c->ev[11]);
-    if (logits) {
-        const LayerState& L = c->L[2];
-        HIPCHECK(c, hipMemcpy(logits, L.out32.p, c->n * L.width() * 4, hipMemcpyDeviceToHost));
-    }
+    if (total_ms) *total_ms = ms_between(c->ev[0], c->ev[12]);
+    if (logits) HIPCHECK(c, hipMemcpy(logits, c->logits.p, c->n * c->L[2].width() * 4, hipMemcpyDeviceToHost));
     return GATGPU_OK;
 }
 
@@ -895,24 +961,19 @@ int gatgpu_get_stage(gatgpu_ctx* c, int layer, int which, float* host) {
             src = bf ? L.outbf.p : L.out32.p;
             break;
     }
-    if (bf && which == GATGPU_STAGE_Z) {
-        const int W = L.width(), zs = z_stride(GATGPU_BF16, L.heads, W, nullptr);
-        std::vector<uint16_t> tmp(c->n * zs);
-        HIPCHECK(c, hipMemcpy(tmp.data(), src, tmp.size() * 2, hipMemcpyDeviceToHost));
-        for (uint64_t i = 0; i < c->n; ++i)
-            for (int f = 0; f < W; ++f) host[i * W + f] = bf16_widen(tmp[i * zs + f]);
-    } else if (which == GATGPU_STAGE_Z) {
-        const int W = L.width(), zs = z_stride(GATGPU_FP32, L.heads, W, nullptr);
-        std::vector<float> tmp(c->n * zs);
-        HIPCHECK(c, hipMemcpy(tmp.data(), src, tmp.size() * 4, hipMemcpyDeviceToHost));
-        for (uint64_t i = 0; i < c->n; ++i)
-            for (int f = 0; f < W; ++f) host[i * W + f] = tmp[i * zs + f];
-    } else if (bf) {
-        std::vector<uint16_t> tmp(count);
-        HIPCHECK(c, hipMemcpy(tmp.data(), src, count * 2, hipMemcpyDeviceToHost));
-        for (uint64_t i = 0; i < count; ++i) host[i] = bf16_widen(tmp[i]);
+    // Device stages are in sorted node order; rows go back to original order.
+    const int W = L.width();
+    const int width = (which == GATGPU_STAGE_Z || which == GATGPU_STAGE_OUT) ? W : L.heads;
+    const uint64_t stride = which == GATGPU_STAGE_Z ? uint64_t(z_stride(bf ? GATGPU_BF16 : GATGPU_FP32, L.heads, W, nullptr))
+                                                    : uint64_t(width);
+    if (bf) {
+        std::vector<uint16_t> rows;
+        if (int r = download_rows_original(c, src, stride, width, rows)) return r;
+        for (uint64_t i = 0; i < count; ++i) host[i] = bf16_widen(rows[i]);
     } else {
-        HIPCHECK(c, hipMemcpy(host, src, count * 4, hipMemcpyDeviceToHost));
+        std::vector<float> rows;
+        if (int r = download_rows_original(c, src, stride, width, rows)) return r;
+        std::memcpy(host, rows.data(), count * 4);
     }
     return GATGPU_OK;
 }

@@ -105,6 +105,14 @@ hipError_t launch_permute_edge_values(const uint64_t* row, const uint32_t* perm,
                                      const float* src, float* dst, uint64_t n, uint64_t e, int K, hipStream_t s);
 hipError_t launch_neighbor_steps(const uint32_t* sorted_deg, uint64_t n, uint64_t* steps,
                                  hipStream_t s);
+// Sorted node order: invperm (invperm[perm[k]] = k), ident (ident[k] = k) and
+// rcol[q] = invperm[pcol[q]] (the sorted CSR's sources as sorted positions).
+hipError_t launch_relabel(const uint32_t* perm, const uint32_t* pcol, uint32_t* invperm, uint32_t* ident,
+                          uint32_t* rcol, uint64_t n, uint64_t e, hipStream_t s);
+// dst row r = src row idx[r] (rows of `words` 4-byte words; strides in words;
+// an index >= n_src gives a zero row).
+hipError_t launch_gather_rows(const void* src, uint64_t src_stride_words, void* dst, uint64_t dst_stride_words,
+                              const uint32_t* idx, uint64_t rows, uint64_t n_src, uint32_t words, hipStream_t s);
 hipError_t launch_count_le(const uint32_t* sorted_deg, uint64_t n, const uint32_t* thresholds,
                            int count, uint64_t* positions, hipStream_t s);
 

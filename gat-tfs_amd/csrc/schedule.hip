@@ -227,6 +227,39 @@ k_permute_edge_values(const uint64_t* __restrict__ row, const uint32_t* __restri
     for (uint64_t q = lane; q < cnt; q += kWave) dst[d0 * K + q] = src[s0 * K + q];
 }
 
+// Sorted node order.  invperm[perm[k]] = k and ident[k] = k.
+__global__ void __launch_bounds__(kThreads)
+k_invert_perm(const uint32_t* __restrict__ perm, uint32_t* __restrict__ invperm, uint32_t* __restrict__ ident,
+              uint64_t n) {
+    for (uint64_t k = uint64_t(blockIdx.x) * kThreads + threadIdx.x; k < n; k += uint64_t(gridDim.x) * kThreads) {
+        const uint32_t r = perm[k];
+        if (r < n) invperm[r] = uint32_t(k);
+        ident[k] = uint32_t(k);
+    }
+}
+
+// rcol[q] = invperm[pcol[q]]: source ids of the sorted CSR as sorted positions.
+__global__ void __launch_bounds__(kThreads)
+k_relabel_cols(const uint32_t* __restrict__ pcol, const uint32_t* __restrict__ invperm, uint32_t* __restrict__ rcol,
+               uint64_t e, uint64_t n) {
+    for (uint64_t q = uint64_t(blockIdx.x) * kThreads + threadIdx.x; q < e; q += uint64_t(gridDim.x) * kThreads) {
+        const uint32_t j = pcol[q];
+        rcol[q] = j < n ? invperm[j] : 0u;
+    }
+}
+
+// dst row r = src row idx[r], rows of `words` 4-byte words (row strides in words).
+__global__ void __launch_bounds__(kThreads)
+k_gather_rows(const uint32_t* __restrict__ src, uint64_t src_stride, uint32_t* __restrict__ dst, uint64_t dst_stride,
+              const uint32_t* __restrict__ idx, uint64_t rows, uint64_t n_src, uint32_t words) {
+    const uint64_t total = rows * words;
+    for (uint64_t t = uint64_t(blockIdx.x) * kThreads + threadIdx.x; t < total; t += uint64_t(gridDim.x) * kThreads) {
+        const uint64_t r = t / words, w = t % words;
+        const uint32_t q = idx[r];
+        dst[r * dst_stride + w] = q < n_src ? src[uint64_t(q) * src_stride + w] : 0u;
+    }
+}
+
 // neighbor_steps = sum over 16-row tiles of the last (= largest) degree.
 __global__ void __launch_bounds__(kThreads)
 k_neighbor_steps(const uint32_t* __restrict__ sorted_deg, uint64_t n, uint64_t* __restrict__ steps) {
@@ -319,6 +352,22 @@ hipError_t launch_permute_edge_values(const uint64_t* row, const uint32_t* perm,
     const uint64_t waves_per_block = kThreads / kWave;
     const uint64_t blocks = (n + waves_per_block - 1) / waves_per_block;
     k_permute_edge_values<<<dim3(uint32_t(blocks)), kThreads, 0, s>>>(row, perm, prow, src, dst, n, e, K);
+    return hipGetLastError();
+}
+
+hipError_t launch_relabel(const uint32_t* perm, const uint32_t* pcol, uint32_t* invperm, uint32_t* ident,
+                          uint32_t* rcol, uint64_t n, uint64_t e, hipStream_t s) {
+    k_invert_perm<<<grid_for(n, kThreads, 4096), kThreads, 0, s>>>(perm, invperm, ident, n);
+    if (e) k_relabel_cols<<<grid_for(e, kThreads, 8192), kThreads, 0, s>>>(pcol, invperm, rcol, e, n);
+    return hipGetLastError();
+}
+
+hipError_t launch_gather_rows(const void* src, uint64_t src_stride_words, void* dst, uint64_t dst_stride_words,
+                              const uint32_t* idx, uint64_t rows, uint64_t n_src, uint32_t words, hipStream_t s) {
+    if (!rows || !words) return hipSuccess;
+    k_gather_rows<<<grid_for(rows * words, kThreads, 8192), kThreads, 0, s>>>(
+        static_cast<const uint32_t*>(src), src_stride_words, static_cast<uint32_t*>(dst), dst_stride_words, idx, rows,
+        n_src, words);
     return hipGetLastError();
 }
 
