@@ -58,7 +58,7 @@ constexpr int kTile = 2 * kWaves;          // rows per block tile (hi + lo S)
 constexpr int kTileBf16 = 32;              // rows per block tile with one bf16 S
 constexpr int kMaxKS = 7;                  // k steps of 16 features: D_in <= 112
 constexpr int kRowWords = kXRStride / 2;   // 64 words of 4 bytes per XR row
-constexpr int kB = 32;                     // edges per batch (MFMA contraction)
+constexpr int kEPL = 4;                    // edges per lane and batch (batches of 4 kEPL edges)
 constexpr int kSB = 4;                     // super-blocks of 16 words per row
 constexpr int kBlk = kTile * 32 + 16;      // bytes per (head, k step, hi|lo) block of S, padded
 constexpr int kSBytes = 8 * kMaxKS * 2 * kBlk;
@@ -68,7 +68,7 @@ constexpr int kPart = 8 * 128 + 8;         // floats per chunk partial (U_h rows
 constexpr int kDenOff = 8 * 128;
 constexpr int kChunkThreads = 256;
 
-static_assert(kB <= int(kPcolPad), "an id request may read kB - 1 entries past the row");
+static_assert(32 <= int(kPcolPad), "an id request may read 31 entries past the row");
 static_assert(kRowWords == 16 * kSB && kXRFeat == 112, "XR row: 4 super-blocks, R in words 56..63");
 
 __device__ inline float lane_f(float x, int lane) {
@@ -83,41 +83,66 @@ struct Sums {
     float m, den, L;
 };
 
+// Batches of 4 EPL edges: lane (g, n) takes edges EPL g .. EPL g + EPL - 1
+// of a batch, the k group of v_mfma_f32_16x16x32_bf16 (EPL 8) or of
+// v_mfma_f32_16x16x16_bf16 (EPL 4; smaller batches waste fewer slots on short
+// rows).  The D layout is the same for both.
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+template <int EPL>
+struct Mfma;
+template <>
+struct Mfma<8> {
+    static __device__ inline f32x4 run(const uint32_t (&a)[4], const uint32_t (&b)[4], f32x4 d) {
+        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, make_uint4(a[0], a[1], a[2], a[3])),
+                                                       __builtin_bit_cast(bf16x8, make_uint4(b[0], b[1], b[2], b[3])),
+                                                       d, 0, 0, 0);
+    }
+};
+template <>
+struct Mfma<4> {
+    static __device__ inline f32x4 run(const uint32_t (&a)[2], const uint32_t (&b)[2], f32x4 d) {
+        return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(s16x4, make_uint2(a[0], a[1])),
+                                                          __builtin_bit_cast(s16x4, make_uint2(b[0], b[1])), d, 0,
+                                                          0, 0);
+    }
+};
+
 // Edges [beg, end).  ids: lane id0 + t holds pcol[beg + t], t < 32 (requested
 // by the caller ahead of time); each batch requests the next batch's ids the
 // same way (pcol is padded past e).  EXACT: s.m holds the exact row max
 // already (a chunk) and never moves.
-template <bool EXACT>
+template <bool EXACT, int EPL = kEPL>
 __device__ inline void gather_sums(const uint32_t* __restrict__ pcol, const uint32_t* __restrict__ xr,
                                    uint64_t beg, uint64_t end, int l, Sums& s, uint32_t ids, int id0) {
+    constexpr int B = 4 * EPL;  // edges per batch
     if (beg >= end) return;
     const int g = l / 16, n = l % 16;
     const bool head = n < 8;
-    for (uint64_t base = beg; base < end; base += kB) {
-        const uint32_t nids = pcol[(base + kB < end ? base + kB : end) + uint32_t(l % 32)];
+    for (uint64_t base = beg; base < end; base += B) {
+        const uint32_t nids = pcol[(base + B < end ? base + B : end) + uint32_t(l % 32)];
         const uint64_t rem = end - base;
-        const int cnt = rem < uint64_t(kB) ? int(rem) : kB;
-        // This lane's 8 edges; edges past the end re-read the batch's first row
-        // (weight 0).
-        uint32_t jl[8];
+        const int cnt = rem < uint64_t(B) ? int(rem) : B;
+        // This lane's EPL edges; edges past the end re-read the batch's first
+        // row (weight 0).
+        uint32_t jl[EPL];
 #pragma unroll
-        for (int t = 0; t < 8; ++t) jl[t] = __shfl(ids, id0 + (8 * g + t < cnt ? 8 * g + t : 0));
+        for (int t = 0; t < EPL; ++t) jl[t] = __shfl(ids, id0 + (EPL * g + t < cnt ? EPL * g + t : 0));
         // 32-bit byte offsets (n * 256 < 2^32 is checked at launch).
         const unsigned char* xb = reinterpret_cast<const unsigned char*>(xr);
-        uint32_t raw[kSB][8];
+        uint32_t raw[kSB][EPL];
 #pragma unroll
-        for (int t = 0; t < 8; ++t) {
+        for (int t = 0; t < EPL; ++t) {
             const uint32_t off = jl[t] * uint32_t(4 * kRowWords) + 4u * uint32_t(n);
 #pragma unroll
             for (int sb = 0; sb < kSB; ++sb) raw[sb][t] = *reinterpret_cast<const uint32_t*>(xb + off + 64 * sb);
         }
-        // ---- head lanes: scores of their 8 edges, batch max over the 4 k groups
-        float sc[8];
+        // ---- head lanes: scores of their edges, batch max over the 4 k groups
+        float sc[EPL];
         float mb = -INFINITY;
 #pragma unroll
-        for (int t = 0; t < 8; ++t) {
+        for (int t = 0; t < EPL; ++t) {
             const float r = __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(int(raw[3][t]), 0x128, 0xF, 0xF, false));
-            sc[t] = (head && 8 * g + t < cnt) ? leaky(s.L + r) : -INFINITY;
+            sc[t] = (head && EPL * g + t < cnt) ? leaky(s.L + r) : -INFINITY;
             mb = fmaxf(mb, sc[t]);
         }
         mb = fmaxf(mb, __shfl_xor(mb, 16));
@@ -128,11 +153,11 @@ __device__ inline void gather_sums(const uint32_t* __restrict__ pcol, const uint
             scale = mn > s.m ? exp_w(s.m - mn) : 1.0f;  // exp(-inf) = 0 on the first batch
             s.m = mn;
         }
-        // ---- A operands: row h = hi (then lo) part of p_h for edges 8g + t
-        uint32_t ah[4], al[4];
+        // ---- A operands: row h = hi (then lo) part of p_h for the lane's edges
+        uint32_t ah[EPL / 2], al[EPL / 2];
         float ps = 0.0f;
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
+        for (int q = 0; q < EPL / 2; ++q) {
             const float p0 = head ? exp_w(sc[2 * q] - s.m) : 0.0f;  // -inf past the end: 0
             const float p1 = head ? exp_w(sc[2 * q + 1] - s.m) : 0.0f;
             ps += p0 + p1;
@@ -149,24 +174,20 @@ __device__ inline void gather_sums(const uint32_t* __restrict__ pcol, const uint
                 for (int b = 0; b < 2 * kSB; ++b) s.d[b][r] *= f;
             }
         }
-        const bf16x8 Ah = __builtin_bit_cast(bf16x8, make_uint4(ah[0], ah[1], ah[2], ah[3]));
-        const bf16x8 Al = __builtin_bit_cast(bf16x8, make_uint4(al[0], al[1], al[2], al[3]));
-        // ---- B operands from the low / high halves of the 8 words, and the MFMAs
+        // ---- B operands from the low / high halves of the words, and the MFMAs
 #pragma unroll
         for (int sb = 0; sb < kSB; ++sb) {
-            uint32_t ev[4], od[4];
+            uint32_t ev[EPL / 2], od[EPL / 2];
 #pragma unroll
-            for (int q = 0; q < 4; ++q) {
+            for (int q = 0; q < EPL / 2; ++q) {
                 const uint32_t w0 = raw[sb][2 * q], w1 = raw[sb][2 * q + 1];
                 ev[q] = (w0 & 0xffffu) | (w1 << 16);
                 od[q] = (w0 >> 16) | (w1 & 0xffff0000u);
             }
-            const bf16x8 Be = __builtin_bit_cast(bf16x8, make_uint4(ev[0], ev[1], ev[2], ev[3]));
-            const bf16x8 Bo = __builtin_bit_cast(bf16x8, make_uint4(od[0], od[1], od[2], od[3]));
-            s.d[2 * sb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(Ah, Be, s.d[2 * sb], 0, 0, 0);
-            s.d[2 * sb + 1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(Ah, Bo, s.d[2 * sb + 1], 0, 0, 0);
-            s.d[2 * sb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(Al, Be, s.d[2 * sb], 0, 0, 0);
-            s.d[2 * sb + 1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(Al, Bo, s.d[2 * sb + 1], 0, 0, 0);
+            s.d[2 * sb] = Mfma<EPL>::run(ah, ev, s.d[2 * sb]);
+            s.d[2 * sb + 1] = Mfma<EPL>::run(ah, od, s.d[2 * sb + 1]);
+            s.d[2 * sb] = Mfma<EPL>::run(al, ev, s.d[2 * sb]);
+            s.d[2 * sb + 1] = Mfma<EPL>::run(al, od, s.d[2 * sb + 1]);
         }
         ids = nids;
         id0 = 0;
