@@ -26,10 +26,14 @@
 // scores head h for its 8 edges, keeps the running max m_h and the
 // denominator, and splits p into hi + lo bf16 (p enters to about 2^-17): A
 // row h holds the hi parts in one MFMA and the lo parts in a second one into
-// the same accumulators (rows 8..15 of A are zero).  A batch that raises some
-// m_h first rescales the sums by exp(m_old - m_new) (the running-maximum form
-// of gat_tfs_online.cpp:86-117); the final m_h is leaky(L_h + max_j R_jh) bit
-// for bit, as leaky and the addition are monotone.  Lane (g, n), g = 0, 1,
+// the same accumulators (rows 8..15 of A are zero).  The weights are taken
+// against a reference max m_h: the first batch's max, moved (with the sums
+// rescaled by exp(m_old - m_new), the running-maximum form of
+// gat_tfs_online.cpp:86-117) only when a batch's max exceeds it by more than
+// kLazyMax, so p <= e^8 and most batches rescale nothing.  The exact row max
+// M_h = leaky(L_h + max_j R_jh) is kept beside it (bit for bit, as leaky and
+// the addition are monotone); the stored denominator is sum_j e^(s_j - M_h) =
+// den e^(m_h - M_h), and U / den is the same quotient either way.  Lane (g, n), g = 0, 1,
 // register r of block (sb, par) holds U of head 4g + r, feature
 // 2(16 sb + n) + par.
 //
@@ -78,10 +82,17 @@ __device__ inline float lane_f(float x, int lane) {
 // Running sums of one row or chunk.  d[2 sb + par] are the D accumulators of
 // the feature blocks; m, den and L live in the head lanes (n < 8, head n;
 // den of the lane's own k group until combined).
+// m is the reference max the weights p = e^(s - m) are taken against; mx is
+// the running row max (exact).
 struct Sums {
     f32x4 d[2 * kSB];
-    float m, den, L;
+    float m, mx, den, L;
 };
+
+// A batch moves the reference max only when its own max exceeds it by more
+// than this (so p <= e^8, far inside FP32 and bf16 range): most batches then
+// need no rescaling of the sums.
+constexpr float kLazyMax = 8.0f;
 
 // Batches of 4 EPL edges: lane (g, n) takes edges EPL g .. EPL g + EPL - 1
 // of a batch, the k group of v_mfma_f32_16x16x32_bf16 (EPL 8) or of
@@ -148,9 +159,15 @@ __device__ inline void gather_sums(const uint32_t* __restrict__ pcol, const uint
         mb = fmaxf(mb, __shfl_xor(mb, 16));
         mb = fmaxf(mb, __shfl_xor(mb, 32));
         float scale = 1.0f;
+        bool resc = false;
         if constexpr (!EXACT) {
-            const float mn = fmaxf(s.m, mb);
-            scale = mn > s.m ? exp_w(s.m - mn) : 1.0f;  // exp(-inf) = 0 on the first batch
+            s.mx = fmaxf(s.mx, mb);
+            // The first batch (m = -inf) sets m; a later one moves it (and
+            // rescales the sums) only beyond m + kLazyMax.
+            const bool up = mb > s.m + kLazyMax;
+            resc = up && s.m != -INFINITY;
+            const float mn = up ? mb : s.m;
+            scale = up ? exp_w(s.m - mn) : 1.0f;  // exp(-inf) = 0 on the first batch (the sums are 0)
             s.m = mn;
         }
         // ---- A operands: row h = hi (then lo) part of p_h for the lane's edges
@@ -165,7 +182,7 @@ __device__ inline void gather_sums(const uint32_t* __restrict__ pcol, const uint
             al[q] = bf16x2(p0 - __builtin_bit_cast(float, ah[q] << 16), p1 - __builtin_bit_cast(float, ah[q] & 0xffff0000u));
         }
         s.den = s.den * scale + ps;
-        if (!EXACT && __any(head && scale != 1.0f)) {
+        if (!EXACT && __any(head && resc)) {
             // D register r of lane group g belongs to head 4 (g % 2) + r.
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
@@ -180,9 +197,10 @@ __device__ inline void gather_sums(const uint32_t* __restrict__ pcol, const uint
             uint32_t ev[EPL / 2], od[EPL / 2];
 #pragma unroll
             for (int q = 0; q < EPL / 2; ++q) {
+                // low halves of w0, w1 (even features) and high halves (odd)
                 const uint32_t w0 = raw[sb][2 * q], w1 = raw[sb][2 * q + 1];
-                ev[q] = (w0 & 0xffffu) | (w1 << 16);
-                od[q] = (w0 >> 16) | (w1 & 0xffff0000u);
+                ev[q] = __builtin_amdgcn_perm(w1, w0, 0x05040100u);
+                od[q] = __builtin_amdgcn_perm(w1, w0, 0x07060302u);
             }
             s.d[2 * sb] = Mfma<EPL>::run(ah, ev, s.d[2 * sb]);
             s.d[2 * sb + 1] = Mfma<EPL>::run(ah, od, s.d[2 * sb + 1]);
@@ -246,29 +264,40 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4
             fe = a.prow[k + 1];
         }
     };
-    uint32_t mi;
-    uint64_t mb, me;
+    // First source ids (lane 32 (q % 2) + t of ids[q / 2]) and L (lane
+    // 8 q + h) of the wave's rows; a row with malformed bounds becomes kNoRow.
+    constexpr int NID = (RPW + 1) / 2;
+    auto fetch_ids = [&](uint32_t& fi, uint64_t fb, uint64_t fe, uint32_t (&ids)[NID], float& Lv) {
+        if (fi != kNoRow && (fi >= a.n || fb > fe || fe > a.e)) fi = kNoRow;
+#pragma unroll
+        for (int c = 0; c < NID; ++c) {
+            const int q = 2 * c + l / 32;
+            const uint32_t qi = __shfl(fi, q);
+            const uint64_t qb = (uint64_t(__shfl(uint32_t(fb >> 32), q)) << 32) | __shfl(uint32_t(fb), q);
+            ids[c] = a.pcol[(q < RPW && qi != kNoRow ? qb : 0) + uint32_t(l % 32)];
+        }
+        Lv = 0.0f;
+        const uint32_t qi = __shfl(fi, l / 8);
+        if (l / 8 < RPW && qi != kNoRow) Lv = a.L[uint64_t(qi) * 8 + l % 8];
+    };
+    // Pipeline over the block's tiles: the bounds of tile t + 2 and the first
+    // ids and L of tile t + 1 are requested at the start of tile t, so a tile
+    // starts with its rows' first batches.
+    uint32_t mi, nmi;
+    uint64_t mb, me, nmb, nme;
+    uint32_t idr[NID], nidr[NID];
+    float Lall, nLall;
     fetch_bounds(blockIdx.x, mi, mb, me);
+    fetch_bounds(blockIdx.x + gridDim.x, nmi, nmb, nme);
+    fetch_ids(mi, mb, me, idr, Lall);
     for (uint64_t tile = blockIdx.x; tile < tiles; tile += gridDim.x, buf ^= DB ? 1 : 0) {
         uint32_t* const trow = trow_all + buf * TR;
-        // ---- RPW rows per wave (tile rows w + 8 q).  Their bounds (lane q), L
-        // (lane 8 q + h) and first ids (lane 32 (q % 2) + t of ids[q / 2]) are
-        // requested together at the start of the tile, so a row waits only on
-        // its own source rows.
-        if (mi != kNoRow && (mi >= a.n || mb > me || me > a.e)) mi = kNoRow;
-        uint32_t idr[(RPW + 1) / 2];
-#pragma unroll
-        for (int c = 0; c < (RPW + 1) / 2; ++c) {
-            const int q = 2 * c + l / 32;
-            const uint32_t qi = __shfl(mi, q);
-            const uint64_t qb = (uint64_t(__shfl(uint32_t(mb >> 32), q)) << 32) | __shfl(uint32_t(mb), q);
-            idr[c] = a.pcol[(q < RPW && qi != kNoRow ? qb : 0) + uint32_t(l % 32)];
-        }
-        float Lall = 0.0f;
-        {
-            const uint32_t qi = __shfl(mi, l / 8);
-            if (l / 8 < RPW && qi != kNoRow) Lall = a.L[uint64_t(qi) * 8 + l % 8];
-        }
+        // ---- RPW rows per wave (tile rows w + 8 q): bounds in lane q, L in
+        // lanes 8 q + h, first ids in idr.
+        uint32_t n2mi;
+        uint64_t n2mb, n2me;
+        fetch_ids(nmi, nmb, nme, nidr, nLall);
+        fetch_bounds(tile + 2 * uint64_t(gridDim.x), n2mi, n2mb, n2me);
 #pragma unroll 1
         for (int rr = 0; rr < RPW; ++rr) {
             const int r = w + kWaves * rr;
@@ -284,12 +313,14 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4
             Sums s;
             zero_sums(s);
             s.L = head ? Lr : 0.0f;
-            s.m = -INFINITY;
+            s.m = s.mx = -INFINITY;
             gather_sums<false>(a.pcol, a.xr, beg, end, l, s, ids, 32 * (rr % 2));
-            const float den = total_den(s.den);
+            const float den = total_den(s.den);  // against the reference max s.m
             if (head && g == 0) {
-                a.mx[uint64_t(i) * 8 + n] = end > beg ? s.m : 0.0f;  // empty row: max 0 (ref_fp32.cpp:11)
-                a.den[uint64_t(i) * 8 + n] = den;
+                // empty row: max 0, denominator 0 (ref_fp32.cpp:11); else the
+                // denominator against the row max, sum e^(s - M) = den e^(m - M)
+                a.mx[uint64_t(i) * 8 + n] = end > beg ? s.mx : 0.0f;
+                a.den[uint64_t(i) * 8 + n] = end > beg ? den * exp_w(s.m - s.mx) : 0.0f;
             }
             const float inv = den > 0.0f ? 1.0f / den : 0.0f;
             // 1 / den of head 4g + q for the lanes g = 0, 1, gathered before any
@@ -329,9 +360,6 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4
         // resident), requested before the barrier.  A wave-uniform base plus a
         // 32-bit lane offset, made opaque so that the addresses are formed here
         // instead of being held across the gather.
-        uint32_t nmi;
-        uint64_t nmb, nme;
-        fetch_bounds(tile + gridDim.x, nmi, nmb, nme);
         bf16x8 wf[KS];
         {
             uint32_t lo = uint32_t(l) * uint32_t(sizeof(uint4));
@@ -403,6 +431,12 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4
         mi = nmi;
         mb = nmb;
         me = nme;
+        nmi = n2mi;
+        nmb = n2mb;
+        nme = n2me;
+#pragma unroll
+        for (int c = 0; c < NID; ++c) idr[c] = nidr[c];
+        Lall = nLall;
     }
 }
 
@@ -431,7 +465,7 @@ __global__ void __launch_bounds__(kChunkThreads) k_afs_chunks(AfsArgs a) {
         s.L = a.L[uint64_t(i) * 8 + h];
         float mc = -INFINITY;
         for (uint32_t q = 0; q < nch; ++q) mc = fmaxf(mc, a.mchunk[(first + q) * 8 + h]);
-        s.m = leaky(s.L + mc);
+        s.m = s.mx = leaky(s.L + mc);
     }
     gather_sums<true>(a.pcol, a.xr, beg, end, l, s, a.pcol[beg + uint32_t(l % 32)], 0);
     const float den = total_den(s.den);
