@@ -15,15 +15,17 @@
 // Gather table XR [n][128] bf16 (256-byte rows, 64 words of 4 bytes): X_j at
 // [0, D_in), zeros up to 112, R_jh as FP32 in word 56 + h.
 //
-// The per-edge sums run on the matrix cores.  Per batch of 32 edges,
-// v_mfma_f32_16x16x32_bf16 forms D[row][feature] += P[row][edge] X[edge][feature]
-// with the edge as the contraction index.  Lane l = 16 g + n (k group g takes
-// edges 8g .. 8g + 7 of the batch) loads word 16 sb + n of each of its 8
-// edges' rows, sb = 0..3 (features 2(16 sb + n) and 2(16 sb + n) + 1): the low
-// halves of those 8 words are the B operand of an even-feature block, the
-// high halves that of an odd-feature block.  Word 56 + h of a row is R_jh; a
-// DPP rotation by 8 hands it from lane 8 + h of super-block 3 to lane h, which
-// scores head h for its 8 edges, keeps the running max m_h and the
+// The per-edge sums run on the matrix cores.  Per batch of 16 edges,
+// v_mfma_f32_16x16x16_bf16 forms D[row][feature] += P[row][edge] X[edge][feature]
+// with the edge as the contraction index (16x16x32 with 32-edge batches is the
+// other instance of the same code: EPL edges per lane).  Lane l = 16 g + n
+// (k group g takes edges 4g .. 4g + 3 of the batch) loads word 16 sb + n of
+// each of its 4 edges' rows, sb = 0..3 (features 2(16 sb + n) and
+// 2(16 sb + n) + 1): the low halves of those words are the B operand of an
+// even-feature block, the high halves that of an odd-feature block.  Word
+// 56 + h of a row is R_jh; a DPP rotation by 8 hands it from lane 8 + h of
+// super-block 3 to lane h, which scores head h for its edges, keeps the
+// running max m_h and the
 // denominator, and splits p into hi + lo bf16 (p enters to about 2^-17): A
 // row h holds the hi parts in one MFMA and the lo parts in a second one into
 // the same accumulators (rows 8..15 of A are zero).  The weights are taken
