@@ -50,6 +50,7 @@ struct K1Args {
     const float* mchunk;
     float* part;
     uint32_t* counter;
+    const uint32_t* operm;  // output row of sorted position k: operm[k] (null: the node index)
 };
 
 __device__ inline void unpack(const uint4& v, float (&f)[8]) {
@@ -239,7 +240,7 @@ __global__ void __launch_bounds__(kThreads) k_agg_k1(K1Args<ZT> a) {
             a.den[i] = dtot;
             a.counter[first] = 0;
         }
-        if (g == 0) store_row<C>(i, a.W, sub, tot, dtot, a.hidden, a.out32, a.outbf);
+        if (g == 0) store_row<C>(a.operm ? a.operm[k] : i, a.W, sub, tot, dtot, a.hidden, a.out32, a.outbf);
         return;
     }
     // ---------------- 64/G whole rows per wave, heaviest first
@@ -265,7 +266,7 @@ __global__ void __launch_bounds__(kThreads) k_agg_k1(K1Args<ZT> a) {
         a.mx[i] = Mi;
         a.den[i] = dloc;
     }
-    store_row<C>(i, a.W, sub, acc, dloc, a.hidden, a.out32, a.outbf);
+    store_row<C>(a.operm ? a.operm[k] : i, a.W, sub, acc, dloc, a.hidden, a.out32, a.outbf);
 }
 
 template <int G, class ZT>
@@ -278,7 +279,7 @@ hipError_t run(const AggArgs& g, const RowBins& bins, const SplitTable& t, hipSt
     const int rs = g.r_in_feat ? int(g.fstride * sizeof(ZT) / 4) : 1;
     K1Args<ZT> a{g.prow, g.pcol, g.perm, g.left, rptr, static_cast<const ZT*>(g.feat), g.heads * g.dim,
                  g.fstride, rs, g.hidden, g.mx, g.den, g.out32, g.outbf, g.n, g.e, bins.split_begin, t.chunks,
-                 t.chunk_k, t.chunk_first, t.chunk_edges, t.mchunk, t.part, t.counter};
+                 t.chunk_k, t.chunk_first, t.chunk_edges, t.mchunk, t.part, t.counter, g.out_perm};
     if (t.chunks) {
         hipError_t e = launch_split_prescan(g.prow, g.pcol, g.right, 1, t, g.e, s);
         if (e != hipSuccess) return e;

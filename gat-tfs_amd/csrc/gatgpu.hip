@@ -53,6 +53,7 @@ struct LayerState {
     DevBuf z32, zbf, zscratch, left, right, mx, den, out32, outbf, in32, inbf;
     // What the last forward of this layer produced.
     bool ran = false, z_valid = false, out32_valid = false, outbf_valid = false;
+    bool out_original = false;  // out32 rows in original node order (else sorted order)
     int precision = -1;
     // bf16 MFMA projection weights (pack_projection_weights order)
     DevBuf wpk;
@@ -407,6 +408,7 @@ int run_layer_af(gatgpu_ctx* c, int l, bool hidden, const float* src32, const ui
     HIPCHECK(c, launch_aggregate_af(a, c->stream, c->cus));
     }
     if (ev_base >= 0) HIPCHECK(c, hipEventRecord(c->ev[ev_base + 3], c->stream));
+    Ls.out_original = false;
     Ls.ran = true;
     Ls.precision = GATGPU_BF16;
     Ls.dataflow = dataflow;
@@ -461,8 +463,10 @@ int sort_features(gatgpu_ctx* c) {
 
 // Runs layer l on the device.  ev_base: first of 4 events (start, after
 // convert, after projection, after aggregate) or -1 for no timing.
+// orig_out: write the FP32 output rows in original node order where the
+// aggregation kernel can (the one-head kernel); Ls.out_original tells.
 int run_layer(gatgpu_ctx* c, int l, int precision, int dataflow, bool hidden, const float* host_input,
-              int ev_base, bool fixed = false) {
+              int ev_base, bool fixed = false, bool orig_out = false) {
     LayerState& Ls = c->L[l];
     const uint64_t n = c->n;
     const int K = Ls.heads, dim = Ls.dim, W = Ls.width(), D = Ls.in;
@@ -586,6 +590,8 @@ int run_layer(gatgpu_ctx* c, int l, int precision, int dataflow, bool hidden, co
     a.e = c->e;
     a.r_from_z = pa.r_from_z;
     a.ar = Ls.ar.as<float>();
+    const bool direct_orig = orig_out && a.out32 && !fixed && !aggregate_vec_supported(a) && aggregate_k1_supported(a);
+    if (direct_orig) a.out_perm = c->perm;
     if (fixed)
         HIPCHECK(c, launch_aggregate_fixed(a, Ls.fixp.as<float>(), Ls.fixden.as<float>(), c->bins, c->split,
                                            c->stream));
@@ -598,6 +604,7 @@ int run_layer(gatgpu_ctx* c, int l, int precision, int dataflow, bool hidden, co
     Ls.z_valid = true;
     Ls.out32_valid = !want_outbf;
     Ls.outbf_valid = want_outbf;
+    Ls.out_original = direct_orig;
     return GATGPU_OK;
 }
 
@@ -896,21 +903,27 @@ int gatgpu_model_forward(gatgpu_ctx* c, int precision, int dataflow, float* logi
         // In the chained model, aggregate-first applies where the layer supports it.
         int flow = resolve_dataflow(c->L[l], precision, dataflow, c->n);
         if (flow < 0) flow = GATGPU_TRANSFORM_FIRST;
-        if (int r = run_layer(c, l, precision, flow, l < 2, nullptr, timed ? 4 * l : -1)) return r;
+        if (int r = run_layer(c, l, precision, flow, l < 2, nullptr, timed ? 4 * l : -1, false, l == 2)) return r;
     }
-    // Logits back to original node order (row i = sorted row invperm[i]),
-    // inside the timed forward.
+    // Logits in original node order, inside the timed forward: written so by
+    // the last aggregation where it can, else gathered back (row i = sorted
+    // row invperm[i]).
     const LayerState& L2 = c->L[2];
     const uint32_t C = uint32_t(L2.width());
-    HIPCHECK(c, c->logits.ensure(c->n * C * 4));
-    HIPCHECK(c, launch_gather_rows(L2.out32.p, C, c->logits.p, C, c->invperm.as<uint32_t>(), c->n, c->n, C, c->stream));
+    const void* logits_dev = L2.out32.p;
+    if (!L2.out_original) {
+        HIPCHECK(c, c->logits.ensure(c->n * C * 4));
+        HIPCHECK(c, launch_gather_rows(L2.out32.p, C, c->logits.p, C, c->invperm.as<uint32_t>(), c->n, c->n, C,
+                                       c->stream));
+        logits_dev = c->logits.p;
+    }
     if (timed) HIPCHECK(c, hipEventRecord(c->ev[12], c->stream));
     HIPCHECK(c, hipStreamSynchronize(c->stream));
     HIPCHECK(c, hipGetLastError());
     if (times)
         for (int l = 0; l < 3; ++l) fill_times(c, 4 * l, &times[l], c->L[l].dataflow);
     if (total_ms) *total_ms = ms_between(c->ev[0], c->ev[12]);
-    if (logits) HIPCHECK(c, hipMemcpy(logits, c->logits.p, c->n * c->L[2].width() * 4, hipMemcpyDeviceToHost));
+    if (logits) HIPCHECK(c, hipMemcpy(logits, logits_dev, c->n * C * 4, hipMemcpyDeviceToHost));
     return GATGPU_OK;
 }
 
@@ -966,7 +979,9 @@ int gatgpu_get_stage(gatgpu_ctx* c, int layer, int which, float* host) {
     const int width = (which == GATGPU_STAGE_Z || which == GATGPU_STAGE_OUT) ? W : L.heads;
     const uint64_t stride = which == GATGPU_STAGE_Z ? uint64_t(z_stride(bf ? GATGPU_BF16 : GATGPU_FP32, L.heads, W, nullptr))
                                                     : uint64_t(width);
-    if (bf) {
+    if (which == GATGPU_STAGE_OUT && !bf && L.out_original) {
+        HIPCHECK(c, hipMemcpy(host, src, count * 4, hipMemcpyDeviceToHost));
+    } else if (bf) {
         std::vector<uint16_t> rows;
         if (int r = download_rows_original(c, src, stride, width, rows)) return r;
         for (uint64_t i = 0; i < count; ++i) host[i] = bf16_widen(rows[i]);

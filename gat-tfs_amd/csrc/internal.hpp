@@ -199,6 +199,9 @@ struct AggArgs {
     uint64_t n, e;           // nodes and CSR entries (bounds of perm/prow values)
     bool r_from_z = false;   // bf16 8 x 32: recompute R = Z_bf16 . aR from the gathered rows
     const float* ar = nullptr;
+    // Output row of sorted position k (one-head kernel only): out_perm[k]
+    // instead of the node index perm[k].  Null: the node index.
+    const uint32_t* out_perm = nullptr;
 };
 // The permuted column array carries kPcolPad zero entries past its e
 // edges, so that kernels may load a whole batch of wave-uniform source ids

@@ -248,15 +248,24 @@ k_relabel_cols(const uint32_t* __restrict__ pcol, const uint32_t* __restrict__ i
     }
 }
 
-// dst row r = src row idx[r], rows of `words` 4-byte words (row strides in words).
+// dst row r = src row idx[r], rows of `words` 4-byte words (row strides in
+// words).  A block copies 64 rows at a time as one flat range of
+// 64 * words words (32-bit index arithmetic within the range), so every
+// thread has several independent loads in flight.
+constexpr uint32_t kGatherRows = 64;
 __global__ void __launch_bounds__(kThreads)
 k_gather_rows(const uint32_t* __restrict__ src, uint64_t src_stride, uint32_t* __restrict__ dst, uint64_t dst_stride,
               const uint32_t* __restrict__ idx, uint64_t rows, uint64_t n_src, uint32_t words) {
-    const uint64_t total = rows * words;
-    for (uint64_t t = uint64_t(blockIdx.x) * kThreads + threadIdx.x; t < total; t += uint64_t(gridDim.x) * kThreads) {
-        const uint64_t r = t / words, w = t % words;
-        const uint32_t q = idx[r];
-        dst[r * dst_stride + w] = q < n_src ? src[uint64_t(q) * src_stride + w] : 0u;
+    const uint64_t chunks = (rows + kGatherRows - 1) / kGatherRows;
+    for (uint64_t c = blockIdx.x; c < chunks; c += gridDim.x) {
+        const uint64_t r0 = c * kGatherRows;
+        const uint32_t nr = uint32_t(rows - r0 < kGatherRows ? rows - r0 : kGatherRows);
+        const uint32_t total = nr * words;
+        for (uint32_t t = threadIdx.x; t < total; t += kThreads) {
+            const uint32_t rr = t / words, w = t - rr * words;
+            const uint32_t q = idx[r0 + rr];
+            dst[(r0 + rr) * dst_stride + w] = q < n_src ? src[uint64_t(q) * src_stride + w] : 0u;
+        }
     }
 }
 
@@ -365,7 +374,8 @@ hipError_t launch_relabel(const uint32_t* perm, const uint32_t* pcol, uint32_t* 
 hipError_t launch_gather_rows(const void* src, uint64_t src_stride_words, void* dst, uint64_t dst_stride_words,
                               const uint32_t* idx, uint64_t rows, uint64_t n_src, uint32_t words, hipStream_t s) {
     if (!rows || !words) return hipSuccess;
-    k_gather_rows<<<grid_for(rows * words, kThreads, 8192), kThreads, 0, s>>>(
+    if (words > (uint32_t(1) << 24)) return hipErrorInvalidValue;  // 64 * words must fit 32 bits
+    k_gather_rows<<<grid_for((rows + kGatherRows - 1) / kGatherRows, 1, 16384), kThreads, 0, s>>>(
         static_cast<const uint32_t*>(src), src_stride_words, static_cast<uint32_t*>(dst), dst_stride_words, idx, rows,
         n_src, words);
     return hipGetLastError();
