@@ -68,6 +68,22 @@ struct LayerState {
     int width() const { return heads * dim; }
 };
 
+// Split rows: rows of in-degree >= min are cut into chunks of `chunk` edges
+// on separate waves.  Each aggregation family has its own plan; the values
+// below were measured best on the 64.3M-edge power-law graph
+// (100 -> 8x32 -> 8x32 -> 1x47): the sum form keeps many short chunks, the
+// one-row-per-wave 8-head kernel fewer, longer ones, and the one-head kernel
+// (8 rows per wave) splits only its heaviest rows.
+enum { kPlanAf = 0, kPlanVec = 1, kPlanOne = 2, kPlans = 3 };
+constexpr uint32_t kPlanMin[kPlans] = {1024, 1536, 2048};
+constexpr uint32_t kPlanChunk[kPlans] = {256, 512, 1024};
+struct SplitPlan {
+    uint32_t min = 0, chunk = 0;
+    RowBins bins;        // split_begin: first split row (sorted position)
+    SplitTable table;
+    DevBuf k, first, mchunk, part, counter;
+};
+
 }  // namespace
 
 struct gatgpu_ctx {
@@ -99,10 +115,9 @@ struct gatgpu_ctx {
     // options (in-degree thresholds)
     uint32_t small_max = 0;          // rows <= this share a wave (0: off)
     uint32_t block_min = 512;        // rows >= this take a block
-    uint32_t split_min = 1024;         // rows >= this are split into chunks
-    uint32_t split_chunk = 256;        // edges per chunk of a split row
-    DevBuf split_k, split_first, mchunk, part, counter;
-    SplitTable split;
+    uint32_t split_min = 0;            // user option: rows >= this are split (0: per-kernel defaults)
+    uint32_t split_chunk = 0;          // user option: edges per chunk (0: per-kernel defaults)
+    SplitPlan plans[kPlans];
     hipEvent_t ev[16] = {};
     int cus = 256;  // compute units of the device
 };
@@ -142,60 +157,71 @@ int bind(gatgpu_ctx* c) {
 
 // Sorted-position boundaries of the degree bins.
 int compute_bins(gatgpu_ctx* c) {
-    uint32_t thr[3] = {c->small_max, c->block_min ? c->block_min - 1 : 0,
-                       c->split_min ? c->split_min - 1 : 0};
+    // Thresholds: shared-wave bin, block bin, then each plan's split degree.
+    uint32_t thr[2 + kPlans] = {c->small_max, c->block_min ? c->block_min - 1 : 0};
+    for (int q = 0; q < kPlans; ++q) {
+        SplitPlan& P = c->plans[q];
+        P.min = c->split_min ? c->split_min : kPlanMin[q];
+        P.chunk = c->split_chunk ? c->split_chunk : kPlanChunk[q];
+        thr[2 + q] = P.min - 1;
+    }
     // small (0) disables the shared-wave bin; block_min 0 means every row takes a block.
-    HIPCHECK(c, c->small.ensure(64));
-    // small[]: [0,4) max degree, [8,16) neighbor steps, [16,28) thresholds, [32,56) positions
+    HIPCHECK(c, c->small.ensure(128));
+    // small[]: [0,4) max degree, [8,16) neighbor steps, [16,36) thresholds, [40,80) positions
     uint32_t* dthr = reinterpret_cast<uint32_t*>(c->small.as<char>() + 16);
-    uint64_t* dpos = reinterpret_cast<uint64_t*>(c->small.as<char>() + 32);
+    uint64_t* dpos = reinterpret_cast<uint64_t*>(c->small.as<char>() + 40);
     HIPCHECK(c, hipMemcpyAsync(dthr, thr, sizeof(thr), hipMemcpyHostToDevice, c->stream));
-    HIPCHECK(c, launch_count_le(c->sorted_deg, c->n, dthr, 3, dpos, c->stream));
-    uint64_t pos[3];
+    HIPCHECK(c, launch_count_le(c->sorted_deg, c->n, dthr, 2 + kPlans, dpos, c->stream));
+    uint64_t pos[2 + kPlans];
     HIPCHECK(c, hipMemcpyAsync(pos, dpos, sizeof(pos), hipMemcpyDeviceToHost, c->stream));
     HIPCHECK(c, hipStreamSynchronize(c->stream));
     RowBins b;
     b.n = c->n;
     b.small_end = c->small_max ? pos[0] : 0;
     b.block_begin = c->block_min ? pos[1] : 0;
-    b.split_begin = c->split_min ? pos[2] : 0;
     if (b.block_begin < b.small_end) b.block_begin = b.small_end;
-    if (b.split_begin < b.block_begin) b.split_begin = b.block_begin;
     c->bins = b;
-    // Chunk table of the split rows, heaviest row first.
-    const uint64_t nsplit = b.n - b.split_begin;
-    std::vector<uint64_t> prow(nsplit + 1);
-    if (nsplit)
-        HIPCHECK(c, hipMemcpy(prow.data(), c->prow.as<uint64_t>() + b.split_begin, (nsplit + 1) * 8,
-                              hipMemcpyDeviceToHost));
-    std::vector<uint32_t> ck, cf;
-    for (uint64_t q = nsplit; q-- > 0;) {
-        const uint64_t deg = prow[q + 1] - prow[q];
-        const uint64_t nch = (deg + c->split_chunk - 1) / c->split_chunk;
-        const uint32_t first = uint32_t(ck.size());
-        for (uint64_t t = 0; t < nch; ++t) {
-            ck.push_back(uint32_t(b.split_begin + q));
-            cf.push_back(first);
+    std::vector<uint64_t> prow;
+    for (int q = 0; q < kPlans; ++q) {
+        SplitPlan& P = c->plans[q];
+        P.bins = b;
+        P.bins.split_begin = pos[2 + q] < b.block_begin ? b.block_begin : pos[2 + q];
+        // Chunk table of the split rows, heaviest row first.
+        const uint64_t split_begin = P.bins.split_begin;
+        const uint64_t nsplit = b.n - split_begin;
+        prow.resize(nsplit + 1);
+        if (nsplit)
+            HIPCHECK(c, hipMemcpy(prow.data(), c->prow.as<uint64_t>() + split_begin, (nsplit + 1) * 8,
+                                  hipMemcpyDeviceToHost));
+        std::vector<uint32_t> ck, cf;
+        for (uint64_t r = nsplit; r-- > 0;) {
+            const uint64_t deg = prow[r + 1] - prow[r];
+            const uint64_t nch = (deg + P.chunk - 1) / P.chunk;
+            const uint32_t first = uint32_t(ck.size());
+            for (uint64_t t = 0; t < nch; ++t) {
+                ck.push_back(uint32_t(split_begin + r));
+                cf.push_back(first);
+            }
         }
-    }
-    SplitTable& t = c->split;
-    t = SplitTable{};
-    t.chunks = ck.size();
-    t.chunk_edges = c->split_chunk;
-    if (t.chunks) {
-        HIPCHECK(c, c->split_k.ensure(ck.size() * 4));
-        HIPCHECK(c, c->split_first.ensure(cf.size() * 4));
-        HIPCHECK(c, c->mchunk.ensure(ck.size() * 8 * 4));
-        HIPCHECK(c, c->part.ensure(ck.size() * (8 * 128 + 8) * 4));  // largest partial: aggregate-first U
-        HIPCHECK(c, c->counter.ensure(ck.size() * 4));
-        HIPCHECK(c, hipMemcpy(c->split_k.p, ck.data(), ck.size() * 4, hipMemcpyHostToDevice));
-        HIPCHECK(c, hipMemcpy(c->split_first.p, cf.data(), cf.size() * 4, hipMemcpyHostToDevice));
-        HIPCHECK(c, hipMemset(c->counter.p, 0, ck.size() * 4));
-        t.chunk_k = c->split_k.as<uint32_t>();
-        t.chunk_first = c->split_first.as<uint32_t>();
-        t.mchunk = c->mchunk.as<float>();
-        t.part = c->part.as<float>();
-        t.counter = c->counter.as<uint32_t>();
+        SplitTable& t = P.table;
+        t = SplitTable{};
+        t.chunks = ck.size();
+        t.chunk_edges = P.chunk;
+        if (t.chunks) {
+            HIPCHECK(c, P.k.ensure(ck.size() * 4));
+            HIPCHECK(c, P.first.ensure(cf.size() * 4));
+            HIPCHECK(c, P.mchunk.ensure(ck.size() * 8 * 4));
+            HIPCHECK(c, P.part.ensure(ck.size() * (8 * 128 + 8) * 4));  // largest partial: aggregate-first U
+            HIPCHECK(c, P.counter.ensure(ck.size() * 4));
+            HIPCHECK(c, hipMemcpy(P.k.p, ck.data(), ck.size() * 4, hipMemcpyHostToDevice));
+            HIPCHECK(c, hipMemcpy(P.first.p, cf.data(), cf.size() * 4, hipMemcpyHostToDevice));
+            HIPCHECK(c, hipMemset(P.counter.p, 0, ck.size() * 4));
+            t.chunk_k = P.k.as<uint32_t>();
+            t.chunk_first = P.first.as<uint32_t>();
+            t.mchunk = P.mchunk.as<float>();
+            t.part = P.part.as<float>();
+            t.counter = P.counter.as<uint32_t>();
+        }
     }
     return GATGPU_OK;
 }
@@ -364,14 +390,15 @@ int run_layer_af(gatgpu_ctx* c, int l, bool hidden, const float* src32, const ui
         a.outbf = hidden ? Ls.outbf.as<uint16_t>() : nullptr;
         a.n = n;
         a.e = c->e;
-        a.rows = c->bins.split_begin;
-        a.chunks = c->split.chunks;
-        a.chunk_k = c->split.chunk_k;
-        a.chunk_first = c->split.chunk_first;
-        a.chunk_edges = c->split.chunk_edges;
-        a.mchunk = c->split.mchunk;
-        a.part = c->split.part;
-        HIPCHECK(c, launch_aggregate_afsum(a, c->split, c->stream, c->cus));
+        const SplitPlan& P = c->plans[kPlanAf];
+        a.rows = P.bins.split_begin;
+        a.chunks = P.table.chunks;
+        a.chunk_k = P.table.chunk_k;
+        a.chunk_first = P.table.chunk_first;
+        a.chunk_edges = P.table.chunk_edges;
+        a.mchunk = P.table.mchunk;
+        a.part = P.table.part;
+        HIPCHECK(c, launch_aggregate_afsum(a, P.table, c->stream, c->cus));
     } else {
     AfArgs a{};
     a.prow = c->prow.as<uint64_t>();
@@ -393,15 +420,16 @@ int run_layer_af(gatgpu_ctx* c, int l, bool hidden, const float* src32, const ui
     a.outbf = hidden ? Ls.outbf.as<uint16_t>() : nullptr;
     a.n = n;
     a.e = c->e;
-    a.rows = c->bins.split_begin;
+    const SplitPlan& P = c->plans[kPlanAf];
+    a.rows = P.bins.split_begin;
     a.tiles = (a.rows + 31) / 32;
-    a.chunks = c->split.chunks;
-    a.chunk_k = c->split.chunk_k;
-    a.chunk_first = c->split.chunk_first;
-    a.chunk_edges = c->split.chunk_edges;
-    a.mchunk = c->split.mchunk;
-    a.part = c->split.part;
-    a.counter = c->split.counter;
+    a.chunks = P.table.chunks;
+    a.chunk_k = P.table.chunk_k;
+    a.chunk_first = P.table.chunk_first;
+    a.chunk_edges = P.table.chunk_edges;
+    a.mchunk = P.table.mchunk;
+    a.part = P.table.part;
+    a.counter = P.table.counter;
     a.b1 = dataflow == GATGPU_TFS_B1;
     a.fixp = fixed ? Ls.fixp.as<float>() : nullptr;
     a.fixden = fixed ? Ls.fixden.as<float>() : nullptr;
@@ -592,11 +620,15 @@ int run_layer(gatgpu_ctx* c, int l, int precision, int dataflow, bool hidden, co
     a.ar = Ls.ar.as<float>();
     const bool direct_orig = orig_out && a.out32 && !fixed && !aggregate_vec_supported(a) && aggregate_k1_supported(a);
     if (direct_orig) a.out_perm = c->perm;
+    // The one-head kernel takes its own split plan; the 8-head, generic and
+    // fixed-p kernels the 8-head one.
+    const SplitPlan& P = c->plans[!fixed && !aggregate_vec_supported(a) && aggregate_k1_supported(a) ? kPlanOne
+                                                                                                    : kPlanVec];
     if (fixed)
-        HIPCHECK(c, launch_aggregate_fixed(a, Ls.fixp.as<float>(), Ls.fixden.as<float>(), c->bins, c->split,
+        HIPCHECK(c, launch_aggregate_fixed(a, Ls.fixp.as<float>(), Ls.fixden.as<float>(), P.bins, P.table,
                                            c->stream));
     else
-        HIPCHECK(c, launch_aggregate_tf(a, c->bins, c->split, c->stream));
+        HIPCHECK(c, launch_aggregate_tf(a, P.bins, P.table, c->stream));
     if (ev_base >= 0) HIPCHECK(c, hipEventRecord(c->ev[ev_base + 3], c->stream));
     Ls.ran = true;
     Ls.precision = precision;
@@ -998,12 +1030,11 @@ int gatgpu_set_option(gatgpu_ctx* c, int key, int64_t value) {
     if (value < 0 || value > int64_t(UINT32_MAX)) return fail(c, GATGPU_EINVAL, "option value out of range");
     switch (key) {
         case GATGPU_OPT_BLOCK_ROW_MIN_DEGREE: c->block_min = uint32_t(value); break;
-        case GATGPU_OPT_SPLIT_ROW_MIN_DEGREE:
-            if (value < 1) return fail(c, GATGPU_EINVAL, "split threshold must be >= 1 edge");
+        case GATGPU_OPT_SPLIT_ROW_MIN_DEGREE:  // 0: the per-kernel defaults
             c->split_min = uint32_t(value);
             break;
-        case GATGPU_OPT_SPLIT_CHUNK_EDGES:
-            if (value < 64) return fail(c, GATGPU_EINVAL, "split chunk must be >= 64 edges");
+        case GATGPU_OPT_SPLIT_CHUNK_EDGES:  // 0: the per-kernel defaults
+            if (value != 0 && value < 64) return fail(c, GATGPU_EINVAL, "split chunk must be >= 64 edges");
             c->split_chunk = uint32_t(value);
             break;
         case GATGPU_OPT_SMALL_ROW_MAX_DEGREE: c->small_max = uint32_t(value); break;

@@ -106,8 +106,13 @@ typedef struct gatgpu_times {
 /* Options (gatgpu_set_option).  Thresholds are in-degrees. */
 enum {
     GATGPU_OPT_BLOCK_ROW_MIN_DEGREE = 1, /* rows at/above use a block per row  */
-    GATGPU_OPT_SPLIT_ROW_MIN_DEGREE = 2, /* rows at/above are split over blocks */
-    GATGPU_OPT_SPLIT_CHUNK_EDGES = 3,    /* edges per block for split rows      */
+    GATGPU_OPT_SPLIT_ROW_MIN_DEGREE = 2, /* rows at/above are split over waves
+                                            (default per kernel: 1024 sum form,
+                                            1536 8-head, 2048 one-head; a value
+                                            applies to all, 0 restores them)  */
+    GATGPU_OPT_SPLIT_CHUNK_EDGES = 3,    /* edges per split chunk (default per
+                                            kernel: 256, 512, 1024; a value
+                                            >= 64 applies to all, 0 restores) */
     GATGPU_OPT_SMALL_ROW_MAX_DEGREE = 4  /* rows at/below share one wave        */
 };
 

@@ -18,8 +18,9 @@ FP32_MAX_ABS = 1e-4
 BF16_REL_L2 = 1e-2
 
 
-DEFAULT_OPTIONS = {gatgpu.OPT_BLOCK_ROW_MIN_DEGREE: 512, gatgpu.OPT_SPLIT_ROW_MIN_DEGREE: 1024,
-                   gatgpu.OPT_SPLIT_CHUNK_EDGES: 256}
+# 0 for the split options restores the per-kernel split plans.
+DEFAULT_OPTIONS = {gatgpu.OPT_BLOCK_ROW_MIN_DEGREE: 512, gatgpu.OPT_SPLIT_ROW_MIN_DEGREE: 0,
+                   gatgpu.OPT_SPLIT_CHUNK_EDGES: 0}
 # Schedules that route the small graphs' rows through every kernel variant:
 # default, every row a block (generic path), rows >= 16 split into 64-edge chunks.
 SCHEDULES = [{}, {gatgpu.OPT_BLOCK_ROW_MIN_DEGREE: 1},
@@ -364,6 +365,9 @@ def test_error_codes(gpu_ctx):
         assert err.value.code == gatgpu.EINVAL
     with pytest.raises(gatgpu.GatGpuError) as err:
         gpu_ctx.set_layer(3, p)
+    assert err.value.code == gatgpu.EINVAL
+    with pytest.raises(gatgpu.GatGpuError) as err:  # split chunks of at least 64 edges (0: per-kernel plans)
+        gpu_ctx.set_option(gatgpu.OPT_SPLIT_CHUNK_EDGES, 32)
     assert err.value.code == gatgpu.EINVAL
     ctx2 = gatgpu.Context(0)
     with pytest.raises(gatgpu.GatGpuError) as err:
