@@ -19,7 +19,9 @@
 // Work split: one wave per 32-row tile, 8 waves per workgroup, persistent
 // workgroups that copy their group's packed W into LDS once.  Output features
 // are cut into groups of up to 8 blocks of 32; the last group also carries the
-// L/R block.
+// L/R block.  Where W does not fit LDS (several groups, or one group of many
+// k steps) the wide path keeps each tile's input in registers and streams W
+// through LDS instead.
 #include "internal.hpp"
 
 namespace gatgpu {
@@ -284,6 +286,161 @@ __global__ void __launch_bounds__(kThreads) k_proj_fast(ProjArgs a) {
     }
 }
 
+// Wide path: several output groups (more than 8 head blocks), or a group
+// whose W fragments exceed LDS (e.g. 512 -> 8 x 64: 32 k steps x 17 blocks).
+// Each wave keeps the whole input of its 32-row tile in registers (KS B
+// fragments) and the block streams W^T one 32-feature output block at a time
+// (KS fragments, KS KB) through a two-slot LDS ring its waves share: X is
+// read from HBM once, each output block's fragments once per block from L2,
+// and every output block (head blocks, then the L/R block) leaves straight
+// from the accumulators.  The MFMA chain per block runs k steps in the order
+// of the other paths, so Z and L/R carry the same bits.
+constexpr int kWideThreads = 256;
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+constexpr int kWideWaves = kWideThreads / kWave;
+
+template <int KS, bool F32IN>
+__global__ void __launch_bounds__(kWideThreads) k_proj_wide(ProjArgs a) {
+    extern __shared__ u32x4 ring[];  // [2][KS][kWave]
+    constexpr int kFrags = KS * kWave;
+    constexpr int kPer = (kFrags + kWideThreads - 1) / kWideThreads;
+    const int w = threadIdx.x / kWave, l = threadIdx.x % kWave;
+    const int half = l / 32, col = l % 32;
+    const uint64_t row = (uint64_t(blockIdx.x) * kWideWaves + w) * 32 + col;
+    // Lanes past n recompute row n - 1 and store its own values to it.
+    const uint64_t rs = row < a.n ? row : a.n - 1;
+    bf16x8 xr[KS];
+    if constexpr (F32IN) {
+        // FP32 rows rounded to bf16 here (the convert stage, common.cpp:80-93,
+        // fused); features >= in are zeroed, and the buffer's 16 floats of
+        // padding keep the last row's tail loads inside it.
+        const float* p = a.x32 + rs * a.xs + 8 * half;
+        uint4 raw[KS][2];
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+            raw[ks][0] = *reinterpret_cast<const uint4*>(p + 16 * ks);
+            raw[ks][1] = *reinterpret_cast<const uint4*>(p + 16 * ks + 4);
+        }
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+            const int f0 = 16 * ks + 8 * half;
+            const uint32_t e[8] = {raw[ks][0].x, raw[ks][0].y, raw[ks][0].z, raw[ks][0].w,
+                                   raw[ks][1].x, raw[ks][1].y, raw[ks][1].z, raw[ks][1].w};
+            uint32_t w4[4];
+#pragma unroll
+            for (int x = 0; x < 4; ++x)
+                w4[x] = bf16x2(f0 + 2 * x < a.in ? __builtin_bit_cast(float, e[2 * x]) : 0.0f,
+                               f0 + 2 * x + 1 < a.in ? __builtin_bit_cast(float, e[2 * x + 1]) : 0.0f);
+            xr[ks] = __builtin_bit_cast(bf16x8, make_uint4(w4[0], w4[1], w4[2], w4[3]));
+        }
+    } else {
+        const uint16_t* p = a.x + rs * a.xs + 8 * half;
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) xr[ks] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(p + 16 * ks));
+    }
+    // Output block ob: head block ob (group ob / 8, block ob % 8), then the
+    // L/R block, which sits after the head blocks of the last group.
+    const int nob = a.head_blocks + 1;
+    const int last_g = a.groups - 1;
+    u32x4 st[kPer];
+    auto fetch = [&](int ob) {
+        const int g = ob < a.head_blocks ? ob / 8 : last_g;
+        const int b = ob < a.head_blocks ? ob % 8 : a.head_blocks - 8 * last_g;
+        const u32x4* src = reinterpret_cast<const u32x4*>(a.wpk) + (size_t(g) * KS * a.nmb + b) * kWave;
+#pragma unroll
+        for (int i = 0; i < kPer; ++i) {
+            const int q = threadIdx.x + i * kWideThreads;
+            if (kFrags % kWideThreads == 0 || q < kFrags) st[i] = src[size_t(q / kWave) * a.nmb * kWave + q % kWave];
+        }
+    };
+    auto put = [&](int slot) {
+#pragma unroll
+        for (int i = 0; i < kPer; ++i) {
+            const int q = threadIdx.x + i * kWideThreads;
+            if (kFrags % kWideThreads == 0 || q < kFrags) ring[slot * kFrags + q] = st[i];
+        }
+    };
+    fetch(0);
+    put(0);
+    // The tile's input is complete before the loop, so the only loads in
+    // flight inside it are the next block's fragments (waited for after the
+    // MFMAs, not before them).
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) asm volatile("" ::"v"(xr[ks]));
+    __syncthreads();
+    for (int ob = 0; ob < nob; ++ob) {
+        const int cur = ob & 1;
+        const bool more = ob + 1 < nob;
+        if (more) fetch(ob + 1);  // lands in registers while this block multiplies
+        f32x16 acc;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[r] = 0.0f;
+        const u32x4* wk = ring + cur * kFrags + l;
+        // Fragments read four k steps ahead of their MFMA.
+        constexpr int kAhead = KS < 4 ? KS : 4;
+        u32x4 fr[kAhead];
+#pragma unroll
+        for (int ks = 0; ks < kAhead; ++ks) fr[ks] = wk[ks * kWave];
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+            const u32x4 av = fr[ks % kAhead];
+            if (ks + kAhead < KS) fr[ks % kAhead] = wk[(ks + kAhead) * kWave];
+            acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, av), xr[ks], acc, 0, 0, 0);
+        }
+        // Keep that order in the schedule: kAhead LDS reads, then one MFMA and
+        // one read per k step.
+        __builtin_amdgcn_sched_group_barrier(0x100, kAhead, 0);
+#pragma unroll
+        for (int ks = 0; ks + kAhead < KS; ++ks) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        }
+        __builtin_amdgcn_sched_group_barrier(0x008, kAhead, 0);
+        if (ob < a.head_blocks) {
+            // Permuted packing: lane (half, col) holds features 32 ob + 16 half + {0..15}.
+#pragma unroll
+            for (int q8 = 0; q8 < 2; ++q8) {
+                const int f0 = 32 * ob + 16 * half + 8 * q8;
+                if (f0 < a.width) {
+                    uint32_t w4[4];
+#pragma unroll
+                    for (int x = 0; x < 4; ++x) w4[x] = bf16x2(acc[8 * q8 + 2 * x], acc[8 * q8 + 2 * x + 1]);
+                    *reinterpret_cast<uint4*>(a.z + rs * a.zs + f0) = make_uint4(w4[0], w4[1], w4[2], w4[3]);
+                }
+            }
+        } else {
+            // L/R block: lane half h4 holds heads 4 h4 + {0..3} of each quarter
+            // (L hi, R hi, L lo, R lo) in registers {0..3}, {4..7}, {8..11}, {12..15}.
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int h = 4 * half + q;
+                if (h < a.heads) {
+                    const float rv = acc[4 + q] + acc[12 + q];
+                    a.left[rs * a.heads + h] = acc[q] + acc[8 + q];
+                    a.right[rs * a.heads + h] = rv;
+                    if (a.r_in_z) *reinterpret_cast<float*>(a.z + rs * a.zs + a.r_off + 2 * h) = rv;
+                }
+            }
+        }
+        if (more) put(cur ^ 1);  // the slot every wave finished reading before the last barrier
+        __syncthreads();
+    }
+}
+
+template <int KS, bool F32IN>
+hipError_t launch_wide_io(const ProjArgs& a, hipStream_t s) {
+    const size_t lds = size_t(2) * KS * kWave * sizeof(uint4);
+    if (lds > 64 * 1024) {
+        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_proj_wide<KS, F32IN>),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, int(lds));
+        if (e != hipSuccess) return e;
+    }
+    const uint64_t blocks = (a.tiles + kWideWaves - 1) / kWideWaves;
+    if (blocks < 1 || blocks > 0x7fffffffu) return hipErrorInvalidValue;
+    k_proj_wide<KS, F32IN><<<dim3(uint32_t(blocks)), kWideThreads, lds, s>>>(a);
+    return hipGetLastError();
+}
+
 template <int KS, int HB, bool F32IN, bool FULL>
 hipError_t launch_fast_io(const ProjArgs& a, hipStream_t s, int cus) {
     const size_t lds = size_t(KS) * (HB + 1) * kWave * sizeof(uint4) + (FULL ? 256 * sizeof(float) : 0);
@@ -366,6 +523,24 @@ int proj_blocks_per_group(int width) {
     return need <= 2 ? 2 : need <= 3 ? 3 : need <= 5 ? 5 : 9;
 }
 
+// Wide path: 8, 16, 24 or 32 k steps where the fast path does not apply and
+// there are several output groups or one group's fragments exceed LDS.
+bool wide_supported_impl(const ProjArgs& a) {
+    const bool ks_ok = a.ksteps == 8 || a.ksteps == 16 || a.ksteps == 24 || a.ksteps == 32;
+    const size_t group_lds = size_t(a.ksteps) * a.nmb * kWave * sizeof(uint4);
+    return ks_ok && a.n > 0 && !a.r_from_z && !fast_supported_impl(a) && (a.groups > 1 || group_lds > 160 * 1024);
+}
+
+hipError_t launch_wide(const ProjArgs& a, hipStream_t s) {
+    switch (a.ksteps) {
+        case 8: return a.x32 ? launch_wide_io<8, true>(a, s) : launch_wide_io<8, false>(a, s);
+        case 16: return a.x32 ? hipErrorInvalidValue : launch_wide_io<16, false>(a, s);
+        case 24: return a.x32 ? hipErrorInvalidValue : launch_wide_io<24, false>(a, s);
+        case 32: return a.x32 ? hipErrorInvalidValue : launch_wide_io<32, false>(a, s);
+        default: return hipErrorInvalidValue;
+    }
+}
+
 bool projection_fast_path(const ProjArgs& a) { return fast_supported_impl(a); }
 
 bool r_from_z_supported(const ProjArgs& a) {
@@ -374,12 +549,15 @@ bool r_from_z_supported(const ProjArgs& a) {
 
 // The FP32-input form holds 32 bytes per k step; at 16 k steps and 8 head
 // blocks that no longer fits the registers.
+// The wide path takes it at 8 k steps (the raw rows and their bf16 fragments
+// both fit the registers).
 bool projection_fp32_input(const ProjArgs& a) {
-    return fast_supported_impl(a) && (a.ksteps <= 8 || a.head_blocks <= 2);
+    return (fast_supported_impl(a) && (a.ksteps <= 8 || a.head_blocks <= 2)) ||
+           (wide_supported_impl(a) && a.ksteps == 8);
 }
 
 hipError_t launch_projection_mfma(const ProjArgs& a, hipStream_t s, int cus) {
-    if (a.x32 && !fast_supported_impl(a)) return hipErrorInvalidValue;  // FP32 input needs the fast path
+    if (a.x32 && !projection_fp32_input(a)) return hipErrorInvalidValue;
     if (fast_supported_impl(a)) {
         switch (a.head_blocks) {
             case 0: return launch_fast_ks<0>(a, s, cus);
@@ -388,6 +566,7 @@ hipError_t launch_projection_mfma(const ProjArgs& a, hipStream_t s, int cus) {
             default: return launch_fast_ks<8>(a, s, cus);
         }
     }
+    if (wide_supported_impl(a)) return launch_wide(a, s);
     switch (a.nmb) {
         case 2: return launch_nmb<2>(a, s, cus);
         case 3: return launch_nmb<3>(a, s, cus);

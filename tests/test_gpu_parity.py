@@ -376,7 +376,8 @@ def test_error_codes(gpu_ctx):
     ctx2.close()
 
 
-@pytest.mark.parametrize("D,K,d", [(128, 8, 32), (100, 8, 32), (256, 8, 32), (256, 1, 47), (128, 8, 64), (33, 4, 40)])
+@pytest.mark.parametrize("D,K,d", [(128, 8, 32), (100, 8, 32), (256, 8, 32), (256, 1, 47), (128, 8, 64), (33, 4, 40),
+                                   (256, 8, 64), (384, 8, 64), (512, 8, 64), (512, 1, 64)])
 def test_bf16_projection_stages(gpu_ctx, D, K, d):
     """bf16 MFMA projection against R0 run on bf16-rounded X and W: Z within one
     bf16 ulp of RNE(FP32 Z) (accumulation order may flip a rounding), L from
