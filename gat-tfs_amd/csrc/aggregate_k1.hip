@@ -51,6 +51,7 @@ struct K1Args {
     float* part;
     uint32_t* counter;
     const uint32_t* operm;  // output row of sorted position k: operm[k] (null: the node index)
+    const float* ar;        // aR [W] when R is recomputed from the gathered rows
 };
 
 __device__ inline void unpack(const uint4& v, float (&f)[8]) {
@@ -122,12 +123,19 @@ __device__ inline void group_accumulate(uint64_t beg, uint64_t end, const uint32
 // accumulators and the denominator are rescaled by exp(m_old - m_new).  The
 // final m equals leaky(L + max R) bit for bit, because leaky and the addition
 // are monotone.
-template <class C>
+//
+// RZ: rows of exactly G * 8 = 64 bf16 features with no room for R.  R of each
+// gathered row is recomputed from it as the projection wrote it: lane sub
+// takes the FMA chain of its 8 features with aR (p_sub), and the group adds
+// ((p0 + p1) + (p2 + p3)) + ((p4 + p5) + (p6 + p7)) by xor shuffles, so every
+// lane gets the same bits as the R stage and each edge still fetches one line.
+template <class C, bool RZ>
 __device__ inline void group_online(uint64_t beg, uint64_t end, const uint32_t* __restrict__ pcol,
                                     const uint16_t* __restrict__ Z, int zs, int W, float Li, int gbase, int sub,
-                                    float (&acc)[C::VEC], float& dsum, float& m) {
+                                    const float (&arl)[C::VEC], float (&acc)[C::VEC], float& dsum, float& m) {
     static_assert(C::VEC == 8, "bf16 rows only");
-    const bool reader = sub * C::VEC < W || sub == C::G - 1;
+    static_assert(!RZ || C::G == 8, "R from Z needs the 8-lane reduction order");
+    const bool reader = RZ || sub * C::VEC < W || sub == C::G - 1;
     for (uint64_t base = beg; base < end; base += C::G) {
         const uint64_t e = base + sub;
         const uint32_t j = e < end ? pcol[e] : 0u;
@@ -144,9 +152,30 @@ __device__ inline void group_online(uint64_t beg, uint64_t end, const uint32_t* 
         float mb = -INFINITY;
 #pragma unroll
         for (int t = 0; t < C::G; ++t) {
-            const float r = __builtin_bit_cast(float, __shfl(raw[t].w, gbase + C::G - 1));
+            float r;
+            if constexpr (RZ) {
+                float f[C::VEC];
+                unpack(raw[t], f);
+                float pr = 0.0f;
+#pragma unroll
+                for (int x = 0; x < C::VEC; ++x) pr = __builtin_fmaf(f[x], arl[x], pr);
+                pr += __shfl_xor(pr, 1);
+                pr += __shfl_xor(pr, 2);
+                r = pr + __shfl_xor(pr, 4);
+            } else {
+                r = __builtin_bit_cast(float, __shfl(raw[t].w, gbase + C::G - 1));
+            }
             s[t] = t < cnt ? leaky(Li + r) : -INFINITY;
             mb = fmaxf(mb, s[t]);
+        }
+        if constexpr (RZ) {
+            // Unpack the rows again below rather than keep 8 unpacked rows live.
+#pragma unroll
+            for (int t = 0; t < C::G; ++t) {
+                uint32_t w0 = raw[t].x, w1 = raw[t].y, w2 = raw[t].z, w3 = raw[t].w;
+                asm volatile("" : "+v"(w0), "+v"(w1), "+v"(w2), "+v"(w3));
+                raw[t] = make_uint4(w0, w1, w2, w3);
+            }
         }
         const float mn = fmaxf(m, mb);
         const float sc = exp_w(m - mn);  // 0 on the first batch (m = -inf)
@@ -181,7 +210,10 @@ __device__ inline void store_row(uint32_t i, int W, int sub, const float (&acc)[
     }
 }
 
-template <class C, class ZT, bool ONE_PASS>
+// MODE 0: max pre-scan, then the accumulation pass (R from its own array);
+// 1: one online pass, R in the last four bytes of each Z row; 2: one online
+// pass, R recomputed from each Z row (one head of 64).
+template <class C, class ZT, int MODE>
 __global__ void __launch_bounds__(kThreads) k_agg_k1(K1Args<ZT> a) {
     const int w = threadIdx.x / kWave, lane = threadIdx.x % kWave;
     const int g = lane / C::G, sub = lane % C::G, gbase = g * C::G;
@@ -252,9 +284,12 @@ __global__ void __launch_bounds__(kThreads) k_agg_k1(K1Args<ZT> a) {
     if (i >= a.n || beg > end || end > a.e) return;
     const float Li = a.L[i];
     float Mi;
-    if constexpr (ONE_PASS) {
+    if constexpr (MODE > 0) {
+        float arl[C::VEC];
+#pragma unroll
+        for (int x = 0; x < C::VEC; ++x) arl[x] = MODE == 2 ? a.ar[sub * C::VEC + x] : 0.0f;
         float m = -INFINITY;
-        group_online<C>(beg, end, a.pcol, a.Z, a.zs, a.W, Li, gbase, sub, acc, dloc, m);
+        group_online<C, MODE == 2>(beg, end, a.pcol, a.Z, a.zs, a.W, Li, gbase, sub, arl, acc, dloc, m);
         Mi = end > beg ? m : 0.0f;
     } else {
         const float m = group_max<C>(beg, end, a.pcol, a.R, a.rs, sub);
@@ -279,7 +314,7 @@ hipError_t run(const AggArgs& g, const RowBins& bins, const SplitTable& t, hipSt
     const int rs = g.r_in_feat ? int(g.fstride * sizeof(ZT) / 4) : 1;
     K1Args<ZT> a{g.prow, g.pcol, g.perm, g.left, rptr, static_cast<const ZT*>(g.feat), g.heads * g.dim,
                  g.fstride, rs, g.hidden, g.mx, g.den, g.out32, g.outbf, g.n, g.e, bins.split_begin, t.chunks,
-                 t.chunk_k, t.chunk_first, t.chunk_edges, t.mchunk, t.part, t.counter, g.out_perm};
+                 t.chunk_k, t.chunk_first, t.chunk_edges, t.mchunk, t.part, t.counter, g.out_perm, g.ar};
     if (t.chunks) {
         hipError_t e = launch_split_prescan(g.prow, g.pcol, g.right, 1, t, g.e, s);
         if (e != hipSuccess) return e;
@@ -287,14 +322,20 @@ hipError_t run(const AggArgs& g, const RowBins& bins, const SplitTable& t, hipSt
     const uint64_t waves = t.chunks + (bins.split_begin + C::GPW - 1) / C::GPW;
     const dim3 grid(uint32_t((waves + kWavesPerBlock - 1) / kWavesPerBlock));
     if (!waves) return hipSuccess;
-    if constexpr (sizeof(ZT) == 2) {
+    if constexpr (sizeof(ZT) == 2 && G == 8) {
         if (g.r_in_feat) {
             // whole rows in one pass over their Z lines (R rides in the line)
-            k_agg_k1<C, ZT, true><<<grid, kThreads, 0, s>>>(a);
+            k_agg_k1<C, ZT, 1><<<grid, kThreads, 0, s>>>(a);
+            return hipGetLastError();
+        }
+        if (g.r_from_z) {
+            // whole rows in one pass, R recomputed from each line
+            if (!g.ar || g.dim != 64 || g.fstride != 64) return hipErrorInvalidValue;
+            k_agg_k1<C, ZT, 2><<<grid, kThreads, 0, s>>>(a);
             return hipGetLastError();
         }
     }
-    k_agg_k1<C, ZT, false><<<grid, kThreads, 0, s>>>(a);
+    k_agg_k1<C, ZT, 0><<<grid, kThreads, 0, s>>>(a);
     return hipGetLastError();
 }
 

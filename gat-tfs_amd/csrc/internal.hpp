@@ -153,7 +153,7 @@ struct ProjArgs {
     int r_off;           // bf16 offset of R in the z row when r_in_z (one head: zs - 2)
     uint16_t* xout;      // FP32 input, L/R only (head_blocks 0): also store the rounded
     int xouts;           // bf16 input rows, features [0, 16 ksteps), at xout[row * xouts]
-    bool r_from_z;       // 8 x 32 bf16: R = Z_bf16 . aR (the aggregation recomputes it)
+    bool r_from_z;       // bf16 8 x 32 or one head x 64: R = Z_bf16 . aR (the aggregation recomputes it)
     const float* ar;     // aR [256] when r_from_z
 };
 // R from the stored bf16 Z: the fast projection writes R = Z_bf16 . aR and
@@ -197,7 +197,7 @@ struct AggArgs {
     float* out32;    // [n][W] or null
     uint16_t* outbf; // [n][W] or null
     uint64_t n, e;           // nodes and CSR entries (bounds of perm/prow values)
-    bool r_from_z = false;   // bf16 8 x 32: recompute R = Z_bf16 . aR from the gathered rows
+    bool r_from_z = false;   // bf16 8 x 32 or one head x 64: recompute R = Z_bf16 . aR from the gathered rows
     const float* ar = nullptr;
     // Output row of sorted position k (one-head kernel only): out_perm[k]
     // instead of the node index perm[k].  Null: the node index.

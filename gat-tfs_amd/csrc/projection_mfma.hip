@@ -360,6 +360,11 @@ __global__ void __launch_bounds__(kWideThreads) k_proj_wide(ProjArgs a) {
             if (kFrags % kWideThreads == 0 || q < kFrags) ring[slot * kFrags + q] = st[i];
         }
     };
+    // One head of 64 with r_from_z: R = Z_bf16 . aR in the order the one-head
+    // aggregation recomputes it from a gathered row -- an FMA chain over each
+    // 8 features (p0..p7), then ((p0 + p1) + (p2 + p3)) + ((p4 + p5) + (p6 + p7)).
+    // Lane half 0 holds p0, p1 (block 0) and p4, p5 (block 1); half 1 the others.
+    float rlo = 0.0f, rhi = 0.0f;  // pair sums of head blocks 0 and 1
     fetch(0);
     put(0);
     // The tile's input is complete before the loop, so the only loads in
@@ -406,16 +411,32 @@ __global__ void __launch_bounds__(kWideThreads) k_proj_wide(ProjArgs a) {
 #pragma unroll
                     for (int x = 0; x < 4; ++x) w4[x] = bf16x2(acc[8 * q8 + 2 * x], acc[8 * q8 + 2 * x + 1]);
                     *reinterpret_cast<uint4*>(a.z + rs * a.zs + f0) = make_uint4(w4[0], w4[1], w4[2], w4[3]);
+                    if (a.r_from_z) {
+                        float t = 0.0f;
+#pragma unroll
+                        for (int x = 0; x < 4; ++x) {
+                            t = __builtin_fmaf(__builtin_bit_cast(float, w4[x] << 16), a.ar[f0 + 2 * x], t);
+                            t = __builtin_fmaf(__builtin_bit_cast(float, w4[x] & 0xffff0000u), a.ar[f0 + 2 * x + 1], t);
+                        }
+                        if (ob == 0) rlo = q8 == 0 ? t : rlo + t;
+                        else rhi = q8 == 0 ? t : rhi + t;
+                    }
                 }
             }
         } else {
+            float rz = 0.0f;
+            if (a.r_from_z) {
+                const float lo = rlo + __shfl_xor(rlo, 32);
+                const float hi = rhi + __shfl_xor(rhi, 32);
+                rz = lo + hi;
+            }
             // L/R block: lane half h4 holds heads 4 h4 + {0..3} of each quarter
             // (L hi, R hi, L lo, R lo) in registers {0..3}, {4..7}, {8..11}, {12..15}.
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
                 const int h = 4 * half + q;
                 if (h < a.heads) {
-                    const float rv = acc[4 + q] + acc[12 + q];
+                    const float rv = a.r_from_z ? rz : acc[4 + q] + acc[12 + q];
                     a.left[rs * a.heads + h] = acc[q] + acc[8 + q];
                     a.right[rs * a.heads + h] = rv;
                     if (a.r_in_z) *reinterpret_cast<float*>(a.z + rs * a.zs + a.r_off + 2 * h) = rv;
@@ -525,10 +546,18 @@ int proj_blocks_per_group(int width) {
 
 // Wide path: 8, 16, 24 or 32 k steps where the fast path does not apply and
 // there are several output groups or one group's fragments exceed LDS.
+bool wide_ks(const ProjArgs& a) {
+    return a.n > 0 && (a.ksteps == 8 || a.ksteps == 16 || a.ksteps == 24 || a.ksteps == 32);
+}
+
+// One head of exactly 64 (no room for R in the 128-byte row): the wide path
+// writes R = Z_bf16 . aR for the aggregation to recompute.
+bool rz_one_head(const ProjArgs& a) { return wide_ks(a) && a.heads == 1 && a.width == 64 && !a.r_in_z; }
+
 bool wide_supported_impl(const ProjArgs& a) {
-    const bool ks_ok = a.ksteps == 8 || a.ksteps == 16 || a.ksteps == 24 || a.ksteps == 32;
+    if (a.r_from_z) return rz_one_head(a);
     const size_t group_lds = size_t(a.ksteps) * a.nmb * kWave * sizeof(uint4);
-    return ks_ok && a.n > 0 && !a.r_from_z && !fast_supported_impl(a) && (a.groups > 1 || group_lds > 160 * 1024);
+    return wide_ks(a) && !fast_supported_impl(a) && (a.groups > 1 || group_lds > 160 * 1024);
 }
 
 hipError_t launch_wide(const ProjArgs& a, hipStream_t s) {
@@ -544,7 +573,8 @@ hipError_t launch_wide(const ProjArgs& a, hipStream_t s) {
 bool projection_fast_path(const ProjArgs& a) { return fast_supported_impl(a); }
 
 bool r_from_z_supported(const ProjArgs& a) {
-    return fast_supported_impl(a) && a.head_blocks == 8 && a.width == 256 && a.heads == 8 && !a.r_in_z;
+    return (fast_supported_impl(a) && a.head_blocks == 8 && a.width == 256 && a.heads == 8 && !a.r_in_z) ||
+           rz_one_head(a);
 }
 
 // The FP32-input form holds 32 bytes per k step; at 16 k steps and 8 head
@@ -552,12 +582,14 @@ bool r_from_z_supported(const ProjArgs& a) {
 // The wide path takes it at 8 k steps (the raw rows and their bf16 fragments
 // both fit the registers).
 bool projection_fp32_input(const ProjArgs& a) {
+    if (a.r_from_z && a.heads == 1) return rz_one_head(a) && a.ksteps == 8;
     return (fast_supported_impl(a) && (a.ksteps <= 8 || a.head_blocks <= 2)) ||
            (wide_supported_impl(a) && a.ksteps == 8);
 }
 
 hipError_t launch_projection_mfma(const ProjArgs& a, hipStream_t s, int cus) {
     if (a.x32 && !projection_fp32_input(a)) return hipErrorInvalidValue;
+    if (a.r_from_z && a.heads == 1) return rz_one_head(a) && a.ar ? launch_wide(a, s) : hipErrorInvalidValue;
     if (fast_supported_impl(a)) {
         switch (a.head_blocks) {
             case 0: return launch_fast_ks<0>(a, s, cus);

@@ -96,7 +96,7 @@ def test_boundary_shapes_fp32(gpu_ctx, D, K, d):
 
 
 @pytest.mark.parametrize("D,K,d", [(17, 8, 7), (128, 8, 32), (256, 1, 47), (33, 4, 40), (128, 8, 64),
-                                   (256, 8, 64)])
+                                   (256, 8, 64), (128, 1, 64), (512, 1, 64), (512, 8, 64)])
 def test_boundary_shapes_bf16_and_hidden(gpu_ctx, D, K, d):
     g = oracle.boundary_graph(D)
     p = oracle.boundary_param(D, K, d)
@@ -382,8 +382,9 @@ def test_bf16_projection_stages(gpu_ctx, D, K, d):
     """bf16 MFMA projection against R0 run on bf16-rounded X and W: Z within one
     bf16 ulp of RNE(FP32 Z) (accumulation order may flip a rounding), L from
     the hi/lo B_LR block within 1e-5 relative L2 of the FP32 dots of Z.  R the
-    same, except for 8 heads x 32 features, where R is the dot of the stored
-    bf16 Z row with a_r (the aggregation then needs no R gathers): that R is
+    same, except for 8 heads x 32 features and one head x 64, where R is the
+    dot of the stored bf16 Z row with a_r (the aggregation then needs no R
+    gathers): that R is
     checked against the float64 dot of the GPU's own Z stage to FP32
     summation accuracy, and against R0 to the bf16 rounding of Z."""
     w = inputs.WORKLOADS["smoke"]
@@ -413,7 +414,7 @@ def test_bf16_projection_stages(gpu_ctx, D, K, d):
     e = oracle.errors(r["left"], gpu_ctx.stage(0, "left"))
     assert e["relative_l2"] < 1e-5, ("left", e)
     right = gpu_ctx.stage(0, "right").astype(np.float64)
-    if (K, d) == (8, 32):
+    if (K, d) in ((8, 32), (1, 64)):
         terms = z.reshape(w.n, K, d) * p["ar"].astype(np.float64).reshape(K, d)
         want = terms.sum(axis=2)
         bound = 4 * d * 2.0 ** -24 * np.abs(terms).sum(axis=2) + 1e-30
