@@ -71,12 +71,19 @@ struct LayerState {
 // Split rows: rows of in-degree >= min are cut into chunks of `chunk` edges
 // on separate waves.  Each aggregation family has its own plan; the values
 // below were measured best on the 64.3M-edge power-law graph
-// (100 -> 8x32 -> 8x32 -> 1x47): the sum form keeps many short chunks, the
-// one-row-per-wave 8-head kernel fewer, longer ones, and the one-head kernel
-// (8 rows per wave) splits only its heaviest rows.
+// (100 -> 8x32 -> 8x32 -> 1x47, max in-degree 17 000): the sum form keeps
+// many short chunks, the one-row-per-wave 8-head kernel fewer, longer ones,
+// and the one-head kernel (8 rows per wave) splits only its heaviest rows.
+// Graphs with heavier rows scale a plan (chunk and min) by the smallest power
+// of two that keeps the heaviest row within kMaxChunksPerRow chunks: each
+// chunk reduces the maxima of all chunks of its row and the last one adds
+// all partial sums, so many chunks per row cost more than they balance.  On
+// the 100M-edge R-MAT graph (max in-degree 132 270) that gives 6144/2048
+// (8-head) and 4096/2048 (one head), the best of a measured sweep there.
 enum { kPlanAf = 0, kPlanVec = 1, kPlanOne = 2, kPlans = 3 };
 constexpr uint32_t kPlanMin[kPlans] = {1024, 1536, 2048};
 constexpr uint32_t kPlanChunk[kPlans] = {256, 512, 1024};
+constexpr uint64_t kMaxChunksPerRow = 96;
 struct SplitPlan {
     uint32_t min = 0, chunk = 0;
     RowBins bins;        // split_begin: first split row (sorted position)
@@ -159,10 +166,14 @@ int bind(gatgpu_ctx* c) {
 int compute_bins(gatgpu_ctx* c) {
     // Thresholds: shared-wave bin, block bin, then each plan's split degree.
     uint32_t thr[2 + kPlans] = {c->small_max, c->block_min ? c->block_min - 1 : 0};
+    uint32_t maxdeg = 0;  // degrees are sorted ascending
+    if (c->n) HIPCHECK(c, hipMemcpy(&maxdeg, c->sorted_deg + (c->n - 1), 4, hipMemcpyDeviceToHost));
     for (int q = 0; q < kPlans; ++q) {
         SplitPlan& P = c->plans[q];
-        P.min = c->split_min ? c->split_min : kPlanMin[q];
-        P.chunk = c->split_chunk ? c->split_chunk : kPlanChunk[q];
+        uint32_t f = 1;
+        while (uint64_t(kPlanChunk[q]) * f * kMaxChunksPerRow < maxdeg && f < (1u << 12)) f *= 2;
+        P.min = c->split_min ? c->split_min : kPlanMin[q] * f;
+        P.chunk = c->split_chunk ? c->split_chunk : kPlanChunk[q] * f;
         thr[2 + q] = P.min - 1;
     }
     // small (0) disables the shared-wave bin; block_min 0 means every row takes a block.

@@ -108,11 +108,14 @@ enum {
     GATGPU_OPT_BLOCK_ROW_MIN_DEGREE = 1, /* rows at/above use a block per row  */
     GATGPU_OPT_SPLIT_ROW_MIN_DEGREE = 2, /* rows at/above are split over waves
                                             (default per kernel: 1024 sum form,
-                                            1536 8-head, 2048 one-head; a value
+                                            1536 8-head, 2048 one-head, both
+                                            defaults doubled until the heaviest
+                                            row has <= 96 chunks; a value
                                             applies to all, 0 restores them)  */
     GATGPU_OPT_SPLIT_CHUNK_EDGES = 3,    /* edges per split chunk (default per
-                                            kernel: 256, 512, 1024; a value
-                                            >= 64 applies to all, 0 restores) */
+                                            kernel: 256, 512, 1024, scaled as
+                                            above; a value >= 64 applies to
+                                            all, 0 restores)                  */
     GATGPU_OPT_SMALL_ROW_MAX_DEGREE = 4  /* rows at/below share one wave        */
 };
 
