@@ -62,7 +62,7 @@ constexpr int kThreads = 512;
 constexpr int kWaves = kThreads / kWave;   // 8 = heads
 constexpr int kTile = 2 * kWaves;          // rows per block tile (hi + lo S)
 constexpr int kTileBf16 = 32;              // rows per block tile with one bf16 S
-constexpr int kMaxKS = 7;                  // k steps of 16 features: D_in <= 112
+constexpr int kMaxKS = 8;                  // k steps of 16 features: D_in <= 128
 constexpr int kRowWords = kXRStride / 2;   // 64 words of 4 bytes per XR row
 constexpr int kEPL = 4;                    // edges per lane and batch (batches of 4 kEPL edges)
 constexpr int kSB = 4;                     // super-blocks of 16 words per row
@@ -75,7 +75,7 @@ constexpr int kDenOff = 8 * 128;
 constexpr int kChunkThreads = 256;
 
 static_assert(32 <= int(kPcolPad), "an id request may read 31 entries past the row");
-static_assert(kRowWords == 16 * kSB && kXRFeat == 112, "XR row: 4 super-blocks, R in words 56..63");
+static_assert(kRowWords == 16 * kSB && kXRFeat == 112, "XR row: 4 super-blocks, R in words 56..63 (D <= 112)");
 
 __device__ inline float lane_f(float x, int lane) {
     return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), lane));
@@ -124,9 +124,12 @@ struct Mfma<4> {
 // by the caller ahead of time); each batch requests the next batch's ids the
 // same way (pcol is padded past e).  EXACT: s.m holds the exact row max
 // already (a chunk) and never moves.
-template <bool EXACT, int EPL = kEPL>
+// RSEP: the rows hold 128 input features and R comes from its own array
+// ([n][8], loaded by the head lanes beside the row words).
+template <bool EXACT, bool RSEP, int EPL = kEPL>
 __device__ inline void gather_sums(const uint32_t* __restrict__ pcol, const uint32_t* __restrict__ xr,
-                                   uint64_t beg, uint64_t end, int l, Sums& s, uint32_t ids, int id0) {
+                                   const float* __restrict__ R, uint64_t beg, uint64_t end, int l, Sums& s,
+                                   uint32_t ids, int id0) {
     constexpr int B = 4 * EPL;  // edges per batch
     if (beg >= end) return;
     const int g = l / 16, n = l % 16;
@@ -143,18 +146,21 @@ __device__ inline void gather_sums(const uint32_t* __restrict__ pcol, const uint
         // 32-bit byte offsets (n * 256 < 2^32 is checked at launch).
         const unsigned char* xb = reinterpret_cast<const unsigned char*>(xr);
         uint32_t raw[kSB][EPL];
+        float rsep[EPL];
 #pragma unroll
         for (int t = 0; t < EPL; ++t) {
             const uint32_t off = jl[t] * uint32_t(4 * kRowWords) + 4u * uint32_t(n);
 #pragma unroll
             for (int sb = 0; sb < kSB; ++sb) raw[sb][t] = *reinterpret_cast<const uint32_t*>(xb + off + 64 * sb);
+            if constexpr (RSEP) rsep[t] = head ? R[uint64_t(jl[t]) * 8 + n] : 0.0f;
         }
         // ---- head lanes: scores of their edges, batch max over the 4 k groups
         float sc[EPL];
         float mb = -INFINITY;
 #pragma unroll
         for (int t = 0; t < EPL; ++t) {
-            const float r = __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(int(raw[3][t]), 0x128, 0xF, 0xF, false));
+            const float r = RSEP ? rsep[t]
+                                 : __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(int(raw[3][t]), 0x128, 0xF, 0xF, false));
             sc[t] = (head && EPL * g + t < cnt) ? leaky(s.L + r) : -INFINITY;
             mb = fmaxf(mb, sc[t]);
         }
@@ -237,9 +243,13 @@ __device__ inline float total_den(float den) {
 // barrier of tile t - 1, which every wave reaches after projecting tile t - 2
 // from the same buffer).  Single-buffered tiles take a barrier before and
 // after the projection.
-template <int KS, bool HL, int TR>
+// DIM: head width, 32 or 64 (wave h then multiplies S_h by the two 32-column
+// blocks of W_h in turn).  KS = 8 (D_in > 112): R from its own array.
+template <int KS, bool HL, int TR, int DIM>
 __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) k_afs_tiles(AfsArgs a) {
     static_assert(TR == 16 || (TR == 32 && !HL), "16-row tiles, or 32-row tiles of one bf16");
+    static_assert(DIM == 32 || DIM == 64, "heads of 32 or 64");
+    constexpr bool RSEP = KS == 8;
     constexpr int RPW = TR / kWaves;          // rows per wave and tile
     constexpr bool DB = !HL && TR == 16;      // two alternating S buffers
     constexpr int BLK = TR * 32 + 16;         // bytes per (head, k step[, hi|lo]) block of S
@@ -316,7 +326,7 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4
             zero_sums(s);
             s.L = head ? Lr : 0.0f;
             s.m = s.mx = -INFINITY;
-            gather_sums<false>(a.pcol, a.xr, beg, end, l, s, ids, 32 * (rr % 2));
+            gather_sums<false, RSEP>(a.pcol, a.xr, a.R, beg, end, l, s, ids, 32 * (rr % 2));
             const float den = total_den(s.den);  // against the reference max s.m
             if (head && g == 0) {
                 // empty row: max 0, denominator 0 (ref_fp32.cpp:11); else the
@@ -334,13 +344,15 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4
                 // Element (head h, feature pair P = 16 sb + n) of tile row r sits at
                 // block (h, P / 8[, hl]) + 32 r + 4 (P % 8): a per-lane base plus a
                 // compile-time offset for each (q, sb, hl); block index
-                // ((h * 7 + ks) * 2 + hl) with hi + lo, (buf * 8 + h) * 7 + ks without.
-                unsigned char* base = slds + 32 * r + 4 * (n % 8) +
-                                      (HL ? 56 * g + 2 * (n / 8) : buf * 56 + 28 * g + n / 8) * BLK;
+                // ((h * kMaxKS + ks) * 2 + hl) with hi + lo, (buf * 8 + h) * kMaxKS + ks
+                // without.  (With KS <= 7 the words of R, 56..63, fall in k step 7.)
+                unsigned char* base =
+                    slds + 32 * r + 4 * (n % 8) +
+                    (HL ? 8 * kMaxKS * g + 2 * (n / 8) : buf * 8 * kMaxKS + 4 * kMaxKS * g + n / 8) * BLK;
 #pragma unroll
                 for (int sb = 0; sb < kSB; ++sb) {
                     const int ks = 2 * sb + n / 8;
-                    if (16 * sb + n >= kXRFeat / 2 || ks >= KS) continue;
+                    if (ks >= KS) continue;
 #pragma unroll
                     for (int q = 0; q < 4; ++q) {
                         const float s0 = s.d[2 * sb][q] * iq[q], s1 = s.d[2 * sb + 1][q] * iq[q];
@@ -348,34 +360,42 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4
                         if constexpr (HL) {
                             const uint32_t lw = bf16x2(s0 - __builtin_bit_cast(float, hw << 16),
                                                        s1 - __builtin_bit_cast(float, hw & 0xffff0000u));
-                            unsigned char* e = base + (14 * q + 4 * sb) * BLK;
+                            unsigned char* e = base + (2 * kMaxKS * q + 4 * sb) * BLK;
                             *reinterpret_cast<uint32_t*>(e) = hw;
                             *reinterpret_cast<uint32_t*>(e + BLK) = lw;
                         } else {
-                            *reinterpret_cast<uint32_t*>(base + (7 * q + 2 * sb) * BLK) = hw;
+                            *reinterpret_cast<uint32_t*>(base + (kMaxKS * q + 2 * sb) * BLK) = hw;
                         }
                     }
                 }
             }
         }
-        // W_h^T fragments of this wave's head (h = w; 1 KB per k step, L2
-        // resident), requested before the barrier.  A wave-uniform base plus a
-        // 32-bit lane offset, made opaque so that the addresses are formed here
-        // instead of being held across the gather.
+        // W_h^T fragments of this wave's head (h = w; 1 KB per k step and
+        // 32-column block, L2 resident), the first block's requested before
+        // the barrier.  A wave-uniform base plus a 32-bit lane offset, made
+        // opaque so that the addresses are formed here instead of being held
+        // across the gather.  Head block NBH h + b sits in group (NBH h + b) / 8,
+        // block (NBH h + b) % 8 of the packing.
+        constexpr int NBH = DIM / 32;
         bf16x8 wf[KS];
-        {
+        auto load_w = [&](int b) {
             uint32_t lo = uint32_t(l) * uint32_t(sizeof(uint4));
             asm volatile("" : "+v"(lo));
-            const unsigned char* wb = reinterpret_cast<const unsigned char*>(a.wpk) + uint64_t(w) * kWave * sizeof(uint4);
+            const int hb = NBH * w + b;
+            const unsigned char* wb = reinterpret_cast<const unsigned char*>(a.wpk) +
+                                      (uint64_t(hb / 8) * a.ksteps * a.nmb + hb % 8) * kWave * sizeof(uint4);
 #pragma unroll
             for (int ks = 0; ks < KS; ++ks)
                 wf[ks] = __builtin_bit_cast(
                     bf16x8, *reinterpret_cast<const uint4*>(wb + uint64_t(ks) * a.nmb * kWave * sizeof(uint4) + lo));
-        }
+        };
+        load_w(0);
         __syncthreads();
         // ---- wave h: the tile's S_h W_h.  B lane l reads tile row l % 16 (lanes
         // with l % 32 >= 16 repeat rows 0..15; their output columns are dropped).
-        {
+#pragma unroll
+        for (int b = 0; b < NBH; ++b) {
+            if (b > 0) load_w(b);
             const int h = w;
             f32x16 dh, dl;
 #pragma unroll
@@ -392,24 +412,25 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4
                     dl = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wf[ks], bl, dl, 0, 0, 0);
                 } else {
                     // even / odd k steps in two chains
-                    const bf16x8 b = __builtin_bit_cast(
+                    const bf16x8 bv = __builtin_bit_cast(
                         bf16x8, *reinterpret_cast<const uint4*>(slds + ((buf * 8 + h) * kMaxKS + ks) * BLK + boff));
-                    if (ks % 2 == 0) dh = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wf[ks], b, dh, 0, 0, 0);
-                    else dl = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wf[ks], b, dl, 0, 0, 0);
+                    if (ks % 2 == 0) dh = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wf[ks], bv, dh, 0, 0, 0);
+                    else dl = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wf[ks], bv, dl, 0, 0, 0);
                 }
             }
             const int r = l % 32, half = l / 32;
             const uint32_t i = trow[r % TR];
             if (r < TR) {
                 if (i != kNoRow) {
-                    // Lane (half, r) holds features 32 h + 16 half + {0..15} (permuted packing).
+                    // Lane (half, r) holds features DIM h + 32 b + 16 half + {0..15}
+                    // (permuted packing).
                     float o[16];
 #pragma unroll
                     for (int x = 0; x < 16; ++x) {
                         const float y = dh[x] + dl[x];
                         o[x] = HL ? y : elu_bf16(y);  // FP32 outputs: the last layer; bf16: hidden
                     }
-                    const uint64_t off = uint64_t(i) * 256 + 32 * h + 16 * half;
+                    const uint64_t off = uint64_t(i) * (8 * DIM) + DIM * h + 32 * b + 16 * half;
                     if (a.outbf) {
 #pragma unroll
                         for (int q = 0; q < 2; ++q) {
@@ -469,14 +490,16 @@ __global__ void __launch_bounds__(kChunkThreads) k_afs_chunks(AfsArgs a) {
         for (uint32_t q = 0; q < nch; ++q) mc = fmaxf(mc, a.mchunk[(first + q) * 8 + h]);
         s.m = s.mx = leaky(s.L + mc);
     }
-    gather_sums<true>(a.pcol, a.xr, beg, end, l, s, a.pcol[beg + uint32_t(l % 32)], 0);
+    const bool rsep = a.in > kXRFeat;
+    if (rsep) gather_sums<true, true>(a.pcol, a.xr, a.R, beg, end, l, s, a.pcol[beg + uint32_t(l % 32)], 0);
+    else gather_sums<true, false>(a.pcol, a.xr, a.R, beg, end, l, s, a.pcol[beg + uint32_t(l % 32)], 0);
     const float den = total_den(s.den);
     float* part = a.part + c * kPart;
     if (g < 2) {
 #pragma unroll
         for (int sb = 0; sb < kSB; ++sb) {
             const int P = 16 * sb + n;
-            if (P >= kXRFeat / 2) continue;
+            if (P >= (rsep ? kRowWords : kXRFeat / 2)) continue;
 #pragma unroll
             for (int q = 0; q < 4; ++q)
                 *reinterpret_cast<float2*>(part + (4 * g + q) * 128 + 2 * P) =
@@ -488,10 +511,10 @@ __global__ void __launch_bounds__(kChunkThreads) k_afs_chunks(AfsArgs a) {
 
 // One wave per split row (found at its first chunk): adds the chunks' sums
 // and denominators in chunk order, then out_h = (U_h / den_h) W_h on the VALU
-// with the FP32 (bf16-rounded) W; lane l computes columns 4 (l % 8) .. + 3 of
-// head l / 8.
+// with the FP32 (bf16-rounded) W; lane l computes columns 32 cb + 4 (l % 8)
+// .. + 3 of head l / 8, for each 32-column block cb of the head.
 __global__ void __launch_bounds__(kChunkThreads) k_afs_merge(AfsArgs a) {
-    __shared__ float s[kChunkThreads / kWave][8 * kXRFeat];
+    __shared__ float s[kChunkThreads / kWave][8 * kRowWords * 2];
     const int w = threadIdx.x / kWave, l = threadIdx.x % kWave;
     const uint64_t c = uint64_t(blockIdx.x) * (kChunkThreads / kWave) + w;
     if (c >= a.chunks || a.chunk_first[c] != c) return;
@@ -517,7 +540,7 @@ __global__ void __launch_bounds__(kChunkThreads) k_afs_merge(AfsArgs a) {
     float dall[8];  // read before any lane is masked off
 #pragma unroll
     for (int h = 0; h < 8; ++h) dall[h] = lane_f(d, h);
-    if (l < kXRFeat / 2) {
+    if (l < (a.in > kXRFeat ? kRowWords : kXRFeat / 2)) {
         // Chunk by chunk (the order of the sums), the 8 heads' loads of a chunk
         // independent of each other.
         float t[8][2];
@@ -538,50 +561,52 @@ __global__ void __launch_bounds__(kChunkThreads) k_afs_merge(AfsArgs a) {
 #pragma unroll
         for (int h = 0; h < 8; ++h) {
             const float inv = dall[h] > 0.0f ? 1.0f / dall[h] : 0.0f;
-            s[w][h * kXRFeat + 2 * l] = t[h][0] * inv;
-            s[w][h * kXRFeat + 2 * l + 1] = t[h][1] * inv;
+            s[w][h * 128 + 2 * l] = t[h][0] * inv;
+            s[w][h * 128 + 2 * l + 1] = t[h][1] * inv;
         }
     }
     wave_sync();
-    const int h = l / 8, c0 = 4 * (l % 8);
-    float o[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-    const float* wcol = a.wq + 32 * h + c0;
-    auto fma4 = [&](float sv, const float4& wv) {
-        o[0] = __builtin_fmaf(sv, wv.x, o[0]);
-        o[1] = __builtin_fmaf(sv, wv.y, o[1]);
-        o[2] = __builtin_fmaf(sv, wv.z, o[2]);
-        o[3] = __builtin_fmaf(sv, wv.w, o[3]);
-    };
-    // 16 rows of W requested at a time (L2-resident), then their FMAs in order.
-    int f = 0;
-    for (; f + 16 <= a.in; f += 16) {
-        float4 wv[16];
+    const int h = l / 8, width = 8 * a.dim;
+    for (int cb = 0; cb < a.dim / 32; ++cb) {
+        const int c0 = a.dim * h + 32 * cb + 4 * (l % 8);
+        float o[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        const float* wcol = a.wq + c0;
+        auto fma4 = [&](float sv, const float4& wv) {
+            o[0] = __builtin_fmaf(sv, wv.x, o[0]);
+            o[1] = __builtin_fmaf(sv, wv.y, o[1]);
+            o[2] = __builtin_fmaf(sv, wv.z, o[2]);
+            o[3] = __builtin_fmaf(sv, wv.w, o[3]);
+        };
+        // 16 rows of W requested at a time (L2-resident), then their FMAs in order.
+        int f = 0;
+        for (; f + 16 <= a.in; f += 16) {
+            float4 wv[16];
 #pragma unroll
-        for (int x = 0; x < 16; ++x) wv[x] = *reinterpret_cast<const float4*>(wcol + uint64_t(f + x) * 256);
+            for (int x = 0; x < 16; ++x) wv[x] = *reinterpret_cast<const float4*>(wcol + uint64_t(f + x) * width);
 #pragma unroll
-        for (int x = 0; x < 16; ++x) fma4(s[w][h * kXRFeat + f + x], wv[x]);
+            for (int x = 0; x < 16; ++x) fma4(s[w][h * 128 + f + x], wv[x]);
+        }
+        for (; f < a.in; ++f) fma4(s[w][h * 128 + f], *reinterpret_cast<const float4*>(wcol + uint64_t(f) * width));
+        if (a.hidden)
+#pragma unroll
+            for (int x = 0; x < 4; ++x) o[x] = elu_bf16(o[x]);
+        const uint64_t off = uint64_t(i) * width + c0;
+        if (a.outbf)
+            *reinterpret_cast<uint2*>(a.outbf + off) = make_uint2(bf16x2(o[0], o[1]), bf16x2(o[2], o[3]));
+        if (a.out32) *reinterpret_cast<float4*>(a.out32 + off) = make_float4(o[0], o[1], o[2], o[3]);
     }
-    for (; f < a.in; ++f) fma4(s[w][h * kXRFeat + f], *reinterpret_cast<const float4*>(wcol + uint64_t(f) * 256));
-    if (a.hidden)
-#pragma unroll
-        for (int x = 0; x < 4; ++x) o[x] = elu_bf16(o[x]);
-    const uint64_t off = uint64_t(i) * 256 + 32 * h + c0;
-    if (a.outbf)
-        *reinterpret_cast<uint2*>(a.outbf + off) =
-            make_uint2(bf16x2(o[0], o[1]), bf16x2(o[2], o[3]));
-    if (a.out32) *reinterpret_cast<float4*>(a.out32 + off) = make_float4(o[0], o[1], o[2], o[3]);
 }
 
-template <int KS, bool HL, int TR>
+template <int KS, bool HL, int TR, int DIM>
 hipError_t launch_tiles_hl(const AfsArgs& a, hipStream_t s, int cus) {
     const uint64_t tiles = (a.rows + TR - 1) / TR;
     if (!tiles) return hipSuccess;
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_afs_tiles<KS, HL, TR>),
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_afs_tiles<KS, HL, TR, DIM>),
                                        hipFuncAttributeMaxDynamicSharedMemorySize, kLdsBytes);
     if (e != hipSuccess) return e;
     uint64_t blocks = uint64_t(cus) * 2;
     if (blocks > tiles) blocks = tiles;
-    k_afs_tiles<KS, HL, TR><<<dim3(uint32_t(blocks)), kThreads, kLdsBytes, s>>>(a);
+    k_afs_tiles<KS, HL, TR, DIM><<<dim3(uint32_t(blocks)), kThreads, kLdsBytes, s>>>(a);
     return hipGetLastError();
 }
 
@@ -590,17 +615,23 @@ hipError_t launch_tiles_hl(const AfsArgs& a, hipStream_t s, int cus) {
 template <int KS>
 hipError_t launch_tiles(const AfsArgs& a, hipStream_t s, int cus) {
     if (a.hidden != (a.out32 == nullptr) || (a.out32 == nullptr) == (a.outbf == nullptr)) return hipErrorInvalidValue;
-    return a.out32 ? launch_tiles_hl<KS, true, 16>(a, s, cus) : launch_tiles_hl<KS, false, kTileBf16>(a, s, cus);
+    if (a.dim == 64)
+        return a.out32 ? launch_tiles_hl<KS, true, 16, 64>(a, s, cus) : launch_tiles_hl<KS, false, kTileBf16, 64>(a, s, cus);
+    return a.out32 ? launch_tiles_hl<KS, true, 16, 32>(a, s, cus) : launch_tiles_hl<KS, false, kTileBf16, 32>(a, s, cus);
 }
 
 }  // namespace
 
+// Up to 128 inputs (up to 112 with R in the row tail, else R from its own
+// array), 8 heads of 32 or 64.
 bool aggregate_afsum_supported(int in, int heads, int dim, uint64_t n) {
-    return in >= 1 && in <= kXRFeat && heads == 8 && dim == 32 && n <= (uint64_t(1) << 32) / (4 * kRowWords);
+    return in >= 1 && in <= kXRStride && heads == 8 && (dim == 32 || dim == 64) &&
+           n <= (uint64_t(1) << 32) / (4 * kRowWords);
 }
 
 hipError_t launch_aggregate_afsum(const AfsArgs& a, const SplitTable& t, hipStream_t s, int cus) {
-    if (!aggregate_afsum_supported(a.in, 8, 32, a.n) || a.nmb < 8 || a.ksteps != (a.in + 15) / 16 || !a.xr || !a.wq)
+    if (!aggregate_afsum_supported(a.in, 8, a.dim, a.n) || a.nmb < 8 || a.ksteps != (a.in + 15) / 16 || !a.xr ||
+        !a.wq || !a.R)
         return hipErrorInvalidValue;
     if (a.chunks) {
         hipError_t e = launch_split_prescan(a.prow, a.pcol, a.R, 8, t, a.e, s);
@@ -617,7 +648,8 @@ hipError_t launch_aggregate_afsum(const AfsArgs& a, const SplitTable& t, hipStre
         case 4: e = launch_tiles<4>(a, s, cus); break;
         case 5: e = launch_tiles<5>(a, s, cus); break;
         case 6: e = launch_tiles<6>(a, s, cus); break;
-        default: e = launch_tiles<7>(a, s, cus); break;
+        case 7: e = launch_tiles<7>(a, s, cus); break;
+        default: e = launch_tiles<8>(a, s, cus); break;
     }
     if (e != hipSuccess) return e;
     if (a.chunks) {

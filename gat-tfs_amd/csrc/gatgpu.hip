@@ -74,15 +74,21 @@ struct LayerState {
 // (100 -> 8x32 -> 8x32 -> 1x47, max in-degree 17 000): the sum form keeps
 // many short chunks, the one-row-per-wave 8-head kernel fewer, longer ones,
 // and the one-head kernel (8 rows per wave) splits only its heaviest rows.
-// Graphs with heavier rows scale a plan (chunk and min) by the smallest power
-// of two that keeps the heaviest row within kMaxChunksPerRow chunks: each
-// chunk reduces the maxima of all chunks of its row and the last one adds
-// all partial sums, so many chunks per row cost more than they balance.  On
-// the 100M-edge R-MAT graph (max in-degree 132 270) that gives 6144/2048
-// (8-head) and 4096/2048 (one head), the best of a measured sweep there.
+// Small graphs (below kSmallGraphEdges edges) split more rows into shorter
+// chunks, 512/256 for every kernel: their heaviest rows are a larger share of
+// a short launch (169K-node, 2.5M-edge power-law graph: 0.88 ms against 1.23
+// with the plans above).  Graphs with heavier rows scale a plan (chunk and
+// min) by the smallest power of two that keeps the heaviest row within
+// kMaxChunksPerRow chunks: each chunk reduces the maxima of all chunks of its
+// row and the last one adds all partial sums, so many chunks per row cost
+// more than they balance.  On the 100M-edge R-MAT graph (max in-degree
+// 132 270) that gives 6144/2048 (8-head) and 4096/2048 (one head), the best
+// of a measured sweep there.
 enum { kPlanAf = 0, kPlanVec = 1, kPlanOne = 2, kPlans = 3 };
 constexpr uint32_t kPlanMin[kPlans] = {1024, 1536, 2048};
 constexpr uint32_t kPlanChunk[kPlans] = {256, 512, 1024};
+constexpr uint64_t kSmallGraphEdges = 16u << 20;
+constexpr uint32_t kSmallPlanMin = 512, kSmallPlanChunk = 256;
 constexpr uint64_t kMaxChunksPerRow = 96;
 struct SplitPlan {
     uint32_t min = 0, chunk = 0;
@@ -168,12 +174,14 @@ int compute_bins(gatgpu_ctx* c) {
     uint32_t thr[2 + kPlans] = {c->small_max, c->block_min ? c->block_min - 1 : 0};
     uint32_t maxdeg = 0;  // degrees are sorted ascending
     if (c->n) HIPCHECK(c, hipMemcpy(&maxdeg, c->sorted_deg + (c->n - 1), 4, hipMemcpyDeviceToHost));
+    const bool small = c->e < kSmallGraphEdges;
     for (int q = 0; q < kPlans; ++q) {
         SplitPlan& P = c->plans[q];
+        const uint32_t min0 = small ? kSmallPlanMin : kPlanMin[q], chunk0 = small ? kSmallPlanChunk : kPlanChunk[q];
         uint32_t f = 1;
-        while (uint64_t(kPlanChunk[q]) * f * kMaxChunksPerRow < maxdeg && f < (1u << 12)) f *= 2;
-        P.min = c->split_min ? c->split_min : kPlanMin[q] * f;
-        P.chunk = c->split_chunk ? c->split_chunk : kPlanChunk[q] * f;
+        while (uint64_t(chunk0) * f * kMaxChunksPerRow < maxdeg && f < (1u << 12)) f *= 2;
+        P.min = c->split_min ? c->split_min : min0 * f;
+        P.chunk = c->split_chunk ? c->split_chunk : chunk0 * f;
         thr[2 + q] = P.min - 1;
     }
     // small (0) disables the shared-wave bin; block_min 0 means every row takes a block.
@@ -295,16 +303,19 @@ int z_stride(int precision, int heads, int width, bool* r_in_z) {
     return precision == GATGPU_BF16 ? (width + 7) / 8 * 8 : (width + 3) / 4 * 4;
 }
 
-// AUTO selects aggregate-first where its sum form applies (bf16, 8 x 32,
-// D_in <= 112: it gathers 256-byte input rows instead of 512-byte Z rows;
-// measured on the 64.3M-edge graph, 100 -> 8 x 32: 5.9 ms against 6.8 ms
-// for transform-first) and transform-first everywhere else.
-int resolve_dataflow(const LayerState& L, int precision, int dataflow, uint64_t n) {
-    const bool af_ok = precision == GATGPU_BF16 && aggregate_af_supported(L.in, L.heads, L.dim);
-    if (dataflow == GATGPU_AUTO)
-        return precision == GATGPU_BF16 && aggregate_afsum_supported(L.in, L.heads, L.dim, n) ? GATGPU_AGGREGATE_FIRST
-                                                                                              : GATGPU_TRANSFORM_FIRST;
-    if ((dataflow == GATGPU_AGGREGATE_FIRST || dataflow == GATGPU_TFS_B1) && !af_ok) return -1;
+// AUTO selects aggregate-first where its sum form applies (bf16, 8 heads of
+// 32 or 64, D_in <= 128: it gathers 256-byte input rows, plus R from its own
+// array beyond 112 inputs, instead of 512- or 1024-byte Z rows; measured on
+// the 64.3M-edge graph, 100 -> 8 x 32: 5.9 ms against 6.8 ms for
+// transform-first) and transform-first everywhere else.
+// fixed: the fixed-p operator, whose aggregate-first form is the neighbour-step kernel only.
+int resolve_dataflow(const LayerState& L, int precision, int dataflow, uint64_t n, bool fixed = false) {
+    const bool bf16 = precision == GATGPU_BF16;
+    const bool sum_ok = bf16 && !fixed && aggregate_afsum_supported(L.in, L.heads, L.dim, n);
+    const bool step_ok = bf16 && aggregate_af_supported(L.in, L.heads, L.dim);  // neighbour-step kernel
+    if (dataflow == GATGPU_AUTO) return sum_ok ? GATGPU_AGGREGATE_FIRST : GATGPU_TRANSFORM_FIRST;
+    if (dataflow == GATGPU_AGGREGATE_FIRST && !sum_ok && !step_ok) return -1;
+    if (dataflow == GATGPU_TFS_B1 && !step_ok) return -1;
     return dataflow;
 }
 
@@ -338,8 +349,10 @@ int run_layer_af(gatgpu_ctx* c, int l, bool hidden, const float* src32, const ui
     if (src32) HIPCHECK(c, Ls.inbf.ensure(n * xs * 2));
     // The fixed-p operator has no row max (the reference leaves it unset).
     if (fixed) HIPCHECK(c, hipMemsetAsync(Ls.mx.p, 0, n * K * 4, c->stream));
-    // Sum form: the gather table is the bf16 input rows with R in their tail.
+    // Sum form: the gather table is the bf16 input rows, with R in their tail
+    // up to 112 inputs (beyond, the rows are full and R stays in its array).
     const bool sum_form = !fixed && dataflow == GATGPU_AGGREGATE_FIRST && aggregate_afsum_supported(D, K, Ls.dim, n);
+    const bool r_tail = sum_form && D <= kXRFeat;
     ProjArgs pa{};
     pa.n = n;
     pa.ksteps = Ls.lr_ksteps;
@@ -349,9 +362,9 @@ int run_layer_af(gatgpu_ctx* c, int l, bool hidden, const float* src32, const ui
     pa.nmb = 2;
     // FP32 input, sum form: the L/R projection rounds the rows itself and
     // writes them into the gather table (the convert stage fused); with 7 k
-    // steps it writes all 112 feature slots, zero past D.
-    const bool fused_convert =
-        sum_form && src32 && D % 4 == 0 && Ls.lr_ksteps * 16 == kXRFeat && projection_fp32_input(pa);
+    // steps it writes all 112 feature slots, zero past D (8 k steps: all 128).
+    const bool fused_convert = sum_form && src32 && D % 4 == 0 &&
+                               Ls.lr_ksteps * 16 == (r_tail ? kXRFeat : kXRStride) && projection_fp32_input(pa);
     if (ev_base >= 0) HIPCHECK(c, hipEventRecord(c->ev[ev_base], c->stream));
     if (src32 && !fused_convert) {
         HIPCHECK(c, launch_to_bf16_pad(src32, Ls.inbf.as<uint16_t>(), n, D, xs, c->stream));
@@ -373,7 +386,7 @@ int run_layer_af(gatgpu_ctx* c, int l, bool hidden, const float* src32, const ui
     pa.left = Ls.left.as<float>();
     pa.right = Ls.right.as<float>();
     pa.tiles = (n + 31) / 32;
-    if (sum_form) {  // R also goes into the tail of each input row
+    if (r_tail) {  // R also goes into the tail of each input row
         pa.z = Ls.inbf.as<uint16_t>();
         pa.zs = kXRStride;
         pa.r_in_z = true;
@@ -388,12 +401,15 @@ int run_layer_af(gatgpu_ctx* c, int l, bool hidden, const float* src32, const ui
         a.perm = c->ident.as<uint32_t>();
         a.L = Ls.left.as<float>();
         a.R = Ls.right.as<float>();
-        a.xr = reinterpret_cast<const uint32_t*>(Ls.inbf.as<uint16_t>());
+        // The rounded input rows: written by the fused convert, else the
+        // converted (or chained bf16) rows the front end read.
+        a.xr = reinterpret_cast<const uint32_t*>(fused_convert ? Ls.inbf.as<uint16_t>() : srcbf);
         a.wpk = Ls.wpk.as<uint4>();
         a.nmb = Ls.nmb;
         a.ksteps = Ls.ksteps;
         a.wq = Ls.wq32.as<float>();
         a.in = D;
+        a.dim = Ls.dim;
         a.hidden = hidden;
         a.mx = Ls.mx.as<float>();
         a.den = Ls.den.as<float>();
@@ -853,7 +869,7 @@ int gatgpu_layer_forward(gatgpu_ctx* c, int layer, int precision, int dataflow, 
             return fail(c, GATGPU_ENONFINITE, "nonfinite layer input index=" + std::to_string(bad));
     }
     const int flow = resolve_dataflow(c->L[layer], precision, dataflow, c->n);
-    if (flow < 0) return fail(c, GATGPU_EINVAL, "aggregate-first needs bf16, head_dim 32, 1/2/4/8 heads and in <= 128");
+    if (flow < 0) return fail(c, GATGPU_EINVAL, "aggregate-first needs bf16 and in <= 128 with head_dim 32 (1/2/4/8 heads) or 8 heads of 64; TFS B1 head_dim 32");
     if (int r = run_layer(c, layer, precision, flow, hidden != 0, input, times ? 0 : -1)) return r;
     HIPCHECK(c, hipStreamSynchronize(c->stream));
     HIPCHECK(c, hipGetLastError());
@@ -920,9 +936,9 @@ int gatgpu_fixed_p_forward(gatgpu_ctx* c, int layer, int precision, int dataflow
     }
     int flow = dataflow == GATGPU_AUTO ? GATGPU_TRANSFORM_FIRST : dataflow;
     if (flow != GATGPU_TRANSFORM_FIRST) {
-        flow = resolve_dataflow(c->L[layer], precision, flow, c->n);
+        flow = resolve_dataflow(c->L[layer], precision, flow, c->n, true);
         if (flow < 0)
-            return fail(c, GATGPU_EINVAL, "aggregate-first needs bf16, head_dim 32, 1/2/4/8 heads and in <= 128");
+            return fail(c, GATGPU_EINVAL, "fixed-p aggregate-first needs bf16, head_dim 32, 1/2/4/8 heads and in <= 128");
     }
     if (int r = run_layer(c, layer, precision, flow, false, input, times ? 0 : -1, true)) return r;
     HIPCHECK(c, hipStreamSynchronize(c->stream));

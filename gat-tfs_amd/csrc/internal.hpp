@@ -275,12 +275,13 @@ struct AfsArgs {
     const uint32_t* pcol;
     const uint32_t* perm;
     const float* L;      // [n][8]
-    const float* R;      // [n][8] (per-chunk maxima of split rows)
-    const uint32_t* xr;  // XR as 4-byte words [n][64]
+    const float* R;      // [n][8] (per-chunk maxima of split rows; the scores when in > 112)
+    const uint32_t* xr;  // XR as 4-byte words [n][64]: X, and R in words 56..63 when in <= 112
     const uint4* wpk;    // projection weights in pack_projection_weights() order (one group)
     int nmb, ksteps;     // blocks per group and k steps of wpk
-    const float* wq;     // [in][256] bf16-rounded W as FP32 (split rows)
+    const float* wq;     // [in][8 dim] bf16-rounded W as FP32 (split rows)
     int in;
+    int dim;             // head width: 32 or 64
     bool hidden;
     float* mx;
     float* den;

@@ -60,8 +60,8 @@ enum { GATGPU_FP32 = 0, GATGPU_BF16 = 1 };
  * rows (standard_layer, baseline/src/baseline_standard.cpp:98-108).
  * AGGREGATE_FIRST gathers the layer's input rows instead of Z
  * (tfs_online_fused, implementation/src/gat_tfs_online.cpp:200-283); bf16
- * only, head_dim 32, 1, 2, 4 or 8 heads and in <= 128.  For 8 heads and
- * in <= 112 it runs in the sum form of tfs_online_fused: U_h = sum_j p_jh X_j
+ * only, in <= 128, and head_dim 32 with 1, 2, 4 or 8 heads or 8 heads of 64.
+ * For 8 heads it runs in the sum form of tfs_online_fused: U_h = sum_j p_jh X_j
  * per row (FP32 sums of the bf16 rows, p entering as hi + lo bf16), then
  * (U_h / den_h) W_h on the MFMA units, with U_h / den_h entering as hi + lo
  * bf16 for FP32 outputs and as one bf16 for bf16-stored hidden outputs (the
@@ -108,14 +108,15 @@ enum {
     GATGPU_OPT_BLOCK_ROW_MIN_DEGREE = 1, /* rows at/above use a block per row  */
     GATGPU_OPT_SPLIT_ROW_MIN_DEGREE = 2, /* rows at/above are split over waves
                                             (default per kernel: 1024 sum form,
-                                            1536 8-head, 2048 one-head, both
+                                            1536 8-head, 2048 one-head; 512 on
+                                            graphs below 16M edges; both
                                             defaults doubled until the heaviest
                                             row has <= 96 chunks; a value
                                             applies to all, 0 restores them)  */
     GATGPU_OPT_SPLIT_CHUNK_EDGES = 3,    /* edges per split chunk (default per
-                                            kernel: 256, 512, 1024, scaled as
-                                            above; a value >= 64 applies to
-                                            all, 0 restores)                  */
+                                            kernel: 256, 512, 1024; 256 below
+                                            16M edges; scaled as above; a value
+                                            >= 64 applies to all, 0 restores) */
     GATGPU_OPT_SMALL_ROW_MAX_DEGREE = 4  /* rows at/below share one wave        */
 };
 

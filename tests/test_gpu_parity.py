@@ -428,9 +428,11 @@ def test_bf16_projection_stages(gpu_ctx, D, K, d):
 
 
 AF_SHAPES = [(100, 8, 32), (128, 8, 32), (33, 4, 32), (17, 1, 32), (128, 2, 32), (64, 8, 32)]
+# The sum form beyond 112 inputs (R from its own array) and with heads of 64.
+SUM_FORM_SHAPES = [(116, 8, 32), (120, 8, 64), (128, 8, 64), (100, 8, 64)]
 
 
-@pytest.mark.parametrize("D,K,d", AF_SHAPES)
+@pytest.mark.parametrize("D,K,d", AF_SHAPES + SUM_FORM_SHAPES)
 def test_aggregate_first_layer(gpu_ctx, D, K, d):
     """Aggregate-first (tfs_online_fused semantics, exact max): equals R0 run on
     bf16-rounded X and W (the AF path projects FP32 sums of bf16 inputs with
@@ -461,6 +463,32 @@ def test_aggregate_first_layer(gpu_ctx, D, K, d):
             assert oracle.errors(r32["out"], out)["relative_l2"] < BF16_REL_L2
             for k_ in ("max", "den"):
                 assert oracle.errors(r[k_], gpu_ctx.stage(0, k_))["relative_l2"] < 1e-4, (k_, opts)
+
+
+def test_sum_form_chained_bf16_input(gpu_ctx):
+    """A hidden 4 x 32 layer's bf16 output (128 features) feeding a 128 -> 8 x 64
+    aggregate-first layer: the chained rows are the gather table as they are.
+    Equals R0 on the GPU's own layer-1 output and the bf16-rounded W."""
+    w = inputs.WORKLOADS["smoke"]
+    row, col = w.graph()
+    x = inputs.normal((w.n, 64), 31)
+    p0 = inputs.glorot_param(64, 4, 32, 32)
+    p1 = inputs.glorot_param(128, 8, 64, 33)
+    gpu_ctx.set_graph(row, col)
+    gpu_ctx.set_layer(0, p0)
+    gpu_ctx.set_layer(1, p1)
+    gpu_ctx.set_input(x)
+    gpu_ctx.layer_forward(0, gatgpu.BF16, gatgpu.TRANSFORM_FIRST, True)
+    h0 = gpu_ctx.stage(0, "out")
+    assert np.array_equal(h0, oracle.quantize_bf16(h0))  # stored bf16
+    qp = dict(p1, w=oracle.quantize_bf16(p1["w"]))
+    for hidden in (True, False):
+        gpu_ctx.layer_forward(1, gatgpu.BF16, gatgpu.AGGREGATE_FIRST, hidden)
+        assert gpu_ctx.stage(1, "z") is None
+        r = oracle.ref_layer(row, col, h0, qp, hidden)
+        out = gpu_ctx.stage(1, "out")
+        e = oracle.errors(oracle.quantize_bf16(r["out"]) if hidden else r["out"], out)
+        assert e["finite"] and e["relative_l2"] < (4e-3 if hidden else 1e-4), (hidden, e)
 
 
 @pytest.mark.parametrize("D,K,d", AF_SHAPES)
@@ -583,7 +611,11 @@ def test_large_model_auto_sum_form(gpu_ctx):
 def test_skew_model_properties(gpu_ctx):
     """Full-size check on the R-MAT graph (2^22 nodes, 100.6M edges, max
     in-degree 132 270, 9 109 split rows; 128 -> 8x64 -> 8x64 -> 1x64, bf16):
-    on 1000 sampled rows plus the 32 heaviest, for layer 2 (8 x 64) and layer 3
+    on 1000 sampled rows plus the 32 heaviest, for layer 1 (aggregate-first sum
+    form, R from its own array) the row max equals the scalar max of
+    LeakyReLU(L + R) bit for bit and the denominator and the bf16 output equal
+    a float64 recomputation from the bf16-rounded X and W (to one bf16
+    rounding of the staged sums and of the output); for layer 2 (8 x 64) and layer 3
     (one head of 64), the row max equals the scalar max of LeakyReLU(L + R)
     over the GPU's own L/R bit for bit, the denominator equals a float64 sum of
     p, and the output equals the float64 sum_j p Z_j / den over the GPU's own
@@ -601,6 +633,26 @@ def test_skew_model_properties(gpu_ctx):
     deg = np.diff(row.astype(np.int64))
     rng = np.random.default_rng(7)
     rows = np.concatenate((rng.choice(w.n, 1000, replace=False), np.argsort(deg)[-32:]))
+    assert gpu_ctx.stage(0, "z") is None  # layer 1 ran aggregate-first
+    L, R = gpu_ctx.stage(0, "left"), gpu_ctx.stage(0, "right")
+    M, den, out = gpu_ctx.stage(0, "max"), gpu_ctx.stage(0, "den"), gpu_ctx.stage(0, "out")
+    K, d = m[0]["heads"], m[0]["dim"]
+    wq = oracle.quantize_bf16(m[0]["w"]).astype(np.float64)
+    for i in rows:
+        js = col[int(row[i]):int(row[i + 1])].astype(np.int64)
+        s = L[i][None, :] + R[js]
+        s = np.where(s >= 0, s, np.float32(0.2) * s).astype(np.float32)
+        assert np.array_equal(M[i], s.max(axis=0)), (0, i)
+        p = np.exp(s.astype(np.float64) - M[i].astype(np.float64))
+        dsum = p.sum(axis=0)
+        assert np.all(np.abs(den[i] - dsum) <= 1e-5 * dsum), (0, i)
+        xq = oracle.quantize_bf16(x[js]).astype(np.float64)
+        u = p.T @ xq / dsum[:, None]  # [K][D]
+        y = np.concatenate([u[h] @ wq[:, h * d:(h + 1) * d] for h in range(K)])
+        mag = np.concatenate([np.abs(u[h]) @ np.abs(wq[:, h * d:(h + 1) * d]) for h in range(K)])
+        y = np.where(y >= 0, y, np.expm1(y))
+        tol = np.abs(y) * 2.0 ** -8 + mag * 2.0 ** -8 + 1e-6
+        assert np.all(np.abs(out[i] - y) <= tol), (0, i, np.max(np.abs(out[i] - y) - tol))
     for layer, hidden in ((1, True), (2, False)):
         K, d = m[layer]["heads"], m[layer]["dim"]
         Z = gpu_ctx.stage(layer, "z").astype(np.float64)
