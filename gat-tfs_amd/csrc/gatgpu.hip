@@ -305,15 +305,21 @@ int z_stride(int precision, int heads, int width, bool* r_in_z) {
 
 // AUTO selects aggregate-first where its sum form applies (bf16, 8 heads of
 // 32 or 64, D_in <= 128: it gathers 256-byte input rows, plus R from its own
-// array beyond 112 inputs, instead of 512- or 1024-byte Z rows; measured on
-// the 64.3M-edge graph, 100 -> 8 x 32: 5.9 ms against 6.8 ms for
-// transform-first) and transform-first everywhere else.
+// array beyond 112 inputs, instead of 512- or 1024-byte Z rows) and the Z
+// table would not fit the 256 MB Infinity Cache, so that transform-first
+// gathers would come from HBM; transform-first everywhere else.  Measured:
+// 64.3M-edge graph, 100 -> 8 x 32 (Z 1.25 GB): 5.9 ms against 6.8 ms for
+// transform-first; R-MAT, 128 -> 8 x 64 (Z 4.3 GB): 8.4 ms against 17.9;
+// 169K-node graph, 128 -> 8 x 32 (Z 87 MB): 0.30 ms against 0.29.
+constexpr uint64_t kAfMinZBytes = uint64_t(256) << 20;
 // fixed: the fixed-p operator, whose aggregate-first form is the neighbour-step kernel only.
 int resolve_dataflow(const LayerState& L, int precision, int dataflow, uint64_t n, bool fixed = false) {
     const bool bf16 = precision == GATGPU_BF16;
     const bool sum_ok = bf16 && !fixed && aggregate_afsum_supported(L.in, L.heads, L.dim, n);
     const bool step_ok = bf16 && aggregate_af_supported(L.in, L.heads, L.dim);  // neighbour-step kernel
-    if (dataflow == GATGPU_AUTO) return sum_ok ? GATGPU_AGGREGATE_FIRST : GATGPU_TRANSFORM_FIRST;
+    if (dataflow == GATGPU_AUTO)
+        return sum_ok && n * uint64_t(L.heads) * uint64_t(L.dim) * 2 > kAfMinZBytes ? GATGPU_AGGREGATE_FIRST
+                                                                                  : GATGPU_TRANSFORM_FIRST;
     if (dataflow == GATGPU_AGGREGATE_FIRST && !sum_ok && !step_ok) return -1;
     if (dataflow == GATGPU_TFS_B1 && !step_ok) return -1;
     return dataflow;

@@ -68,7 +68,8 @@ enum { GATGPU_FP32 = 0, GATGPU_BF16 = 1 };
  * rounding of a bf16 projection input); otherwise each gathered row is projected
  * and p (X_j W_h) summed, in the neighbour-step order of
  * baseline/src/baseline_tfs.cpp:16-110.  AUTO selects the sum form where it
- * applies (bf16) and transform-first elsewhere.  gatgpu_model_forward with
+ * applies (bf16) and the layer's bf16 Z table (n x heads x head_dim x 2 bytes)
+ * exceeds 256 MB, and transform-first elsewhere.  gatgpu_model_forward with
  * AGGREGATE_FIRST uses it on the layers that support it and transform-first
  * on the others. */
 /* TFS_B1 is the faithful neighbour-step TFS ("tfs_bf16",
