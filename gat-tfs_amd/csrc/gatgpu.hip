@@ -50,6 +50,7 @@ struct LayerState {
     int in = 0, heads = 0, dim = 0;
     std::vector<float> w_host;
     DevBuf w32, wq32, al, ar, blr;
+    DevBuf wpk32;  // FP32 MFMA fragments (projection_f32_supported shapes), else empty
     DevBuf z32, zbf, zscratch, left, right, mx, den, out32, outbf, in32, inbf;
     // What the last forward of this layer produced.
     bool ran = false, z_valid = false, out32_valid = false, outbf_valid = false;
@@ -623,6 +624,23 @@ int run_layer(gatgpu_ctx* c, int l, int precision, int dataflow, bool hidden, co
             pa.x = srcbf;
         }
         HIPCHECK(c, launch_projection_mfma(pa, c->stream, c->cus));
+    } else if (projection_f32_supported(D, K, dim)) {
+        // FP32 MFMA: Z = X W and L/R = X B_LR (FP32 products and sums)
+        ProjF32Args fa{};
+        fa.x = src32;
+        fa.n = n;
+        fa.in = D;
+        fa.xs = D;
+        fa.wpk = Ls.wpk32.as<float>();
+        fa.head_blocks = (W + 31) / 32;
+        fa.width = W;
+        fa.heads = K;
+        fa.z = Ls.z32.as<float>();
+        fa.zs = zs;
+        fa.left = Ls.left.as<float>();
+        fa.right = Ls.right.as<float>();
+        fa.tiles = (n + 31) / 32;
+        HIPCHECK(c, launch_projection_f32(fa, c->stream));
     } else {
         HIPCHECK(c, launch_projection(src32, nullptr, Ls.w32.as<float>(), n, D, K, dim, Ls.al.as<float>(),
                                       Ls.ar.as<float>(), Ls.z32.as<float>(), nullptr, Ls.left.as<float>(),
@@ -815,6 +833,12 @@ int gatgpu_set_layer(gatgpu_ctx* c, int layer, int in, int heads, int dim, const
     HIPCHECK(c, hipMemcpyAsync(L.al.p, al, W * 4, hipMemcpyHostToDevice, c->stream));
     HIPCHECK(c, hipMemcpyAsync(L.ar.p, ar, W * 4, hipMemcpyHostToDevice, c->stream));
     HIPCHECK(c, hipMemcpyAsync(L.blr.p, blr.data(), blr.size() * 4, hipMemcpyHostToDevice, c->stream));
+    std::vector<float> f32pk;
+    if (projection_f32_supported(in, heads, dim)) {
+        pack_projection_f32(w, blr.data(), in, heads, dim, f32pk);
+        HIPCHECK(c, L.wpk32.ensure(f32pk.size() * 4));
+        HIPCHECK(c, hipMemcpyAsync(L.wpk32.p, f32pk.data(), f32pk.size() * 4, hipMemcpyHostToDevice, c->stream));
+    }
     HIPCHECK(c, hipStreamSynchronize(c->stream));
     L.set = true;
     return GATGPU_OK;

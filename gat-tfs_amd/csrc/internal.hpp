@@ -173,6 +173,23 @@ hipError_t launch_projection_mfma(const ProjArgs& a, hipStream_t s, int cus);
 void pack_lr_weights(const float* wq, const float* al, const float* ar, int in, int heads, int dim,
                      std::vector<uint16_t>& out, int& ksteps);
 
+// FP32 projection on the MFMA units (projection_mfma.hip).
+struct ProjF32Args {
+    const float* x;      // [n][xs] FP32 input, xs == in
+    uint64_t n;
+    int in, xs;
+    const float* wpk;    // pack_projection_f32() order
+    int head_blocks, width, heads;
+    float* z;            // [n][zs] FP32 output
+    int zs;
+    float* left;         // [n][heads]
+    float* right;        // [n][heads]
+    uint64_t tiles;      // ceil(n / 32)
+};
+bool projection_f32_supported(int in, int heads, int dim);
+hipError_t launch_projection_f32(const ProjF32Args& a, hipStream_t s);
+void pack_projection_f32(const float* w, const float* blr, int in, int heads, int dim, std::vector<float>& out);
+
 // aggregate.hip
 struct RowBins {
     // Sorted positions [0, n) split by degree: [0, small_end) share waves,

@@ -462,6 +462,116 @@ hipError_t launch_wide_io(const ProjArgs& a, hipStream_t s) {
     return hipGetLastError();
 }
 
+// FP32 projection (the FP32 path's Z = X W and L/R = X B_LR) on
+// v_mfma_f32_32x32x2_f32: FP32 products, FP32 accumulation.  Same work split
+// as the wide path: a wave keeps the FP32 input of its 32-row tile in
+// registers -- lane half h holds inputs [h KH, (h + 1) KH) of row col, so the
+// MFMA's k index pair at step ks is (ks, KH + ks) and the loads are
+// contiguous 16-byte vectors -- and the block streams W^T one 32-feature
+// output block at a time (KH / 4 x 64 float4, 4 k steps per LDS read) through
+// a two-slot LDS ring.  Head blocks use the permuted packing, so a lane ends
+// with 16 consecutive features of its row; the last block is [B_L | B_R]
+// (columns h and 8 + h), giving L and R of the reordered contraction
+// (lr_reordered, baseline_standard.cpp:29-43) in FP32.
+template <int KH>
+__global__ void __launch_bounds__(kWideThreads) k_proj_f32(ProjF32Args a) {
+    typedef float f32x4v __attribute__((ext_vector_type(4)));
+    extern __shared__ f32x4v fring[];  // [2][KH / 4][kWave]
+    constexpr int kFrags = KH / 4 * kWave;
+    constexpr int kPer = (kFrags + kWideThreads - 1) / kWideThreads;
+    const int w = threadIdx.x / kWave, l = threadIdx.x % kWave;
+    const int half = l / 32, col = l % 32;
+    const uint64_t row = (uint64_t(blockIdx.x) * kWideWaves + w) * 32 + col;
+    const uint64_t rs = row < a.n ? row : a.n - 1;  // lanes past n repeat row n - 1
+    float xr[KH];
+    {
+        const f32x4v* p = reinterpret_cast<const f32x4v*>(a.x + rs * a.xs + half * KH);
+#pragma unroll
+        for (int m = 0; m < KH / 4; ++m) {
+            const f32x4v v = p[m];
+            xr[4 * m] = v.x;
+            xr[4 * m + 1] = v.y;
+            xr[4 * m + 2] = v.z;
+            xr[4 * m + 3] = v.w;
+        }
+    }
+    const int nob = a.head_blocks + 1;
+    f32x4v st[kPer];
+    auto fetch = [&](int ob) {
+        const f32x4v* src = reinterpret_cast<const f32x4v*>(a.wpk) + size_t(ob) * kFrags;
+#pragma unroll
+        for (int i = 0; i < kPer; ++i) {
+            const int q = threadIdx.x + i * kWideThreads;
+            if (kFrags % kWideThreads == 0 || q < kFrags) st[i] = src[q];
+        }
+    };
+    auto put = [&](int slot) {
+#pragma unroll
+        for (int i = 0; i < kPer; ++i) {
+            const int q = threadIdx.x + i * kWideThreads;
+            if (kFrags % kWideThreads == 0 || q < kFrags) fring[slot * kFrags + q] = st[i];
+        }
+    };
+    fetch(0);
+    put(0);
+#pragma unroll
+    for (int k = 0; k < KH; ++k) asm volatile("" ::"v"(xr[k]));  // input complete before the loop
+    __syncthreads();
+    for (int ob = 0; ob < nob; ++ob) {
+        const int cur = ob & 1;
+        const bool more = ob + 1 < nob;
+        if (more) fetch(ob + 1);
+        f32x16 acc;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[r] = 0.0f;
+        const f32x4v* wk = fring + cur * kFrags + l;
+#pragma unroll
+        for (int k4 = 0; k4 < KH / 4; ++k4) {
+            const f32x4v av = wk[k4 * kWave];
+            acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av.x, xr[4 * k4], acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av.y, xr[4 * k4 + 1], acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av.z, xr[4 * k4 + 2], acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av.w, xr[4 * k4 + 3], acc, 0, 0, 0);
+        }
+        if (ob < a.head_blocks) {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int f0 = 32 * ob + 16 * half + 4 * q;
+                if (f0 < a.width)
+                    *reinterpret_cast<float4*>(a.z + rs * a.zs + f0) =
+                        make_float4(acc[4 * q], acc[4 * q + 1], acc[4 * q + 2], acc[4 * q + 3]);
+            }
+        } else {
+            // Lane half h4 holds L of heads 4 h4 + {0..3} in registers 0..3 and
+            // R of the same heads in registers 4..7.
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int h = 4 * half + q;
+                if (h < a.heads) {
+                    a.left[rs * a.heads + h] = acc[q];
+                    a.right[rs * a.heads + h] = acc[4 + q];
+                }
+            }
+        }
+        if (more) put(cur ^ 1);
+        __syncthreads();
+    }
+}
+
+template <int KH>
+hipError_t launch_f32_kh(const ProjF32Args& a, hipStream_t s) {
+    const size_t lds = size_t(2) * (KH / 4) * kWave * 16;
+    if (lds > 64 * 1024) {
+        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_proj_f32<KH>),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, int(lds));
+        if (e != hipSuccess) return e;
+    }
+    const uint64_t blocks = (a.tiles + kWideWaves - 1) / kWideWaves;
+    if (blocks < 1 || blocks > 0x7fffffffu) return hipErrorInvalidValue;
+    k_proj_f32<KH><<<dim3(uint32_t(blocks)), kWideThreads, lds, s>>>(a);
+    return hipGetLastError();
+}
+
 template <int KS, int HB, bool F32IN, bool FULL>
 hipError_t launch_fast_io(const ProjArgs& a, hipStream_t s, int cus) {
     const size_t lds = size_t(KS) * (HB + 1) * kWave * sizeof(uint4) + (FULL ? 256 * sizeof(float) : 0);
@@ -661,6 +771,54 @@ void pack_projection_weights(const float* wq, const float* al, const float* ar, 
                     }
             }
     }
+}
+
+// FP32 MFMA projection: 2 KH = in inputs with KH in {16, 32, 48, 64, 96, 128},
+// any heads x dim up to 8 x 64.
+bool projection_f32_supported(int in, int heads, int dim) {
+    const int kh = in / 2;
+    return in % 2 == 0 && (kh == 16 || kh == 32 || kh == 48 || kh == 64 || kh == 96 || kh == 128) && heads >= 1 &&
+           heads <= 8 && dim >= 1 && heads * dim <= 512;
+}
+
+hipError_t launch_projection_f32(const ProjF32Args& a, hipStream_t s) {
+    if (a.n == 0) return hipSuccess;
+    if (!projection_f32_supported(a.in, a.heads, a.width / a.heads) || a.xs != a.in || a.zs % 4 != 0 ||
+        a.zs < (a.width + 3) / 4 * 4 || a.head_blocks != (a.width + 31) / 32)
+        return hipErrorInvalidValue;
+    switch (a.in / 2) {
+        case 16: return launch_f32_kh<16>(a, s);
+        case 32: return launch_f32_kh<32>(a, s);
+        case 48: return launch_f32_kh<48>(a, s);
+        case 64: return launch_f32_kh<64>(a, s);
+        case 96: return launch_f32_kh<96>(a, s);
+        default: return launch_f32_kh<128>(a, s);
+    }
+}
+
+// FP32 fragments [block][k4][lane][4] for k_proj_f32: head block b, lane
+// (half, c), k step ks = 4 k4 + j holds W[half KH + ks][32 b + phi(c)] (phi
+// as in pack_projection_weights); the last block holds B_L in rows 0..heads-1
+// and B_R in rows 8..8+heads-1.  blr is [in][2 heads] (L columns, then R).
+void pack_projection_f32(const float* w, const float* blr, int in, int heads, int dim, std::vector<float>& out) {
+    const int width = heads * dim, hb = (width + 31) / 32, kh = in / 2;
+    out.assign(size_t(hb + 1) * kh * kWave, 0.0f);
+    for (int b = 0; b <= hb; ++b)
+        for (int k4 = 0; k4 < kh / 4; ++k4)
+            for (int l = 0; l < kWave; ++l)
+                for (int j = 0; j < 4; ++j) {
+                    const int c = l % 32, k = (l / 32) * kh + 4 * k4 + j;
+                    float v = 0.0f;
+                    if (b < hb) {
+                        const int f = 32 * b + 16 * ((c % 8) / 4) + 4 * (c / 8) + c % 4;
+                        if (f < width) v = w[size_t(k) * width + f];
+                    } else if (c < heads) {
+                        v = blr[size_t(k) * 2 * heads + c];
+                    } else if (c >= 8 && c < 8 + heads) {
+                        v = blr[size_t(k) * 2 * heads + heads + (c - 8)];
+                    }
+                    out[((size_t(b) * (kh / 4) + k4) * kWave + l) * 4 + j] = v;
+                }
 }
 
 // Only the L/R block ([kstep][2][lane][8], block 1 zero): the reordered
