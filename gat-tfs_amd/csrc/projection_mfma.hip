@@ -268,14 +268,26 @@ __global__ void __launch_bounds__(kThreads) k_proj_fast(ProjArgs a) {
         }
         // L/R block: lane half h4 holds heads 4 h4 + {0..3} of each quarter
         // (L hi, R hi, L lo, R lo) in registers {0..3}, {4..7}, {8..11}, {12..15}.
+        if (full || a.heads == 8) {
+            // 8 heads: the lane's 4 consecutive L, R values leave as 16-byte
+            // vectors (and R's 16 bytes in the Z row tail).
+            const float4 lv = make_float4(acc[HB][0] + acc[HB][8], acc[HB][1] + acc[HB][9], acc[HB][2] + acc[HB][10],
+                                          acc[HB][3] + acc[HB][11]);
+            const float4 rv = make_float4(acc[HB][4] + acc[HB][12], acc[HB][5] + acc[HB][13], acc[HB][6] + acc[HB][14],
+                                          acc[HB][7] + acc[HB][15]);
+            *reinterpret_cast<float4*>(a.left + rs * 8 + 4 * half) = lv;
+            if (!(FULL && a.r_from_z)) *reinterpret_cast<float4*>(a.right + rs * 8 + 4 * half) = rv;
+            if (!full && a.r_in_z) *reinterpret_cast<float4*>(a.z + rs * a.zs + a.r_off + 8 * half) = rv;
+        } else {
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            const int h = 4 * half + q;
-            if (full || h < a.heads) {
-                const float rv = acc[HB][4 + q] + acc[HB][12 + q];
-                a.left[rs * a.heads + h] = acc[HB][q] + acc[HB][8 + q];
-                if (!(FULL && a.r_from_z)) a.right[rs * a.heads + h] = rv;
-                if (!full && a.r_in_z) *reinterpret_cast<float*>(a.z + rs * a.zs + a.r_off + 2 * h) = rv;
+            for (int q = 0; q < 4; ++q) {
+                const int h = 4 * half + q;
+                if (h < a.heads) {
+                    const float rv = acc[HB][4 + q] + acc[HB][12 + q];
+                    a.left[rs * a.heads + h] = acc[HB][q] + acc[HB][8 + q];
+                    a.right[rs * a.heads + h] = rv;
+                    if (a.r_in_z) *reinterpret_cast<float*>(a.z + rs * a.zs + a.r_off + 2 * h) = rv;
+                }
             }
         }
         if (FULL && a.r_from_z && half == 0)
