@@ -444,14 +444,21 @@ __global__ void __launch_bounds__(kWideThreads) k_proj_wide(ProjArgs a) {
             }
             // L/R block: lane half h4 holds heads 4 h4 + {0..3} of each quarter
             // (L hi, R hi, L lo, R lo) in registers {0..3}, {4..7}, {8..11}, {12..15}.
+            if (a.heads == 8 && !a.r_in_z) {  // 16-byte vectors of the lane's 4 heads
+                *reinterpret_cast<float4*>(a.left + rs * 8 + 4 * half) =
+                    make_float4(acc[0] + acc[8], acc[1] + acc[9], acc[2] + acc[10], acc[3] + acc[11]);
+                *reinterpret_cast<float4*>(a.right + rs * 8 + 4 * half) =
+                    make_float4(acc[4] + acc[12], acc[5] + acc[13], acc[6] + acc[14], acc[7] + acc[15]);
+            } else {
 #pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                const int h = 4 * half + q;
-                if (h < a.heads) {
-                    const float rv = a.r_from_z ? rz : acc[4 + q] + acc[12 + q];
-                    a.left[rs * a.heads + h] = acc[q] + acc[8 + q];
-                    a.right[rs * a.heads + h] = rv;
-                    if (a.r_in_z) *reinterpret_cast<float*>(a.z + rs * a.zs + a.r_off + 2 * h) = rv;
+                for (int q = 0; q < 4; ++q) {
+                    const int h = 4 * half + q;
+                    if (h < a.heads) {
+                        const float rv = a.r_from_z ? rz : acc[4 + q] + acc[12 + q];
+                        a.left[rs * a.heads + h] = acc[q] + acc[8 + q];
+                        a.right[rs * a.heads + h] = rv;
+                        if (a.r_in_z) *reinterpret_cast<float*>(a.z + rs * a.zs + a.r_off + 2 * h) = rv;
+                    }
                 }
             }
         }
@@ -556,12 +563,17 @@ __global__ void __launch_bounds__(kWideThreads) k_proj_f32(ProjF32Args a) {
         } else {
             // Lane half h4 holds L of heads 4 h4 + {0..3} in registers 0..3 and
             // R of the same heads in registers 4..7.
+            if (a.heads == 8) {
+                *reinterpret_cast<float4*>(a.left + rs * 8 + 4 * half) = make_float4(acc[0], acc[1], acc[2], acc[3]);
+                *reinterpret_cast<float4*>(a.right + rs * 8 + 4 * half) = make_float4(acc[4], acc[5], acc[6], acc[7]);
+            } else {
 #pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                const int h = 4 * half + q;
-                if (h < a.heads) {
-                    a.left[rs * a.heads + h] = acc[q];
-                    a.right[rs * a.heads + h] = acc[4 + q];
+                for (int q = 0; q < 4; ++q) {
+                    const int h = 4 * half + q;
+                    if (h < a.heads) {
+                        a.left[rs * a.heads + h] = acc[q];
+                        a.right[rs * a.heads + h] = acc[4 + q];
+                    }
                 }
             }
         }
