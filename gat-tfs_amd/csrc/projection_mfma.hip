@@ -130,6 +130,7 @@ __global__ void __launch_bounds__(kThreads) k_proj_mfma(ProjArgs a) {
 // Z leaves as two 16-byte stores per block.
 template <int KS, int HB, bool F32IN, bool FULL>
 __global__ void __launch_bounds__(kThreads) k_proj_fast(ProjArgs a) {
+    static_assert(!FULL || HB == 8, "FULL layers are 8 heads x 32");
     constexpr int NB = HB + 1;
     extern __shared__ uint4 wlds[];
     for (int q = threadIdx.x; q < KS * NB * kWave; q += kThreads) {
@@ -290,9 +291,13 @@ __global__ void __launch_bounds__(kThreads) k_proj_fast(ProjArgs a) {
                 }
             }
         }
-        if (FULL && a.r_from_z && half == 0)
-#pragma unroll
-            for (int mb = 0; mb < HB; ++mb) a.right[rs * a.heads + mb] = rz[mb];
+        if constexpr (FULL) {
+            // 8 heads: R of the row as two 16-byte vectors
+            if (a.r_from_z && half == 0) {
+                *reinterpret_cast<float4*>(a.right + rs * 8) = make_float4(rz[0], rz[1], rz[2], rz[3]);
+                *reinterpret_cast<float4*>(a.right + rs * 8 + 4) = make_float4(rz[4], rz[5], rz[6], rz[7]);
+            }
+        }
 #pragma unroll
         for (int ks = KA; ks < KS; ++ks) load_ks(next, ks);
     }
