@@ -67,6 +67,8 @@ def test_degree_schedule_bit_exact(gpu_ctx, case):
 
 # ---------------------------------------------------------------- boundary shapes
 SHAPES = [(D, K, d) for D in (17, 33, 128, 256) for K in (1, 2, 4, 8) for d in (7, 32, 40, 47)]
+# The other input widths of the FP32 MFMA projection (D = 2 KH, KH = 16, 32, 48, 96), up to 8 x 64.
+SHAPES += [(32, 8, 32), (64, 4, 40), (96, 8, 64), (192, 2, 47), (192, 1, 64), (256, 8, 64)]
 
 
 @pytest.mark.parametrize("D,K,d", SHAPES)
