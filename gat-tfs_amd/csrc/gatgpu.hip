@@ -82,9 +82,13 @@ struct LayerState {
 // min) by the smallest power of two that keeps the heaviest row within
 // kMaxChunksPerRow chunks: each chunk reduces the maxima of all chunks of its
 // row and the last one adds all partial sums, so many chunks per row cost
-// more than they balance.  On the 100M-edge R-MAT graph (max in-degree
-// 132 270) that gives 6144/2048 (8-head) and 4096/2048 (one head), the best
-// of a measured sweep there.
+// more than they balance.  The 8-head kernel (one row per wave) scales min
+// with the chunk; the sum form (32-row tiles) and the one-head kernel (8 rows
+// per wave) hold a heavy row's neighbours at the same pace, and split from
+// twice the chunk instead.  On the 100M-edge R-MAT graph (max in-degree
+// 132 270) that gives 6144/2048 (8-head) and 4096/2048 (sum form, one head),
+// the best of measured sweeps there (sum form: 7.4 ms against 8.4 at
+// 8192/2048).
 enum { kPlanAf = 0, kPlanVec = 1, kPlanOne = 2, kPlans = 3 };
 constexpr uint32_t kPlanMin[kPlans] = {1024, 1536, 2048};
 constexpr uint32_t kPlanChunk[kPlans] = {256, 512, 1024};
@@ -181,7 +185,8 @@ int compute_bins(gatgpu_ctx* c) {
         const uint32_t min0 = small ? kSmallPlanMin : kPlanMin[q], chunk0 = small ? kSmallPlanChunk : kPlanChunk[q];
         uint32_t f = 1;
         while (uint64_t(chunk0) * f * kMaxChunksPerRow < maxdeg && f < (1u << 12)) f *= 2;
-        P.min = c->split_min ? c->split_min : min0 * f;
+        const uint32_t min_scaled = q == kPlanVec ? min0 * f : std::max(min0, 2 * chunk0 * f);
+        P.min = c->split_min ? c->split_min : min_scaled;
         P.chunk = c->split_chunk ? c->split_chunk : chunk0 * f;
         thr[2 + q] = P.min - 1;
     }

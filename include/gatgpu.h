@@ -110,10 +110,12 @@ enum {
     GATGPU_OPT_SPLIT_ROW_MIN_DEGREE = 2, /* rows at/above are split over waves
                                             (default per kernel: 1024 sum form,
                                             1536 8-head, 2048 one-head; 512 on
-                                            graphs below 16M edges; both
-                                            defaults doubled until the heaviest
-                                            row has <= 96 chunks; a value
-                                            applies to all, 0 restores them)  */
+                                            graphs below 16M edges; chunks
+                                            doubled until the heaviest row has
+                                            <= 96 of them, the degree with them
+                                            (8-head) or at least 2 chunks (the
+                                            others); a value applies to all,
+                                            0 restores them)                  */
     GATGPU_OPT_SPLIT_CHUNK_EDGES = 3,    /* edges per split chunk (default per
                                             kernel: 256, 512, 1024; 256 below
                                             16M edges; scaled as above; a value
