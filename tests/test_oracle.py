@@ -114,6 +114,50 @@ def test_bf16_chain_matches_reference_log(boundary_model_stages):
     assert e["relative_l2"] == pytest.approx(0.004291375487, rel=1e-2)
 
 
+# standard_fp32 against R0 in the same correctness.log: (layer, stage) -> (max_abs, relative_l2).
+# Both projections are the same FP32 GEMM there (Z error 0); the other stages
+# differ by FP32 summation order only.
+REF_LOG_FP32 = {
+    (1, "left"): (1.192092896e-07, 1.183600213e-07), (1, "right"): (1.490116119e-07, 1.396092515e-07),
+    (1, "max"): (1.937150955e-07, 1.197095449e-07), (1, "den"): (2.288818359e-05, 8.52657852e-08),
+    (1, "out"): (3.725290298e-07, 4.71836136e-07),
+    (2, "left"): (5.960464478e-08, 9.68646956e-08), (2, "right"): (1.192092896e-07, 1.204838034e-07),
+    (2, "max"): (1.490116119e-07, 1.150838718e-07), (2, "den"): (3.814697266e-05, 1.179198227e-07),
+    (2, "out"): (2.682209015e-07, 8.086332288e-07),
+    (3, "left"): (2.607703209e-08, 2.749406484e-07), (3, "right"): (2.980232239e-08, 1.197223014e-07),
+    (3, "max"): (2.235174179e-08, 1.857700975e-07), (3, "den"): (1.907348633e-06, 1.676655795e-08),
+    (3, "out"): (2.086162567e-07, 2.150315736e-07),
+}
+
+
+def test_b0_fp32_matches_reference_log():
+    """The oracle's B0 in FP32 mode (the CPU baseline of --precision fp32)
+    against R0 on the boundary graph, as the reference's correctness mode
+    logs standard_fp32: Z equal bit for bit (both are the same ascending-k
+    FP32 dot), every other stage within 10x of the logged summation-order
+    error (a bf16 rounding, a dropped term or a wrong head moves them by
+    orders of magnitude: the bf16 path's are ~2e-3), and the three-layer
+    chain within 10x of the logged standard_fp32 model_path_specific_chain
+    (max_abs 2.384e-07, relative_l2 8.833e-07)."""
+    g = oracle.boundary_graph(128)
+    m = oracle.random_model(128, 40, 11)
+    x = g["x"]
+    xb = g["x"]
+    for l, p in enumerate(m):
+        r = oracle.ref_layer(g["row"], g["col"], x, p, l < 2)
+        s, _ = oracle.standard_layer(g["row"], g["col"], x, p, l < 2, bf16=False)
+        assert np.array_equal(r["z"], s["z"]), l
+        for stage in ("left", "right", "max", "den", "out"):
+            ref_max, ref_rel = REF_LOG_FP32[(l + 1, stage)]
+            e = oracle.errors(r[stage], s[stage])
+            assert e["finite"] and e["max_abs"] <= 10 * ref_max + 1e-12, (l, stage, e)
+            assert e["relative_l2"] <= 10 * ref_rel + 1e-12, (l, stage, e)
+        xb = oracle.standard_layer(g["row"], g["col"], xb, p, l < 2, bf16=False)[0]["out"].copy()
+        x = r["out"]
+    e = oracle.errors(x, xb)
+    assert e["max_abs"] <= 10 * 2.384185791e-07 and e["relative_l2"] <= 10 * 8.833375272e-07, e
+
+
 SHAPES = [(D, K, d) for D in (17, 33, 128, 256) for K in (1, 2, 4, 8) for d in (7, 32, 40, 47)]
 
 
