@@ -558,11 +558,19 @@ __global__ void __launch_bounds__(kChunkThreads) k_afs_merge(AfsArgs a) {
                 t[h][1] += v[h].y;
             }
         }
+        // bf16-stored hidden outputs: S enters the projection as one bf16, as
+        // in the tile path (the rounding of a bf16 projection input).
+        const bool round_s = a.outbf != nullptr;
 #pragma unroll
         for (int h = 0; h < 8; ++h) {
             const float inv = dall[h] > 0.0f ? 1.0f / dall[h] : 0.0f;
-            s[w][h * 128 + 2 * l] = t[h][0] * inv;
-            s[w][h * 128 + 2 * l + 1] = t[h][1] * inv;
+            float s0 = t[h][0] * inv, s1 = t[h][1] * inv;
+            if (round_s) {
+                s0 = bf16_widen(bf16_hw(s0));
+                s1 = bf16_widen(bf16_hw(s1));
+            }
+            s[w][h * 128 + 2 * l] = s0;
+            s[w][h * 128 + 2 * l + 1] = s1;
         }
     }
     wave_sync();

@@ -3,144 +3,22 @@
 #include "gatgpu.h"
 
 #include <algorithm>
+#include <chrono>
 #include <cmath>
 #include <cstdio>
 #include <cstring>
 #include <string>
 #include <vector>
 
-#include "internal.hpp"
+#include "context.hpp"
 
 using namespace gatgpu;
 
 namespace {
-
 std::string g_create_error;  // message for failures before a context exists
-
-struct DevBuf {
-    void* p = nullptr;
-    size_t bytes = 0;
-    DevBuf() = default;
-    DevBuf(const DevBuf&) = delete;
-    DevBuf& operator=(const DevBuf&) = delete;
-    ~DevBuf() { release(); }
-    void release() {
-        if (p) (void)hipFree(p);
-        p = nullptr;
-        bytes = 0;
-    }
-    // Grows to at least `b` bytes; contents are not preserved.
-    hipError_t ensure(size_t b) {
-        if (b <= bytes && p) return hipSuccess;
-        release();
-        if (b == 0) b = 1;
-        hipError_t e = hipMalloc(&p, b);
-        if (e == hipSuccess) bytes = b;
-        else p = nullptr;
-        return e;
-    }
-    template <class T>
-    T* as() const {
-        return static_cast<T*>(p);
-    }
-};
-
-struct LayerState {
-    bool set = false;
-    int in = 0, heads = 0, dim = 0;
-    std::vector<float> w_host;
-    DevBuf w32, wq32, al, ar, blr;
-    DevBuf wpk32;  // FP32 MFMA fragments (projection_f32_supported shapes), else empty
-    DevBuf z32, zbf, zscratch, left, right, mx, den, out32, outbf, in32, inbf;
-    // What the last forward of this layer produced.
-    bool ran = false, z_valid = false, out32_valid = false, outbf_valid = false;
-    bool out_original = false;  // out32 rows in original node order (else sorted order)
-    int precision = -1;
-    // bf16 MFMA projection weights (pack_projection_weights order)
-    DevBuf wpk;
-    int ksteps = 0, groups = 0, nmb = 0;
-    // L/R-only block for the aggregate-first front end
-    DevBuf wlr;
-    int lr_ksteps = 0;
-    int dataflow = 0;  // dataflow of the last forward
-    // fixed-p fixture: p in degree-sorted edge order [e][heads], den [n][heads]
-    DevBuf fixp, fixden;
-    bool fixed_set = false;
-    int width() const { return heads * dim; }
-};
-
-// Split rows: rows of in-degree >= min are cut into chunks of `chunk` edges
-// on separate waves.  Each aggregation family has its own plan; the values
-// below were measured best on the 64.3M-edge power-law graph
-// (100 -> 8x32 -> 8x32 -> 1x47, max in-degree 17 000): the sum form keeps
-// many short chunks, the one-row-per-wave 8-head kernel fewer, longer ones,
-// and the one-head kernel (8 rows per wave) splits only its heaviest rows.
-// Small graphs (below kSmallGraphEdges edges) split more rows into shorter
-// chunks, 512/256 for every kernel: their heaviest rows are a larger share of
-// a short launch (169K-node, 2.5M-edge power-law graph: 0.88 ms against 1.23
-// with the plans above).  Graphs with heavier rows scale a plan (chunk and
-// min) by the smallest power of two that keeps the heaviest row within
-// kMaxChunksPerRow chunks: each chunk reduces the maxima of all chunks of its
-// row and the last one adds all partial sums, so many chunks per row cost
-// more than they balance.  The 8-head kernel (one row per wave) scales min
-// with the chunk; the sum form (32-row tiles) and the one-head kernel (8 rows
-// per wave) hold a heavy row's neighbours at the same pace, and split from
-// twice the chunk instead.  On the 100M-edge R-MAT graph (max in-degree
-// 132 270) that gives 6144/2048 (8-head) and 4096/2048 (sum form, one head),
-// the best of measured sweeps there (sum form: 7.4 ms against 8.4 at
-// 8192/2048).
-enum { kPlanAf = 0, kPlanVec = 1, kPlanOne = 2, kPlans = 3 };
-constexpr uint32_t kPlanMin[kPlans] = {1024, 1536, 2048};
-constexpr uint32_t kPlanChunk[kPlans] = {256, 512, 1024};
-constexpr uint64_t kSmallGraphEdges = 16u << 20;
-constexpr uint32_t kSmallPlanMin = 512, kSmallPlanChunk = 256;
-constexpr uint64_t kMaxChunksPerRow = 96;
-struct SplitPlan {
-    uint32_t min = 0, chunk = 0;
-    RowBins bins;        // split_begin: first split row (sorted position)
-    SplitTable table;
-    DevBuf k, first, mchunk, part, counter;
-};
-
 }  // namespace
 
-struct gatgpu_ctx {
-    int device = 0;
-    hipStream_t stream = nullptr;
-    std::string err;
-    // graph and schedule
-    bool graph = false;
-    uint64_t n = 0, e = 0;
-    DevBuf row, col, keys_a, keys_b, vals_a, vals_b, hist, scan_tmp, prow, pcol, small;
-    uint32_t* sorted_deg = nullptr;
-    uint32_t* perm = nullptr;     // sorted position -> original node
-    // Node-indexed device state (features, Z, L, R, max, den, outputs) is kept
-    // in sorted node order: node k is original node perm[k], rcol holds the
-    // sorted CSR's sources as sorted positions, and the kernels get the
-    // identity as their row permutation.  Inputs are gathered into this order
-    // when they are uploaded and outputs are put back in original order.
-    DevBuf invperm, ident, rcol, logits;
-    std::vector<uint32_t> perm_h;
-    uint64_t neighbor_steps = 0;
-    uint32_t max_degree = 0;
-    RowBins bins;
-    // input
-    bool input = false;
-    int din = 0;
-    DevBuf x32, xbf;
-    DevBuf xorig;  // the features in original node order (x32 is their sorted-order copy)
-    LayerState L[3];
-    // options (in-degree thresholds)
-    uint32_t small_max = 0;          // rows <= this share a wave (0: off)
-    uint32_t block_min = 512;        // rows >= this take a block
-    uint32_t split_min = 0;            // user option: rows >= this are split (0: per-kernel defaults)
-    uint32_t split_chunk = 0;          // user option: edges per chunk (0: per-kernel defaults)
-    SplitPlan plans[kPlans];
-    hipEvent_t ev[16] = {};
-    int cus = 256;  // compute units of the device
-};
-
-namespace {
+namespace gatgpu {
 
 int fail(gatgpu_ctx* c, int code, const std::string& msg) {
     if (c) c->err = msg;
@@ -151,11 +29,25 @@ int hip_fail(gatgpu_ctx* c, const char* what, hipError_t e) {
     return fail(c, e == hipErrorOutOfMemory ? GATGPU_ENOMEM : GATGPU_EDEVICE,
                 std::string(what) + ": " + hipGetErrorString(e));
 }
-#define HIPCHECK(ctx, expr)                                         \
-    do {                                                            \
-        hipError_t _e = (expr);                                     \
-        if (_e != hipSuccess) return hip_fail((ctx), #expr, _e);    \
-    } while (0)
+
+// Row stride (elements) of Z.  bf16: a multiple of 8 for 16-byte vector
+// stores; a single-head layer with at most 60 features gets a 128-byte row
+// (one cache line per gather) whose last 4 bytes hold R.  FP32: a multiple of 4.
+int z_stride(int precision, int heads, int width, bool* r_in_z) {
+    const bool rz = precision == GATGPU_BF16 && heads == 1 && width <= 60;
+    if (r_in_z) *r_in_z = rz;
+    if (rz) return 64;
+    return precision == GATGPU_BF16 ? (width + 7) / 8 * 8 : (width + 3) / 4 * 4;
+}
+
+}  // namespace gatgpu
+
+namespace {
+
+using Clock = std::chrono::steady_clock;
+double ms_wall(Clock::time_point a, Clock::time_point b) {
+    return std::chrono::duration<double, std::milli>(b - a).count();
+}
 
 bool mul_overflows(uint64_t a, uint64_t b) { return b && a > UINT64_MAX / b; }
 
@@ -175,8 +67,8 @@ int bind(gatgpu_ctx* c) {
 
 // Sorted-position boundaries of the degree bins.
 int compute_bins(gatgpu_ctx* c) {
-    // Thresholds: shared-wave bin, block bin, then each plan's split degree.
-    uint32_t thr[2 + kPlans] = {c->small_max, c->block_min ? c->block_min - 1 : 0};
+    // Thresholds: block bin, then each plan's split degree.
+    uint32_t thr[1 + kPlans] = {c->block_min ? c->block_min - 1 : 0};
     uint32_t maxdeg = 0;  // degrees are sorted ascending
     if (c->n) HIPCHECK(c, hipMemcpy(&maxdeg, c->sorted_deg + (c->n - 1), 4, hipMemcpyDeviceToHost));
     const bool small = c->e < kSmallGraphEdges;
@@ -188,29 +80,27 @@ int compute_bins(gatgpu_ctx* c) {
         const uint32_t min_scaled = q == kPlanVec ? min0 * f : std::max(min0, 2 * chunk0 * f);
         P.min = c->split_min ? c->split_min : min_scaled;
         P.chunk = c->split_chunk ? c->split_chunk : chunk0 * f;
-        thr[2 + q] = P.min - 1;
+        thr[1 + q] = P.min - 1;
     }
-    // small (0) disables the shared-wave bin; block_min 0 means every row takes a block.
+    // block_min 0 means every row takes a block.
     HIPCHECK(c, c->small.ensure(128));
-    // small[]: [0,4) max degree, [8,16) neighbor steps, [16,36) thresholds, [40,80) positions
+    // small[]: [0,4) max degree, [8,16) neighbor steps, [16,32) thresholds, [40,72) positions
     uint32_t* dthr = reinterpret_cast<uint32_t*>(c->small.as<char>() + 16);
     uint64_t* dpos = reinterpret_cast<uint64_t*>(c->small.as<char>() + 40);
     HIPCHECK(c, hipMemcpyAsync(dthr, thr, sizeof(thr), hipMemcpyHostToDevice, c->stream));
-    HIPCHECK(c, launch_count_le(c->sorted_deg, c->n, dthr, 2 + kPlans, dpos, c->stream));
-    uint64_t pos[2 + kPlans];
+    HIPCHECK(c, launch_count_le(c->sorted_deg, c->n, dthr, 1 + kPlans, dpos, c->stream));
+    uint64_t pos[1 + kPlans];
     HIPCHECK(c, hipMemcpyAsync(pos, dpos, sizeof(pos), hipMemcpyDeviceToHost, c->stream));
     HIPCHECK(c, hipStreamSynchronize(c->stream));
     RowBins b;
     b.n = c->n;
-    b.small_end = c->small_max ? pos[0] : 0;
-    b.block_begin = c->block_min ? pos[1] : 0;
-    if (b.block_begin < b.small_end) b.block_begin = b.small_end;
+    b.block_begin = c->block_min ? pos[0] : 0;
     c->bins = b;
     std::vector<uint64_t> prow;
     for (int q = 0; q < kPlans; ++q) {
         SplitPlan& P = c->plans[q];
         P.bins = b;
-        P.bins.split_begin = pos[2 + q] < b.block_begin ? b.block_begin : pos[2 + q];
+        P.bins.split_begin = pos[1 + q] < b.block_begin ? b.block_begin : pos[1 + q];
         // Chunk table of the split rows, heaviest row first.
         const uint64_t split_begin = P.bins.split_begin;
         const uint64_t nsplit = b.n - split_begin;
@@ -299,16 +189,6 @@ int build_schedule(gatgpu_ctx* c) {
     return compute_bins(c);
 }
 
-// Row stride (elements) of Z.  bf16: a multiple of 8 for 16-byte vector
-// stores; a single-head layer with at most 60 features gets a 128-byte row
-// (one cache line per gather) whose last 4 bytes hold R.  FP32: a multiple of 4.
-int z_stride(int precision, int heads, int width, bool* r_in_z) {
-    const bool rz = precision == GATGPU_BF16 && heads == 1 && width <= 60;
-    if (r_in_z) *r_in_z = rz;
-    if (rz) return 64;
-    return precision == GATGPU_BF16 ? (width + 7) / 8 * 8 : (width + 3) / 4 * 4;
-}
-
 // AUTO selects aggregate-first where its sum form applies (bf16, 8 heads of
 // 32 or 64, D_in <= 128: it gathers 256-byte input rows, plus R from its own
 // array beyond 112 inputs, instead of 512- or 1024-byte Z rows) and the Z
@@ -359,6 +239,7 @@ int run_layer_af(gatgpu_ctx* c, int l, bool hidden, const float* src32, const ui
         srcbf = nullptr;
     }
     if (src32) HIPCHECK(c, Ls.inbf.ensure(n * xs * 2));
+    const bool rounds_input = src32 != nullptr;  // the rounded rows land in inbf
     // The fixed-p operator has no row max (the reference leaves it unset).
     if (fixed) HIPCHECK(c, hipMemsetAsync(Ls.mx.p, 0, n * K * 4, c->stream));
     // Sum form: the gather table is the bf16 input rows, with R in their tail
@@ -476,6 +357,8 @@ int run_layer_af(gatgpu_ctx* c, int l, bool hidden, const float* src32, const ui
     }
     if (ev_base >= 0) HIPCHECK(c, hipEventRecord(c->ev[ev_base + 3], c->stream));
     Ls.out_original = false;
+    Ls.xbf_valid = rounds_input;
+    Ls.xbf_stride = xs;
     Ls.ran = true;
     Ls.precision = GATGPU_BF16;
     Ls.dataflow = dataflow;
@@ -536,7 +419,7 @@ int run_layer(gatgpu_ctx* c, int l, int precision, int dataflow, bool hidden, co
               int ev_base, bool fixed = false, bool orig_out = false) {
     LayerState& Ls = c->L[l];
     const uint64_t n = c->n;
-    const int K = Ls.heads, dim = Ls.dim, W = Ls.width(), D = Ls.in;
+    const int K = Ls.heads, W = Ls.width(), D = Ls.in;
     // ---- input (explicit host input is uploaded before the timed region)
     const float* src32 = nullptr;
     const uint16_t* srcbf = nullptr;
@@ -572,8 +455,7 @@ int run_layer(gatgpu_ctx* c, int l, int precision, int dataflow, bool hidden, co
     // bf16 path: X as [n][xs] bf16 (xs = ksteps*16, zero-padded), Z as [n][zs]
     // bf16 (zs = W rounded up to 8 for aligned vector stores).
     const int xs = Ls.ksteps * 16;
-    bool r_in_z = false;
-    const int zs = z_stride(precision, K, W, &r_in_z);
+    const int zs = z_stride(precision, K, W, nullptr);
     if (bf16) {
         HIPCHECK(c, Ls.zbf.ensure(n * zs * 2));
         if (srcbf && D != xs) {  // chained bf16 input without the padded layout
@@ -586,8 +468,50 @@ int run_layer(gatgpu_ctx* c, int l, int precision, int dataflow, bool hidden, co
     } else {
         HIPCHECK(c, Ls.z32.ensure(n * zs * 4));
     }
+    TfBufs b;
+    b.pcol = c->rcol.as<uint32_t>();
+    b.perm = c->ident.as<uint32_t>();
+    b.left = Ls.left.as<float>();
+    b.right = Ls.right.as<float>();
+    b.mx = Ls.mx.as<float>();
+    b.den = Ls.den.as<float>();
+    b.z = bf16 ? Ls.zbf.p : Ls.z32.p;
+    b.xbf = Ls.inbf.as<uint16_t>();
+    b.out32 = want_outbf ? nullptr : Ls.out32.as<float>();
+    b.outbf = want_outbf ? Ls.outbf.as<uint16_t>() : nullptr;
+    b.fused_convert_ok = true;  // the context's FP32 buffers carry kF32Pad floats of padding
+    b.keep_xbf = c->keep_xbf;
+    // Layer 3's one-head kernel writes its FP32 rows straight to original rows.
+    if (orig_out && b.out32 && !fixed) b.out_perm = c->perm;
+    TfDone done;
+    if (int r = run_tf(c, l, precision, hidden, src32, srcbf, ev_base, fixed, b, &done)) return r;
+    Ls.ran = true;
+    Ls.precision = precision;
+    Ls.dataflow = GATGPU_TRANSFORM_FIRST;
+    Ls.z_valid = true;
+    Ls.out32_valid = !want_outbf;
+    Ls.outbf_valid = want_outbf;
+    Ls.out_original = done.out_perm_used;
+    Ls.xbf_valid = bf16 && src32 && (!done.fused_convert || c->keep_xbf);
+    Ls.xbf_stride = xs;
+    return GATGPU_OK;
+}
+
+}  // namespace
+
+namespace gatgpu {
+
+int run_tf(gatgpu_ctx* c, int l, int precision, bool hidden, const float* src32, const uint16_t* srcbf,
+           int ev_base, bool fixed, const TfBufs& b, TfDone* done) {
+    LayerState& Ls = c->L[l];
+    const uint64_t n = c->n;
+    const int K = Ls.heads, dim = Ls.dim, W = Ls.width(), D = Ls.in;
+    const bool bf16 = precision == GATGPU_BF16;
+    const int xs = Ls.ksteps * 16;
+    bool r_in_z = false;
+    const int zs = z_stride(precision, K, W, &r_in_z);
     // The fixed-p operator has no row max (the reference leaves it unset).
-    if (fixed) HIPCHECK(c, hipMemsetAsync(Ls.mx.p, 0, n * K * 4, c->stream));
+    if (fixed) HIPCHECK(c, hipMemsetAsync(b.mx, 0, n * K * 4, c->stream));
     if (ev_base >= 0) HIPCHECK(c, hipEventRecord(c->ev[ev_base], c->stream));
     // ---- projection arguments (bf16 path)
     ProjArgs pa{};
@@ -600,10 +524,10 @@ int run_layer(gatgpu_ctx* c, int l, int precision, int dataflow, bool hidden, co
     pa.nmb = Ls.nmb;
     pa.width = W;
     pa.heads = K;
-    pa.z = Ls.zbf.as<uint16_t>();
+    pa.z = static_cast<uint16_t*>(b.z);
     pa.zs = zs;
-    pa.left = Ls.left.as<float>();
-    pa.right = Ls.right.as<float>();
+    pa.left = b.left;
+    pa.right = b.right;
     pa.tiles = (n + 31) / 32;
     pa.r_in_z = r_in_z;
     pa.r_off = zs - 2;
@@ -612,19 +536,25 @@ int run_layer(gatgpu_ctx* c, int l, int precision, int dataflow, bool hidden, co
     // ---- convert (bf16 path, FP32 source only; a bf16 source was rounded in
     // the previous layer's epilogue, which equals convert() of that output).
     // Where the fast projection applies, the rounding happens in its loads.
-    const bool fused_convert = bf16 && src32 && D % 4 == 0 && projection_fp32_input(pa);  // 16-byte aligned rows
-    if (bf16 && src32 && !fused_convert) {
-        HIPCHECK(c, launch_to_bf16_pad(src32, Ls.inbf.as<uint16_t>(), n, D, xs, c->stream));
-        srcbf = Ls.inbf.as<uint16_t>();
+    const bool fused = bf16 && src32 && b.fused_convert_ok && D % 4 == 0 &&
+                       projection_fp32_input(pa);  // 16-byte aligned rows
+    if (done) done->fused_convert = fused;
+    if (bf16 && src32 && !fused) {
+        HIPCHECK(c, launch_to_bf16_pad(src32, b.xbf, n, D, xs, c->stream));
+        srcbf = b.xbf;
         src32 = nullptr;
     }
     if (ev_base >= 0) HIPCHECK(c, hipEventRecord(c->ev[ev_base + 1], c->stream));
     // ---- projection + L/R
     if (bf16) {
-        if (fused_convert) {
-            pa.x32 = src32;  // FP32 buffers of the context carry 16 floats of padding
+        if (fused) {
+            pa.x32 = src32;
             pa.xs = D;
             pa.in = D;
+            if (b.keep_xbf) {  // the rounded rows also leave the kernel
+                pa.xout = b.xbf;
+                pa.xouts = xs;
+            }
         } else {
             pa.x = srcbf;
         }
@@ -640,61 +570,61 @@ int run_layer(gatgpu_ctx* c, int l, int precision, int dataflow, bool hidden, co
         fa.head_blocks = (W + 31) / 32;
         fa.width = W;
         fa.heads = K;
-        fa.z = Ls.z32.as<float>();
+        fa.z = static_cast<float*>(b.z);
         fa.zs = zs;
-        fa.left = Ls.left.as<float>();
-        fa.right = Ls.right.as<float>();
+        fa.left = b.left;
+        fa.right = b.right;
         fa.tiles = (n + 31) / 32;
         HIPCHECK(c, launch_projection_f32(fa, c->stream));
     } else {
         HIPCHECK(c, launch_projection(src32, nullptr, Ls.w32.as<float>(), n, D, K, dim, Ls.al.as<float>(),
-                                      Ls.ar.as<float>(), Ls.z32.as<float>(), nullptr, Ls.left.as<float>(),
-                                      Ls.right.as<float>(), nullptr, zs, c->stream));
+                                      Ls.ar.as<float>(), static_cast<float*>(b.z), nullptr, b.left, b.right,
+                                      nullptr, zs, c->stream));
     }
     if (ev_base >= 0) HIPCHECK(c, hipEventRecord(c->ev[ev_base + 2], c->stream));
     // ---- fused prescan + softmax + aggregation + normalise + ELU
     AggArgs a{};
     a.prow = c->prow.as<uint64_t>();
-    a.pcol = c->rcol.as<uint32_t>();
-    a.perm = c->ident.as<uint32_t>();
-    a.left = Ls.left.as<float>();
-    a.right = Ls.right.as<float>();
-    a.feat = bf16 ? static_cast<const void*>(Ls.zbf.p) : Ls.z32.p;
+    a.pcol = b.pcol;
+    a.perm = b.perm;
+    a.left = b.left;
+    a.right = b.right;
+    a.feat = b.z;
     a.feat_bf16 = bf16;
     a.fstride = zs;
     a.r_in_feat = r_in_z;
     a.heads = K;
     a.dim = dim;
     a.hidden = hidden;
-    a.mx = Ls.mx.as<float>();
-    a.den = Ls.den.as<float>();
-    a.out32 = want_outbf ? nullptr : Ls.out32.as<float>();
-    a.outbf = want_outbf ? Ls.outbf.as<uint16_t>() : nullptr;
+    a.mx = b.mx;
+    a.den = b.den;
+    a.out32 = b.out32;
+    a.outbf = b.outbf;
     a.n = c->n;
     a.e = c->e;
     a.r_from_z = pa.r_from_z;
     a.ar = Ls.ar.as<float>();
-    const bool direct_orig = orig_out && a.out32 && !fixed && !aggregate_vec_supported(a) && aggregate_k1_supported(a);
-    if (direct_orig) a.out_perm = c->perm;
+    const bool one_head = !fixed && !aggregate_vec_supported(a) && aggregate_k1_supported(a);
+    if (one_head && a.out32) a.out_perm = b.out_perm;
+    if (done) done->out_perm_used = a.out_perm != nullptr;
     // The one-head kernel takes its own split plan; the 8-head, generic and
     // fixed-p kernels the 8-head one.
-    const SplitPlan& P = c->plans[!fixed && !aggregate_vec_supported(a) && aggregate_k1_supported(a) ? kPlanOne
-                                                                                                    : kPlanVec];
+    const SplitPlan& P = c->plans[one_head ? kPlanOne : kPlanVec];
+    SplitTable t = P.table;
+    if (b.mchunk) t.mchunk = b.mchunk;
+    if (b.part) t.part = b.part;
+    if (b.counter) t.counter = b.counter;
     if (fixed)
-        HIPCHECK(c, launch_aggregate_fixed(a, Ls.fixp.as<float>(), Ls.fixden.as<float>(), P.bins, P.table,
-                                           c->stream));
+        HIPCHECK(c, launch_aggregate_fixed(a, Ls.fixp.as<float>(), Ls.fixden.as<float>(), P.bins, t, c->stream));
     else
-        HIPCHECK(c, launch_aggregate_tf(a, P.bins, P.table, c->stream));
+        HIPCHECK(c, launch_aggregate_tf(a, P.bins, t, c->stream));
     if (ev_base >= 0) HIPCHECK(c, hipEventRecord(c->ev[ev_base + 3], c->stream));
-    Ls.ran = true;
-    Ls.precision = precision;
-    Ls.dataflow = GATGPU_TRANSFORM_FIRST;
-    Ls.z_valid = true;
-    Ls.out32_valid = !want_outbf;
-    Ls.outbf_valid = want_outbf;
-    Ls.out_original = direct_orig;
     return GATGPU_OK;
 }
+
+}  // namespace gatgpu
+
+namespace {
 
 void fill_times(gatgpu_ctx* c, int ev_base, gatgpu_times* t, int dataflow) {
     std::memset(t, 0, sizeof(*t));
@@ -707,6 +637,24 @@ void fill_times(gatgpu_ctx* c, int ev_base, gatgpu_times* t, int dataflow) {
     else t->projection_ms = ms_between(c->ev[ev_base + 1], c->ev[ev_base + 2]);
     t->aggregate_ms = ms_between(c->ev[ev_base + 2], c->ev[ev_base + 3]);
     t->total_ms = ms_between(c->ev[ev_base], c->ev[ev_base + 3]);
+}
+
+// Graph::validate (baseline/src/common.cpp:23-30) on the CSR arrays, plus
+// the limits of this build: n < 2^31, e <= 2^40, in-degrees below 2^32 (the
+// degree schedule sorts 32-bit degrees).  Rows are checked before sources.
+int validate_csr(gatgpu_ctx* c, uint64_t n, uint64_t e, const uint64_t* row, const uint32_t* col) {
+    if (!row || (e && !col)) return fail(c, GATGPU_EINVAL, "null CSR pointer");
+    if (n == 0 || n > uint64_t(INT32_MAX)) return fail(c, GATGPU_EINVAL, "invalid graph sizes");
+    if (e > (uint64_t(1) << 40)) return fail(c, GATGPU_EOVERFLOW, "edge count too large");
+    if (row[0] != 0 || row[n] != e) return fail(c, GATGPU_EINVAL, "bad CSR bounds");
+    for (uint64_t i = 0; i < n; ++i) {
+        if (row[i] > row[i + 1]) return fail(c, GATGPU_EINVAL, "nonmonotone CSR");
+        if (row[i + 1] - row[i] > UINT32_MAX)
+            return fail(c, GATGPU_EOVERFLOW, "in-degree of row " + std::to_string(i) + " exceeds 2^32 - 1");
+    }
+    for (uint64_t k = 0; k < e; ++k)
+        if (col[k] >= n) return fail(c, GATGPU_EINVAL, "source index out of bounds");
+    return GATGPU_OK;
 }
 
 int check_ctx(gatgpu_ctx* c) {
@@ -760,26 +708,30 @@ int gatgpu_destroy(gatgpu_ctx* c) {
 
 const char* gatgpu_last_error(const gatgpu_ctx* c) { return c ? c->err.c_str() : g_create_error.c_str(); }
 
+int gatgpu_validate_graph(uint64_t n, uint64_t e, const uint64_t* row, const uint32_t* col) {
+    return validate_csr(nullptr, n, e, row, col);
+}
+
 int gatgpu_set_graph(gatgpu_ctx* c, uint64_t n, uint64_t e, const uint64_t* row, const uint32_t* col) {
     if (int r = check_ctx(c)) return r;
-    if (!row || (e && !col)) return fail(c, GATGPU_EINVAL, "null CSR pointer");
-    if (n == 0 || n > uint64_t(INT32_MAX)) return fail(c, GATGPU_EINVAL, "invalid graph sizes");
-    if (e > (uint64_t(1) << 40)) return fail(c, GATGPU_EOVERFLOW, "edge count too large");
-    if (row[0] != 0 || row[n] != e) return fail(c, GATGPU_EINVAL, "bad CSR bounds");
-    for (uint64_t i = 0; i < n; ++i)
-        if (row[i] > row[i + 1]) return fail(c, GATGPU_EINVAL, "nonmonotone CSR");
-    for (uint64_t k = 0; k < e; ++k)
-        if (col[k] >= n) return fail(c, GATGPU_EINVAL, "source index out of bounds");
+    auto t0 = Clock::now();
+    if (int r = validate_csr(c, n, e, row, col)) return r;
     if (c->input && c->n != n) c->input = false;
     c->graph = false;
     for (auto& L : c->L) L.ran = L.fixed_set = false;
     c->n = n;
     c->e = e;
+    auto t1 = Clock::now();
     HIPCHECK(c, c->row.ensure((n + 1) * 8));
     HIPCHECK(c, c->col.ensure(e * 4));
     HIPCHECK(c, hipMemcpyAsync(c->row.p, row, (n + 1) * 8, hipMemcpyHostToDevice, c->stream));
     if (e) HIPCHECK(c, hipMemcpyAsync(c->col.p, col, e * 4, hipMemcpyHostToDevice, c->stream));
+    HIPCHECK(c, hipStreamSynchronize(c->stream));
+    auto t2 = Clock::now();
     if (int r = build_schedule(c)) return r;
+    c->st.graph_check_ms = ms_wall(t0, t1);
+    c->st.graph_h2d_ms = ms_wall(t1, t2);
+    c->st.degree_sort_ms = ms_wall(t2, Clock::now());
     c->graph = true;
     if (c->input)  // the features follow the new node order
         if (int r = sort_features(c)) return r;
@@ -789,6 +741,7 @@ int gatgpu_set_graph(gatgpu_ctx* c, uint64_t n, uint64_t e, const uint64_t* row,
 int gatgpu_set_layer(gatgpu_ctx* c, int layer, int in, int heads, int dim, const float* w,
                      const float* al, const float* ar) {
     if (int r = check_ctx(c)) return r;
+    const auto t0 = Clock::now();
     if (layer < 0 || layer > 2) return fail(c, GATGPU_EINVAL, "layer must be 0, 1 or 2");
     if (in <= 0 || heads <= 0 || heads > 8 || dim <= 0 || dim > 64)
         return fail(c, GATGPU_EINVAL, "invalid parameter shape (heads <=8, head_dim <=64)");
@@ -846,6 +799,10 @@ int gatgpu_set_layer(gatgpu_ctx* c, int layer, int in, int heads, int dim, const
     }
     HIPCHECK(c, hipStreamSynchronize(c->stream));
     L.set = true;
+    L.prepare_ms = ms_wall(t0, Clock::now());
+    c->st.model_prepare_ms = 0;
+    for (const auto& q : c->L)
+        if (q.set) c->st.model_prepare_ms += q.prepare_ms;
     return GATGPU_OK;
 }
 
@@ -854,12 +811,17 @@ int gatgpu_set_input(gatgpu_ctx* c, uint64_t n, int din, const float* x) {
     if (!c->graph) return fail(c, GATGPU_ESTATE, "graph not set");
     if (n != c->n || din <= 0 || !x) return fail(c, GATGPU_EINVAL, "feature matrix does not match the graph");
     if (mul_overflows(n, uint64_t(din) * 4)) return fail(c, GATGPU_EOVERFLOW, "size overflow");
+    const auto t0 = Clock::now();
     uint64_t bad = 0;
     if (!all_finite(x, n * din, &bad)) return fail(c, GATGPU_ENONFINITE, "nonfinite graph input index=" + std::to_string(bad));
     HIPCHECK(c, c->xorig.ensure(n * din * 4));
     HIPCHECK(c, hipMemcpyAsync(c->xorig.p, x, n * din * 4, hipMemcpyHostToDevice, c->stream));
+    HIPCHECK(c, hipStreamSynchronize(c->stream));
+    const auto t1 = Clock::now();
     c->din = din;
     if (int r = sort_features(c)) return r;
+    c->st.input_h2d_ms = ms_wall(t0, t1);
+    c->st.input_permute_ms = ms_wall(t1, Clock::now());
     c->input = true;
     c->L[0].ran = false;
     return GATGPU_OK;
@@ -1017,7 +979,17 @@ int gatgpu_model_forward(gatgpu_ctx* c, int precision, int dataflow, float* logi
     if (times)
         for (int l = 0; l < 3; ++l) fill_times(c, 4 * l, &times[l], c->L[l].dataflow);
     if (total_ms) *total_ms = ms_between(c->ev[0], c->ev[12]);
-    if (logits) HIPCHECK(c, hipMemcpy(logits, logits_dev, c->n * C * 4, hipMemcpyDeviceToHost));
+    if (logits) {
+        const auto t0 = Clock::now();
+        HIPCHECK(c, hipMemcpy(logits, logits_dev, c->n * C * 4, hipMemcpyDeviceToHost));
+        c->st.logits_d2h_ms = ms_wall(t0, Clock::now());
+    }
+    return GATGPU_OK;
+}
+
+int gatgpu_get_static_times(gatgpu_ctx* c, gatgpu_static_times* out) {
+    if (!c || !out) return fail(c, GATGPU_EINVAL, "null argument");
+    *out = c->st;
     return GATGPU_OK;
 }
 
@@ -1039,6 +1011,9 @@ int gatgpu_stage_size(gatgpu_ctx* c, int layer, int which, uint64_t* count) {
             break;
         case GATGPU_STAGE_OUT:
             *count = c->n * L.width();
+            break;
+        case GATGPU_STAGE_XBF:
+            *count = L.xbf_valid ? c->n * L.in : 0;
             break;
         default:
             return fail(c, GATGPU_EINVAL, "bad stage selector");
@@ -1067,12 +1042,19 @@ int gatgpu_get_stage(gatgpu_ctx* c, int layer, int which, float* host) {
             bf = !L.out32_valid;
             src = bf ? L.outbf.p : L.out32.p;
             break;
+        case GATGPU_STAGE_XBF:
+            bf = true;
+            src = L.inbf.p;
+            break;
     }
     // Device stages are in sorted node order; rows go back to original order.
     const int W = L.width();
-    const int width = (which == GATGPU_STAGE_Z || which == GATGPU_STAGE_OUT) ? W : L.heads;
-    const uint64_t stride = which == GATGPU_STAGE_Z ? uint64_t(z_stride(bf ? GATGPU_BF16 : GATGPU_FP32, L.heads, W, nullptr))
-                                                    : uint64_t(width);
+    const int width = which == GATGPU_STAGE_XBF                             ? L.in
+                      : (which == GATGPU_STAGE_Z || which == GATGPU_STAGE_OUT) ? W
+                                                                               : L.heads;
+    const uint64_t stride = which == GATGPU_STAGE_Z   ? uint64_t(z_stride(bf ? GATGPU_BF16 : GATGPU_FP32, L.heads, W, nullptr))
+                            : which == GATGPU_STAGE_XBF ? uint64_t(L.xbf_stride)
+                                                        : uint64_t(width);
     if (which == GATGPU_STAGE_OUT && !bf && L.out_original) {
         HIPCHECK(c, hipMemcpy(host, src, count * 4, hipMemcpyDeviceToHost));
     } else if (bf) {
@@ -1099,7 +1081,10 @@ int gatgpu_set_option(gatgpu_ctx* c, int key, int64_t value) {
             if (value != 0 && value < 64) return fail(c, GATGPU_EINVAL, "split chunk must be >= 64 edges");
             c->split_chunk = uint32_t(value);
             break;
-        case GATGPU_OPT_SMALL_ROW_MAX_DEGREE: c->small_max = uint32_t(value); break;
+        case GATGPU_OPT_KEEP_INPUT_BF16:
+            if (value > 1) return fail(c, GATGPU_EINVAL, "keep-input option is 0 or 1");
+            c->keep_xbf = value != 0;
+            return GATGPU_OK;
         default: return fail(c, GATGPU_EINVAL, "unknown option");
     }
     if (c->graph) return compute_bins(c);

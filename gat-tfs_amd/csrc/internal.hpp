@@ -151,8 +151,8 @@ struct ProjArgs {
     uint64_t tiles;      // ceil(n / 32)
     bool r_in_z;         // also store R of head h as FP32 in z[row][r_off + 2h ..]
     int r_off;           // bf16 offset of R in the z row when r_in_z (one head: zs - 2)
-    uint16_t* xout;      // FP32 input, L/R only (head_blocks 0): also store the rounded
-    int xouts;           // bf16 input rows, features [0, 16 ksteps), at xout[row * xouts]
+    uint16_t* xout;      // FP32 input (or null): also store the rounded bf16 input
+    int xouts;           // rows, features [0, 16 ksteps), at xout[row * xouts]
     bool r_from_z;       // bf16 8 x 32 or one head x 64: R = Z_bf16 . aR (the aggregation recomputes it)
     const float* ar;     // aR [256] when r_from_z
 };
@@ -192,10 +192,10 @@ void pack_projection_f32(const float* w, const float* blr, int in, int heads, in
 
 // aggregate.hip
 struct RowBins {
-    // Sorted positions [0, n) split by degree: [0, small_end) share waves,
-    // [small_end, block_begin) one wave per row, [block_begin, split_begin)
-    // one block per row, [split_begin, n) several blocks per row.
-    uint64_t small_end = 0, block_begin = 0, split_begin = 0, n = 0;
+    // Sorted positions [0, n) split by degree: [0, block_begin) one wave per
+    // row, [block_begin, split_begin) one block per row, [split_begin, n)
+    // several blocks per row.
+    uint64_t block_begin = 0, split_begin = 0, n = 0;
 };
 struct AggArgs {
     const uint64_t* prow;

@@ -202,7 +202,7 @@ __global__ void __launch_bounds__(kThreads) k_proj_fast(ProjArgs a) {
         const uint64_t rs = row < a.n ? row : a.n - 1;  // lanes past n repeat row n - 1
         auto kstep = [&](int ks) {
             const bf16x8 b = operand(ks);
-            if constexpr (F32IN && HB == 0) {
+            if constexpr (F32IN) {
                 if (a.xout)
                     *reinterpret_cast<uint4*>(a.xout + rs * a.xouts + 16 * ks + 8 * half) = __builtin_bit_cast(uint4, b);
             }
@@ -349,6 +349,8 @@ __global__ void __launch_bounds__(kWideThreads) k_proj_wide(ProjArgs a) {
                 w4[x] = bf16x2(f0 + 2 * x < a.in ? __builtin_bit_cast(float, e[2 * x]) : 0.0f,
                                f0 + 2 * x + 1 < a.in ? __builtin_bit_cast(float, e[2 * x + 1]) : 0.0f);
             xr[ks] = __builtin_bit_cast(bf16x8, make_uint4(w4[0], w4[1], w4[2], w4[3]));
+            if (a.xout)  // the rounded rows also leave the kernel (lanes past n rewrite row n - 1)
+                *reinterpret_cast<uint4*>(a.xout + rs * a.xouts + f0) = make_uint4(w4[0], w4[1], w4[2], w4[3]);
         }
     } else {
         const uint16_t* p = a.x + rs * a.xs + 8 * half;

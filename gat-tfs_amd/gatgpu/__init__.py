@@ -19,11 +19,11 @@ LIB_PATH = PKG_ROOT / "lib" / "libgatgpu.so"
 OK, EINVAL, ESTATE, ENODEV, ENOMEM, EDEVICE, ENONFINITE, EOVERFLOW = 0, -1, -2, -3, -4, -5, -6, -7
 FP32, BF16 = 0, 1
 AUTO, TRANSFORM_FIRST, AGGREGATE_FIRST, TFS_B1 = 0, 1, 2, 3
-STAGE_Z, STAGE_LEFT, STAGE_RIGHT, STAGE_MAX, STAGE_DEN, STAGE_OUT = range(6)
-OPT_BLOCK_ROW_MIN_DEGREE, OPT_SPLIT_ROW_MIN_DEGREE, OPT_SPLIT_CHUNK_EDGES, OPT_SMALL_ROW_MAX_DEGREE = 1, 2, 3, 4
+STAGE_Z, STAGE_LEFT, STAGE_RIGHT, STAGE_MAX, STAGE_DEN, STAGE_OUT, STAGE_XBF = range(7)
+OPT_BLOCK_ROW_MIN_DEGREE, OPT_SPLIT_ROW_MIN_DEGREE, OPT_SPLIT_CHUNK_EDGES, OPT_KEEP_INPUT_BF16 = 1, 2, 3, 5
 
 STAGE_NAMES = {"z": STAGE_Z, "left": STAGE_LEFT, "right": STAGE_RIGHT, "max": STAGE_MAX,
-               "den": STAGE_DEN, "out": STAGE_OUT}
+               "den": STAGE_DEN, "out": STAGE_OUT, "xbf": STAGE_XBF}
 
 # Every symbol include/gatgpu.h declares.
 EXPORTS = (
@@ -31,6 +31,7 @@ EXPORTS = (
     "gatgpu_set_input", "gatgpu_degree_schedule", "gatgpu_permuted_csr", "gatgpu_choose_R",
     "gatgpu_layer_forward", "gatgpu_model_forward", "gatgpu_get_stage", "gatgpu_stage_size",
     "gatgpu_set_option", "gatgpu_synchronize", "gatgpu_stream", "gatgpu_set_fixed_p", "gatgpu_fixed_p_forward",
+    "gatgpu_get_static_times", "gatgpu_validate_graph",
 )
 
 
@@ -39,6 +40,16 @@ class Times(ctypes.Structure):
     _fields_ = [(name, ctypes.c_double) for name in (
         "convert_ms", "projection_ms", "lr_ms", "max_prescan_ms", "aggregate_ms", "normalize_ms",
         "activation_ms", "total_ms")]
+
+    def as_dict(self):
+        return {name: getattr(self, name) for name, _ in self._fields_}
+
+
+class StaticTimes(ctypes.Structure):
+    """gatgpu_static_times: wall times (ms) of the static, untimed steps."""
+    _fields_ = [(name, ctypes.c_double) for name in (
+        "graph_check_ms", "graph_h2d_ms", "degree_sort_ms", "model_prepare_ms", "input_h2d_ms",
+        "input_permute_ms", "logits_d2h_ms")]
 
     def as_dict(self):
         return {name: getattr(self, name) for name, _ in self._fields_}
@@ -83,6 +94,8 @@ def load_library(path: os.PathLike | None = None):
     L.gatgpu_set_fixed_p.argtypes = [P, i32, P, P]
     L.gatgpu_fixed_p_forward.argtypes = [P, i32, i32, i32, P, P]
     L.gatgpu_stream.restype = P
+    L.gatgpu_get_static_times.argtypes = [P, ctypes.POINTER(StaticTimes)]
+    L.gatgpu_validate_graph.argtypes = [u64, u64, P, P]
     for name in EXPORTS:
         if name not in ("gatgpu_last_error", "gatgpu_stream"):
             getattr(L, name).restype = i32
@@ -93,6 +106,19 @@ def load_library(path: os.PathLike | None = None):
 
 def _ptr(a):
     return None if a is None else a.ctypes.data
+
+
+def validate_graph(row, col, n=None, e=None):
+    """gatgpu_validate_graph: raises GatGpuError for a CSR set_graph would
+    reject (no device needed).  n and e default to the arrays' sizes."""
+    L = load_library()
+    row = np.ascontiguousarray(row, np.uint64)
+    col = np.ascontiguousarray(col, np.uint32)
+    n = row.size - 1 if n is None else n
+    e = col.size if e is None else e
+    rc = L.gatgpu_validate_graph(n, e, _ptr(row), _ptr(col))
+    if rc != OK:
+        raise GatGpuError(rc, L.gatgpu_last_error(None).decode())
 
 
 class Context:
@@ -216,6 +242,11 @@ class Context:
         out = np.empty(cnt.value, np.float32)
         self._check(self.lib.gatgpu_get_stage(self.h, layer, code, _ptr(out)))
         return out.reshape(self.n, -1)
+
+    def static_times(self):
+        t = StaticTimes()
+        self._check(self.lib.gatgpu_get_static_times(self.h, ctypes.byref(t)))
+        return t.as_dict()
 
     def synchronize(self):
         self._check(self.lib.gatgpu_synchronize(self.h))

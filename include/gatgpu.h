@@ -86,7 +86,16 @@ enum {
     GATGPU_STAGE_RIGHT = 2,/* [n][heads]                                     */
     GATGPU_STAGE_MAX = 3,  /* [n][heads] exact row max M = leaky(L + max R)  */
     GATGPU_STAGE_DEN = 4,  /* [n][heads] sum of exp(score - M)               */
-    GATGPU_STAGE_OUT = 5   /* [n][heads*dim] normalised (+ELU) layer output  */
+    GATGPU_STAGE_OUT = 5,  /* [n][heads*dim] normalised (+ELU) layer output  */
+    GATGPU_STAGE_XBF = 6   /* [n][in] the layer input rounded to bf16, as
+                              convert() writes Workspace::xbf (common.cpp:
+                              85-93): bf16 layers whose FP32 input the layer
+                              rounds itself -- by the convert kernel, by the
+                              projection (kept only with option
+                              GATGPU_OPT_KEEP_INPUT_BF16) or into the
+                              aggregate-first gather table.  Absent for a
+                              chained bf16 input: that is the previous
+                              layer's OUT stage, rounded in its epilogue.  */
 };
 
 /* Per-layer stage times in milliseconds, measured with HIP events on the
@@ -120,7 +129,13 @@ enum {
                                             kernel: 256, 512, 1024; 256 below
                                             16M edges; scaled as above; a value
                                             >= 64 applies to all, 0 restores) */
-    GATGPU_OPT_SMALL_ROW_MAX_DEGREE = 4  /* rows at/below share one wave        */
+    /* 4 is not a key: rows of small degree take one wave each like the rest
+       (the one-head kernel already packs 8 rows of equal degree per wave). */
+    GATGPU_OPT_KEEP_INPUT_BF16 = 5       /* 1: bf16 transform-first layers also
+                                            store the input rows their
+                                            projection rounds (stage XBF);
+                                            0 (default): they are rounded in
+                                            registers only                    */
 };
 
 /* ---- lifetime -------------------------------------------------------- */
@@ -133,10 +148,15 @@ int gatgpu_destroy(gatgpu_ctx* ctx);
 const char* gatgpu_last_error(const gatgpu_ctx* ctx);
 
 /* ---- static inputs (untimed, like load_graph/prepare: baseline/README.md:52) ---- */
-/* Validates and uploads the CSR, then builds the degree schedule on the GPU.
- * Replaces load_graph + Graph::validate (baseline/src/common.cpp:23-39) and
- * degree_schedule (common.cpp:120-125).  Checks row[0]==0, row[n]==e,
- * monotone rows, col[k] < n, 0 < n <= INT32_MAX. */
+/* The host checks of gatgpu_set_graph without a context or device
+ * (Graph::validate, baseline/src/common.cpp:23-30): row[0] == 0, row[n] == e,
+ * monotone rows, col[k] < n, 0 < n <= INT32_MAX, e <= 2^40, and every
+ * in-degree below 2^32 (GATGPU_EOVERFLOW).  Rows are checked before sources.
+ * The message is gatgpu_last_error(NULL). */
+int gatgpu_validate_graph(uint64_t n, uint64_t e, const uint64_t* row, const uint32_t* col);
+/* Validates (as gatgpu_validate_graph) and uploads the CSR, then builds the
+ * degree schedule on the GPU.  Replaces load_graph + Graph::validate
+ * (baseline/src/common.cpp:23-39) and degree_schedule (common.cpp:120-125). */
 int gatgpu_set_graph(gatgpu_ctx* ctx, uint64_t n, uint64_t e, const uint64_t* row,
                      const uint32_t* col);
 /* Uploads one layer (0..2) of weights and prepares its bf16 copy.  Replaces
@@ -207,6 +227,23 @@ int gatgpu_fixed_p_forward(gatgpu_ctx* ctx, int layer, int precision, int datafl
 int gatgpu_get_stage(gatgpu_ctx* ctx, int layer, int which, float* host_out);
 /* Size in floats of a stage buffer (0 if absent). */
 int gatgpu_stage_size(gatgpu_ctx* ctx, int layer, int which, uint64_t* count);
+
+/* Wall-clock times (ms) of the static steps, outside every forward timer
+ * (the reference prints them as STATIC degree_sort_ms / model_prepare_ms and
+ * COLD startup_before_inference_ms, baseline/bench/main.cpp:56,168-169;
+ * baseline/README.md:52).  Each field holds its step's last run. */
+typedef struct gatgpu_static_times {
+    double graph_check_ms;   /* set_graph: host CSR validation (Graph::validate)      */
+    double graph_h2d_ms;     /* set_graph: rowptr and col upload                     */
+    double degree_sort_ms;   /* set_graph: degree schedule on the device (sort,
+                                permuted CSR, relabelling, split tables)             */
+    double model_prepare_ms; /* set_layer: checks, bf16 W, B_LR, fragment packing
+                                and upload, summed over the layers set             */
+    double input_h2d_ms;     /* set_input: feature checks and upload                 */
+    double input_permute_ms; /* set_input: features gathered into degree order       */
+    double logits_d2h_ms;    /* model_forward: the logits copied to the host         */
+} gatgpu_static_times;
+int gatgpu_get_static_times(gatgpu_ctx* ctx, gatgpu_static_times* out);
 
 /* ---- misc ------------------------------------------------------------ */
 int gatgpu_set_option(gatgpu_ctx* ctx, int key, int64_t value);
