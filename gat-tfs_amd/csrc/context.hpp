@@ -157,6 +157,7 @@ struct gatgpu_ctx {
     hipEvent_t ev[16] = {};
     int cus = 256;  // compute units of the device
     gatgpu_static_times st{};  // wall times of the static steps
+    void* scratch = nullptr;   // device address of this GPU's static scratch array (layer_static.hip)
 };
 
 namespace gatgpu {
@@ -185,5 +186,9 @@ struct TfDone {
 // fixed: the fixed-p operator (the layer's fixture p and den).
 int run_tf(gatgpu_ctx* c, int l, int precision, bool hidden, const float* src32, const uint16_t* srcbf,
            int ev_base, bool fixed, const TfBufs& b, TfDone* done);
+
+// Resolves the device address of the static scratch array of c->device
+// (layer_static.hip) once per device; the device must be current.
+int static_scratch_init(gatgpu_ctx* c);
 
 }  // namespace gatgpu

@@ -691,6 +691,11 @@ int gatgpu_create(int device, gatgpu_ctx** out) {
             gatgpu_destroy(c);
             return fail(nullptr, GATGPU_EDEVICE, "cannot create events");
         }
+    if (static_scratch_init(c) != GATGPU_OK) {
+        const std::string msg = c->err;
+        gatgpu_destroy(c);
+        return fail(nullptr, GATGPU_EDEVICE, msg);
+    }
     *out = c;
     return GATGPU_OK;
 }

@@ -22,6 +22,8 @@ AUTO, TRANSFORM_FIRST, AGGREGATE_FIRST, TFS_B1 = 0, 1, 2, 3
 STAGE_Z, STAGE_LEFT, STAGE_RIGHT, STAGE_MAX, STAGE_DEN, STAGE_OUT, STAGE_XBF = range(7)
 OPT_BLOCK_ROW_MIN_DEGREE, OPT_SPLIT_ROW_MIN_DEGREE, OPT_SPLIT_CHUNK_EDGES, OPT_KEEP_INPUT_BF16 = 1, 2, 3, 5
 
+STATIC_SCRATCH_BYTES = 64 << 20  # GATGPU_STATIC_SCRATCH_BYTES
+
 STAGE_NAMES = {"z": STAGE_Z, "left": STAGE_LEFT, "right": STAGE_RIGHT, "max": STAGE_MAX,
                "den": STAGE_DEN, "out": STAGE_OUT, "xbf": STAGE_XBF}
 
@@ -31,7 +33,8 @@ EXPORTS = (
     "gatgpu_set_input", "gatgpu_degree_schedule", "gatgpu_permuted_csr", "gatgpu_choose_R",
     "gatgpu_layer_forward", "gatgpu_model_forward", "gatgpu_get_stage", "gatgpu_stage_size",
     "gatgpu_set_option", "gatgpu_synchronize", "gatgpu_stream", "gatgpu_set_fixed_p", "gatgpu_fixed_p_forward",
-    "gatgpu_get_static_times", "gatgpu_validate_graph",
+    "gatgpu_get_static_times", "gatgpu_validate_graph", "gatgpu_layer_forward_static",
+    "gatgpu_static_scratch_need",
 )
 
 
@@ -96,6 +99,8 @@ def load_library(path: os.PathLike | None = None):
     L.gatgpu_stream.restype = P
     L.gatgpu_get_static_times.argtypes = [P, ctypes.POINTER(StaticTimes)]
     L.gatgpu_validate_graph.argtypes = [u64, u64, P, P]
+    L.gatgpu_layer_forward_static.argtypes = [P, i32, i32, i32, P, P]
+    L.gatgpu_static_scratch_need.argtypes = [P, i32, i32, i32, ctypes.POINTER(u64)]
     for name in EXPORTS:
         if name not in ("gatgpu_last_error", "gatgpu_stream"):
             getattr(L, name).restype = i32
@@ -242,6 +247,17 @@ class Context:
         out = np.empty(cnt.value, np.float32)
         self._check(self.lib.gatgpu_get_stage(self.h, layer, code, _ptr(out)))
         return out.reshape(self.n, -1)
+
+    def layer_forward_static(self, layer, precision, hidden, x_dev, out_dev):
+        """gatgpu_layer_forward_static on device pointers (ints): x [n][in],
+        out [n][heads*dim], FP32, original node order.  Enqueued on the
+        context's stream; call synchronize() before reading out."""
+        self._check(self.lib.gatgpu_layer_forward_static(self.h, layer, precision, int(hidden), x_dev, out_dev))
+
+    def static_scratch_need(self, layer, precision, hidden):
+        b = ctypes.c_uint64()
+        self._check(self.lib.gatgpu_static_scratch_need(self.h, layer, precision, int(hidden), ctypes.byref(b)))
+        return b.value
 
     def static_times(self):
         t = StaticTimes()

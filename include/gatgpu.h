@@ -245,6 +245,32 @@ typedef struct gatgpu_static_times {
 } gatgpu_static_times;
 int gatgpu_get_static_times(gatgpu_ctx* ctx, gatgpu_static_times* out);
 
+/* ---- allocation-free layer ------------------------------------------- */
+/* No counterpart in the reference.  For callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops): the
+ * transform-first gatgpu_layer_forward of `layer` on device-resident rows,
+ * with every intermediate (bf16 input rows, Z, L, R, max, den, the output
+ * before its final copy, split-row partial sums and arrival counters) in one
+ * static device array of GATGPU_STATIC_SCRATCH_BYTES per GPU, held until the
+ * process ends.  It calls no allocator.
+ *   x   device FP32 [n][in], original node order
+ *   out device FP32 [n][heads*dim], original node order: the values
+ *       gatgpu_get_stage(OUT) returns after gatgpu_layer_forward with the
+ *       same input, precision and hidden (bf16 hidden outputs widened)
+ * Graph, layer weights and options come from the context (set-up calls,
+ * which do allocate).  The work is enqueued on the context's stream
+ * (gatgpu_stream) and the call returns without waiting; the stages of the
+ * context are not touched.  Rejects (GATGPU_EOVERFLOW, before any launch) a
+ * layer whose intermediates exceed the array.  Every call on one GPU shares
+ * that GPU's array: calls that overlap on one GPU (several contexts or host
+ * threads, or streams not ordered against each other) race. */
+#define GATGPU_STATIC_SCRATCH_BYTES (64u << 20)
+int gatgpu_layer_forward_static(gatgpu_ctx* ctx, int layer, int precision, int hidden, const float* x,
+                                float* out);
+/* Bytes of the static array gatgpu_layer_forward_static would use for
+ * `layer` of the context's graph (0 if the layer is not set). */
+int gatgpu_static_scratch_need(gatgpu_ctx* ctx, int layer, int precision, int hidden, uint64_t* bytes);
+
 /* ---- misc ------------------------------------------------------------ */
 int gatgpu_set_option(gatgpu_ctx* ctx, int key, int64_t value);
 /* Blocks until all work on the context's stream is done. */
