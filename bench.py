@@ -6,14 +6,22 @@ inputs resident in HBM.  Default workload: the 64.3M-edge power-law graph
 (2,449,029 nodes, 100 -> 8x32 -> 8x32 -> 1x47, bf16 storage with FP32
 softmax/accumulation).  Prints ONE JSON line (rank 0).
 
-  python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload large|arxiv|smoke]
-                  [--precision bf16|fp32] [--no-cpu-baseline]
+  python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload large|skew|arxiv|smoke]
+                  [--precision bf16|fp32] [--dataflow auto|transform_first|aggregate_first]
+                  [--no-cpu-baseline] [--cpu-threads T] [--cpu-warmups 2] [--cpu-repeats 7]
+
+Besides the contract fields the line carries, per layer, the aggregation's
+and the projection's time and fraction of the HBM (and MFMA) peaks
+("layers"), the dominant projection against both peaks ("roofline_gemm"),
+the cold-start times ("cold_start_ms") and the host CPU baseline with its
+protocol and host description ("cpu_baseline").
 """
 from __future__ import annotations
 
 import argparse
 import json
 import os
+import subprocess
 import sys
 import time
 from pathlib import Path
@@ -26,6 +34,7 @@ sys.path.insert(0, str(ROOT / "gat-tfs_amd"))
 METRIC = "3-layer GAT fwd latency (ms), GEdge/s & % HBM roofline, 2.5M/64M-edge graphs"
 HBM_PEAK_GBS = 8000.0
 MFMA_BF16_PEAK_TFLOPS = 2500.0
+MFMA_FP32_PEAK_TFLOPS = 157.3
 
 
 def agg_bytes(n, e, heads, dim, s_z, s_out, r_gather=True):
@@ -50,38 +59,16 @@ def pmc_traffic(workload, precision):
     return None
 
 
-def cpu_baseline(w, row, col, x, model, precision, threads, reps=1):
-    """The oracle's B0 restatement (standard_bf16 / standard_fp32 semantics,
-    baseline/src/baseline_standard.cpp) on the host cores.  Workspaces are
-    allocated and touched by one untimed forward first (the reference times
-    with preallocated workspaces, baseline/README.md:52), then `reps` timed
-    three-layer forwards; the median is reported."""
-    sys.path.insert(0, str(ROOT))
-    import oracle
-
-    bf16 = precision == "bf16"
-    n = int(row.size - 1)
-    wq = [oracle.quantize_bf16(p["w"]) if bf16 else p["w"] for p in model]
-    ws = [oracle.standard_workspace(n, p) for p in model]
-
-    def forward():
-        h = x
-        for l, p in enumerate(model):
-            st, _ = oracle.standard_layer(row, col, h, p, l < 2, bf16, threads, wq[l], ws[l])
-            h = st["out"]
-
-    forward()  # warm-up: page-in and first touch
-    times = []
-    for _ in range(reps):
-        t0 = time.perf_counter()
-        forward()
-        times.append(time.perf_counter() - t0)
-    dt = float(np.median(times))
-    e = int(row[-1])
-    return {"value": round(3 * e / dt / 1e9, 6), "unit": "GEdge/s", "cores": threads, "kind": "port",
-            "sample": f"full {w.name} graph, median of {reps} three-layer B0 forward(s) "
-                      f"({'standard_bf16' if bf16 else 'standard_fp32'}) after one warm-up forward",
-            "ms_per_forward": round(dt * 1e3, 3)}
+def cpu_baseline(workload, precision, threads, warmups, repeats):
+    """The oracle's B0 forward timed on the host cores (oracle/cpu_baseline.py),
+    in a child process started before this one touches the GPU, so that its
+    OpenMP threads are placed one per physical core of the first socket."""
+    cmd = [sys.executable, str(ROOT / "oracle" / "cpu_baseline.py"), "--workload", workload, "--precision", precision,
+           "--threads", str(threads), "--warmups", str(warmups), "--repeats", str(repeats)]
+    r = subprocess.run(cmd, capture_output=True, text=True, timeout=900)
+    if r.returncode != 0:
+        raise RuntimeError(f"CPU baseline failed ({r.returncode}): {r.stderr[-2000:]}")
+    return json.loads(r.stdout.strip().splitlines()[-1])
 
 
 def main():
@@ -94,13 +81,21 @@ def main():
     ap.add_argument("--dataflow", default="auto", choices=["auto", "transform_first", "aggregate_first"],
                     help="per-layer dataflow; aggregate_first applies where the layer supports it")
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--cpu-threads", type=int, default=int(os.environ.get("OMP_NUM_THREADS", "0") or 0))
+    ap.add_argument("--cpu-threads", type=int, default=0,
+                    help="CPU baseline threads (default: the first socket's physical cores, at most OMP_NUM_THREADS)")
+    ap.add_argument("--cpu-warmups", type=int, default=2)
+    ap.add_argument("--cpu-repeats", type=int, default=7)
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="run one 1 GiB device-to-device copy first (counter calibration under rocprofv3 --pmc)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (run with --gpus 1).", file=sys.stderr)
         sys.exit(2)
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        print("# CPU baseline (child process) ...", file=sys.stderr, flush=True)
+        cpu = cpu_baseline(args.workload, args.precision, args.cpu_threads, args.cpu_warmups, args.cpu_repeats)
 
     import torch
     import gatgpu
@@ -121,6 +116,7 @@ def main():
     ctx.set_graph(row, col)
     ctx.set_model(model)
     ctx.set_input(x)
+    static = ctx.static_times()
     print(f"# workload {w.name}: N={n} E={e} gen {gen_s:.1f}s", file=sys.stderr, flush=True)
 
     if args.calibrate_copy:
@@ -129,7 +125,9 @@ def main():
         dst.copy_(src)
         torch.cuda.synchronize()
         del src, dst
-    for _ in range(args.warmup):
+    # The first forward allocates the per-layer device buffers: the cold forward.
+    _, _, cold_ms = ctx.model_forward(prec, flow, want_logits=False, timed=True)
+    for _ in range(max(args.warmup - 1, 0)):
         ctx.model_forward(prec, flow, want_logits=False, timed=False)
     torch.cuda.synchronize()
     ctx.synchronize()
@@ -144,17 +142,51 @@ def main():
     wall = time.perf_counter() - t0
     ms = float(np.mean(step_ms))  # HIP-event model time (first kernel of layer 1 to last of layer 3)
     value = 3 * e / (ms * 1e-3) / 1e9
+    # Cold-start: the static steps (graph checks, uploads, degree schedule,
+    # weight preparation, feature permutation), the first forward, and the
+    # logits copied back to the host after a forward.
+    ctx.model_forward(prec, flow, want_logits=True, timed=False)
+    cold = {k: round(v, 3) for k, v in ctx.static_times().items()}
+    cold.update({k: round(static[k], 3) for k in static if k != "logits_d2h_ms"})
+    cold["first_forward_ms"] = round(cold_ms, 3)
 
-    # Dominant kernel: the layer-2 aggregation (fused prescan/softmax/SpMM/ELU), 8x32 heads.
-    s_z = 2 if prec == gatgpu.BF16 else 4
-    L2 = model[1]
-    agg_ms = float(np.mean([t[1]["aggregate_ms"] for t in layer_times]))
-    rz = prec == gatgpu.BF16 and (L2["heads"], L2["dim"]) == (8, 32)
-    b2 = agg_bytes(n, e, L2["heads"], L2["dim"], s_z, s_z, r_gather=not rz)
-    achieved = b2 / (agg_ms * 1e-3) / 1e9
+    bf16 = prec == gatgpu.BF16
+    s_z = 2 if bf16 else 4
+    layers = []
+    for l, p in enumerate(model):
+        K, d, D = p["heads"], p["dim"], p["in"]
+        W = K * d
+        t = {k: float(np.mean([lt[l][k] for lt in layer_times])) for k in layer_times[0][l]}
+        af = t["lr_ms"] > 0  # aggregate-first layers report the L/R front end as lr_ms
+        hidden = l < 2
+        s_out = 2 if (bf16 and hidden) else 4
+        s_x = 4 if (l == 0 or not bf16) else 2  # layer 1 reads the FP32 features; later layers the bf16 output
+        if af:
+            agg_b = 8 * (n + 1) + 4 * e + 4 * K * e + 4 * K * n + e * D * 2 + n * W * s_out
+        else:
+            no_r = bf16 and ((K, d) == (8, 32) or (K, d) == (1, 64))  # R formed from the gathered Z row
+            agg_b = agg_bytes(n, e, K, d, s_z, s_out, r_gather=not no_r)
+        rec = {"layer": l + 1, "dataflow": "aggregate_first" if af else "transform_first",
+               "aggregate_ms": round(t["aggregate_ms"], 4), "aggregate_bytes": int(agg_b),
+               "aggregate_gbs": round(agg_b / (t["aggregate_ms"] * 1e-3) / 1e9, 1),
+               "aggregate_frac": round(agg_b / (t["aggregate_ms"] * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+               "total_ms": round(t["total_ms"], 4)}
+        if af:
+            rec["lr_front_end_ms"] = round(t["lr_ms"], 4)
+        else:
+            flop = 2 * n * D * W
+            gb = n * D * s_x + D * W * s_x + n * W * s_z + 8 * K * n
+            pm = t["projection_ms"]
+            rec.update({"projection_ms": round(pm, 4), "projection_tflops": round(flop / (pm * 1e-3) / 1e12, 1),
+                        "projection_mfma_frac": round(flop / (pm * 1e-3) / 1e12 / (MFMA_BF16_PEAK_TFLOPS if bf16 else
+                                                                                   MFMA_FP32_PEAK_TFLOPS), 4),
+                        "projection_bytes": int(gb),
+                        "projection_hbm_frac": round(gb / (pm * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)})
+        layers.append(rec)
+    # Dominant kernel: the layer-2 aggregation (fused prescan/softmax/SpMM/ELU).
+    dom = layers[1]
     pmc = pmc_traffic(w.name, args.precision)
-    per_layer = [{k: round(float(np.mean([t[l][k] for t in layer_times])), 4)
-                  for k in ("convert_ms", "projection_ms", "aggregate_ms", "total_ms")} for l in range(3)]
+    gemm = max((r for r in layers if "projection_ms" in r), key=lambda r: r["projection_ms"])
     out = {
         "metric": METRIC,
         "value": round(value, 4),
@@ -166,21 +198,29 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "bf16" if prec == gatgpu.BF16 else "f32",
+        "dtype": "bf16" if bf16 else "f32",
         "data": "synthetic",
         "config": {"workload": f"{w.name}: 3-layer GAT {w.din}->{w.heads}x{w.dim}->{w.heads}x{w.dim}->1x{w.classes}, "
                                f"N={n}, E={e} (incl. self-loops), max in-degree {int(np.diff(row).max())}",
-                   "precision": args.precision, "wall_ms_per_step": round(wall / args.steps * 1e3, 4),
-                   "layers": per_layer},
-        "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4),
+                   "precision": args.precision, "wall_ms_per_step": round(wall / args.steps * 1e3, 4)},
+        "roofline": {"bound": "hbm", "achieved": dom["aggregate_gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": dom["aggregate_frac"],
                      "traffic": int(pmc["bytes_per_launch"]) if pmc else None,
-                     "kernel": "layer-2 aggregation", "algorithmic_bytes": int(b2), "avg_ms": round(agg_ms, 4)},
+                     "kernel": "layer-2 aggregation", "algorithmic_bytes": dom["aggregate_bytes"],
+                     "avg_ms": dom["aggregate_ms"]},
+        "roofline_gemm": {"kernel": f"layer-{gemm['layer']} projection", "bound": "hbm",
+                          "flop": int(2 * n * model[gemm["layer"] - 1]["in"] * model[gemm["layer"] - 1]["heads"]
+                                      * model[gemm["layer"] - 1]["dim"]),
+                          "avg_ms": gemm["projection_ms"], "achieved_tflops": gemm["projection_tflops"],
+                          "peak_tflops": MFMA_BF16_PEAK_TFLOPS if bf16 else MFMA_FP32_PEAK_TFLOPS,
+                          "mfma_frac": gemm["projection_mfma_frac"], "hbm_bytes": gemm["projection_bytes"],
+                          "hbm_frac": gemm["projection_hbm_frac"]},
+        "layers": layers,
+        "cold_start_ms": cold,
     }
     ctx.close()
-    if not args.no_cpu_baseline:
-        threads = args.cpu_threads or os.cpu_count()
-        out["cpu_baseline"] = cpu_baseline(w, row, col, x, model, args.precision, threads)
+    if cpu is not None:
+        out["cpu_baseline"] = cpu
     print(json.dumps(out), flush=True)
 
 
