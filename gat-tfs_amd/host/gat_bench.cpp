@@ -8,6 +8,8 @@
 // Registered paths: gpu_fp32 and gpu_bf16 (include/gatgpu.h through
 // gat_gpu_path.hpp).  Correctness compares against R0 stage dumps in the
 // reference's --dump-prefix naming (<prefix>_layer<l>_<stage>.f32, :74-77);
+// its own --dump-prefix writes the path's stages (<prefix>_<path>_layer<l>_
+// <stage>.f32) and chained logits (<prefix>_model_<path>.f32, :96);
 // `inspect` only loads and validates the inputs (no GPU).
 #include <algorithm>
 #include <chrono>
@@ -241,8 +243,11 @@ int run(int argc, char** argv) {
             std::vector<float> ref_out = read_dump(lp + "_output.f32", nw);
             check(l + 1, "layer", ref_out, w.out, true);
             print_times(path, "correctness", l + 1, 0, g, p, t);
-            if (a.has("--dump-prefix")) {  // the path's stages in the reference's dump naming (main.cpp:74-77)
-                const std::string dp = a.get("--dump-prefix") + "_layer" + std::to_string(l + 1) + "_";
+            if (a.has("--dump-prefix")) {
+                // The reference dumps R0's stages here (main.cpp:74-77), which this
+                // harness reads instead (--reference-prefix); it dumps the path's
+                // own stages, named with the path: <prefix>_<path>_layer<l>_<stage>.f32.
+                const std::string dp = a.get("--dump-prefix") + "_" + path + "_layer" + std::to_string(l + 1) + "_";
                 for (auto item : {std::make_pair("output", &w.out), {"z", &w.z}, {"left", &w.left}, {"right", &w.right},
                                   {"max", &w.max}, {"den", &w.den}})
                     if (!item.second->empty()) write_dump(dp + item.first + ".f32", *item.second);
@@ -255,6 +260,8 @@ int run(int argc, char** argv) {
         check(3, "model_path_specific_chain",
               read_dump(pre + "_layer3_output.f32", checked(g.n, uint64_t(model[2].width()))), logits, true);
         if (a.has("--output")) write_dump(a.get("--output"), logits);
+        // The path's chained logits under the reference's name (main.cpp:96).
+        if (a.has("--dump-prefix")) write_dump(a.get("--dump-prefix") + "_model_" + path + ".f32", logits);
         std::cout << "CORRECTNESS finite=" << finite << " accuracy_gate="
                   << (have_abs ? (pass ? "PASS" : "FAIL") : "UNCONFIGURED_NOT_ACCEPTED") << "\n";
         return pass ? 0 : 1;

@@ -64,11 +64,12 @@ class GpuPath {
         if (fixture_layer_ == layer) fixture_ = nullptr;  // set_layer drops the layer's fixture
     }
 
-    // The per-layer path: input -> w.out (plus the stage vectors the
-    // reference's correctness mode compares), times in seconds.
+    // The per-layer path: input -> w.out, times in seconds.  With `stages`
+    // (the reference's correctness mode) also the stage vectors it compares
+    // (z, left, right, max, den); without, w.out is the only copy back.
     template <class Graph, class Param, class Workspace, class Times>
     void layer(const Graph& g, const Param& p, int layer_index, const std::vector<float>& input, Workspace& w,
-               bool hidden, Times& t, int precision, int dataflow = GATGPU_AUTO) {
+               bool hidden, Times& t, int precision, int dataflow = GATGPU_AUTO, bool stages = true) {
         set_graph(g);
         set_layer(layer_index, p);
         gatgpu_times gt{};
@@ -84,6 +85,7 @@ class GpuPath {
         t.activation = gt.activation_ms * 1e-3;
         t.total = gt.total_ms * 1e-3;
         fetch(layer_index, GATGPU_STAGE_OUT, w.out);
+        if (!stages) return;
         fetch(layer_index, GATGPU_STAGE_LEFT, w.left);
         fetch(layer_index, GATGPU_STAGE_RIGHT, w.right);
         fetch(layer_index, GATGPU_STAGE_MAX, w.max);
@@ -119,16 +121,38 @@ class GpuPath {
     }
 
     // Three layers chained on the device; returns the model time in seconds
-    // (HIP events from layer 1's first kernel to layer 3's last).
+    // (HIP events from layer 1's first kernel to layer 3's last; the logits
+    // are copied back after the timer stops).
+    template <class Graph, class Model>
+    double model(const Graph& g, const Model& m, int precision, std::vector<float>* logits,
+                 int dataflow = GATGPU_AUTO) {
+        set_graph(g);
+        for (int l = 0; l < 3; ++l) set_layer(l, m[l]);
+        set_classes_hint(int(m[2].heads * m[2].dim));
+        return model(precision, logits, dataflow);
+    }
     double model(int precision, std::vector<float>* logits, int dataflow = GATGPU_AUTO) {
         double ms = 0;
-        gatgpu_times t[3];
         if (logits) logits->resize(size_t(n_) * classes_hint_);
-        check(ctx_, gatgpu_model_forward(ctx_, precision, dataflow, logits ? logits->data() : nullptr, t, &ms),
+        check(ctx_,
+              gatgpu_model_forward(ctx_, precision, dataflow, logits ? logits->data() : nullptr, model_times_, &ms),
               "gatgpu_model_forward");
         return ms * 1e-3;
     }
     void set_classes_hint(int c) { classes_hint_ = c; }
+    // Stage times (seconds) of layer l of the last model() call.
+    template <class Times>
+    void model_layer_times(int l, Times& t) const {
+        const gatgpu_times& g = model_times_[l];
+        t.convert = g.convert_ms * 1e-3;
+        t.projection = g.projection_ms * 1e-3;
+        t.lr = g.lr_ms * 1e-3;
+        t.max_prescan = g.max_prescan_ms * 1e-3;
+        t.aggregate = g.aggregate_ms * 1e-3;
+        t.normalize = g.normalize_ms * 1e-3;
+        t.activation = g.activation_ms * 1e-3;
+        t.total = g.total_ms * 1e-3;
+    }
 
    private:
     void fetch(int layer, int which, std::vector<float>& v) {
@@ -148,6 +172,7 @@ class GpuPath {
     const void* layer_[3] = {nullptr, nullptr, nullptr};
     uint64_t n_ = 0, e_ = 0;
     int classes_hint_ = 0;
+    gatgpu_times model_times_[3] = {};
 };
 
 }  // namespace gatgpu_host

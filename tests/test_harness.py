@@ -187,3 +187,42 @@ def test_fixed_p_mode_runs_tfs_operator_on_layer1(smoke_file, tmp_path):
     for key in ("path=gpu_bf16_fixed_p stage=vs_master_fixed_p", "path=tfs_b1_fixed_p stage=vs_master_fixed_p"):
         assert float(lines[key]["relative_l2"]) < 1e-2, (key, lines[key])
     assert "median_tfs_ms=" in p.stdout and "speedup=" in p.stdout
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("path,precision", [("gpu_fp32", 0), ("gpu_bf16", 1)])
+def test_dump_prefix_writes_path_stages(smoke_file, tmp_path, path, precision):
+    """--dump-prefix in correctness mode: the path's stages per layer
+    (<prefix>_<path>_layer<l>_<stage>.f32) and its chained logits
+    (<prefix>_model_<path>.f32, the reference's name, main.cpp:96), equal bit
+    for bit to what the C ABI returns for the same layer inputs (the R0-chained
+    inputs of correctness mode, main.cpp:71-90)."""
+    import gatgpu
+
+    g = smoke1024()
+    model = oracle.random_model(128, 40, 11)
+    write_r0_dumps(tmp_path / "r0", g, model)
+    run("--mode", "correctness", "--graph", smoke_file, "--seed", 11, "--path", path,
+        "--reference-prefix", tmp_path / "r0", "--dump-prefix", tmp_path / "d", check_rc=0)
+    n = g["n"]
+    with gatgpu.Context(0) as ctx:
+        ctx.set_graph(g["row"], g["col"])
+        ctx.set_model(model)
+        ctx.set_input(g["x"])
+        x = g["x"]
+        for l, p in enumerate(model):
+            ctx.layer_forward(l, precision, gatgpu.AUTO, l < 2, input=x)
+            for stage, key in (("output", "out"), ("z", "z"), ("left", "left"), ("right", "right"), ("max", "max"),
+                               ("den", "den")):
+                f = tmp_path / f"d_{path}_layer{l + 1}_{stage}.f32"
+                want = ctx.stage(l, key)
+                if want is None:  # no Z stage in the aggregate-first dataflow
+                    assert not f.exists(), f
+                    continue
+                got = np.fromfile(f, np.float32)
+                assert got.size == want.size, (f, got.size, want.size)
+                assert np.array_equal(got, want.ravel()), f
+            x = np.fromfile(f"{tmp_path / 'r0'}_layer{l + 1}_output.f32", np.float32).reshape(n, -1)
+        logits, _, _ = ctx.model_forward(precision, gatgpu.AUTO)
+    got = np.fromfile(tmp_path / f"d_model_{path}.f32", np.float32)
+    assert got.size == n * 40 and np.array_equal(got, logits.ravel())
