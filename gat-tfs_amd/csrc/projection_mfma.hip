@@ -127,8 +127,10 @@ __global__ void __launch_bounds__(kThreads) k_proj_mfma(ProjArgs a) {
 // unconditionally (rows past n re-read row n - 1 and are not stored).
 // Head blocks use the permuted packing (pack_projection_weights): lane
 // (half, col) ends with features 32 mb + 16 half + {0..15} of row col, so
-// Z leaves as two 16-byte stores per block.
-template <int KS, int HB, bool F32IN, bool FULL>
+// Z leaves as two 16-byte stores per block.  FULL: 0 any shape; 1 a layer of
+// 8 heads x 32 with every store unconditional; 2 the same with R = Z_bf16 aR
+// (what the aggregation recomputes from the gathered row).
+template <int KS, int HB, bool F32IN, int FULL>
 __global__ void __launch_bounds__(kThreads) k_proj_fast(ProjArgs a) {
     static_assert(!FULL || HB == 8, "FULL layers are 8 heads x 32");
     constexpr int NB = HB + 1;
@@ -190,6 +192,10 @@ __global__ void __launch_bounds__(kThreads) k_proj_fast(ProjArgs a) {
         const uint64_t t0 = tile < a.tiles ? tile : last;
 #pragma unroll
         for (int ks = 0; ks < KS; ++ks) load_ks(t0, ks);
+        // The first tile waits for all of its input here, so that the wait in
+        // the loop only has the loop's own issue order to follow (a merge with
+        // the prologue's order would make it wait for every store as well).
+        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
     }
     for (; tile < a.tiles; tile += stride) {
         const uint64_t row = tile * 32 + col;
@@ -230,7 +236,7 @@ __global__ void __launch_bounds__(kThreads) k_proj_fast(ProjArgs a) {
         // FULL: all 8 heads and 32 HB features present (8 x 32): no per-store
         // bounds tests either.
         const bool full = FULL;
-        float rz[HB > 0 ? HB : 1];  // R from the stored (bf16) Z, per head
+        float rz4[4] = {};  // R from the stored (bf16) Z of the lane's 4 heads (4 half + q)
 #pragma unroll
         for (int mb = 0; mb < HB; ++mb) {
             float zr[16];
@@ -251,7 +257,7 @@ __global__ void __launch_bounds__(kThreads) k_proj_fast(ProjArgs a) {
                 for (int x = 0; x < 4; ++x) w4[x] = zp[4 * q8 + x];
                 *reinterpret_cast<uint4*>(a.z + rs * a.zs + f0) = make_uint4(w4[0], w4[1], w4[2], w4[3]);
             }
-            if (FULL && a.r_from_z) {
+            if constexpr (FULL == 2) {
                 // R = Z_bf16 . aR with the summation the aggregation kernel uses:
                 // an FMA chain over each 8 features, then (s0 + s1) + (s2 + s3).
                 float s8[2];
@@ -264,7 +270,8 @@ __global__ void __launch_bounds__(kThreads) k_proj_fast(ProjArgs a) {
                     s8[q8] = t;
                 }
                 const float part = s8[0] + s8[1];
-                rz[mb] = part + __shfl_xor(part, 32);
+                const float r = part + __shfl_xor(part, 32);
+                rz4[mb & 3] = (mb >> 2) == half ? r : rz4[mb & 3];
             }
         }
         // L/R block: lane half h4 holds heads 4 h4 + {0..3} of each quarter
@@ -277,8 +284,16 @@ __global__ void __launch_bounds__(kThreads) k_proj_fast(ProjArgs a) {
             const float4 rv = make_float4(acc[HB][4] + acc[HB][12], acc[HB][5] + acc[HB][13], acc[HB][6] + acc[HB][14],
                                           acc[HB][7] + acc[HB][15]);
             *reinterpret_cast<float4*>(a.left + rs * 8 + 4 * half) = lv;
-            if (!(FULL && a.r_from_z)) *reinterpret_cast<float4*>(a.right + rs * 8 + 4 * half) = rv;
-            if (!full && a.r_in_z) *reinterpret_cast<float4*>(a.z + rs * a.zs + a.r_off + 8 * half) = rv;
+            if constexpr (FULL) {
+                // Always one R store per lane (the lane's 4 heads), R from the
+                // stored Z or from the L/R block: with no store under a branch
+                // the waits for the next tile's loads stay exact.
+                *reinterpret_cast<float4*>(a.right + rs * 8 + 4 * half) =
+                    FULL == 2 ? make_float4(rz4[0], rz4[1], rz4[2], rz4[3]) : rv;
+            } else {
+                *reinterpret_cast<float4*>(a.right + rs * 8 + 4 * half) = rv;
+                if (a.r_in_z) *reinterpret_cast<float4*>(a.z + rs * a.zs + a.r_off + 8 * half) = rv;
+            }
         } else {
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
@@ -289,13 +304,6 @@ __global__ void __launch_bounds__(kThreads) k_proj_fast(ProjArgs a) {
                     a.right[rs * a.heads + h] = rv;
                     if (a.r_in_z) *reinterpret_cast<float*>(a.z + rs * a.zs + a.r_off + 2 * h) = rv;
                 }
-            }
-        }
-        if constexpr (FULL) {
-            // 8 heads: R of the row as two 16-byte vectors
-            if (a.r_from_z && half == 0) {
-                *reinterpret_cast<float4*>(a.right + rs * 8) = make_float4(rz[0], rz[1], rz[2], rz[3]);
-                *reinterpret_cast<float4*>(a.right + rs * 8 + 4) = make_float4(rz[4], rz[5], rz[6], rz[7]);
             }
         }
 #pragma unroll
@@ -420,27 +428,44 @@ __global__ void __launch_bounds__(kWideThreads) k_proj_wide(ProjArgs a) {
             __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
         }
         __builtin_amdgcn_sched_group_barrier(0x008, kAhead, 0);
+        // The next block's fragments go to the slot every wave finished
+        // reading before the last barrier -- before this block's stores are
+        // issued, so the wait for the fragments does not also wait for them
+        // (the vector memory counter counts stores and loads in issue order).
+        if (more) put(cur ^ 1);
+        __builtin_amdgcn_sched_barrier(0);  // keep the LDS writes ahead of the stores
         if (ob < a.head_blocks) {
             // Permuted packing: lane (half, col) holds features 32 ob + 16 half + {0..15}.
+            uint32_t w4[2][4];
 #pragma unroll
-            for (int q8 = 0; q8 < 2; ++q8) {
-                const int f0 = 32 * ob + 16 * half + 8 * q8;
-                if (f0 < a.width) {
-                    uint32_t w4[4];
+            for (int q8 = 0; q8 < 2; ++q8)
 #pragma unroll
-                    for (int x = 0; x < 4; ++x) w4[x] = bf16x2(acc[8 * q8 + 2 * x], acc[8 * q8 + 2 * x + 1]);
-                    *reinterpret_cast<uint4*>(a.z + rs * a.zs + f0) = make_uint4(w4[0], w4[1], w4[2], w4[3]);
-                    if (a.r_from_z) {
+                for (int x = 0; x < 4; ++x) w4[q8][x] = bf16x2(acc[8 * q8 + 2 * x], acc[8 * q8 + 2 * x + 1]);
+            if (a.r_from_z) {
+                // aR is read before this block's stores are issued: a load
+                // behind them would wait for them (one in-order counter).
+#pragma unroll
+                for (int q8 = 0; q8 < 2; ++q8) {
+                    const int f0 = 32 * ob + 16 * half + 8 * q8;
+                    if (f0 < a.width) {
                         float t = 0.0f;
 #pragma unroll
                         for (int x = 0; x < 4; ++x) {
-                            t = __builtin_fmaf(__builtin_bit_cast(float, w4[x] << 16), a.ar[f0 + 2 * x], t);
-                            t = __builtin_fmaf(__builtin_bit_cast(float, w4[x] & 0xffff0000u), a.ar[f0 + 2 * x + 1], t);
+                            t = __builtin_fmaf(__builtin_bit_cast(float, w4[q8][x] << 16), a.ar[f0 + 2 * x], t);
+                            t = __builtin_fmaf(__builtin_bit_cast(float, w4[q8][x] & 0xffff0000u), a.ar[f0 + 2 * x + 1],
+                                               t);
                         }
                         if (ob == 0) rlo = q8 == 0 ? t : rlo + t;
                         else rhi = q8 == 0 ? t : rhi + t;
                     }
                 }
+            }
+#pragma unroll
+            for (int q8 = 0; q8 < 2; ++q8) {
+                const int f0 = 32 * ob + 16 * half + 8 * q8;
+                if (f0 < a.width)
+                    *reinterpret_cast<uint4*>(a.z + rs * a.zs + f0) =
+                        make_uint4(w4[q8][0], w4[q8][1], w4[q8][2], w4[q8][3]);
             }
         } else {
             float rz = 0.0f;
@@ -469,7 +494,6 @@ __global__ void __launch_bounds__(kWideThreads) k_proj_wide(ProjArgs a) {
                 }
             }
         }
-        if (more) put(cur ^ 1);  // the slot every wave finished reading before the last barrier
         __syncthreads();
     }
 }
@@ -559,6 +583,8 @@ __global__ void __launch_bounds__(kWideThreads) k_proj_f32(ProjF32Args a) {
             acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av.z, xr[4 * k4 + 2], acc, 0, 0, 0);
             acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av.w, xr[4 * k4 + 3], acc, 0, 0, 0);
         }
+        if (more) put(cur ^ 1);  // before the stores, as in the wide path
+        __builtin_amdgcn_sched_barrier(0);
         if (ob < a.head_blocks) {
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
@@ -584,7 +610,6 @@ __global__ void __launch_bounds__(kWideThreads) k_proj_f32(ProjF32Args a) {
                 }
             }
         }
-        if (more) put(cur ^ 1);
         __syncthreads();
     }
 }
@@ -603,7 +628,7 @@ hipError_t launch_f32_kh(const ProjF32Args& a, hipStream_t s) {
     return hipGetLastError();
 }
 
-template <int KS, int HB, bool F32IN, bool FULL>
+template <int KS, int HB, bool F32IN, int FULL>
 hipError_t launch_fast_io(const ProjArgs& a, hipStream_t s, int cus) {
     const size_t lds = size_t(KS) * (HB + 1) * kWave * sizeof(uint4) + (FULL ? 256 * sizeof(float) : 0);
     if (lds > 64 * 1024) {
@@ -616,7 +641,7 @@ hipError_t launch_fast_io(const ProjArgs& a, hipStream_t s, int cus) {
     const uint64_t wg_needed = (a.tiles + kWaves - 1) / kWaves;
     if (gx > wg_needed) gx = wg_needed;
     if (gx < 1) gx = 1;
-    if (FULL && a.r_from_z && !a.ar) return hipErrorInvalidValue;
+    if (FULL == 2 && !a.ar) return hipErrorInvalidValue;
     k_proj_fast<KS, HB, F32IN, FULL><<<dim3(uint32_t(gx)), kThreads, lds, s>>>(a);
     return hipGetLastError();
 }
@@ -624,11 +649,13 @@ hipError_t launch_fast_io(const ProjArgs& a, hipStream_t s, int cus) {
 template <int KS, int HB>
 hipError_t launch_fast(const ProjArgs& a, hipStream_t s, int cus) {
     if constexpr (HB == 8) {
-        if (a.width == 256 && a.heads == 8 && !a.r_in_z)
-            return a.x32 ? launch_fast_io<KS, HB, true, true>(a, s, cus)
-                         : launch_fast_io<KS, HB, false, true>(a, s, cus);
+        if (a.width == 256 && a.heads == 8 && !a.r_in_z) {
+            if (a.r_from_z)
+                return a.x32 ? launch_fast_io<KS, HB, true, 2>(a, s, cus) : launch_fast_io<KS, HB, false, 2>(a, s, cus);
+            return a.x32 ? launch_fast_io<KS, HB, true, 1>(a, s, cus) : launch_fast_io<KS, HB, false, 1>(a, s, cus);
+        }
     }
-    return a.x32 ? launch_fast_io<KS, HB, true, false>(a, s, cus) : launch_fast_io<KS, HB, false, false>(a, s, cus);
+    return a.x32 ? launch_fast_io<KS, HB, true, 0>(a, s, cus) : launch_fast_io<KS, HB, false, 0>(a, s, cus);
 }
 
 template <int HB>
