@@ -66,8 +66,12 @@ constexpr int kMaxKS = 8;                  // k steps of 16 features: D_in <= 12
 constexpr int kRowWords = kXRStride / 2;   // 64 words of 4 bytes per XR row
 constexpr int kEPL = 4;                    // edges per lane and batch (batches of 4 kEPL edges)
 constexpr int kSB = 4;                     // super-blocks of 16 words per row
-constexpr int kBlk = kTile * 32 + 16;      // bytes per (head, k step, hi|lo) block of S, padded
-constexpr int kSBytes = 8 * kMaxKS * 2 * kBlk;
+constexpr int kBlk = kTile * 32 + 32;      // bytes per (head, k step, hi|lo) block of S, padded
+// Heads 4..7 sit this many bytes further on: with blocks 8 words apart modulo
+// the banks, the 32 lanes that write S (k group g, lanes n) land on 32
+// distinct banks: n % 8, + 8 for n / 8, + 16 for g.
+constexpr int kHalfOff = 64;
+constexpr int kSBytes = 8 * kMaxKS * 2 * kBlk + kHalfOff;
 constexpr int kLdsBytes = kSBytes + 2 * 2 * kTile * 4;  // S, then the tile's node ids (up to 2 x 32)
 constexpr uint32_t kNoRow = 0xffffffffu;
 constexpr int kPart = 8 * 128 + 8;         // floats per chunk partial (U_h rows of 128, then den)
@@ -252,8 +256,8 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4
     constexpr bool RSEP = KS == 8;
     constexpr int RPW = TR / kWaves;          // rows per wave and tile
     constexpr bool DB = !HL && TR == 16;      // two alternating S buffers
-    constexpr int BLK = TR * 32 + 16;         // bytes per (head, k step[, hi|lo]) block of S
-    static_assert(8 * kMaxKS * (HL ? 2 : DB ? 2 : 1) * BLK <= kSBytes, "S fits");
+    constexpr int BLK = TR * 32 + 32;         // bytes per (head, k step[, hi|lo]) block of S
+    static_assert(8 * kMaxKS * (HL ? 2 : DB ? 2 : 1) * BLK + kHalfOff <= kSBytes, "S fits");
     extern __shared__ __attribute__((aligned(16))) unsigned char slds[];
     // Destination node of each tile row (kNoRow: none), for the projection stores.
     uint32_t* const trow_all = reinterpret_cast<uint32_t*>(slds + kSBytes);
@@ -347,7 +351,7 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4
                 // ((h * kMaxKS + ks) * 2 + hl) with hi + lo, (buf * 8 + h) * kMaxKS + ks
                 // without.  (With KS <= 7 the words of R, 56..63, fall in k step 7.)
                 unsigned char* base =
-                    slds + 32 * r + 4 * (n % 8) +
+                    slds + 32 * r + 4 * (n % 8) + kHalfOff * g +
                     (HL ? 8 * kMaxKS * g + 2 * (n / 8) : buf * 8 * kMaxKS + 4 * kMaxKS * g + n / 8) * BLK;
 #pragma unroll
                 for (int sb = 0; sb < kSB; ++sb) {
@@ -400,7 +404,7 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4
             f32x16 dh, dl;
 #pragma unroll
             for (int x = 0; x < 16; ++x) dh[x] = dl[x] = 0.0f;
-            const int boff = (l % TR) * 32 + 16 * (l / 32);
+            const int boff = (l % TR) * 32 + 16 * (l / 32) + (h >= 4 ? kHalfOff : 0);
 #pragma unroll
             for (int ks = 0; ks < KS; ++ks) {
                 if constexpr (HL) {
