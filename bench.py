@@ -152,6 +152,10 @@ def main():
 
     bf16 = prec == gatgpu.BF16
     s_z = 2 if bf16 else 4
+    # The output layer's projection ran inside layer 2's aggregation (its
+    # output rows never stored): layer 2's kernel writes layer 3's Z rows and
+    # L/R instead of its own output rows.
+    fused23 = not ctx.has_stage(1, "out")
     layers = []
     for l, p in enumerate(model):
         K, d, D = p["heads"], p["dim"], p["in"]
@@ -166,13 +170,20 @@ def main():
         else:
             no_r = bf16 and ((K, d) == (8, 32) or (K, d) == (1, 64))  # R formed from the gathered Z row
             agg_b = agg_bytes(n, e, K, d, s_z, s_out, r_gather=not no_r)
+            if fused23 and l == 1:
+                nxt = model[2]
+                agg_b += n * (nxt["heads"] * nxt["dim"] * 2 + 8 * nxt["heads"]) - n * W * s_out
         rec = {"layer": l + 1, "dataflow": "aggregate_first" if af else "transform_first",
                "aggregate_ms": round(t["aggregate_ms"], 4), "aggregate_bytes": int(agg_b),
                "aggregate_gbs": round(agg_b / (t["aggregate_ms"] * 1e-3) / 1e9, 1),
                "aggregate_frac": round(agg_b / (t["aggregate_ms"] * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
                "total_ms": round(t["total_ms"], 4)}
+        if fused23 and l == 1:
+            rec["fused"] = "layer-3 projection in the epilogue (32-row tiles on MFMA); layer-2 output rows not stored"
         if af:
             rec["lr_front_end_ms"] = round(t["lr_ms"], 4)
+        elif fused23 and l == 2:
+            rec["projection"] = "fused into the layer-2 aggregation"
         else:
             flop = 2 * n * D * W
             gb = n * D * s_x + D * W * s_x + n * W * s_z + 8 * K * n

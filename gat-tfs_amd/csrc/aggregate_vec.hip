@@ -433,6 +433,139 @@ __global__ void __launch_bounds__(kThreads) k_agg_vec(VArgs<ZT> a) {
 // Edge loads per lane and batch of the R-from-Z form.
 constexpr int kURz = 4;
 
+// ---------------- the next layer's projection fused into the tile epilogue
+// (bf16 8 x 32 rows, R from Z; the next layer one head of at most 64 columns
+// in rows of 64 bf16 with R as FP32 in the last four bytes).
+//
+// A block takes a tile of kNextTile consecutive non-split rows (sorted
+// positions, heaviest tile first; the row buffers are in sorted order, so the
+// position is the row index), wave w rows w, w + 4, ...  Each row is
+// aggregated as in k_agg_vec and its output -- normalised, ELU, rounded to
+// bf16, the bits the output store would write -- goes to an LDS tile row
+// instead of HBM.  The tile is then multiplied by the next layer's W on
+// v_mfma_f32_32x32x16_bf16 exactly as k_proj_fast does it (Z^T = W^T H^T,
+// the same fragments, k steps in the same order into zeroed accumulators), so
+// Z, L and R of the next layer carry the bits of the unfused projection.
+// Wave 0 forms Z columns 0..31; wave 1 columns 32..63 (HB = 2) and the L/R
+// block, so each 128-byte Z row is written by two waves together, and L / R
+// of the tile as whole lines.  Split rows store their output rows as usual;
+// the caller projects them afterwards.
+constexpr int kNextTile = 32;
+constexpr int kNextRowBytes = 512 + 16;  // padded: the 32 lanes of a B read hit distinct bank groups
+
+template <class C>
+__device__ inline void finish_row_tile(uint32_t i, const Lane<C>& st, int slot, int sub, float* mx, float* dn,
+                                       unsigned char* trow) {
+    static_assert(C::VEC == 8 && C::VPL == 1 && C::W == 256, "bf16 8 x 32 rows");
+    if (slot != 0) return;
+    if ((sub * C::VEC) % C::DIM == 0) {
+        mx[uint64_t(i) * C::K + st.h[0]] = st.m[0];
+        dn[uint64_t(i) * C::K + st.h[0]] = st.den[0];
+    }
+    const float scale = st.den[0] > 0.0f ? 1.0f / st.den[0] : 0.0f;
+    uint32_t wv[4];
+#pragma unroll
+    for (int x = 0; x < 4; ++x) wv[x] = bf16x2(elu_bf16(st.acc[2 * x] * scale), elu_bf16(st.acc[2 * x + 1] * scale));
+    *reinterpret_cast<uint4*>(trow + 16 * sub) = make_uint4(wv[0], wv[1], wv[2], wv[3]);
+}
+
+template <class C, int HB>
+__global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(8)))
+k_agg_vec_next(VArgs<uint16_t> a, NextProj f, uint64_t chunk_blocks) {
+    static_assert(HB == 1 || HB == 2, "one head of at most 64 columns");
+    __shared__ __attribute__((aligned(16))) unsigned char tile[kNextTile * kNextRowBytes + kNextTile * 4];
+    const int w = __builtin_amdgcn_readfirstlane(int(threadIdx.x) / kWave);
+    const int lane = threadIdx.x % kWave;
+    const int slot = lane / C::LPR, sub = lane % C::LPR;
+    if (blockIdx.x < chunk_blocks) {
+        const uint64_t item = uint64_t(blockIdx.x) * kWavesPerBlock + w;
+        if (item < a.sp.chunks) run_chunk<C, uint16_t, true>(a, item, lane, slot, sub);
+        return;
+    }
+    const uint64_t p0 = (f.tiles - 1 - (uint64_t(blockIdx.x) - chunk_blocks)) * kNextTile;
+    const int cnt = a.rows - p0 < uint64_t(kNextTile) ? int(a.rows - p0) : kNextTile;
+#pragma unroll 1
+    for (int r = w; r < kNextTile; r += kWavesPerBlock) {
+        unsigned char* trow = tile + r * kNextRowBytes;
+        bool stored = false;
+        if (r < cnt) {
+            const uint64_t k = p0 + r;
+            const uint64_t beg = a.prow[k], end = a.prow[k + 1];
+            if (beg <= end && end <= a.e) {
+                Lane<C> st;
+                init_lane<C, uint16_t, true>(a, sub, st);
+                st.L[0] = a.L[k * C::K + st.h[0]];
+                st.m[0] = -INFINITY;
+                aggregate<C, uint16_t, true>(beg, end, a.pcol, a.R, a.Z, slot, sub, st);
+                if (end == beg) st.m[0] = 0.0f;  // empty row: max 0, den 0, output 0
+                finish_row_tile<C>(uint32_t(k), st, slot, sub, a.mx, a.den, trow);
+                stored = true;
+            }
+        }
+        if (!stored && slot == 0) *reinterpret_cast<uint4*>(trow + 16 * sub) = make_uint4(0, 0, 0, 0);
+    }
+    __syncthreads();
+    // ---- the tile's Z^T = W^T H^T: lane (half, col) supplies H[col][16 ks + 8 half .. + 7].
+    // Wave b < HB forms Z columns 32 b .. 32 b + 31, wave HB the L/R block
+    // (head 0: L hi, R hi, L lo, R lo in registers 0, 4, 8, 12 of the lanes of
+    // half 0), whose R goes to LDS for the row tails.
+    typedef float f32x16 __attribute__((__vector_size__(16 * sizeof(float))));
+    typedef __bf16 bf16x8 __attribute__((__vector_size__(8 * sizeof(__bf16))));
+    const int half = lane / 32, col = lane % 32;
+    const uint64_t k = p0 + col;
+    const bool ok = col < cnt;
+    float* const rsh = reinterpret_cast<float*>(tile + kNextTile * kNextRowBytes);
+    uint32_t zp[8] = {};
+    if (w <= HB) {
+        const unsigned char* bsrc = tile + col * kNextRowBytes + 16 * half;
+        const uint4* wsrc = f.wpk + size_t(w) * kWave + lane;
+        f32x16 acc;
+#pragma unroll
+        for (int x = 0; x < 16; ++x) acc[x] = 0.0f;
+        // Four k steps' fragments requested at a time (L2-resident W, LDS H):
+        // the tile loop's registers, not more, are what the phase may use.
+#pragma unroll
+        for (int k4 = 0; k4 < 16; k4 += 4) {
+            uint4 av[4], bv[4];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                av[q] = wsrc[size_t(k4 + q) * f.nmb * kWave];
+                bv[q] = *reinterpret_cast<const uint4*>(bsrc + 32 * (k4 + q));
+            }
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+                acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, av[q]),
+                                                              __builtin_bit_cast(bf16x8, bv[q]), acc, 0, 0, 0);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        if (w == HB) {
+            const float lv = acc[0] + acc[8], rv = acc[4] + acc[12];
+            if (half == 0) {
+                rsh[col] = rv;
+                if (ok) {
+                    f.left[k] = lv;
+                    f.right[k] = rv;
+                }
+            }
+        } else {
+#pragma unroll
+            for (int x = 0; x < 8; ++x) zp[x] = bf16x2(acc[2 * x], acc[2 * x + 1]);
+        }
+    }
+    __syncthreads();
+    if (!ok || w > 1) return;
+    // Row col: wave 0 stores bytes 0..63 (columns 0..31), wave 1 bytes 64..127
+    // (columns 32..61 and R in the last four bytes).
+    uint16_t* zr = f.z + k * 64 + 32 * w + 16 * half;
+    uint4 v0 = make_uint4(zp[0], zp[1], zp[2], zp[3]), v1 = make_uint4(zp[4], zp[5], zp[6], zp[7]);
+    if (w == 1) {
+        if (HB == 1) v0 = v1 = make_uint4(0, 0, 0, 0);  // no columns past 31
+        if (half == 1) v1.w = __builtin_bit_cast(uint32_t, rsh[col]);
+    }
+    *reinterpret_cast<uint4*>(zr) = v0;
+    *reinterpret_cast<uint4*>(zr + 8) = v1;
+}
+
 template <class C, class ZT>
 hipError_t run(const AggArgs& g, const RowBins& bins, const SplitTable& t, hipStream_t s) {
     VArgs<ZT> a{g.prow, g.pcol, g.perm, g.left, g.right, static_cast<const ZT*>(g.feat), g.hidden, g.mx, g.den,
@@ -476,6 +609,34 @@ hipError_t launch_split_prescan(const uint64_t* prow, const uint32_t* pcol, cons
 bool aggregate_vec_supported(const AggArgs& g) {
     const int W = g.heads * g.dim;
     return g.heads == 8 && (W == 256 || W == 512) && g.fstride == W;
+}
+
+bool aggregate_vec_next_supported(const AggArgs& g, const NextProj& f) {
+    return aggregate_vec_supported(g) && g.feat_bf16 && g.heads * g.dim == 256 && g.r_from_z && g.ar && g.hidden &&
+           g.outbf && !g.out32 && (f.head_blocks == 1 || f.head_blocks == 2) && f.nmb > f.head_blocks && f.wpk &&
+           f.z && f.left && f.right;
+}
+
+hipError_t launch_aggregate_vec_next(const AggArgs& g, const RowBins& bins, const SplitTable& t, NextProj f,
+                                     hipStream_t s) {
+    if (!aggregate_vec_next_supported(g, f)) return hipErrorInvalidValue;
+    using C = Cfg<uint16_t, 256, 8, kURz>;
+    VArgs<uint16_t> a{g.prow, g.pcol, g.perm, g.left, g.right, static_cast<const uint16_t*>(g.feat), g.hidden,
+                      g.mx, g.den, g.out32, g.outbf, g.n, g.e, bins.split_begin,
+                      SplitArgs{t.chunks, t.chunk_k, t.chunk_first, t.chunk_edges, t.mchunk, t.part, t.counter},
+                      g.ar};
+    if (t.chunks) {
+        hipError_t e = launch_split_prescan(g.prow, g.pcol, g.right, C::K, t, g.e, s);
+        if (e != hipSuccess) return e;
+    }
+    f.tiles = (bins.split_begin + kNextTile - 1) / kNextTile;
+    const uint64_t chunk_blocks = (t.chunks + kWavesPerBlock - 1) / kWavesPerBlock;
+    const uint64_t blocks = chunk_blocks + f.tiles;
+    if (!blocks) return hipSuccess;
+    if (blocks > 0x7fffffffu) return hipErrorInvalidValue;
+    if (f.head_blocks == 2) k_agg_vec_next<C, 2><<<dim3(uint32_t(blocks)), kThreads, 0, s>>>(a, f, chunk_blocks);
+    else k_agg_vec_next<C, 1><<<dim3(uint32_t(blocks)), kThreads, 0, s>>>(a, f, chunk_blocks);
+    return hipGetLastError();
 }
 
 hipError_t launch_aggregate_vec(const AggArgs& g, const RowBins& bins, const SplitTable& t, hipStream_t s) {

@@ -118,6 +118,10 @@ struct TfBufs {
     bool fused_convert_ok = false;   // the FP32 input carries kF32Pad floats past its last row
     bool keep_xbf = false;           // write the rounded input rows to xbf even when the convert is fused
     const uint32_t* out_perm = nullptr;  // one-head kernel: output row of sorted position k
+    // The next layer's projection in this layer's aggregation epilogue
+    // (launch_aggregate_vec_next); the next layer then runs with projected.
+    const NextProj* next = nullptr;
+    bool projected = false;          // Z, L and R were written by the previous layer's epilogue
 };
 
 }  // namespace gatgpu
@@ -153,6 +157,7 @@ struct gatgpu_ctx {
     uint32_t split_min = 0;          // user option: rows >= this are split (0: per-kernel defaults)
     uint32_t split_chunk = 0;        // user option: edges per chunk (0: per-kernel defaults)
     bool keep_xbf = false;           // option GATGPU_OPT_KEEP_INPUT_BF16
+    bool fuse_next = true;           // option GATGPU_OPT_FUSE_NEXT_PROJECTION
     gatgpu::SplitPlan plans[gatgpu::kPlans];
     hipEvent_t ev[16] = {};
     int cus = 256;  // compute units of the device

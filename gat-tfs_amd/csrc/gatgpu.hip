@@ -415,15 +415,38 @@ int sort_features(gatgpu_ctx* c) {
 // convert, after projection, after aggregate) or -1 for no timing.
 // orig_out: write the FP32 output rows in original node order where the
 // aggregation kernel can (the one-head kernel); Ls.out_original tells.
+// Layer l's aggregation can carry layer l + 1's projection (model forward):
+// both transform-first bf16, layer l of 8 heads x 32 whose projection takes
+// the fast path (R then comes from its bf16 Z rows), layer l + 1 of one head
+// of at most 60 columns over those 256 inputs (Z rows of 64 with R inside).
+bool can_fuse_next(const gatgpu_ctx* c, int l, int precision, const int (&flows)[3]) {
+    if (precision != GATGPU_BF16 || l < 0 || l > 1) return false;
+    if (flows[l] != GATGPU_TRANSFORM_FIRST || flows[l + 1] != GATGPU_TRANSFORM_FIRST) return false;
+    const LayerState& A = c->L[l];
+    const LayerState& B = c->L[l + 1];
+    const bool a_fast = A.groups == 1 && ((A.ksteps >= 1 && A.ksteps <= 8) || A.ksteps == 16);
+    bool r_in_z = false;
+    (void)z_stride(precision, B.heads, B.width(), &r_in_z);
+    return A.heads == 8 && A.dim == 32 && a_fast && B.heads == 1 && r_in_z && B.in == 256 && B.ksteps == 16 &&
+           B.groups == 1 && B.nmb > (B.width() + 31) / 32;
+}
+
+// fuse: kFuseNone; kFuseNext: this layer's aggregation also projects its
+// output rows with layer l + 1's weights (launch_aggregate_vec_next);
+// kProjected: layer l's Z, L and R were written that way by layer l - 1.
+enum { kFuseNone = 0, kFuseNext = 1, kProjected = 2 };
+
 int run_layer(gatgpu_ctx* c, int l, int precision, int dataflow, bool hidden, const float* host_input,
-              int ev_base, bool fixed = false, bool orig_out = false) {
+              int ev_base, bool fixed = false, bool orig_out = false, int fuse = kFuseNone) {
     LayerState& Ls = c->L[l];
     const uint64_t n = c->n;
     const int K = Ls.heads, W = Ls.width(), D = Ls.in;
     // ---- input (explicit host input is uploaded before the timed region)
     const float* src32 = nullptr;
     const uint16_t* srcbf = nullptr;
-    if (host_input) {
+    if (fuse == kProjected) {
+        // the input rows were consumed by the previous layer's epilogue
+    } else if (host_input) {
         HIPCHECK(c, Ls.in32.ensure((n * D + kF32Pad) * 4));
         HIPCHECK(c, upload_rows_sorted(c, host_input, D, Ls.in32.p));
         HIPCHECK(c, hipMemsetAsync(Ls.in32.as<float>() + n * D, 0, kF32Pad * 4, c->stream));
@@ -458,7 +481,7 @@ int run_layer(gatgpu_ctx* c, int l, int precision, int dataflow, bool hidden, co
     const int zs = z_stride(precision, K, W, nullptr);
     if (bf16) {
         HIPCHECK(c, Ls.zbf.ensure(n * zs * 2));
-        if (srcbf && D != xs) {  // chained bf16 input without the padded layout
+        if (fuse != kProjected && srcbf && D != xs) {  // chained bf16 input without the padded layout
             HIPCHECK(c, Ls.in32.ensure((n * D + kF32Pad) * 4));
             HIPCHECK(c, launch_widen_bf16(srcbf, Ls.in32.as<float>(), n * D, c->stream));
             src32 = Ls.in32.as<float>();
@@ -483,14 +506,30 @@ int run_layer(gatgpu_ctx* c, int l, int precision, int dataflow, bool hidden, co
     b.keep_xbf = c->keep_xbf;
     // Layer 3's one-head kernel writes its FP32 rows straight to original rows.
     if (orig_out && b.out32 && !fixed) b.out_perm = c->perm;
+    NextProj nx;
+    if (fuse == kFuseNext) {
+        LayerState& N = c->L[l + 1];
+        HIPCHECK(c, N.zbf.ensure(n * 64 * 2));
+        HIPCHECK(c, N.left.ensure(n * 4));
+        HIPCHECK(c, N.right.ensure(n * 4));
+        nx.wpk = N.wpk.as<uint4>();
+        nx.nmb = N.nmb;
+        nx.head_blocks = (N.width() + 31) / 32;
+        nx.z = N.zbf.as<uint16_t>();
+        nx.left = N.left.as<float>();
+        nx.right = N.right.as<float>();
+        b.next = &nx;
+    }
+    b.projected = fuse == kProjected;
     TfDone done;
     if (int r = run_tf(c, l, precision, hidden, src32, srcbf, ev_base, fixed, b, &done)) return r;
     Ls.ran = true;
     Ls.precision = precision;
     Ls.dataflow = GATGPU_TRANSFORM_FIRST;
     Ls.z_valid = true;
+    // With the next projection fused, only the split rows store their output.
     Ls.out32_valid = !want_outbf;
-    Ls.outbf_valid = want_outbf;
+    Ls.outbf_valid = want_outbf && fuse != kFuseNext;
     Ls.out_original = done.out_perm_used;
     Ls.xbf_valid = bf16 && src32 && (!done.fused_convert || c->keep_xbf);
     Ls.xbf_stride = xs;
@@ -536,17 +575,21 @@ int run_tf(gatgpu_ctx* c, int l, int precision, bool hidden, const float* src32,
     // ---- convert (bf16 path, FP32 source only; a bf16 source was rounded in
     // the previous layer's epilogue, which equals convert() of that output).
     // Where the fast projection applies, the rounding happens in its loads.
-    const bool fused = bf16 && src32 && b.fused_convert_ok && D % 4 == 0 &&
+    const bool fused = !b.projected && bf16 && src32 && b.fused_convert_ok && D % 4 == 0 &&
                        projection_fp32_input(pa);  // 16-byte aligned rows
     if (done) done->fused_convert = fused;
-    if (bf16 && src32 && !fused) {
+    if (b.projected) {
+        // Z, L and R come from the previous layer's epilogue: no convert, no projection.
+    } else if (bf16 && src32 && !fused) {
         HIPCHECK(c, launch_to_bf16_pad(src32, b.xbf, n, D, xs, c->stream));
         srcbf = b.xbf;
         src32 = nullptr;
     }
     if (ev_base >= 0) HIPCHECK(c, hipEventRecord(c->ev[ev_base + 1], c->stream));
     // ---- projection + L/R
-    if (bf16) {
+    if (b.projected) {
+        if (!bf16 || !r_in_z) return fail(c, GATGPU_EINVAL, "projected layer must be bf16 with R in its Z rows");
+    } else if (bf16) {
         if (fused) {
             pa.x32 = src32;
             pa.xs = D;
@@ -614,10 +657,40 @@ int run_tf(gatgpu_ctx* c, int l, int precision, bool hidden, const float* src32,
     if (b.mchunk) t.mchunk = b.mchunk;
     if (b.part) t.part = b.part;
     if (b.counter) t.counter = b.counter;
-    if (fixed)
+    if (b.next) {
+        if (fixed || !aggregate_vec_next_supported(a, *b.next))
+            return fail(c, GATGPU_EINVAL, "next-layer projection cannot be fused into this layer");
+        HIPCHECK(c, launch_aggregate_vec_next(a, P.bins, t, *b.next, c->stream));
+        // The split rows stored their output rows; the next layer's projection of them.
+        const uint64_t s0 = P.bins.split_begin;
+        if (s0 < n) {
+            const LayerState& N = c->L[l + 1];
+            ProjArgs np{};
+            np.n = n - s0;
+            np.xs = N.ksteps * 16;
+            np.x = b.outbf + s0 * uint64_t(np.xs);
+            np.ksteps = N.ksteps;
+            np.wpk = N.wpk.as<uint4>();
+            np.groups = N.groups;
+            np.head_blocks = b.next->head_blocks;
+            np.nmb = N.nmb;
+            np.width = N.width();
+            np.heads = N.heads;
+            np.z = b.next->z + s0 * 64;
+            np.zs = 64;
+            np.left = b.next->left + s0;
+            np.right = b.next->right + s0;
+            np.tiles = (np.n + 31) / 32;
+            np.r_in_z = true;
+            np.r_off = 62;
+            np.ar = N.ar.as<float>();
+            HIPCHECK(c, launch_projection_mfma(np, c->stream, c->cus));
+        }
+    } else if (fixed) {
         HIPCHECK(c, launch_aggregate_fixed(a, Ls.fixp.as<float>(), Ls.fixden.as<float>(), P.bins, t, c->stream));
-    else
+    } else {
         HIPCHECK(c, launch_aggregate_tf(a, P.bins, t, c->stream));
+    }
     if (ev_base >= 0) HIPCHECK(c, hipEventRecord(c->ev[ev_base + 3], c->stream));
     return GATGPU_OK;
 }
@@ -960,11 +1033,17 @@ int gatgpu_model_forward(gatgpu_ctx* c, int precision, int dataflow, float* logi
     if (c->L[0].in != c->din || c->L[1].in != c->L[0].width() || c->L[2].in != c->L[1].width())
         return fail(c, GATGPU_EINVAL, "layer widths do not chain");
     const bool timed = times || total_ms;
+    int flows[3];
     for (int l = 0; l < 3; ++l) {
         // In the chained model, aggregate-first applies where the layer supports it.
-        int flow = resolve_dataflow(c->L[l], precision, dataflow, c->n);
-        if (flow < 0) flow = GATGPU_TRANSFORM_FIRST;
-        if (int r = run_layer(c, l, precision, flow, l < 2, nullptr, timed ? 4 * l : -1, false, l == 2)) return r;
+        flows[l] = resolve_dataflow(c->L[l], precision, dataflow, c->n);
+        if (flows[l] < 0) flows[l] = GATGPU_TRANSFORM_FIRST;
+    }
+    const bool fuse23 = c->fuse_next && can_fuse_next(c, 1, precision, flows);
+    for (int l = 0; l < 3; ++l) {
+        const int fuse = !fuse23 ? kFuseNone : l == 1 ? kFuseNext : l == 2 ? kProjected : kFuseNone;
+        if (int r = run_layer(c, l, precision, flows[l], l < 2, nullptr, timed ? 4 * l : -1, false, l == 2, fuse))
+            return r;
     }
     // Logits in original node order, inside the timed forward: written so by
     // the last aggregation where it can, else gathered back (row i = sorted
@@ -1014,8 +1093,8 @@ int gatgpu_stage_size(gatgpu_ctx* c, int layer, int which, uint64_t* count) {
         case GATGPU_STAGE_DEN:
             *count = c->n * L.heads;
             break;
-        case GATGPU_STAGE_OUT:
-            *count = c->n * L.width();
+        case GATGPU_STAGE_OUT:  // absent where the next projection was fused in
+            *count = L.out32_valid || L.outbf_valid ? c->n * L.width() : 0;
             break;
         case GATGPU_STAGE_XBF:
             *count = L.xbf_valid ? c->n * L.in : 0;
@@ -1089,6 +1168,10 @@ int gatgpu_set_option(gatgpu_ctx* c, int key, int64_t value) {
         case GATGPU_OPT_KEEP_INPUT_BF16:
             if (value > 1) return fail(c, GATGPU_EINVAL, "keep-input option is 0 or 1");
             c->keep_xbf = value != 0;
+            return GATGPU_OK;
+        case GATGPU_OPT_FUSE_NEXT_PROJECTION:
+            if (value > 1) return fail(c, GATGPU_EINVAL, "fuse option is 0 or 1");
+            c->fuse_next = value != 0;
             return GATGPU_OK;
         default: return fail(c, GATGPU_EINVAL, "unknown option");
     }

@@ -323,5 +323,22 @@ hipError_t launch_aggregate_af(const AfArgs& a, hipStream_t s, int cus);
 bool aggregate_vec_supported(const AggArgs& a);
 hipError_t launch_aggregate_vec(const AggArgs& a, const RowBins& bins, const SplitTable& split,
                                 hipStream_t s);
+// The 8 x 32 bf16 aggregation (R from Z, hidden, bf16 output rows) with the
+// next layer's projection in its epilogue: a next layer of one head of at
+// most 60 columns, whose Z rows are 64 bf16 with R as FP32 in the last four
+// bytes.  Row buffers in sorted order (the row permutation is the identity).
+// Non-split rows never store their output; split rows do (a.outbf), and the
+// caller projects those rows afterwards with launch_projection_mfma.
+struct NextProj {
+    const uint4* wpk = nullptr;  // next layer's fragments, pack_projection_weights order (16 k steps, one group)
+    int nmb = 0, head_blocks = 0;
+    uint16_t* z = nullptr;       // [n][64]
+    float* left = nullptr;       // [n]
+    float* right = nullptr;      // [n]
+    uint64_t tiles = 0;          // filled by the launcher
+};
+bool aggregate_vec_next_supported(const AggArgs& a, const NextProj& f);
+hipError_t launch_aggregate_vec_next(const AggArgs& a, const RowBins& bins, const SplitTable& split, NextProj f,
+                                     hipStream_t s);
 
 }  // namespace gatgpu

@@ -21,6 +21,7 @@ FP32, BF16 = 0, 1
 AUTO, TRANSFORM_FIRST, AGGREGATE_FIRST, TFS_B1 = 0, 1, 2, 3
 STAGE_Z, STAGE_LEFT, STAGE_RIGHT, STAGE_MAX, STAGE_DEN, STAGE_OUT, STAGE_XBF = range(7)
 OPT_BLOCK_ROW_MIN_DEGREE, OPT_SPLIT_ROW_MIN_DEGREE, OPT_SPLIT_CHUNK_EDGES, OPT_KEEP_INPUT_BF16 = 1, 2, 3, 5
+OPT_FUSE_NEXT_PROJECTION = 6
 
 STATIC_SCRATCH_BYTES = 64 << 20  # GATGPU_STATIC_SCRATCH_BYTES
 
@@ -237,6 +238,13 @@ class Context:
                                                   times if timed else None,
                                                   ctypes.byref(total) if timed else None))
         return logits, ([t.as_dict() for t in times] if timed else None), total.value
+
+    def has_stage(self, layer, which):
+        """True when the last forward left this stage (gatgpu_stage_size > 0)."""
+        code = STAGE_NAMES[which] if isinstance(which, str) else which
+        cnt = ctypes.c_uint64()
+        self._check(self.lib.gatgpu_stage_size(self.h, layer, code, ctypes.byref(cnt)))
+        return cnt.value > 0
 
     def stage(self, layer, which):
         code = STAGE_NAMES[which] if isinstance(which, str) else which

@@ -131,11 +131,24 @@ enum {
                                             >= 64 applies to all, 0 restores) */
     /* 4 is not a key: rows of small degree take one wave each like the rest
        (the one-head kernel already packs 8 rows of equal degree per wave). */
-    GATGPU_OPT_KEEP_INPUT_BF16 = 5       /* 1: bf16 transform-first layers also
+    GATGPU_OPT_KEEP_INPUT_BF16 = 5,      /* 1: bf16 transform-first layers also
                                             store the input rows their
                                             projection rounds (stage XBF);
                                             0 (default): they are rounded in
                                             registers only                    */
+    GATGPU_OPT_FUSE_NEXT_PROJECTION = 6  /* 1 (default): gatgpu_model_forward
+                                            runs the projection of a bf16
+                                            one-head output layer (<= 60
+                                            classes over 8 x 32 inputs) inside
+                                            the previous layer's aggregation,
+                                            on its output rows staged in LDS:
+                                            Z, L and R of the output layer are
+                                            bit-equal to the unfused run, and
+                                            the hidden layer's OUT stage is not
+                                            stored (gatgpu_stage_size gives 0,
+                                            and a per-layer forward of the
+                                            output layer chained on it fails).
+                                            0: every layer stores its output  */
 };
 
 /* ---- lifetime -------------------------------------------------------- */

@@ -71,9 +71,15 @@ def report(tag, layer, e):
 def test_large_bf16_logits_vs_r0(gpu_ctx, large):
     """The benchmark forward (AUTO: layer 1 aggregate-first, layers 2-3
     transform-first) within relative L2 1e-2 of R0, end to end and per layer
-    (each layer chained on its own path's previous output).  The oracle's B0
-    standard_bf16 chain is printed beside it for scale."""
-    logits = forward(gpu_ctx, large, gatgpu.BF16)
+    (each layer chained on its own path's previous output; layer 2's output
+    is stored when the output projection is not fused into its aggregation).
+    The benchmark's fused forward gives the same logits bit for bit.  The
+    oracle's B0 standard_bf16 chain is printed beside it for scale."""
+    gpu_ctx.set_option(gatgpu.OPT_FUSE_NEXT_PROJECTION, 0)
+    try:
+        logits = forward(gpu_ctx, large, gatgpu.BF16)
+    finally:
+        gpu_ctx.set_option(gatgpu.OPT_FUSE_NEXT_PROJECTION, 1)
     assert gpu_ctx.stage(0, "z") is None  # layer 1 ran aggregate-first
     b0 = b0_chain(large["row"], large["col"], large["x"], large["m"])
     for l in range(3):
@@ -83,6 +89,9 @@ def test_large_bf16_logits_vs_r0(gpu_ctx, large):
         report("large_bf16_b0_vs_r0", l + 1, oracle.errors(large["r0"][l], b0[l]))
         assert e["finite"] and e["relative_l2"] < BF16_REL_L2, (l, e)
     assert np.array_equal(logits, gpu_ctx.stage(2, "out"))
+    fused, _, _ = gpu_ctx.model_forward(gatgpu.BF16, gatgpu.AUTO)
+    assert gpu_ctx.stage(1, "out") is None  # the output projection ran in layer 2's aggregation
+    assert np.array_equal(fused, logits)
 
 
 def test_large_fp32_logits_vs_r0(gpu_ctx, large):
@@ -127,7 +136,11 @@ def test_large_layers_2_3_sampled_rows(gpu_ctx, large):
     """Layers 2 (8 x 32, R formed from the bf16 Z row) and 3 (one head of 47,
     R carried in the Z row, logits written to original rows) of the benchmark
     forward, on 2000 sampled rows plus the 64 heaviest (split into chunks)."""
-    forward(gpu_ctx, large, gatgpu.BF16)
+    gpu_ctx.set_option(gatgpu.OPT_FUSE_NEXT_PROJECTION, 0)  # layer 2 stores its output rows
+    try:
+        forward(gpu_ctx, large, gatgpu.BF16)
+    finally:
+        gpu_ctx.set_option(gatgpu.OPT_FUSE_NEXT_PROJECTION, 1)
     row, col = large["row"], large["col"]
     deg = np.diff(row.astype(np.int64))
     rng = np.random.default_rng(11)

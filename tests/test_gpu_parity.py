@@ -177,6 +177,79 @@ def test_workload_model_parity(gpu_ctx, name, precision):
         assert e["finite"] and e["relative_l2"] < BF16_REL_L2, e
 
 
+# ---------------------------------------------------------------- output projection fused into layer 2
+def ragged_graph(n, seed):
+    """CSR with empty rows, rows of one to a few hundred edges and two rows
+    of about 1 500 and 3 000 edges; n is not a multiple of the 32-row tile."""
+    rng = np.random.default_rng(seed)
+    deg = rng.integers(0, 40, n)
+    deg[rng.choice(n, n // 10, replace=False)] = 0
+    deg[rng.choice(n, 20, replace=False)] = rng.integers(100, 400, 20)
+    deg[3], deg[n - 2] = 1500, 3000
+    row = np.zeros(n + 1, np.uint64)
+    row[1:] = np.cumsum(deg)
+    col = rng.integers(0, n, int(row[-1])).astype(np.uint32)
+    return row, col
+
+
+def fused_and_unfused(ctx, row, col, x, model, options=None):
+    """bf16 model forward (layers 2-3 transform-first) with the output layer's
+    projection fused into layer 2's aggregation (option 1) and without (0):
+    logits and the stages of layers 2 and 3 of each run."""
+    ctx.set_graph(row, col)
+    for k, v in (options or {}).items():
+        ctx.set_option(k, v)
+    ctx.set_model(model)
+    ctx.set_input(x)
+    runs = {}
+    for fuse in (0, 1):
+        ctx.set_option(gatgpu.OPT_FUSE_NEXT_PROJECTION, fuse)
+        logits, _, _ = ctx.model_forward(gatgpu.BF16, gatgpu.TRANSFORM_FIRST)
+        runs[fuse] = (logits, {(l, k): ctx.stage(l, k) for l in (1, 2)
+                               for k in ("z", "left", "right", "max", "den", "out")})
+    ctx.set_option(gatgpu.OPT_FUSE_NEXT_PROJECTION, 1)
+    for k in options or {}:
+        ctx.set_option(k, DEFAULT_OPTIONS[k])
+    return runs
+
+
+@pytest.mark.parametrize("classes", [40, 20, 60])
+@pytest.mark.parametrize("sched", range(len(SCHEDULES)))
+def test_fused_output_projection_bit_exact(gpu_ctx, classes, sched):
+    """Layer 3's projection inside layer 2's aggregation (32-row tiles staged
+    in LDS, the same MFMA sequence as the projection kernel; split rows
+    projected after the launch): logits and layer 3's Z (up to its width), L,
+    R, max and den equal the unfused run bit for bit, as do layer 2's max and
+    den; layer 2's output stage is absent when fused.  Classes 20 use one
+    32-column block, 40 and 60 two; a ragged graph (empty rows, heavy rows,
+    n % 32 != 0) under the three schedules (default, block rows, rows >= 16
+    split into 64-edge chunks)."""
+    row, col = ragged_graph(3001, 5 + classes)
+    x = inputs.normal((3001, 128), 3)
+    model = inputs.random_model(128, classes, 11)
+    runs = fused_and_unfused(gpu_ctx, row, col, x, model, SCHEDULES[sched])
+    (l0, s0), (l1, s1) = runs[0], runs[1]
+    assert np.isfinite(l0).all() and np.array_equal(l0, l1)
+    for (l, k), v in s0.items():
+        if (l, k) == (1, "out"):
+            assert v is not None and s1[(l, k)] is None
+            continue
+        assert np.array_equal(v, s1[(l, k)]), (l, k)
+    ref = oracle.ref_model(row, col, x, model)[2]["out"]
+    e = oracle.errors(ref, l1)
+    assert e["finite"] and e["relative_l2"] < BF16_REL_L2, e
+
+
+def test_fused_output_projection_arxiv(gpu_ctx):
+    """The 169K-node power-law model (128 -> 8x32 -> 8x32 -> 1x40, split rows
+    of up to 13K edges): fused and unfused logits bit-equal."""
+    w = inputs.WORKLOADS["arxiv"]
+    row, col = w.graph()
+    runs = fused_and_unfused(gpu_ctx, row, col, w.features(), w.model())
+    assert np.array_equal(runs[0][0], runs[1][0])
+    assert np.array_equal(runs[0][1][(2, "z")], runs[1][1][(2, "z")])
+
+
 def test_layer2_micro_fp32(gpu_ctx):
     """Single layer 256 -> 8x32 on the arxiv-sized graph, N(0,1) input."""
     w = inputs.WORKLOADS["arxiv"]
