@@ -315,23 +315,36 @@ __global__ void __launch_bounds__(kThreads) k_proj_fast(ProjArgs a) {
 // whose W fragments exceed LDS (e.g. 512 -> 8 x 64: 32 k steps x 17 blocks).
 // Each wave keeps the whole input of its 32-row tile in registers (KS B
 // fragments) and the block streams W^T one 32-feature output block at a time
-// (KS fragments, KS KB) through a two-slot LDS ring its waves share: X is
-// read from HBM once, each output block's fragments once per block from L2,
-// and every output block (head blocks, then the L/R block) leaves straight
-// from the accumulators.  The MFMA chain per block runs k steps in the order
-// of the other paths, so Z and L/R carry the same bits.
-constexpr int kWideThreads = 256;
+// (KS fragments, KS KB) through two LDS slots its waves share: X is read from
+// HBM once, each output block's fragments once per block from L2, and every
+// output block (head blocks, then the L/R block) leaves straight from the
+// accumulators.  The MFMA chain per block runs k steps in the order of the
+// other paths, so Z and L/R carry the same bits.
+//
+// The slots are filled by direct global -> LDS loads (global_load_lds_dwordx4,
+// one 1 KB k step per wave instruction, k steps split over the waves), issued
+// for block ob + 1 while block ob multiplies: no registers hold fragments in
+// transit.  The two slots are distinct LDS arrays and the block loop is
+// unrolled by two, so the compiler can see that the loads into one slot do not
+// alias the reads of the other and leaves them in flight.  Four waves per
+// block, two blocks per CU (2 waves per SIMD at 32 k steps: the tile's input
+// alone is 128 registers).  Measured on the 100.6M-edge R-MAT graph's
+// 512 -> 8 x 64 projection: 2.73 ms with the fragments staged through
+// registers, 2.63 ms with the direct loads; six-wave blocks at three waves
+// per SIMD (168 registers, two-step read-ahead, spilled addresses) 3.04 ms.
+constexpr int kWideThreads = 256;  // the FP32 projection's block (k_proj_f32)
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 constexpr int kWideWaves = kWideThreads / kWave;
+constexpr int kWideBW = 4;  // waves per block of the bf16 wide path
+typedef __attribute__((address_space(3))) void* lds_ptr;
 
-template <int KS, bool F32IN>
-__global__ void __launch_bounds__(kWideThreads) k_proj_wide(ProjArgs a) {
-    extern __shared__ u32x4 ring[];  // [2][KS][kWave]
-    constexpr int kFrags = KS * kWave;
-    constexpr int kPer = (kFrags + kWideThreads - 1) / kWideThreads;
-    const int w = threadIdx.x / kWave, l = threadIdx.x % kWave;
+template <int KS, bool F32IN, bool RZ>
+__global__ void __launch_bounds__(kWideBW * kWave) __attribute__((amdgpu_waves_per_eu(2))) k_proj_wide(ProjArgs a) {
+    __shared__ __attribute__((aligned(16))) u32x4 slot0[KS * kWave];
+    __shared__ __attribute__((aligned(16))) u32x4 slot1[KS * kWave];
+    const int w = __builtin_amdgcn_readfirstlane(int(threadIdx.x) / kWave), l = threadIdx.x % kWave;
     const int half = l / 32, col = l % 32;
-    const uint64_t row = (uint64_t(blockIdx.x) * kWideWaves + w) * 32 + col;
+    const uint64_t row = (uint64_t(blockIdx.x) * kWideBW + w) * 32 + col;
     // Lanes past n recompute row n - 1 and store its own values to it.
     const uint64_t rs = row < a.n ? row : a.n - 1;
     bf16x8 xr[KS];
@@ -369,45 +382,36 @@ __global__ void __launch_bounds__(kWideThreads) k_proj_wide(ProjArgs a) {
     // L/R block, which sits after the head blocks of the last group.
     const int nob = a.head_blocks + 1;
     const int last_g = a.groups - 1;
-    u32x4 st[kPer];
-    auto fetch = [&](int ob) {
+    // Fragments of output block ob into dst: k step ks (64 lanes x 16 bytes)
+    // is one wave instruction, k steps w, w + kWideBW, ... for wave w.
+    // The address is a wave-uniform base plus the lane's 32-bit offset.
+    const unsigned char* wbase = reinterpret_cast<const unsigned char*>(a.wpk);
+    const uint32_t loff = uint32_t(l) * uint32_t(sizeof(u32x4));
+    auto dma = [&](int ob, u32x4* dst) {
         const int g = ob < a.head_blocks ? ob / 8 : last_g;
         const int b = ob < a.head_blocks ? ob % 8 : a.head_blocks - 8 * last_g;
-        const u32x4* src = reinterpret_cast<const u32x4*>(a.wpk) + (size_t(g) * KS * a.nmb + b) * kWave;
-#pragma unroll
-        for (int i = 0; i < kPer; ++i) {
-            const int q = threadIdx.x + i * kWideThreads;
-            if (kFrags % kWideThreads == 0 || q < kFrags) st[i] = src[size_t(q / kWave) * a.nmb * kWave + q % kWave];
-        }
-    };
-    auto put = [&](int slot) {
-#pragma unroll
-        for (int i = 0; i < kPer; ++i) {
-            const int q = threadIdx.x + i * kWideThreads;
-            if (kFrags % kWideThreads == 0 || q < kFrags) ring[slot * kFrags + q] = st[i];
-        }
+        const size_t boff = (size_t(g) * KS * a.nmb + b) * kWave * sizeof(u32x4);
+        for (int ks = w; ks < KS; ks += kWideBW)
+            __builtin_amdgcn_global_load_lds(wbase + (boff + size_t(ks) * a.nmb * kWave * sizeof(u32x4)) + loff,
+                                             (lds_ptr)(dst + ks * kWave), 16, 0, 0);
     };
     // One head of 64 with r_from_z: R = Z_bf16 . aR in the order the one-head
     // aggregation recomputes it from a gathered row -- an FMA chain over each
     // 8 features (p0..p7), then ((p0 + p1) + (p2 + p3)) + ((p4 + p5) + (p6 + p7)).
     // Lane half 0 holds p0, p1 (block 0) and p4, p5 (block 1); half 1 the others.
     float rlo = 0.0f, rhi = 0.0f;  // pair sums of head blocks 0 and 1
-    fetch(0);
-    put(0);
-    // The tile's input is complete before the loop, so the only loads in
-    // flight inside it are the next block's fragments (waited for after the
-    // MFMAs, not before them).
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks) asm volatile("" ::"v"(xr[ks]));
+    dma(0, slot0);
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the tile's input and block 0's fragments
     __syncthreads();
-    for (int ob = 0; ob < nob; ++ob) {
-        const int cur = ob & 1;
-        const bool more = ob + 1 < nob;
-        if (more) fetch(ob + 1);  // lands in registers while this block multiplies
+    // Block ob from rd while block ob + 1's fragments land in wr.  Each wave
+    // waits for its own loads into wr (and its previous stores) after the
+    // MFMAs and before this block's stores, so the barrier then publishes wr.
+    auto step = [&](int ob, const u32x4* rd, u32x4* wr) {
+        if (ob + 1 < nob) dma(ob + 1, wr);
         f32x16 acc;
 #pragma unroll
         for (int r = 0; r < 16; ++r) acc[r] = 0.0f;
-        const u32x4* wk = ring + cur * kFrags + l;
+        const u32x4* wk = rd + l;
         // Fragments read four k steps ahead of their MFMA.
         constexpr int kAhead = KS < 4 ? KS : 4;
         u32x4 fr[kAhead];
@@ -428,12 +432,8 @@ __global__ void __launch_bounds__(kWideThreads) k_proj_wide(ProjArgs a) {
             __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
         }
         __builtin_amdgcn_sched_group_barrier(0x008, kAhead, 0);
-        // The next block's fragments go to the slot every wave finished
-        // reading before the last barrier -- before this block's stores are
-        // issued, so the wait for the fragments does not also wait for them
-        // (the vector memory counter counts stores and loads in issue order).
-        if (more) put(cur ^ 1);
-        __builtin_amdgcn_sched_barrier(0);  // keep the LDS writes ahead of the stores
+        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's loads into wr
+        __builtin_amdgcn_sched_barrier(0);
         if (ob < a.head_blocks) {
             // Permuted packing: lane (half, col) holds features 32 ob + 16 half + {0..15}.
             uint32_t w4[2][4];
@@ -441,7 +441,7 @@ __global__ void __launch_bounds__(kWideThreads) k_proj_wide(ProjArgs a) {
             for (int q8 = 0; q8 < 2; ++q8)
 #pragma unroll
                 for (int x = 0; x < 4; ++x) w4[q8][x] = bf16x2(acc[8 * q8 + 2 * x], acc[8 * q8 + 2 * x + 1]);
-            if (a.r_from_z) {
+            if (RZ) {
                 // aR is read before this block's stores are issued: a load
                 // behind them would wait for them (one in-order counter).
 #pragma unroll
@@ -469,7 +469,7 @@ __global__ void __launch_bounds__(kWideThreads) k_proj_wide(ProjArgs a) {
             }
         } else {
             float rz = 0.0f;
-            if (a.r_from_z) {
+            if (RZ) {
                 const float lo = rlo + __shfl_xor(rlo, 32);
                 const float hi = rhi + __shfl_xor(rhi, 32);
                 rz = lo + hi;
@@ -486,7 +486,7 @@ __global__ void __launch_bounds__(kWideThreads) k_proj_wide(ProjArgs a) {
                 for (int q = 0; q < 4; ++q) {
                     const int h = 4 * half + q;
                     if (h < a.heads) {
-                        const float rv = a.r_from_z ? rz : acc[4 + q] + acc[12 + q];
+                        const float rv = RZ ? rz : acc[4 + q] + acc[12 + q];
                         a.left[rs * a.heads + h] = acc[q] + acc[8 + q];
                         a.right[rs * a.heads + h] = rv;
                         if (a.r_in_z) *reinterpret_cast<float*>(a.z + rs * a.zs + a.r_off + 2 * h) = rv;
@@ -495,20 +495,19 @@ __global__ void __launch_bounds__(kWideThreads) k_proj_wide(ProjArgs a) {
             }
         }
         __syncthreads();
+    };
+    for (int ob = 0; ob < nob; ob += 2) {
+        step(ob, slot0, slot1);
+        if (ob + 1 < nob) step(ob + 1, slot1, slot0);
     }
 }
 
 template <int KS, bool F32IN>
 hipError_t launch_wide_io(const ProjArgs& a, hipStream_t s) {
-    const size_t lds = size_t(2) * KS * kWave * sizeof(uint4);
-    if (lds > 64 * 1024) {
-        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_proj_wide<KS, F32IN>),
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, int(lds));
-        if (e != hipSuccess) return e;
-    }
-    const uint64_t blocks = (a.tiles + kWideWaves - 1) / kWideWaves;
+    const uint64_t blocks = (a.tiles + kWideBW - 1) / kWideBW;
     if (blocks < 1 || blocks > 0x7fffffffu) return hipErrorInvalidValue;
-    k_proj_wide<KS, F32IN><<<dim3(uint32_t(blocks)), kWideThreads, lds, s>>>(a);
+    if (a.r_from_z) k_proj_wide<KS, F32IN, true><<<dim3(uint32_t(blocks)), kWideBW * kWave, 0, s>>>(a);
+    else k_proj_wide<KS, F32IN, false><<<dim3(uint32_t(blocks)), kWideBW * kWave, 0, s>>>(a);
     return hipGetLastError();
 }
 
