@@ -168,8 +168,7 @@ __device__ inline void gather_sums(const uint32_t* __restrict__ pcol, const uint
             sc[t] = (head && EPL * g + t < cnt) ? leaky(s.L + r) : -INFINITY;
             mb = fmaxf(mb, sc[t]);
         }
-        mb = fmaxf(mb, __shfl_xor(mb, 16));
-        mb = fmaxf(mb, __shfl_xor(mb, 32));
+        mb = xor32_max(xor16_max(mb));
         float scale = 1.0f;
         bool resc = false;
         if constexpr (!EXACT) {
@@ -234,8 +233,7 @@ __device__ inline void zero_sums(Sums& s) {
 
 // Denominator of head lane (n = h) over the 4 k groups.
 __device__ inline float total_den(float den) {
-    den += __shfl_xor(den, 16);
-    return den + __shfl_xor(den, 32);
+    return xor32_add(xor16_add(den));
 }
 
 

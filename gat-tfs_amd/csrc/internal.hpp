@@ -34,6 +34,28 @@ __device__ inline uint32_t bf16x2(float lo, float hi) {
 }
 __device__ inline uint16_t bf16_hw(float x) { return __builtin_bit_cast(uint16_t, static_cast<__bf16>(x)); }
 
+// max / sum of x over lanes l and l ^ 16 (l ^ 32): v_permlane16_swap
+// (v_permlane32_swap) hands each lane the other half's value in the VALU,
+// without the LDS round trip of a lane permute.  The swap returns the pair
+// {x_l, x_(l^16)} in some order; max and + are commutative, so the result is
+// that of fmaxf(x, __shfl_xor(x, 16)) (x + __shfl_xor(x, 16)) bit for bit.
+__device__ inline float xor16_max(float x) {
+    const auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return fmaxf(__uint_as_float(p[0]), __uint_as_float(p[1]));
+}
+__device__ inline float xor32_max(float x) {
+    const auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return fmaxf(__uint_as_float(p[0]), __uint_as_float(p[1]));
+}
+__device__ inline float xor16_add(float x) {
+    const auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(p[0]) + __uint_as_float(p[1]);
+}
+__device__ inline float xor32_add(float x) {
+    const auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(p[0]) + __uint_as_float(p[1]);
+}
+
 __device__ inline float leaky(float x) { return x >= 0.0f ? x : 0.2f * x; }
 __device__ inline float elu(float x) { return x >= 0.0f ? x : expm1f(x); }
 
