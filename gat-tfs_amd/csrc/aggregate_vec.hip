@@ -209,26 +209,38 @@ __device__ inline void batch(uint64_t base, uint64_t end, const uint32_t (&js)[C
 
 // The edge slots' states merged: afterwards every lane holds its heads'
 // totals and m is the max over all the edges.
+// (Lane pairs 16 and 32 apart exchange through v_permlane16/32_swap, in the
+// VALU; max and + of the pair are commutative, so the order does not matter.)
+template <int OFF>
+__device__ inline float pair_max(float x) {
+    if constexpr (OFF == 16) return xor16_max(x);
+    else if constexpr (OFF == 32) return xor32_max(x);
+    else return fmaxf(x, __shfl_xor(x, OFF));
+}
+template <int OFF>
+__device__ inline float pair_add(float x) {
+    if constexpr (OFF == 16) return xor16_add(x);
+    else if constexpr (OFF == 32) return xor32_add(x);
+    else return x + __shfl_xor(x, OFF);
+}
+template <class C, int OFF>
+__device__ inline void merge_step(Lane<C>& st) {
+    if constexpr (OFF < kWave) {
+#pragma unroll
+        for (int v = 0; v < C::VPL; ++v) {
+            const float M = pair_max<OFF>(st.m[v]);
+            const float f = st.m[v] == M ? 1.0f : exp_w(st.m[v] - M);
+            st.m[v] = M;
+            st.den[v] = pair_add<OFF>(st.den[v] * f);
+#pragma unroll
+            for (int x = 0; x < C::VEC; ++x) st.acc[v * C::VEC + x] = pair_add<OFF>(st.acc[v * C::VEC + x] * f);
+        }
+        merge_step<C, 2 * OFF>(st);
+    }
+}
 template <class C>
 __device__ inline void merge_slots(Lane<C>& st) {
-    if constexpr (C::EPI > 1) {
-        for (int off = C::LPR; off < kWave; off <<= 1) {
-#pragma unroll
-            for (int v = 0; v < C::VPL; ++v) {
-                const float mo = __shfl_xor(st.m[v], off);
-                const float M = fmaxf(st.m[v], mo);
-                const float f = st.m[v] == M ? 1.0f : exp_w(st.m[v] - M);
-                st.m[v] = M;
-                st.den[v] *= f;
-                st.den[v] += __shfl_xor(st.den[v], off);
-#pragma unroll
-                for (int x = 0; x < C::VEC; ++x) {
-                    float a = st.acc[v * C::VEC + x] * f;
-                    st.acc[v * C::VEC + x] = a + __shfl_xor(a, off);
-                }
-            }
-        }
-    }
+    if constexpr (C::EPI > 1) merge_step<C, C::LPR>(st);
 }
 
 // Edges [beg, end) of a row or chunk, then the edge slots merged.
