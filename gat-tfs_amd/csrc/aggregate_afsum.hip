@@ -158,15 +158,35 @@ __device__ inline void gather_sums(const uint32_t* __restrict__ pcol, const uint
             for (int sb = 0; sb < kSB; ++sb) raw[sb][t] = *reinterpret_cast<const uint32_t*>(xb + off + 64 * sb);
             if constexpr (RSEP) rsep[t] = head ? R[uint64_t(jl[t]) * 8 + n] : 0.0f;
         }
-        // ---- head lanes: scores of their edges, batch max over the 4 k groups
+        // ---- scores, batch max over the 4 k groups.  SPLIT (R in the row
+        // tail, 4 edges per lane): head h's four edges of a k group are
+        // scored by lanes h (edges 0, 1; R from lane h + 8 by a DPP rotation
+        // within the row) and h + 8 (edges 2, 3; R_h is its own row word 56 +
+        // h), whose weights lane h then takes over.  Otherwise the head lanes
+        // score all four.  Both see the same scores in the same operations.
+        constexpr bool SPLIT = !RSEP && !EXACT && EPL == 4;
+        const int hf = n / 8;
         float sc[EPL];
         float mb = -INFINITY;
+        if constexpr (SPLIT) {
 #pragma unroll
-        for (int t = 0; t < EPL; ++t) {
-            const float r = RSEP ? rsep[t]
-                                 : __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(int(raw[3][t]), 0x128, 0xF, 0xF, false));
-            sc[t] = (head && EPL * g + t < cnt) ? leaky(s.L + r) : -INFINITY;
-            mb = fmaxf(mb, sc[t]);
+            for (int j = 0; j < 2; ++j) {
+                const uint32_t from = uint32_t(__builtin_amdgcn_mov_dpp(int(raw[3][j]), 0x128, 0xF, 0xF, false));
+                const float r = __builtin_bit_cast(float, hf ? raw[3][2 + j] : from);
+                sc[j] = EPL * g + 2 * hf + j < cnt ? leaky(s.L + r) : -INFINITY;
+                mb = fmaxf(mb, sc[j]);
+            }
+            mb = fmaxf(mb, __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, mb), 0x128, 0xF,
+                                                                              0xF, false)));
+        } else {
+#pragma unroll
+            for (int t = 0; t < EPL; ++t) {
+                const float r = RSEP ? rsep[t]
+                                     : __builtin_bit_cast(float,
+                                                          __builtin_amdgcn_mov_dpp(int(raw[3][t]), 0x128, 0xF, 0xF, false));
+                sc[t] = (head && EPL * g + t < cnt) ? leaky(s.L + r) : -INFINITY;
+                mb = fmaxf(mb, sc[t]);
+            }
         }
         mb = xor32_max(xor16_max(mb));
         float scale = 1.0f;
@@ -184,13 +204,32 @@ __device__ inline void gather_sums(const uint32_t* __restrict__ pcol, const uint
         // ---- A operands: row h = hi (then lo) part of p_h for the lane's edges
         uint32_t ah[EPL / 2], al[EPL / 2];
         float ps = 0.0f;
+        if constexpr (SPLIT) {
+            const float p0 = exp_w(sc[0] - s.m);  // -inf past the end: 0
+            const float p1 = exp_w(sc[1] - s.m);
+            const uint32_t hw = bf16x2(p0, p1);
+            const uint32_t lw = bf16x2(p0 - __builtin_bit_cast(float, hw << 16), p1 - __builtin_bit_cast(float, hw & 0xffff0000u));
+            const float pp = p0 + p1;
+            // edges 2, 3 from lane h + 8; rows 8..15 of A (lanes n >= 8) are zero
+            const uint32_t ho = uint32_t(__builtin_amdgcn_mov_dpp(int(hw), 0x128, 0xF, 0xF, false));
+            const uint32_t lo = uint32_t(__builtin_amdgcn_mov_dpp(int(lw), 0x128, 0xF, 0xF, false));
+            const float po = __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, pp), 0x128, 0xF,
+                                                                                0xF, false));
+            ah[0] = head ? hw : 0u;
+            ah[1] = head ? ho : 0u;
+            al[0] = head ? lw : 0u;
+            al[1] = head ? lo : 0u;
+            ps = pp + po;  // (p0 + p1) + (p2 + p3) in the head lanes
+        } else {
 #pragma unroll
-        for (int q = 0; q < EPL / 2; ++q) {
-            const float p0 = head ? exp_w(sc[2 * q] - s.m) : 0.0f;  // -inf past the end: 0
-            const float p1 = head ? exp_w(sc[2 * q + 1] - s.m) : 0.0f;
-            ps += p0 + p1;
-            ah[q] = bf16x2(p0, p1);
-            al[q] = bf16x2(p0 - __builtin_bit_cast(float, ah[q] << 16), p1 - __builtin_bit_cast(float, ah[q] & 0xffff0000u));
+            for (int q = 0; q < EPL / 2; ++q) {
+                const float p0 = head ? exp_w(sc[2 * q] - s.m) : 0.0f;  // -inf past the end: 0
+                const float p1 = head ? exp_w(sc[2 * q + 1] - s.m) : 0.0f;
+                ps += p0 + p1;
+                ah[q] = bf16x2(p0, p1);
+                al[q] = bf16x2(p0 - __builtin_bit_cast(float, ah[q] << 16),
+                               p1 - __builtin_bit_cast(float, ah[q] & 0xffff0000u));
+            }
         }
         s.den = s.den * scale + ps;
         if (!EXACT && __any(head && resc)) {
@@ -326,7 +365,7 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4
             if (i == kNoRow) continue;
             Sums s;
             zero_sums(s);
-            s.L = head ? Lr : 0.0f;
+            s.L = head || !RSEP ? Lr : 0.0f;  // (lanes h + 8 score half of head h's edges)
             s.m = s.mx = -INFINITY;
             gather_sums<false, RSEP>(a.pcol, a.xr, a.R, beg, end, l, s, ids, 32 * (rr % 2));
             const float den = total_den(s.den);  // against the reference max s.m
