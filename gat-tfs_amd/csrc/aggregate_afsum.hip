@@ -142,11 +142,13 @@ __device__ inline void gather_sums(const uint32_t* __restrict__ pcol, const uint
         const uint32_t nids = pcol[(base + B < end ? base + B : end) + uint32_t(l % 32)];
         const uint64_t rem = end - base;
         const int cnt = rem < uint64_t(B) ? int(rem) : B;
-        // This lane's EPL edges; edges past the end re-read the batch's first
-        // row (weight 0).
+        // This lane's EPL edges; edges past the end re-read the batch's last
+        // row (weight 0).  Byte indices of ds_bpermute: a lane constant, one
+        // min and one add per edge.
         uint32_t jl[EPL];
 #pragma unroll
-        for (int t = 0; t < EPL; ++t) jl[t] = __shfl(ids, id0 + (EPL * g + t < cnt ? EPL * g + t : 0));
+        for (int t = 0; t < EPL; ++t)
+            jl[t] = uint32_t(__builtin_amdgcn_ds_bpermute(min(4 * (EPL * g + t), 4 * (cnt - 1)) + 4 * id0, int(ids)));
         // 32-bit byte offsets (n * 256 < 2^32 is checked at launch).
         const unsigned char* xb = reinterpret_cast<const unsigned char*>(xr);
         uint32_t raw[kSB][EPL];
