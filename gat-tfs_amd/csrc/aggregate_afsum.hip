@@ -40,12 +40,14 @@
 // 2(16 sb + n) + par.
 //
 // Blocks of 8 waves take tiles of consecutive degree-sorted rows (16 or 32,
-// see k_afs_tiles).  A row's normalised sums S_h = U_h / den_h go to LDS in
-// the B-operand layout of v_mfma_f32_32x32x16_bf16, as a hi + lo pair of bf16
-// (S = hi + lo to about 2^-17 relative) for FP32 outputs and as one bf16 for
-// bf16-stored hidden outputs.  After a barrier, wave h multiplies the tile's
-// S_h by W_h (A fragments packed as for the projection, read from L2; two
-// MFMA chains) and stores the tile's output rows.  Split rows: one wave per chunk sums its edges from
+// see k_afs_tiles).  A row's sums U_h go to LDS in the B-operand layout of
+// v_mfma_f32_32x32x16_bf16, as a hi + lo pair of bf16 (U = hi + lo to about
+// 2^-17 relative) for FP32 outputs and as one bf16 for bf16-stored hidden
+// outputs, with den_h beside them.  After a barrier, wave h multiplies the
+// tile's U_h by W_h (A fragments packed as for the projection, read from L2;
+// two MFMA chains) and scales each output row by 1 / den_h: (U_h W_h) / den_h,
+// the same quotient as (U_h / den_h) W_h, with one scaling per output row and
+// head instead of one per summed feature.  Split rows: one wave per chunk sums its edges from
 // the exact row max (per-chunk maxima of k_split_prescan) into scratch, and
 // one wave per row adds the chunks in chunk order and projects the row on
 // the VALU with the FP32 W.
@@ -66,13 +68,15 @@ constexpr int kMaxKS = 8;                  // k steps of 16 features: D_in <= 12
 constexpr int kRowWords = kXRStride / 2;   // 64 words of 4 bytes per XR row
 constexpr int kEPL = 4;                    // edges per lane and batch (batches of 4 kEPL edges)
 constexpr int kSB = 4;                     // super-blocks of 16 words per row
-constexpr int kBlk = kTile * 32 + 32;      // bytes per (head, k step, hi|lo) block of S, padded
+constexpr int kBlk = kTile * 32 + 32;      // bytes per (head, k step, hi|lo) block of U, padded
 // Heads 4..7 sit this many bytes further on: with blocks 8 words apart modulo
-// the banks, the 32 lanes that write S (k group g, lanes n) land on 32
+// the banks, the 32 lanes that write U (k group g, lanes n) land on 32
 // distinct banks: n % 8, + 8 for n / 8, + 16 for g.
 constexpr int kHalfOff = 64;
 constexpr int kSBytes = 8 * kMaxKS * 2 * kBlk + kHalfOff;
-constexpr int kLdsBytes = kSBytes + 2 * 2 * kTile * 4;  // S, then the tile's node ids (up to 2 x 32)
+constexpr int kTRowBytes = 2 * 2 * kTile * 4;             // the tile's node ids (up to 2 x 32)
+constexpr int kTDenBytes = 2 * 8 * (2 * kTile + 1) * 4;   // their denominators (2 x 8 heads x 33)
+constexpr int kLdsBytes = kSBytes + kTRowBytes + kTDenBytes;  // S, node ids, denominators
 constexpr uint32_t kNoRow = 0xffffffffu;
 constexpr int kPart = 8 * 128 + 8;         // floats per chunk partial (U_h rows of 128, then den)
 constexpr int kDenOff = 8 * 128;
@@ -138,17 +142,23 @@ __device__ inline void gather_sums(const uint32_t* __restrict__ pcol, const uint
     if (beg >= end) return;
     const int g = l / 16, n = l % 16;
     const bool head = n < 8;
+    // Source nodes of this lane's EPL edges of the batch at base, from ids
+    // (lane i0 + t holds the batch's edge t); edges past the end re-read the
+    // batch's last row (weight 0).  Byte indices of ds_bpermute: a lane
+    // constant, one min and one add per edge.
+    auto sources = [&](uint32_t idv, int i0, uint64_t base, uint32_t (&js)[EPL]) {
+        const uint64_t rem = end - base;
+        const int cnt = rem < uint64_t(B) ? int(rem) : B;
+#pragma unroll
+        for (int t = 0; t < EPL; ++t)
+            js[t] = uint32_t(__builtin_amdgcn_ds_bpermute(min(4 * (EPL * g + t), 4 * (cnt - 1)) + 4 * i0, int(idv)));
+    };
+    uint32_t jl[EPL];
+    sources(ids, id0, beg, jl);
     for (uint64_t base = beg; base < end; base += B) {
         const uint32_t nids = pcol[(base + B < end ? base + B : end) + uint32_t(l % 32)];
         const uint64_t rem = end - base;
         const int cnt = rem < uint64_t(B) ? int(rem) : B;
-        // This lane's EPL edges; edges past the end re-read the batch's last
-        // row (weight 0).  Byte indices of ds_bpermute: a lane constant, one
-        // min and one add per edge.
-        uint32_t jl[EPL];
-#pragma unroll
-        for (int t = 0; t < EPL; ++t)
-            jl[t] = uint32_t(__builtin_amdgcn_ds_bpermute(min(4 * (EPL * g + t), 4 * (cnt - 1)) + 4 * id0, int(ids)));
         // 32-bit byte offsets (n * 256 < 2^32 is checked at launch).
         const unsigned char* xb = reinterpret_cast<const unsigned char*>(xr);
         uint32_t raw[kSB][EPL];
@@ -178,8 +188,7 @@ __device__ inline void gather_sums(const uint32_t* __restrict__ pcol, const uint
                 sc[j] = EPL * g + 2 * hf + j < cnt ? leaky(s.L + r) : -INFINITY;
                 mb = fmaxf(mb, sc[j]);
             }
-            mb = fmaxf(mb, __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, mb), 0x128, 0xF,
-                                                                              0xF, false)));
+            mb = max_ror8(mb);
         } else {
 #pragma unroll
             for (int t = 0; t < EPL; ++t) {
@@ -194,7 +203,7 @@ __device__ inline void gather_sums(const uint32_t* __restrict__ pcol, const uint
         float scale = 1.0f;
         bool resc = false;
         if constexpr (!EXACT) {
-            s.mx = fmaxf(s.mx, mb);
+            s.mx = max_quiet(s.mx, mb);
             // The first batch (m = -inf) sets m; a later one moves it (and
             // rescales the sums) only beyond m + kLazyMax.
             const bool up = mb > s.m + kLazyMax;
@@ -259,8 +268,10 @@ __device__ inline void gather_sums(const uint32_t* __restrict__ pcol, const uint
             s.d[2 * sb] = Mfma<EPL>::run(al, ev, s.d[2 * sb]);
             s.d[2 * sb + 1] = Mfma<EPL>::run(al, od, s.d[2 * sb + 1]);
         }
-        ids = nids;
-        id0 = 0;
+        // The next batch's sources, formed while the MFMAs run so that its
+        // loads leave at the top of the next iteration (past the last batch
+        // they go unused).
+        sources(nids, 0, base + B, jl);
     }
 }
 
@@ -278,15 +289,15 @@ __device__ inline float total_den(float den) {
 }
 
 
-// HL: S staged as hi + lo bf16 (FP32 outputs) for 16-row tiles.  Otherwise
-// (bf16-stored hidden outputs) S is staged as one bf16 (its rounding is that
+// HL: U staged as hi + lo bf16 (FP32 outputs) for 16-row tiles.  Otherwise
+// (bf16-stored hidden outputs) U is staged as one bf16 (its rounding is that
 // of a bf16 projection input, 2^-9 relative): 32-row tiles (4 rows per wave,
 // the MFMA's 32 columns all used), or 16-row tiles in two alternating buffers
 // with one barrier per tile (a wave writes buffer t % 2 only after the
 // barrier of tile t - 1, which every wave reaches after projecting tile t - 2
 // from the same buffer).  Single-buffered tiles take a barrier before and
 // after the projection.
-// DIM: head width, 32 or 64 (wave h then multiplies S_h by the two 32-column
+// DIM: head width, 32 or 64 (wave h then multiplies U_h by the two 32-column
 // blocks of W_h in turn).  KS = 8 (D_in > 112): R from its own array.
 template <int KS, bool HL, int TR, int DIM>
 __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) k_afs_tiles(AfsArgs a) {
@@ -294,12 +305,17 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4
     static_assert(DIM == 32 || DIM == 64, "heads of 32 or 64");
     constexpr bool RSEP = KS == 8;
     constexpr int RPW = TR / kWaves;          // rows per wave and tile
-    constexpr bool DB = !HL && TR == 16;      // two alternating S buffers
+    constexpr bool DB = !HL && TR == 16;      // two alternating U buffers
     constexpr int BLK = TR * 32 + 32;         // bytes per (head, k step[, hi|lo]) block of S
-    static_assert(8 * kMaxKS * (HL ? 2 : DB ? 2 : 1) * BLK + kHalfOff <= kSBytes, "S fits");
+    static_assert(8 * kMaxKS * (HL ? 2 : DB ? 2 : 1) * BLK + kHalfOff <= kSBytes, "U fits");
+    static_assert(2 * 8 * (TR + 1) * 4 <= kTDenBytes && 2 * TR * 4 <= kTRowBytes, "ids and denominators fit");
     extern __shared__ __attribute__((aligned(16))) unsigned char slds[];
     // Destination node of each tile row (kNoRow: none), for the projection stores.
     uint32_t* const trow_all = reinterpret_cast<uint32_t*>(slds + kSBytes);
+    // den_h of tile row r at [h][r] (rows of TR + 1 floats: the 8 head lanes
+    // that write a row's values, and the 32 lanes that read a head's, each
+    // meet distinct banks).
+    float* const tden_all = reinterpret_cast<float*>(slds + kSBytes + kTRowBytes);
     int buf = 0;
     const int w = __builtin_amdgcn_readfirstlane(int(threadIdx.x) / kWave);
     const int l = threadIdx.x % kWave;
@@ -347,6 +363,7 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4
     fetch_ids(mi, mb, me, idr, Lall);
     for (uint64_t tile = blockIdx.x; tile < tiles; tile += gridDim.x, buf ^= DB ? 1 : 0) {
         uint32_t* const trow = trow_all + buf * TR;
+        float* const tden = tden_all + buf * 8 * (TR + 1);
         // ---- RPW rows per wave (tile rows w + 8 q): bounds in lane q, L in
         // lanes 8 q + h, first ids in idr.
         uint32_t n2mi;
@@ -376,13 +393,8 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4
                 // denominator against the row max, sum e^(s - M) = den e^(m - M)
                 a.mx[uint64_t(i) * 8 + n] = end > beg ? s.mx : 0.0f;
                 a.den[uint64_t(i) * 8 + n] = end > beg ? den * exp_w(s.m - s.mx) : 0.0f;
+                tden[n * (TR + 1) + r] = den;  // against the reference max, as U
             }
-            const float inv = den > 0.0f ? 1.0f / den : 0.0f;
-            // 1 / den of head 4g + q for the lanes g = 0, 1, gathered before any
-            // lane is masked off
-            float iq[4];
-#pragma unroll
-            for (int q = 0; q < 4; ++q) iq[q] = __shfl(inv, 4 * (g & 1) + q);
             if (g < 2) {
                 // Element (head h, feature pair P = 16 sb + n) of tile row r sits at
                 // block (h, P / 8[, hl]) + 32 r + 4 (P % 8): a per-lane base plus a
@@ -398,7 +410,7 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4
                     if (ks >= KS) continue;
 #pragma unroll
                     for (int q = 0; q < 4; ++q) {
-                        const float s0 = s.d[2 * sb][q] * iq[q], s1 = s.d[2 * sb + 1][q] * iq[q];
+                        const float s0 = s.d[2 * sb][q], s1 = s.d[2 * sb + 1][q];
                         const uint32_t hw = bf16x2(s0, s1);
                         if constexpr (HL) {
                             const uint32_t lw = bf16x2(s0 - __builtin_bit_cast(float, hw << 16),
@@ -434,7 +446,14 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4
         };
         load_w(0);
         __syncthreads();
-        // ---- wave h: the tile's S_h W_h.  B lane l reads tile row l % 16 (lanes
+        // 1 / den of the lane's output row (tile row l % 32) and head w; an
+        // empty row has U = 0 and den = 0, and gives 0.
+        float inv;
+        {
+            const float dv = tden[w * (TR + 1) + (l % 32) % TR];
+            inv = dv > 0.0f ? 1.0f / dv : 0.0f;
+        }
+        // ---- wave h: the tile's U_h W_h / den_h.  B lane l reads tile row l % 16 (lanes
         // with l % 32 >= 16 repeat rows 0..15; their output columns are dropped).
 #pragma unroll
         for (int b = 0; b < NBH; ++b) {
@@ -470,7 +489,7 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4
                     float o[16];
 #pragma unroll
                     for (int x = 0; x < 16; ++x) {
-                        const float y = dh[x] + dl[x];
+                        const float y = (dh[x] + dl[x]) * inv;
                         o[x] = HL ? y : elu_bf16(y);  // FP32 outputs: the last layer; bf16: hidden
                     }
                     const uint64_t off = uint64_t(i) * (8 * DIM) + DIM * h + 32 * b + 16 * half;
@@ -661,7 +680,7 @@ hipError_t launch_tiles_hl(const AfsArgs& a, hipStream_t s, int cus) {
     return hipGetLastError();
 }
 
-// FP32 outputs (the last layer, no ELU) keep S as hi + lo; bf16-stored hidden
+// FP32 outputs (the last layer, no ELU) keep U as hi + lo; bf16-stored hidden
 // outputs stage one bf16.
 template <int KS>
 hipError_t launch_tiles(const AfsArgs& a, hipStream_t s, int cus) {

@@ -34,18 +34,38 @@ __device__ inline uint32_t bf16x2(float lo, float hi) {
 }
 __device__ inline uint16_t bf16_hw(float x) { return __builtin_bit_cast(uint16_t, static_cast<__bf16>(x)); }
 
+// fmaxf for operands that are arithmetic results or lane copies of them,
+// never a signalling NaN: the plain v_max_f32.  fmaxf puts a canonicalizing
+// v_max x, x, x in front of every operand the compiler cannot trace to
+// arithmetic (a DPP or permlane result); on quiet operands that is the
+// identity, so the result is fmaxf's bit for bit.
+__device__ inline float max_quiet(float a, float b) {
+    float r;
+    asm("v_max_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
+    return r;
+}
+// max_quiet(x, x of lane l ^ 8) within each row of 16 lanes: one v_max_f32
+// with a DPP row rotation by 8 on its first operand.  The two wait states
+// ahead of it are the DPP read-after-VALU-write hazard of the operand.
+__device__ inline float max_ror8(float x) {
+    float r;
+    asm("s_nop 1\n\tv_max_f32_dpp %0, %1, %1 row_ror:8 row_mask:0xf bank_mask:0xf" : "=v"(r) : "v"(x));
+    return r;
+}
+
 // max / sum of x over lanes l and l ^ 16 (l ^ 32): v_permlane16_swap
 // (v_permlane32_swap) hands each lane the other half's value in the VALU,
 // without the LDS round trip of a lane permute.  The swap returns the pair
 // {x_l, x_(l^16)} in some order; max and + are commutative, so the result is
 // that of fmaxf(x, __shfl_xor(x, 16)) (x + __shfl_xor(x, 16)) bit for bit.
+// The max forms take quiet operands (see max_quiet).
 __device__ inline float xor16_max(float x) {
     const auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-    return fmaxf(__uint_as_float(p[0]), __uint_as_float(p[1]));
+    return max_quiet(__uint_as_float(p[0]), __uint_as_float(p[1]));
 }
 __device__ inline float xor32_max(float x) {
     const auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-    return fmaxf(__uint_as_float(p[0]), __uint_as_float(p[1]));
+    return max_quiet(__uint_as_float(p[0]), __uint_as_float(p[1]));
 }
 __device__ inline float xor16_add(float x) {
     const auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
