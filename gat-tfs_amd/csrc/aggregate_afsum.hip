@@ -142,23 +142,26 @@ __device__ inline void gather_sums(const uint32_t* __restrict__ pcol, const uint
     if (beg >= end) return;
     const int g = l / 16, n = l % 16;
     const bool head = n < 8;
-    // Source nodes of this lane's EPL edges of the batch at base, from ids
-    // (lane i0 + t holds the batch's edge t); edges past the end re-read the
-    // batch's last row (weight 0).  Byte indices of ds_bpermute: a lane
-    // constant, one min and one add per edge.
-    auto sources = [&](uint32_t idv, int i0, uint64_t base, uint32_t (&js)[EPL]) {
-        const uint64_t rem = end - base;
-        const int cnt = rem < uint64_t(B) ? int(rem) : B;
+    // Edge counts in 32 bits (set_graph rejects rows of 2^32 edges or more),
+    // so that the loop's compares run on the scalar unit.
+    const uint32_t total = uint32_t(end - beg);
+    // Source nodes of this lane's EPL edges of a batch with `left` edges to
+    // go, from ids (lane i0 + t holds the batch's edge t); edges past the end
+    // re-read the batch's last row (weight 0).  Byte indices of ds_bpermute:
+    // a lane constant, one min and one add per edge.
+    auto sources = [&](uint32_t idv, int i0, uint32_t left, uint32_t (&js)[EPL]) {
+        const int cnt = left < uint32_t(B) ? int(left) : B;
 #pragma unroll
         for (int t = 0; t < EPL; ++t)
             js[t] = uint32_t(__builtin_amdgcn_ds_bpermute(min(4 * (EPL * g + t), 4 * (cnt - 1)) + 4 * i0, int(idv)));
     };
     uint32_t jl[EPL];
-    sources(ids, id0, beg, jl);
-    for (uint64_t base = beg; base < end; base += B) {
-        const uint32_t nids = pcol[(base + B < end ? base + B : end) + uint32_t(l % 32)];
-        const uint64_t rem = end - base;
-        const int cnt = rem < uint64_t(B) ? int(rem) : B;
+    sources(ids, id0, total, jl);
+    for (uint32_t done = 0; done < total; done += B) {
+        const uint64_t base = beg + done;
+        const uint32_t left = total - done;
+        const uint32_t nids = pcol[(left > uint32_t(B) ? base + B : end) + uint32_t(l % 32)];
+        const int cnt = left < uint32_t(B) ? int(left) : B;
         // 32-bit byte offsets (n * 256 < 2^32 is checked at launch).
         const unsigned char* xb = reinterpret_cast<const unsigned char*>(xr);
         uint32_t raw[kSB][EPL];
@@ -271,7 +274,7 @@ __device__ inline void gather_sums(const uint32_t* __restrict__ pcol, const uint
         // The next batch's sources, formed while the MFMAs run so that its
         // loads leave at the top of the next iteration (past the last batch
         // they go unused).
-        sources(nids, 0, base + B, jl);
+        sources(nids, 0, left - B, jl);
     }
 }
 

@@ -126,28 +126,31 @@ __device__ inline void load_ids(const uint32_t* __restrict__ pcol, uint64_t base
     for (int t = 0; t < C::BATCH; ++t) js[t] = pc[base + t];
 }
 
+// `left` (>= 1) edges of the row remain from the batch's first.  Edges past
+// the end take the source of the batch's last edge: its row is loaded by this
+// batch anyway, so the repeated load stays in the caches and no load needs a
+// bounds test; their weight is 0 and they leave m alone.
 template <class C, class ZT, bool RZ>
-__device__ inline void batch(uint64_t base, uint64_t end, const uint32_t (&js)[C::BATCH],
-                             const float* __restrict__ R, const ZT* __restrict__ Z, int slot, int sub,
-                             Lane<C>& st) {
+__device__ inline void batch(uint32_t left, const uint32_t (&js)[C::BATCH], const float* __restrict__ R,
+                             const ZT* __restrict__ Z, int slot, int sub, Lane<C>& st) {
+    uint32_t jc[C::BATCH];
+    jc[0] = js[0];
+#pragma unroll
+    for (int t = 1; t < C::BATCH; ++t) jc[t] = uint32_t(t) < left ? js[t] : jc[t - 1];
     uint4 z[C::U][C::VPL];
     float s[C::U][C::VPL];
     bool ok[C::U];
 #pragma unroll
     for (int u = 0; u < C::U; ++u) {
-        uint32_t j = js[u * C::EPI];
+        uint32_t j = jc[u * C::EPI];
 #pragma unroll
-        for (int q = 1; q < C::EPI; ++q) j = slot == q ? js[u * C::EPI + q] : j;
-        ok[u] = base + uint64_t(u * C::EPI + slot) < end;
+        for (int q = 1; q < C::EPI; ++q) j = slot == q ? jc[u * C::EPI + q] : j;
+        ok[u] = slot < int(left) - u * C::EPI;
         const ZT* row = Z + uint64_t(j) * C::W;
 #pragma unroll
         for (int v = 0; v < C::VPL; ++v) {
-            z[u][v] = ok[u] ? *reinterpret_cast<const uint4*>(row + (sub + kWave * v) * C::VEC)
-                            : make_uint4(0, 0, 0, 0);
-            if constexpr (!RZ) {
-                const float r = ok[u] ? R[uint64_t(j) * C::K + st.h[v]] : 0.0f;
-                s[u][v] = leaky(st.L[v] + r);
-            }
+            z[u][v] = *reinterpret_cast<const uint4*>(row + (sub + kWave * v) * C::VEC);
+            if constexpr (!RZ) s[u][v] = leaky(st.L[v] + R[uint64_t(j) * C::K + st.h[v]]);
         }
     }
     if constexpr (RZ) {
@@ -166,7 +169,8 @@ __device__ inline void batch(uint64_t base, uint64_t end, const uint32_t (&js)[C
             t += quad_xor1(t);
             t += quad_xor2(t);
             const float sc_ = leaky(st.L[0] + t);
-            const float mn = ok[u] ? fmaxf(st.m[0], sc_) : st.m[0];
+            const float mx = max_quiet(st.m[0], sc_);  // unconditional: no branch around the asm
+            const float mn = ok[u] ? mx : st.m[0];
             const float scale = mn > st.m[0] ? exp_w(st.m[0] - mn) : 1.0f;  // exp(-inf) = 0 on a slot's first edge
             if (__any(scale != 1.0f)) {
                 st.den[0] *= scale;
@@ -185,8 +189,11 @@ __device__ inline void batch(uint64_t base, uint64_t end, const uint32_t (&js)[C
     for (int v = 0; v < C::VPL; ++v) {
         float mb = -INFINITY;
 #pragma unroll
-        for (int u = 0; u < C::U; ++u) mb = ok[u] ? fmaxf(mb, s[u][v]) : mb;
-        const float mn = fmaxf(st.m[v], mb);
+        for (int u = 0; u < C::U; ++u) {
+            const float mx = max_quiet(mb, s[u][v]);
+            mb = ok[u] ? mx : mb;
+        }
+        const float mn = max_quiet(st.m[v], mb);
         const float sc = mn > st.m[v] ? exp_w(st.m[v] - mn) : 1.0f;  // exp(-inf) = 0 on a slot's first edge
         st.m[v] = mn;
         st.den[v] *= sc;
@@ -250,11 +257,14 @@ __device__ inline void aggregate(uint64_t beg, uint64_t end, const uint32_t* __r
                                  Lane<C>& st) {
     uint32_t js[C::BATCH];
     load_ids<C>(pcol, beg, js);
-    for (uint64_t base = beg; base < end; base += C::BATCH) {
+    // 32-bit edge counts (set_graph rejects rows of 2^32 edges or more): the
+    // loop's and the batch's tests stay on the scalar unit.
+    const uint32_t total = uint32_t(end - beg);
+    for (uint32_t done = 0; done < total; done += C::BATCH) {
         // The next batch's ids are requested before this batch's rows arrive.
         uint32_t jn[C::BATCH];
-        load_ids<C>(pcol, base + C::BATCH, jn);
-        batch<C, ZT, RZ>(base, end, js, R, Z, slot, sub, st);
+        load_ids<C>(pcol, beg + done + C::BATCH, jn);
+        batch<C, ZT, RZ>(total - done, js, R, Z, slot, sub, st);
 #pragma unroll
         for (int t = 0; t < C::BATCH; ++t) js[t] = jn[t];
     }

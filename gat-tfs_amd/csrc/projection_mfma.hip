@@ -130,9 +130,13 @@ __global__ void __launch_bounds__(kThreads) k_proj_mfma(ProjArgs a) {
 // Z leaves as two 16-byte stores per block.  FULL: 0 any shape; 1 a layer of
 // 8 heads x 32 with every store unconditional; 2 the same with R = Z_bf16 aR
 // (what the aggregation recomputes from the gathered row).
+// L/R-only launches (HB = 0: the aggregate-first front end, a streaming pass
+// with KS KB of W) take a full grid, one tile per wave, and W is cheap to
+// refetch; their LDS request holds them to two blocks (16 waves) per CU.
 template <int KS, int HB, bool F32IN, int FULL>
 __global__ void __launch_bounds__(kThreads) k_proj_fast(ProjArgs a) {
     static_assert(!FULL || HB == 8, "FULL layers are 8 heads x 32");
+    constexpr bool ONE = HB == 0;  // one tile per wave, nothing requested ahead
     constexpr int NB = HB + 1;
     extern __shared__ uint4 wlds[];
     for (int q = threadIdx.x; q < KS * NB * kWave; q += kThreads) {
@@ -195,6 +199,8 @@ __global__ void __launch_bounds__(kThreads) k_proj_fast(ProjArgs a) {
         // The first tile waits for all of its input here, so that the wait in
         // the loop only has the loop's own issue order to follow (a merge with
         // the prologue's order would make it wait for every store as well).
+        // A single tile waits here too: waits per k step, between which the
+        // converted input rows are stored, measured slower.
         __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
     }
     for (; tile < a.tiles; tile += stride) {
@@ -226,8 +232,10 @@ __global__ void __launch_bounds__(kThreads) k_proj_fast(ProjArgs a) {
         // next tile.  Every load is unconditional, so each wait is exact.
 #pragma unroll
         for (int ks = 0; ks < KA; ++ks) kstep(ks);
+        if constexpr (!ONE) {
 #pragma unroll
-        for (int ks = 0; ks < KA; ++ks) load_ks(next, ks);
+            for (int ks = 0; ks < KA; ++ks) load_ks(next, ks);
+        }
 #pragma unroll
         for (int ks = KA; ks < KS; ++ks) kstep(ks);
         // A lane past n computed row n - 1 from the same input, so it stores
@@ -306,8 +314,10 @@ __global__ void __launch_bounds__(kThreads) k_proj_fast(ProjArgs a) {
                 }
             }
         }
+        if constexpr (!ONE) {
 #pragma unroll
-        for (int ks = KA; ks < KS; ++ks) load_ks(next, ks);
+            for (int ks = KA; ks < KS; ++ks) load_ks(next, ks);
+        }
     }
 }
 
@@ -627,6 +637,8 @@ hipError_t launch_f32_kh(const ProjF32Args& a, hipStream_t s) {
     return hipGetLastError();
 }
 
+constexpr size_t kOneTileLds = 56 * 1024;  // over a third of the CU's 160 KB
+
 template <int KS, int HB, bool F32IN, int FULL>
 hipError_t launch_fast_io(const ProjArgs& a, hipStream_t s, int cus) {
     const size_t lds = size_t(KS) * (HB + 1) * kWave * sizeof(uint4) + (FULL ? 256 * sizeof(float) : 0);
@@ -635,13 +647,18 @@ hipError_t launch_fast_io(const ProjArgs& a, hipStream_t s, int cus) {
                                            hipFuncAttributeMaxDynamicSharedMemorySize, int(lds));
         if (e != hipSuccess) return e;
     }
-    const int per_cu = lds <= 80 * 1024 ? 2 : 1;
-    uint64_t gx = uint64_t(cus) * per_cu;
+    // resident grid (1 or 2 blocks per CU), or one tile per wave for HB = 0
+    // with the dynamic LDS raised to kOneTileLds (at most two blocks per CU:
+    // a third block's streams measured slower, 0.40 against 0.33 ms on a
+    // 2.45M x 100 input)
     const uint64_t wg_needed = (a.tiles + kWaves - 1) / kWaves;
+    uint64_t gx = HB == 0 ? wg_needed : uint64_t(cus) * (lds <= 80 * 1024 ? 2 : 1);
     if (gx > wg_needed) gx = wg_needed;
     if (gx < 1) gx = 1;
+    if (gx > 0x7fffffffu) return hipErrorInvalidValue;
     if (FULL == 2 && !a.ar) return hipErrorInvalidValue;
-    k_proj_fast<KS, HB, F32IN, FULL><<<dim3(uint32_t(gx)), kThreads, lds, s>>>(a);
+    const size_t req = HB == 0 && lds < kOneTileLds ? kOneTileLds : lds;
+    k_proj_fast<KS, HB, F32IN, FULL><<<dim3(uint32_t(gx)), kThreads, req, s>>>(a);
     return hipGetLastError();
 }
 

@@ -229,8 +229,9 @@ def test_aggregation_output_store_bit_exact(gpu_ctx, D, K, d):
         assert_bits_equal(bits(out), rne(pre.astype(np.float32)), f"output store {D}->{K}x{d} {opts}")
 
 
-# Aggregate-first hidden layers: the sum form (8 x 32, 8 x 64: S = U / den
-# rounded to bf16, then S W_h, rounded again) and the neighbour-step form
+# Aggregate-first hidden layers: the sum form (8 x 32, 8 x 64: U rounded to
+# bf16, then (U W_h) / den, rounded again; with a power-of-two den the first
+# rounding is that of U / den) and the neighbour-step form
 # (4 x 32: sum_j p (X_j W_h) / den; TFS_B1: bf16(p X_j) W_h), all inputs at
 # one feature k0 so that each output is one exact product.
 AF_OUT = [(100, 8, 32, gatgpu.AGGREGATE_FIRST), (128, 8, 64, gatgpu.AGGREGATE_FIRST),
@@ -259,7 +260,8 @@ def test_aggregate_first_output_store_bit_exact(gpu_ctx, D, K, d, flow):
         mean = (u / deg).astype(np.float32)  # exact: 8-bit values in [1, 2), power-of-two degrees
         w0 = p["w"][k0].astype(np.float64)
         if flow == gatgpu.AGGREGATE_FIRST and K == 8:
-            # sum form: S = U / den enters the MFMA as one bf16 (hidden output)
+            # sum form: U enters the MFMA as one bf16 (hidden output), and U / den
+            # has the same significand (den a power of two)
             s = (oracle.rne_bits(mean).astype(np.uint32) << 16).view(np.float32).astype(np.float64)
         else:
             s = mean.astype(np.float64)  # sum_j x_j w / den: each term and the sum exact
