@@ -135,18 +135,22 @@ __device__ inline void group_online(uint64_t beg, uint64_t end, const uint32_t* 
                                     const float (&arl)[C::VEC], float (&acc)[C::VEC], float& dsum, float& m) {
     static_assert(C::VEC == 8, "bf16 rows only");
     static_assert(!RZ || C::G == 8, "R from Z needs the 8-lane reduction order");
-    const bool reader = RZ || sub * C::VEC < W || sub == C::G - 1;
-    for (uint64_t base = beg; base < end; base += C::G) {
-        const uint64_t e = base + sub;
-        const uint32_t j = e < end ? pcol[e] : 0u;
-        const uint64_t rem = end - base;
-        const int cnt = rem < uint64_t(C::G) ? int(rem) : C::G;
+    // 32-bit edge counts (set_graph rejects rows of 2^32 edges or more).
+    // Every lane loads its slice of every edge's line, with no bounds test:
+    // edges past the end read row 0 (cached after its first use) and get
+    // score -inf, weight 0; slices past W feed accumulators that are never
+    // stored.  pcol carries kPcolPad entries past e for the id loads.
+    const uint32_t total = uint32_t(end - beg);
+    for (uint32_t done = 0; done < total; done += C::G) {
+        const uint32_t left = total - done;
+        const int cnt = left < uint32_t(C::G) ? int(left) : C::G;
+        const uint32_t jr = pcol[beg + done + sub];
+        const uint32_t j = sub < cnt ? jr : 0u;
         uint4 raw[C::G];
 #pragma unroll
         for (int t = 0; t < C::G; ++t) {
             const uint32_t jt = __shfl(j, gbase + t);
-            raw[t] = (t < cnt && reader) ? *reinterpret_cast<const uint4*>(Z + uint64_t(jt) * zs + sub * C::VEC)
-                                         : make_uint4(0, 0, 0, 0);
+            raw[t] = *reinterpret_cast<const uint4*>(Z + uint64_t(jt) * zs + sub * C::VEC);
         }
         float s[C::G];
         float mb = -INFINITY;
