@@ -110,6 +110,7 @@ struct Lane {
     float L[C::VPL];
     int h[C::VPL];
     float ar[C::VEC];  // aR of the lane's features (R from the gathered row)
+    uint32_t smask;    // all ones in the lanes of edge slot 1 (batch, O32)
 };
 
 // One batch of edges [base, base + BATCH) clipped to end.  RZ (bf16 8 x 32):
@@ -130,9 +131,21 @@ __device__ inline void load_ids(const uint32_t* __restrict__ pcol, uint64_t base
 // the end take the source of the batch's last edge: its row is loaded by this
 // batch anyway, so the repeated load stays in the caches and no load needs a
 // bounds test; their weight is 0 and they leave m alone.
-template <class C, class ZT, bool RZ>
+// O32 (RZ, two edge slots, n W sizeof(ZT) <= 2^32, checked at launch): a
+// lane's byte offset into Z is j0 RB + ((j1 - j0) RB & smask) + 16 sub for
+// the slot-0 / slot-1 sources j0, j1 of a load (RB bytes per row; smask all
+// ones in the slot-1 lanes), two VALU operations on scalar operands instead
+// of a per-lane select and a 64-bit address.
+// FREE (RZ): every edge slot has seen a valid edge before its first past-end
+// edge (the row has at least EPI edges, or m starts at a chunk's finite row
+// max), so m is finite there: a past-end edge is given the score -inf, which
+// leaves m in place (scale e^0 = 1) and weighs 0 -- the values of the tested
+// form, without its selects.
+template <class C, class ZT, bool RZ, bool O32 = false, bool FREE = false>
 __device__ inline void batch(uint32_t left, const uint32_t (&js)[C::BATCH], const float* __restrict__ R,
                              const ZT* __restrict__ Z, int slot, int sub, Lane<C>& st) {
+    static_assert(!O32 || (RZ && C::EPI == 2 && C::VPL == 1), "32-bit offsets: the two-slot R-from-Z form");
+    static_assert(!FREE || RZ, "unmasked weights: the R-from-Z form");
     uint32_t jc[C::BATCH];
     jc[0] = js[0];
 #pragma unroll
@@ -142,15 +155,25 @@ __device__ inline void batch(uint32_t left, const uint32_t (&js)[C::BATCH], cons
     bool ok[C::U];
 #pragma unroll
     for (int u = 0; u < C::U; ++u) {
-        uint32_t j = jc[u * C::EPI];
-#pragma unroll
-        for (int q = 1; q < C::EPI; ++q) j = slot == q ? jc[u * C::EPI + q] : j;
         ok[u] = slot < int(left) - u * C::EPI;
-        const ZT* row = Z + uint64_t(j) * C::W;
+        if constexpr (O32) {
+            constexpr uint32_t RB = C::W * sizeof(ZT);
+            // scalar products, kept scalar (one v_and and one v_add3 per lane)
+            uint32_t j0 = jc[2 * u] * RB;
+            asm volatile("" : "+s"(j0));
+            const uint32_t dj = (jc[2 * u + 1] - jc[2 * u]) * RB;
+            const uint32_t off = j0 + (dj & st.smask) + uint32_t(sub * 16);
+            z[u][0] = *reinterpret_cast<const uint4*>(reinterpret_cast<const unsigned char*>(Z) + off);
+        } else {
+            uint32_t j = jc[u * C::EPI];
 #pragma unroll
-        for (int v = 0; v < C::VPL; ++v) {
-            z[u][v] = *reinterpret_cast<const uint4*>(row + (sub + kWave * v) * C::VEC);
-            if constexpr (!RZ) s[u][v] = leaky(st.L[v] + R[uint64_t(j) * C::K + st.h[v]]);
+            for (int q = 1; q < C::EPI; ++q) j = slot == q ? jc[u * C::EPI + q] : j;
+            const ZT* row = Z + uint64_t(j) * C::W;
+#pragma unroll
+            for (int v = 0; v < C::VPL; ++v) {
+                z[u][v] = *reinterpret_cast<const uint4*>(row + (sub + kWave * v) * C::VEC);
+                if constexpr (!RZ) s[u][v] = leaky(st.L[v] + R[uint64_t(j) * C::K + st.h[v]]);
+            }
         }
     }
     if constexpr (RZ) {
@@ -169,16 +192,24 @@ __device__ inline void batch(uint32_t left, const uint32_t (&js)[C::BATCH], cons
             t += quad_xor1(t);
             t += quad_xor2(t);
             const float sc_ = leaky(st.L[0] + t);
-            const float mx = max_quiet(st.m[0], sc_);  // unconditional: no branch around the asm
-            const float mn = ok[u] ? mx : st.m[0];
-            const float scale = mn > st.m[0] ? exp_w(st.m[0] - mn) : 1.0f;  // exp(-inf) = 0 on a slot's first edge
+            float mn, scale, p;
+            if constexpr (FREE) {
+                const float sv = ok[u] ? sc_ : -INFINITY;
+                mn = max_quiet(st.m[0], sv);
+                scale = exp_w(st.m[0] - mn);  // exactly 1 when m stays; 0 on a slot's first edge
+                p = exp_w(sv - mn);           // 0 past the end
+            } else {
+                const float mx = max_quiet(st.m[0], sc_);  // unconditional: no branch around the asm
+                mn = ok[u] ? mx : st.m[0];
+                scale = mn > st.m[0] ? exp_w(st.m[0] - mn) : 1.0f;  // exp(-inf) = 0 on a slot's first edge
+                p = ok[u] ? exp_w(sc_ - mn) : 0.0f;
+            }
             if (__any(scale != 1.0f)) {
                 st.den[0] *= scale;
 #pragma unroll
                 for (int x = 0; x < C::VEC; ++x) st.acc[x] *= scale;
             }
             st.m[0] = mn;
-            const float p = ok[u] ? exp_w(sc_ - mn) : 0.0f;
             st.den[0] += p;
 #pragma unroll
             for (int x = 0; x < C::VEC; ++x) st.acc[x] += p * f[x];
@@ -250,8 +281,14 @@ __device__ inline void merge_slots(Lane<C>& st) {
     if constexpr (C::EPI > 1) merge_step<C, C::LPR>(st);
 }
 
-// Edges [beg, end) of a row or chunk, then the edge slots merged.
-template <class C, class ZT, bool RZ>
+template <bool V>
+struct Flag {
+    static constexpr bool value = V;
+};
+
+// Edges [beg, end) of a row or chunk, then the edge slots merged.  EXACT: m
+// holds a chunk's exact (finite) row max already.  O32: see batch.
+template <class C, class ZT, bool RZ, bool O32 = false, bool EXACT = false>
 __device__ inline void aggregate(uint64_t beg, uint64_t end, const uint32_t* __restrict__ pcol,
                                  const float* __restrict__ R, const ZT* __restrict__ Z, int slot, int sub,
                                  Lane<C>& st) {
@@ -260,14 +297,20 @@ __device__ inline void aggregate(uint64_t beg, uint64_t end, const uint32_t* __r
     // 32-bit edge counts (set_graph rejects rows of 2^32 edges or more): the
     // loop's and the batch's tests stay on the scalar unit.
     const uint32_t total = uint32_t(end - beg);
-    for (uint32_t done = 0; done < total; done += C::BATCH) {
-        // The next batch's ids are requested before this batch's rows arrive.
-        uint32_t jn[C::BATCH];
-        load_ids<C>(pcol, beg + done + C::BATCH, jn);
-        batch<C, ZT, RZ>(total - done, js, R, Z, slot, sub, st);
+    auto edges = [&](auto free) {
+        for (uint32_t done = 0; done < total; done += C::BATCH) {
+            // The next batch's ids are requested before this batch's rows arrive.
+            uint32_t jn[C::BATCH];
+            load_ids<C>(pcol, beg + done + C::BATCH, jn);
+            batch<C, ZT, RZ, O32, decltype(free)::value>(total - done, js, R, Z, slot, sub, st);
 #pragma unroll
-        for (int t = 0; t < C::BATCH; ++t) js[t] = jn[t];
-    }
+            for (int t = 0; t < C::BATCH; ++t) js[t] = jn[t];
+        }
+    };
+    // Unmasked weights once every slot starts with a valid edge (rows of at
+    // least EPI edges) or from a finite max (chunks).
+    if (RZ && (EXACT || total >= uint32_t(C::EPI))) edges(Flag<RZ>{});
+    else edges(Flag<false>{});
     merge_slots<C>(st);
 }
 
@@ -346,12 +389,16 @@ __device__ inline void init_lane(const VArgs<ZT>& a, int sub, Lane<C>& st) {
     }
 #pragma unroll
     for (int x = 0; x < C::VEC; ++x) st.ar[x] = RZ ? a.ar[sub * C::VEC + x] : 0.0f;
+    // A mask in a register, not a select on the slot: dj & smask is one AND.
+    uint32_t sm = sub == int(threadIdx.x % kWave) ? 0u : ~0u;  // sub = lane in slot 0
+    asm volatile("" : "+v"(sm));
+    st.smask = sm;
 }
 
 // Chunk c of a split row: its edges from the exact row max, the partial sums
 // to scratch; the last chunk of the row to arrive adds the partials in chunk
 // order and finishes the row.
-template <class C, class ZT, bool RZ>
+template <class C, class ZT, bool RZ, bool O32>
 __device__ inline void run_chunk(const VArgs<ZT>& a, uint64_t c, int lane, int slot, int sub) {
     Lane<C> st;
     init_lane<C, ZT, RZ>(a, sub, st);
@@ -369,7 +416,7 @@ __device__ inline void run_chunk(const VArgs<ZT>& a, uint64_t c, int lane, int s
         st.L[v] = a.L[uint64_t(i) * C::K + st.h[v]];
         st.m[v] = leaky(st.L[v] + m);  // exact row max: no rescale happens in this chunk
     }
-    aggregate<C, ZT, RZ>(beg, end, a.pcol, a.R, a.Z, slot, sub, st);
+    aggregate<C, ZT, RZ, O32, true>(beg, end, a.pcol, a.R, a.Z, slot, sub, st);
     float* part = a.sp.part + c * (C::W + 8);
     if (slot == 0) {
 #pragma unroll
@@ -417,7 +464,7 @@ __device__ inline void run_chunk(const VArgs<ZT>& a, uint64_t c, int lane, int s
     finish_row<C>(i, tot, dtot, st.m, st.h, slot, sub, a.hidden, a.mx, a.den, a.out32, a.outbf);
 }
 
-template <class C, class ZT, bool RZ>
+template <class C, class ZT, bool RZ, bool O32>
 __global__ void __launch_bounds__(kThreads) k_agg_vec(VArgs<ZT> a) {
     // The wave index is made wave-uniform so that row bounds and source ids
     // come in through scalar loads.
@@ -427,7 +474,7 @@ __global__ void __launch_bounds__(kThreads) k_agg_vec(VArgs<ZT> a) {
     const int sub = C::EPI > 1 ? lane % C::LPR : lane;
     const uint64_t item = uint64_t(blockIdx.x) * kWavesPerBlock + w;
     if (item < a.sp.chunks) {
-        run_chunk<C, ZT, RZ>(a, item, lane, slot, sub);
+        run_chunk<C, ZT, RZ, O32>(a, item, lane, slot, sub);
         return;
     }
     // ---------------- whole row, heaviest first
@@ -444,7 +491,7 @@ __global__ void __launch_bounds__(kThreads) k_agg_vec(VArgs<ZT> a) {
         st.L[v] = a.L[uint64_t(i) * C::K + st.h[v]];
         st.m[v] = -INFINITY;
     }
-    aggregate<C, ZT, RZ>(beg, end, a.pcol, a.R, a.Z, slot, sub, st);
+    aggregate<C, ZT, RZ, O32>(beg, end, a.pcol, a.R, a.Z, slot, sub, st);
     // Empty row: max 0, denominator 0, output 0 (baseline/src/ref_fp32.cpp:11).
     if (end == beg)
 #pragma unroll
@@ -491,7 +538,7 @@ __device__ inline void finish_row_tile(uint32_t i, const Lane<C>& st, int slot, 
     *reinterpret_cast<uint4*>(trow + 16 * sub) = make_uint4(wv[0], wv[1], wv[2], wv[3]);
 }
 
-template <class C, int HB>
+template <class C, int HB, bool O32>
 __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(8)))
 k_agg_vec_next(VArgs<uint16_t> a, NextProj f, uint64_t chunk_blocks) {
     static_assert(HB == 1 || HB == 2, "one head of at most 64 columns");
@@ -501,7 +548,7 @@ k_agg_vec_next(VArgs<uint16_t> a, NextProj f, uint64_t chunk_blocks) {
     const int slot = lane / C::LPR, sub = lane % C::LPR;
     if (blockIdx.x < chunk_blocks) {
         const uint64_t item = uint64_t(blockIdx.x) * kWavesPerBlock + w;
-        if (item < a.sp.chunks) run_chunk<C, uint16_t, true>(a, item, lane, slot, sub);
+        if (item < a.sp.chunks) run_chunk<C, uint16_t, true, O32>(a, item, lane, slot, sub);
         return;
     }
     const uint64_t p0 = (f.tiles - 1 - (uint64_t(blockIdx.x) - chunk_blocks)) * kNextTile;
@@ -518,7 +565,7 @@ k_agg_vec_next(VArgs<uint16_t> a, NextProj f, uint64_t chunk_blocks) {
                 init_lane<C, uint16_t, true>(a, sub, st);
                 st.L[0] = a.L[k * C::K + st.h[0]];
                 st.m[0] = -INFINITY;
-                aggregate<C, uint16_t, true>(beg, end, a.pcol, a.R, a.Z, slot, sub, st);
+                aggregate<C, uint16_t, true, O32>(beg, end, a.pcol, a.R, a.Z, slot, sub, st);
                 if (end == beg) st.m[0] = 0.0f;  // empty row: max 0, den 0, output 0
                 finish_row_tile<C>(uint32_t(k), st, slot, sub, a.mx, a.den, trow);
                 stored = true;
@@ -588,6 +635,12 @@ k_agg_vec_next(VArgs<uint16_t> a, NextProj f, uint64_t chunk_blocks) {
     *reinterpret_cast<uint4*>(zr + 8) = v1;
 }
 
+// Byte offsets of every Z row fit 32 bits (the O32 form of batch).
+template <class C, class ZT>
+bool offsets32(uint64_t n) {
+    return n <= (uint64_t(1) << 32) / (uint64_t(C::W) * sizeof(ZT));
+}
+
 template <class C, class ZT>
 hipError_t run(const AggArgs& g, const RowBins& bins, const SplitTable& t, hipStream_t s) {
     VArgs<ZT> a{g.prow, g.pcol, g.perm, g.left, g.right, static_cast<const ZT*>(g.feat), g.hidden, g.mx, g.den,
@@ -603,11 +656,13 @@ hipError_t run(const AggArgs& g, const RowBins& bins, const SplitTable& t, hipSt
     if constexpr (sizeof(ZT) == 2 && C::W == 256) {
         if (g.r_from_z) {
             if (!g.ar) return hipErrorInvalidValue;
-            k_agg_vec<Cfg<ZT, C::W, C::K, kURz>, ZT, true><<<grid, kThreads, 0, s>>>(a);
+            using CR = Cfg<ZT, C::W, C::K, kURz>;
+            if (offsets32<CR, ZT>(g.n)) k_agg_vec<CR, ZT, true, true><<<grid, kThreads, 0, s>>>(a);
+            else k_agg_vec<CR, ZT, true, false><<<grid, kThreads, 0, s>>>(a);
             return hipGetLastError();
         }
     }
-    k_agg_vec<C, ZT, false><<<grid, kThreads, 0, s>>>(a);
+    k_agg_vec<C, ZT, false, false><<<grid, kThreads, 0, s>>>(a);
     return hipGetLastError();
 }
 
@@ -656,8 +711,15 @@ hipError_t launch_aggregate_vec_next(const AggArgs& g, const RowBins& bins, cons
     const uint64_t blocks = chunk_blocks + f.tiles;
     if (!blocks) return hipSuccess;
     if (blocks > 0x7fffffffu) return hipErrorInvalidValue;
-    if (f.head_blocks == 2) k_agg_vec_next<C, 2><<<dim3(uint32_t(blocks)), kThreads, 0, s>>>(a, f, chunk_blocks);
-    else k_agg_vec_next<C, 1><<<dim3(uint32_t(blocks)), kThreads, 0, s>>>(a, f, chunk_blocks);
+    const dim3 grid = dim3(uint32_t(blocks));
+    const bool o32 = offsets32<C, uint16_t>(g.n);
+    if (f.head_blocks == 2) {
+        if (o32) k_agg_vec_next<C, 2, true><<<grid, kThreads, 0, s>>>(a, f, chunk_blocks);
+        else k_agg_vec_next<C, 2, false><<<grid, kThreads, 0, s>>>(a, f, chunk_blocks);
+    } else {
+        if (o32) k_agg_vec_next<C, 1, true><<<grid, kThreads, 0, s>>>(a, f, chunk_blocks);
+        else k_agg_vec_next<C, 1, false><<<grid, kThreads, 0, s>>>(a, f, chunk_blocks);
+    }
     return hipGetLastError();
 }
 
