@@ -548,11 +548,16 @@ __global__ void __launch_bounds__(kChunkThreads) k_afs_chunks(AfsArgs a) {
     zero_sums(s);
     s.L = 0.0f;
     s.m = 0.0f;
+    // Row max over the chunk maxima: lane l reads head l % 8 of chunks l / 8,
+    // l / 8 + 8, ... (independent loads), then the 8 lanes of each head reduce.
+    float mc = -INFINITY;
+    for (uint32_t q = uint32_t(l / 8); q < nch; q += 8) mc = fmaxf(mc, a.mchunk[(first + q) * 8 + l % 8]);
+    mc = fmaxf(mc, __shfl_xor(mc, 8));
+    mc = fmaxf(mc, __shfl_xor(mc, 16));
+    mc = fmaxf(mc, __shfl_xor(mc, 32));
     if (head) {
-        const int h = n;
+        const int h = n;  // = l % 8
         s.L = a.L[uint64_t(i) * 8 + h];
-        float mc = -INFINITY;
-        for (uint32_t q = 0; q < nch; ++q) mc = fmaxf(mc, a.mchunk[(first + q) * 8 + h]);
         s.m = s.mx = leaky(s.L + mc);
     }
     const bool rsep = a.in > kXRFeat;
@@ -575,7 +580,7 @@ __global__ void __launch_bounds__(kChunkThreads) k_afs_chunks(AfsArgs a) {
 }
 
 // One wave per split row (found at its first chunk): adds the chunks' sums
-// and denominators in chunk order, then out_h = (U_h / den_h) W_h on the VALU
+// and denominators in chunk order, then out_h = (U_h W_h) / den_h on the VALU
 // with the FP32 (bf16-rounded) W; lane l computes columns 32 cb + 4 (l % 8)
 // .. + 3 of head l / 8, for each 32-column block cb of the head.
 __global__ void __launch_bounds__(kChunkThreads) k_afs_merge(AfsArgs a) {
@@ -601,7 +606,8 @@ __global__ void __launch_bounds__(kChunkThreads) k_afs_merge(AfsArgs a) {
         a.mx[uint64_t(i) * 8 + l] = leaky(a.L[uint64_t(i) * 8 + l] + mc);
         a.den[uint64_t(i) * 8 + l] = d;
     }
-    // S_h[f] = U_h[f] / den_h into LDS; lane l adds features 2l, 2l + 1.
+    // U_h[f] into LDS (lane l adds features 2l, 2l + 1); the projected row is
+    // scaled by 1 / den_h afterwards, as in the tile path.
     float dall[8];  // read before any lane is masked off
 #pragma unroll
     for (int h = 0; h < 8; ++h) dall[h] = lane_f(d, h);
@@ -623,13 +629,12 @@ __global__ void __launch_bounds__(kChunkThreads) k_afs_merge(AfsArgs a) {
                 t[h][1] += v[h].y;
             }
         }
-        // bf16-stored hidden outputs: S enters the projection as one bf16, as
+        // bf16-stored hidden outputs: U enters the projection as one bf16, as
         // in the tile path (the rounding of a bf16 projection input).
         const bool round_s = a.outbf != nullptr;
 #pragma unroll
         for (int h = 0; h < 8; ++h) {
-            const float inv = dall[h] > 0.0f ? 1.0f / dall[h] : 0.0f;
-            float s0 = t[h][0] * inv, s1 = t[h][1] * inv;
+            float s0 = t[h][0], s1 = t[h][1];
             if (round_s) {
                 s0 = bf16_widen(bf16_hw(s0));
                 s1 = bf16_widen(bf16_hw(s1));
@@ -640,6 +645,10 @@ __global__ void __launch_bounds__(kChunkThreads) k_afs_merge(AfsArgs a) {
     }
     wave_sync();
     const int h = l / 8, width = 8 * a.dim;
+    float inv = 0.0f;
+#pragma unroll
+    for (int q = 0; q < 8; ++q)
+        if (q == h) inv = dall[q] > 0.0f ? 1.0f / dall[q] : 0.0f;
     for (int cb = 0; cb < a.dim / 32; ++cb) {
         const int c0 = a.dim * h + 32 * cb + 4 * (l % 8);
         float o[4] = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -660,6 +669,8 @@ __global__ void __launch_bounds__(kChunkThreads) k_afs_merge(AfsArgs a) {
             for (int x = 0; x < 16; ++x) fma4(s[w][h * 128 + f + x], wv[x]);
         }
         for (; f < a.in; ++f) fma4(s[w][h * 128 + f], *reinterpret_cast<const float4*>(wcol + uint64_t(f) * width));
+#pragma unroll
+        for (int x = 0; x < 4; ++x) o[x] *= inv;
         if (a.hidden)
 #pragma unroll
             for (int x = 0; x < 4; ++x) o[x] = elu_bf16(o[x]);

@@ -371,8 +371,24 @@ k_split_prescan(const uint64_t* __restrict__ prow, const uint32_t* __restrict__ 
     if (end > prow[k + 1]) end = prow[k + 1];
     if (end > e_total) end = e_total;
     const int h = lane % K;
+    // kUnroll rounds of kWave / K edges in flight per lane: the id and R loads
+    // of a round do not wait for the previous round's.  Edges past the end
+    // repeat the chunk's last edge, which leaves the max unchanged.
+    constexpr int kStep = kWave / K, kUnroll = 8;
     float m = -INFINITY;
-    for (uint64_t e = beg + lane / K; e < end; e += kWave / K) m = fmaxf(m, R[uint64_t(pcol[e]) * K + h]);
+    for (uint64_t e0 = beg + lane / K; e0 < end; e0 += uint64_t(kUnroll) * kStep) {
+        uint32_t j[kUnroll];
+#pragma unroll
+        for (int u = 0; u < kUnroll; ++u) {
+            const uint64_t e = e0 + uint64_t(u) * kStep;
+            j[u] = pcol[e < end ? e : end - 1];
+        }
+        float r[kUnroll];
+#pragma unroll
+        for (int u = 0; u < kUnroll; ++u) r[u] = R[uint64_t(j[u]) * K + h];
+#pragma unroll
+        for (int u = 0; u < kUnroll; ++u) m = fmaxf(m, r[u]);
+    }
     for (int off = K; off < kWave; off <<= 1) m = fmaxf(m, __shfl_xor(m, off));
     if (lane < K) sp.mchunk[c * 8 + lane] = m;
 }

@@ -228,8 +228,8 @@ __global__ void __launch_bounds__(kThreads) k_proj_fast(ProjArgs a) {
             __builtin_amdgcn_sched_barrier(0);
         };
         // Part A of this tile, then part A of the next tile requested into the
-        // freed registers; part B of this tile, the stores, then part B of the
-        // next tile.  Every load is unconditional, so each wait is exact.
+        // freed registers; part B of this tile, part B of the next tile, then
+        // the stores.  Every load is unconditional, so each wait is exact.
 #pragma unroll
         for (int ks = 0; ks < KA; ++ks) kstep(ks);
         if constexpr (!ONE) {
@@ -238,6 +238,12 @@ __global__ void __launch_bounds__(kThreads) k_proj_fast(ProjArgs a) {
         }
 #pragma unroll
         for (int ks = KA; ks < KS; ++ks) kstep(ks);
+        // Part B of the next tile ahead of this tile's stores: the in-order
+        // counter then lets the next tile's waits pass without these stores.
+        if constexpr (!ONE) {
+#pragma unroll
+            for (int ks = KA; ks < KS; ++ks) load_ks(next, ks);
+        }
         // A lane past n computed row n - 1 from the same input, so it stores
         // that row's own values to it (rs): no branch around the stores, which
         // keeps the wait counts of the next tile's loads exact.
@@ -313,10 +319,6 @@ __global__ void __launch_bounds__(kThreads) k_proj_fast(ProjArgs a) {
                     if (a.r_in_z) *reinterpret_cast<float*>(a.z + rs * a.zs + a.r_off + 2 * h) = rv;
                 }
             }
-        }
-        if constexpr (!ONE) {
-#pragma unroll
-            for (int ks = KA; ks < KS; ++ks) load_ks(next, ks);
         }
     }
 }
