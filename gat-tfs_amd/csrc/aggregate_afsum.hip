@@ -51,6 +51,8 @@
 // the exact row max (per-chunk maxima of k_split_prescan) into scratch, and
 // one wave per row adds the chunks in chunk order and projects the row on
 // the VALU with the FP32 W.
+#include <type_traits>
+
 #include "internal.hpp"
 
 namespace gatgpu {
@@ -598,7 +600,7 @@ __global__ void __launch_bounds__(kChunkThreads) k_afs_merge(AfsArgs a) {
     float d = 0.0f;
     if (l < 8) {
         float mc = -INFINITY;
-#pragma unroll 4
+#pragma unroll 8
         for (uint32_t q = 0; q < nch; ++q) {
             d += a.part[(c + q) * kPart + kDenOff + l];
             mc = fmaxf(mc, a.mchunk[(c + q) * 8 + l]);
@@ -612,23 +614,32 @@ __global__ void __launch_bounds__(kChunkThreads) k_afs_merge(AfsArgs a) {
 #pragma unroll
     for (int h = 0; h < 8; ++h) dall[h] = lane_f(d, h);
     if (l < (a.in > kXRFeat ? kRowWords : kXRFeat / 2)) {
-        // Chunk by chunk (the order of the sums), the 8 heads' loads of a chunk
-        // independent of each other.
+        // Chunk by chunk (the order of the sums); the loads of kMergeAhead
+        // chunks are requested together, so the chain of partials runs at
+        // L2 bandwidth rather than one round trip per chunk.
+        constexpr uint32_t kMergeAhead = 4;
         float t[8][2];
 #pragma unroll
         for (int h = 0; h < 8; ++h) t[h][0] = t[h][1] = 0.0f;
-#pragma unroll 2
-        for (uint32_t q = 0; q < nch; ++q) {
-            const float* pq = a.part + (c + q) * kPart + 2 * l;
-            float2 v[8];
+        auto add_chunks = [&](uint32_t q0, auto count) {
+            constexpr uint32_t CNT = decltype(count)::value;
+            float2 v[CNT][8];
 #pragma unroll
-            for (int h = 0; h < 8; ++h) v[h] = *reinterpret_cast<const float2*>(pq + h * 128);
+            for (uint32_t u = 0; u < CNT; ++u)
 #pragma unroll
-            for (int h = 0; h < 8; ++h) {
-                t[h][0] += v[h].x;
-                t[h][1] += v[h].y;
-            }
-        }
+                for (int h = 0; h < 8; ++h)
+                    v[u][h] = *reinterpret_cast<const float2*>(a.part + (c + q0 + u) * kPart + 2 * l + h * 128);
+#pragma unroll
+            for (uint32_t u = 0; u < CNT; ++u)
+#pragma unroll
+                for (int h = 0; h < 8; ++h) {
+                    t[h][0] += v[u][h].x;
+                    t[h][1] += v[u][h].y;
+                }
+        };
+        uint32_t q = 0;
+        for (; q + kMergeAhead <= nch; q += kMergeAhead) add_chunks(q, std::integral_constant<uint32_t, kMergeAhead>{});
+        for (; q < nch; ++q) add_chunks(q, std::integral_constant<uint32_t, 1>{});
         // bf16-stored hidden outputs: U enters the projection as one bf16, as
         // in the tile path (the rounding of a bf16 projection input).
         const bool round_s = a.outbf != nullptr;
