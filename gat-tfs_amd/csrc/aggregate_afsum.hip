@@ -27,17 +27,18 @@
 // super-block 3 to lane h, which scores head h for its edges, keeps the
 // running max m_h and the
 // denominator, and splits p into hi + lo bf16 (p enters to about 2^-17): A
-// row h holds the hi parts in one MFMA and the lo parts in a second one into
-// the same accumulators (rows 8..15 of A are zero).  The weights are taken
+// row h holds the hi parts and row 8 + h the lo parts, so one MFMA per
+// feature block takes both and D rows 8..15 sum the lo parts; the two sums
+// of a head fold at the row end (fold_pair).  The weights are taken
 // against a reference max m_h: the first batch's max, moved (with the sums
 // rescaled by exp(m_old - m_new), the running-maximum form of
 // gat_tfs_online.cpp:86-117) only when a batch's max exceeds it by more than
 // kLazyMax, so p <= e^8 and most batches rescale nothing.  The exact row max
 // M_h = leaky(L_h + max_j R_jh) is kept beside it (bit for bit, as leaky and
 // the addition are monotone); the stored denominator is sum_j e^(s_j - M_h) =
-// den e^(m_h - M_h), and U / den is the same quotient either way.  Lane (g, n), g = 0, 1,
-// register r of block (sb, par) holds U of head 4g + r, feature
-// 2(16 sb + n) + par.
+// den e^(m_h - M_h), and U / den is the same quotient either way.  Lane (g, n),
+// register r of block (sb, par) holds the hi sum (g = 0, 1) or the lo sum
+// (g = 2, 3) of head 4 (g % 2) + r, feature 2(16 sb + n) + par.
 //
 // Blocks of 8 waves take tiles of consecutive degree-sorted rows (16 or 32,
 // see k_afs_tiles).  A row's sums U_h go to LDS in the B-operand layout of
@@ -65,7 +66,7 @@ typedef float f32x16 __attribute__((__vector_size__(16 * sizeof(float))));
 constexpr int kThreads = 512;
 constexpr int kWaves = kThreads / kWave;   // 8 = heads
 constexpr int kTile = 2 * kWaves;          // rows per block tile (hi + lo S)
-constexpr int kTileBf16 = 32;              // rows per block tile with one bf16 S
+constexpr int kTileBf16 = 32;              // rows per block tile with one bf16 U
 constexpr int kMaxKS = 8;                  // k steps of 16 features: D_in <= 128
 constexpr int kRowWords = kXRStride / 2;   // 64 words of 4 bytes per XR row
 constexpr int kEPL = 4;                    // edges per lane and batch (batches of 4 kEPL edges)
@@ -217,8 +218,9 @@ __device__ inline void gather_sums(const uint32_t* __restrict__ pcol, const uint
             scale = up ? exp_w(s.m - mn) : 1.0f;  // exp(-inf) = 0 on the first batch (the sums are 0)
             s.m = mn;
         }
-        // ---- A operands: row h = hi (then lo) part of p_h for the lane's edges
-        uint32_t ah[EPL / 2], al[EPL / 2];
+        // ---- A operand: row h = hi part of p_h, row 8 + h = lo part, for the
+        // lane's edges (one MFMA per feature block takes both)
+        uint32_t a[EPL / 2];
         float ps = 0.0f;
         if constexpr (SPLIT) {
             const float p0 = exp_w(sc[0] - s.m);  // -inf past the end: 0
@@ -226,15 +228,15 @@ __device__ inline void gather_sums(const uint32_t* __restrict__ pcol, const uint
             const uint32_t hw = bf16x2(p0, p1);
             const uint32_t lw = bf16x2(p0 - __builtin_bit_cast(float, hw << 16), p1 - __builtin_bit_cast(float, hw & 0xffff0000u));
             const float pp = p0 + p1;
-            // edges 2, 3 from lane h + 8; rows 8..15 of A (lanes n >= 8) are zero
-            const uint32_t ho = uint32_t(__builtin_amdgcn_mov_dpp(int(hw), 0x128, 0xF, 0xF, false));
-            const uint32_t lo = uint32_t(__builtin_amdgcn_mov_dpp(int(lw), 0x128, 0xF, 0xF, false));
+            // Lane h feeds row h: hi of edges 0, 1 (its own) and 2, 3 (lane
+            // h + 8's); lane h + 8 feeds row 8 + h: lo of edges 0, 1 (lane h's)
+            // and 2, 3 (its own).  One DPP exchange carries both halves.
+            const uint32_t give = hf ? hw : lw;
+            const uint32_t got = uint32_t(__builtin_amdgcn_mov_dpp(int(give), 0x128, 0xF, 0xF, false));
+            a[0] = hf ? got : hw;
+            a[1] = hf ? lw : got;
             const float po = __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, pp), 0x128, 0xF,
                                                                                 0xF, false));
-            ah[0] = head ? hw : 0u;
-            ah[1] = head ? ho : 0u;
-            al[0] = head ? lw : 0u;
-            al[1] = head ? lo : 0u;
             ps = pp + po;  // (p0 + p1) + (p2 + p3) in the head lanes
         } else {
 #pragma unroll
@@ -242,9 +244,12 @@ __device__ inline void gather_sums(const uint32_t* __restrict__ pcol, const uint
                 const float p0 = head ? exp_w(sc[2 * q] - s.m) : 0.0f;  // -inf past the end: 0
                 const float p1 = head ? exp_w(sc[2 * q + 1] - s.m) : 0.0f;
                 ps += p0 + p1;
-                ah[q] = bf16x2(p0, p1);
-                al[q] = bf16x2(p0 - __builtin_bit_cast(float, ah[q] << 16),
-                               p1 - __builtin_bit_cast(float, ah[q] & 0xffff0000u));
+                const uint32_t hw = bf16x2(p0, p1);
+                const uint32_t lw = bf16x2(p0 - __builtin_bit_cast(float, hw << 16),
+                                           p1 - __builtin_bit_cast(float, hw & 0xffff0000u));
+                // rows 8..15: the lo parts of lane n - 8
+                const uint32_t lo = uint32_t(__builtin_amdgcn_mov_dpp(int(lw), 0x128, 0xF, 0xF, false));
+                a[q] = head ? hw : lo;
             }
         }
         s.den = s.den * scale + ps;
@@ -268,10 +273,8 @@ __device__ inline void gather_sums(const uint32_t* __restrict__ pcol, const uint
                 ev[q] = __builtin_amdgcn_perm(w1, w0, 0x05040100u);
                 od[q] = __builtin_amdgcn_perm(w1, w0, 0x07060302u);
             }
-            s.d[2 * sb] = Mfma<EPL>::run(ah, ev, s.d[2 * sb]);
-            s.d[2 * sb + 1] = Mfma<EPL>::run(ah, od, s.d[2 * sb + 1]);
-            s.d[2 * sb] = Mfma<EPL>::run(al, ev, s.d[2 * sb]);
-            s.d[2 * sb + 1] = Mfma<EPL>::run(al, od, s.d[2 * sb + 1]);
+            s.d[2 * sb] = Mfma<EPL>::run(a, ev, s.d[2 * sb]);
+            s.d[2 * sb + 1] = Mfma<EPL>::run(a, od, s.d[2 * sb + 1]);
         }
         // The next batch's sources, formed while the MFMAs run so that its
         // loads leave at the top of the next iteration (past the last batch
@@ -291,6 +294,17 @@ __device__ inline void zero_sums(Sums& s) {
 // Denominator of head lane (n = h) over the 4 k groups.
 __device__ inline float total_den(float den) {
     return xor32_add(xor16_add(den));
+}
+
+// U = hi sum + lo sum.  D register r of lane group g holds row 4 g + r: the
+// hi parts' sums of head 4 (g % 2) + r in lanes g < 2, the lo parts' in lanes
+// g >= 2, 32 lanes apart.  Registers r and r + 1 fold through one
+// v_permlane32_swap (odd 32-lane row of the first operand with the even row
+// of the second): afterwards lanes g < 2 hold U of head 4 g + r and lanes
+// g >= 2 U of head 4 (g - 2) + r + 1.
+__device__ inline float fold_pair(float x, float y) {
+    const auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(y), false, false);
+    return __uint_as_float(p[0]) + __uint_as_float(p[1]);
 }
 
 
@@ -400,22 +414,27 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4
                 a.den[uint64_t(i) * 8 + n] = end > beg ? den * exp_w(s.m - s.mx) : 0.0f;
                 tden[n * (TR + 1) + r] = den;  // against the reference max, as U
             }
-            if (g < 2) {
-                // Element (head h, feature pair P = 16 sb + n) of tile row r sits at
-                // block (h, P / 8[, hl]) + 32 r + 4 (P % 8): a per-lane base plus a
-                // compile-time offset for each (q, sb, hl); block index
+            {
+                // After fold_pair, lane (g, n) holds U of head 4 (g % 2) + q + (g >= 2)
+                // for q = 0, 2.  Element (head h, feature pair P = 16 sb + n) of tile
+                // row r sits at block (h, P / 8[, hl]) + 32 r + 4 (P % 8): a per-lane
+                // base plus a compile-time offset for each (q, sb, hl); block index
                 // ((h * kMaxKS + ks) * 2 + hl) with hi + lo, (buf * 8 + h) * kMaxKS + ks
                 // without.  (With KS <= 7 the words of R, 56..63, fall in k step 7.)
+                const int gh = g & 1, up = g >> 1;
                 unsigned char* base =
-                    slds + 32 * r + 4 * (n % 8) + kHalfOff * g +
-                    (HL ? 8 * kMaxKS * g + 2 * (n / 8) : buf * 8 * kMaxKS + 4 * kMaxKS * g + n / 8) * BLK;
+                    slds + 32 * r + 4 * (n % 8) + kHalfOff * gh +
+                    (HL ? 8 * kMaxKS * gh + 2 * kMaxKS * up + 2 * (n / 8)
+                        : buf * 8 * kMaxKS + 4 * kMaxKS * gh + kMaxKS * up + n / 8) *
+                        BLK;
 #pragma unroll
                 for (int sb = 0; sb < kSB; ++sb) {
                     const int ks = 2 * sb + n / 8;
                     if (ks >= KS) continue;
 #pragma unroll
-                    for (int q = 0; q < 4; ++q) {
-                        const float s0 = s.d[2 * sb][q], s1 = s.d[2 * sb + 1][q];
+                    for (int q = 0; q < 4; q += 2) {
+                        const float s0 = fold_pair(s.d[2 * sb][q], s.d[2 * sb][q + 1]);
+                        const float s1 = fold_pair(s.d[2 * sb + 1][q], s.d[2 * sb + 1][q + 1]);
                         const uint32_t hw = bf16x2(s0, s1);
                         if constexpr (HL) {
                             const uint32_t lw = bf16x2(s0 - __builtin_bit_cast(float, hw << 16),
@@ -567,15 +586,18 @@ __global__ void __launch_bounds__(kChunkThreads) k_afs_chunks(AfsArgs a) {
     else gather_sums<true, false>(a.pcol, a.xr, a.R, beg, end, l, s, a.pcol[beg + uint32_t(l % 32)], 0);
     const float den = total_den(s.den);
     float* part = a.part + c * kPart;
-    if (g < 2) {
+    {
+        // lane (g, n): head 4 (g % 2) + q + (g >= 2) after fold_pair, q = 0, 2
+        const int hb = 4 * (g & 1) + (g >> 1);
 #pragma unroll
         for (int sb = 0; sb < kSB; ++sb) {
             const int P = 16 * sb + n;
             if (P >= (rsep ? kRowWords : kXRFeat / 2)) continue;
 #pragma unroll
-            for (int q = 0; q < 4; ++q)
-                *reinterpret_cast<float2*>(part + (4 * g + q) * 128 + 2 * P) =
-                    make_float2(s.d[2 * sb][q], s.d[2 * sb + 1][q]);
+            for (int q = 0; q < 4; q += 2)
+                *reinterpret_cast<float2*>(part + (hb + q) * 128 + 2 * P) =
+                    make_float2(fold_pair(s.d[2 * sb][q], s.d[2 * sb][q + 1]),
+                                fold_pair(s.d[2 * sb + 1][q], s.d[2 * sb + 1][q + 1]));
         }
     }
     if (head && g == 0) part[kDenOff + n] = den;
