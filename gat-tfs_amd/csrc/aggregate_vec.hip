@@ -169,10 +169,18 @@ __device__ inline void batch(uint32_t left, const uint32_t (&js)[C::BATCH], cons
 #pragma unroll
             for (int q = 1; q < C::EPI; ++q) j = slot == q ? jc[u * C::EPI + q] : j;
             const ZT* row = Z + uint64_t(j) * C::W;
+            // R gathered beside the row (one slot, whole rows per edge): edges
+            // past the end issue no loads, which measured faster on graphs of
+            // many short rows than re-reading the last row.
 #pragma unroll
             for (int v = 0; v < C::VPL; ++v) {
-                z[u][v] = *reinterpret_cast<const uint4*>(row + (sub + kWave * v) * C::VEC);
-                if constexpr (!RZ) s[u][v] = leaky(st.L[v] + R[uint64_t(j) * C::K + st.h[v]]);
+                if constexpr (RZ) {
+                    z[u][v] = *reinterpret_cast<const uint4*>(row + (sub + kWave * v) * C::VEC);
+                } else {
+                    z[u][v] = ok[u] ? *reinterpret_cast<const uint4*>(row + (sub + kWave * v) * C::VEC)
+                                    : make_uint4(0, 0, 0, 0);
+                    s[u][v] = leaky(st.L[v] + (ok[u] ? R[uint64_t(j) * C::K + st.h[v]] : 0.0f));
+                }
             }
         }
     }
