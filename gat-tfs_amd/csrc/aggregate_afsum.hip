@@ -622,7 +622,7 @@ __global__ void __launch_bounds__(kChunkThreads) k_afs_merge(AfsArgs a) {
     float d = 0.0f;
     if (l < 8) {
         float mc = -INFINITY;
-#pragma unroll 8
+#pragma unroll 16
         for (uint32_t q = 0; q < nch; ++q) {
             d += a.part[(c + q) * kPart + kDenOff + l];
             mc = fmaxf(mc, a.mchunk[(c + q) * 8 + l]);

@@ -379,10 +379,11 @@ k_split_prescan(const uint64_t* __restrict__ prow, const uint32_t* __restrict__ 
     if (end > prow[k + 1]) end = prow[k + 1];
     if (end > e_total) end = e_total;
     const int h = lane % K;
-    // kUnroll rounds of kWave / K edges in flight per lane: the id and R loads
-    // of a round do not wait for the previous round's.  Edges past the end
-    // repeat the chunk's last edge, which leaves the max unchanged.
-    constexpr int kStep = kWave / K, kUnroll = 8;
+    // kUnroll rounds of kWave / K edges in flight per lane (a 256-edge chunk
+    // of 8 heads in one round trip for its ids and one for its R values):
+    // the loads of a round do not wait for the previous round's.  Edges past
+    // the end repeat the chunk's last edge, which leaves the max unchanged.
+    constexpr int kStep = kWave / K, kUnroll = 32;
     float m = -INFINITY;
     for (uint64_t e0 = beg + lane / K; e0 < end; e0 += uint64_t(kUnroll) * kStep) {
         uint32_t j[kUnroll];
