@@ -137,10 +137,69 @@ struct Mfma<4> {
 // already (a chunk) and never moves.
 // RSEP: the rows hold 128 input features and R comes from its own array
 // ([n][8], loaded by the head lanes beside the row words).
-template <bool EXACT, bool RSEP, int EPL = kEPL>
+// Source nodes of lane l's EPL edges of a batch with `left` (>= 1) edges to
+// go, from ids (lane i0 + t holds the batch's edge t); edges past the end
+// re-read the batch's last row (weight 0).  Byte indices of ds_bpermute: a
+// lane constant, one min and one add per edge.
+template <int EPL>
+__device__ inline void batch_sources(uint32_t idv, int i0, uint32_t left, int l, uint32_t (&js)[EPL]) {
+    constexpr int B = 4 * EPL;
+    const int cnt = left < uint32_t(B) ? int(left) : B;
+    const int g = l / 16;
+#pragma unroll
+    for (int t = 0; t < EPL; ++t)
+        js[t] = uint32_t(__builtin_amdgcn_ds_bpermute(min(4 * (EPL * g + t), 4 * (cnt - 1)) + 4 * i0, int(idv)));
+}
+
+// The row words of lane l for the batch's sources jl (word 16 sb + n of each
+// edge's row), and R of head n beside them when R has its own array.
+// 32-bit byte offsets (n * 256 < 2^32 is checked at launch).
+template <bool RSEP, int EPL>
+__device__ inline void load_batch(const uint32_t* __restrict__ xr, const float* __restrict__ R,
+                                  const uint32_t (&jl)[EPL], int l, uint32_t (&raw)[kSB][EPL], float (&rsep)[EPL]) {
+    const int n = l % 16;
+    const unsigned char* xb = reinterpret_cast<const unsigned char*>(xr);
+    uint32_t off[EPL];
+#pragma unroll
+    for (int t = 0; t < EPL; ++t) off[t] = jl[t] * uint32_t(4 * kRowWords) + 4u * uint32_t(n);
+    // Super-block 3 (the R words when R is in the row) first: scoring waits
+    // only for those.
+#pragma unroll
+    for (int k = 0; k < kSB; ++k) {
+        const int sb = (k + kSB - 1) % kSB;
+#pragma unroll
+        for (int t = 0; t < EPL; ++t) raw[sb][t] = *reinterpret_cast<const uint32_t*>(xb + off[t] + 64 * sb);
+    }
+#pragma unroll
+    for (int t = 0; t < EPL; ++t) {
+        if constexpr (RSEP) rsep[t] = n < 8 ? R[uint64_t(jl[t]) * 8 + n] : 0.0f;
+        else rsep[t] = 0.0f;
+    }
+}
+
+// A batch whose loads were issued ahead (the first batch of a row, requested
+// before the previous row's epilogue).
+template <int EPL>
+struct Batch {
+    uint32_t raw[kSB][EPL];
+    float rsep[EPL];
+};
+
+// The first batch of edges [beg, end) (beg < end) requested into b.
+template <bool RSEP, int EPL = kEPL>
+__device__ inline void first_batch(const uint32_t* __restrict__ xr, const float* __restrict__ R, uint64_t beg,
+                                   uint64_t end, int l, uint32_t ids, int id0, Batch<EPL>& b) {
+    uint32_t jl[EPL];
+    batch_sources<EPL>(ids, id0, uint32_t(end - beg), l, jl);
+    load_batch<RSEP, EPL>(xr, R, jl, l, b.raw, b.rsep);
+}
+
+// The batches pass through b; PRE: b already holds the first batch
+// (first_batch), whose loads are not issued again.
+template <bool EXACT, bool RSEP, int EPL = kEPL, bool PRE = false>
 __device__ inline void gather_sums(const uint32_t* __restrict__ pcol, const uint32_t* __restrict__ xr,
                                    const float* __restrict__ R, uint64_t beg, uint64_t end, int l, Sums& s,
-                                   uint32_t ids, int id0) {
+                                   uint32_t ids, int id0, Batch<EPL>& b) {
     constexpr int B = 4 * EPL;  // edges per batch
     if (beg >= end) return;
     const int g = l / 16, n = l % 16;
@@ -148,34 +207,16 @@ __device__ inline void gather_sums(const uint32_t* __restrict__ pcol, const uint
     // Edge counts in 32 bits (set_graph rejects rows of 2^32 edges or more),
     // so that the loop's compares run on the scalar unit.
     const uint32_t total = uint32_t(end - beg);
-    // Source nodes of this lane's EPL edges of a batch with `left` edges to
-    // go, from ids (lane i0 + t holds the batch's edge t); edges past the end
-    // re-read the batch's last row (weight 0).  Byte indices of ds_bpermute:
-    // a lane constant, one min and one add per edge.
-    auto sources = [&](uint32_t idv, int i0, uint32_t left, uint32_t (&js)[EPL]) {
-        const int cnt = left < uint32_t(B) ? int(left) : B;
-#pragma unroll
-        for (int t = 0; t < EPL; ++t)
-            js[t] = uint32_t(__builtin_amdgcn_ds_bpermute(min(4 * (EPL * g + t), 4 * (cnt - 1)) + 4 * i0, int(idv)));
-    };
-    uint32_t jl[EPL];
-    sources(ids, id0, total, jl);
+    uint32_t jl[EPL] = {};
+    if constexpr (!PRE) batch_sources<EPL>(ids, id0, total, l, jl);
     for (uint32_t done = 0; done < total; done += B) {
         const uint64_t base = beg + done;
         const uint32_t left = total - done;
         const uint32_t nids = pcol[(left > uint32_t(B) ? base + B : end) + uint32_t(l % 32)];
         const int cnt = left < uint32_t(B) ? int(left) : B;
-        // 32-bit byte offsets (n * 256 < 2^32 is checked at launch).
-        const unsigned char* xb = reinterpret_cast<const unsigned char*>(xr);
-        uint32_t raw[kSB][EPL];
-        float rsep[EPL];
-#pragma unroll
-        for (int t = 0; t < EPL; ++t) {
-            const uint32_t off = jl[t] * uint32_t(4 * kRowWords) + 4u * uint32_t(n);
-#pragma unroll
-            for (int sb = 0; sb < kSB; ++sb) raw[sb][t] = *reinterpret_cast<const uint32_t*>(xb + off + 64 * sb);
-            if constexpr (RSEP) rsep[t] = head ? R[uint64_t(jl[t]) * 8 + n] : 0.0f;
-        }
+        if (!PRE || done > 0) load_batch<RSEP, EPL>(xr, R, jl, l, b.raw, b.rsep);
+        uint32_t (&raw)[kSB][EPL] = b.raw;
+        float (&rsep)[EPL] = b.rsep;
         // ---- scores, batch max over the 4 k groups.  SPLIT (R in the row
         // tail, 4 edges per lane): head h's four edges of a k group are
         // scored by lanes h (edges 0, 1; R from lane h + 8 by a DPP rotation
@@ -279,7 +320,7 @@ __device__ inline void gather_sums(const uint32_t* __restrict__ pcol, const uint
         // The next batch's sources, formed while the MFMAs run so that its
         // loads leave at the top of the next iteration (past the last batch
         // they go unused).
-        sources(nids, 0, left - B, jl);
+        batch_sources<EPL>(nids, 0, left - B, l, jl);
     }
 }
 
@@ -389,15 +430,25 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4
         uint64_t n2mb, n2me;
         fetch_ids(nmi, nmb, nme, nidr, nLall);
         fetch_bounds(tile + 2 * uint64_t(gridDim.x), n2mi, n2mb, n2me);
+        // Row q of the wave: node, edge range and first ids.
+        auto row_of = [&](int q, uint32_t& qi, uint64_t& qb, uint64_t& qe, uint32_t& qids) {
+            qi = uint32_t(__builtin_amdgcn_readlane(int(mi), q));
+            qb = (uint64_t(uint32_t(__builtin_amdgcn_readlane(int(mb >> 32), q))) << 32) |
+                 uint32_t(__builtin_amdgcn_readlane(int(uint32_t(mb)), q));
+            qe = (uint64_t(uint32_t(__builtin_amdgcn_readlane(int(me >> 32), q))) << 32) |
+                 uint32_t(__builtin_amdgcn_readlane(int(uint32_t(me)), q));
+            qids = q / 2 == 0 ? idr[0] : idr[(RPW + 1) / 2 - 1];
+        };
+        // Each row's first batch is requested before the previous row's
+        // epilogue (its loads then travel while that row's sums are staged).
+        Batch<kEPL> pre;
+        bool have_pre = false;  // wave-uniform
 #pragma unroll 1
         for (int rr = 0; rr < RPW; ++rr) {
             const int r = w + kWaves * rr;
-            const uint32_t i = uint32_t(__builtin_amdgcn_readlane(int(mi), rr));
-            const uint64_t beg = (uint64_t(uint32_t(__builtin_amdgcn_readlane(int(mb >> 32), rr))) << 32) |
-                                 uint32_t(__builtin_amdgcn_readlane(int(uint32_t(mb)), rr));
-            const uint64_t end = (uint64_t(uint32_t(__builtin_amdgcn_readlane(int(me >> 32), rr))) << 32) |
-                                 uint32_t(__builtin_amdgcn_readlane(int(uint32_t(me)), rr));
-            const uint32_t ids = rr / 2 == 0 ? idr[0] : idr[(RPW + 1) / 2 - 1];
+            uint32_t i, ids;
+            uint64_t beg, end;
+            row_of(rr, i, beg, end, ids);
             const float Lr = __shfl(Lall, 8 * rr + n % 8);
             if (l == 0) trow[r] = i;
             if (i == kNoRow) continue;
@@ -405,7 +456,18 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4
             zero_sums(s);
             s.L = head || !RSEP ? Lr : 0.0f;  // (lanes h + 8 score half of head h's edges)
             s.m = s.mx = -INFINITY;
-            gather_sums<false, RSEP>(a.pcol, a.xr, a.R, beg, end, l, s, ids, 32 * (rr % 2));
+            if (!have_pre && beg < end) first_batch<RSEP>(a.xr, a.R, beg, end, l, ids, 32 * (rr % 2), pre);
+            gather_sums<false, RSEP, kEPL, true>(a.pcol, a.xr, a.R, beg, end, l, s, ids, 32 * (rr % 2), pre);
+            have_pre = false;
+            if (rr + 1 < RPW) {
+                uint32_t ni, nids;
+                uint64_t nb, ne;
+                row_of(rr + 1, ni, nb, ne, nids);
+                if (ni != kNoRow && nb < ne) {
+                    first_batch<RSEP>(a.xr, a.R, nb, ne, l, nids, 32 * ((rr + 1) % 2), pre);
+                    have_pre = true;
+                }
+            }
             const float den = total_den(s.den);  // against the reference max s.m
             if (head && g == 0) {
                 // empty row: max 0, denominator 0 (ref_fp32.cpp:11); else the
@@ -582,8 +644,9 @@ __global__ void __launch_bounds__(kChunkThreads) k_afs_chunks(AfsArgs a) {
         s.m = s.mx = leaky(s.L + mc);
     }
     const bool rsep = a.in > kXRFeat;
-    if (rsep) gather_sums<true, true>(a.pcol, a.xr, a.R, beg, end, l, s, a.pcol[beg + uint32_t(l % 32)], 0);
-    else gather_sums<true, false>(a.pcol, a.xr, a.R, beg, end, l, s, a.pcol[beg + uint32_t(l % 32)], 0);
+    Batch<kEPL> b;
+    if (rsep) gather_sums<true, true>(a.pcol, a.xr, a.R, beg, end, l, s, a.pcol[beg + uint32_t(l % 32)], 0, b);
+    else gather_sums<true, false>(a.pcol, a.xr, a.R, beg, end, l, s, a.pcol[beg + uint32_t(l % 32)], 0, b);
     const float den = total_den(s.den);
     float* part = a.part + c * kPart;
     {
