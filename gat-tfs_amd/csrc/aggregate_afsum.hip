@@ -48,10 +48,11 @@
 // tile's U_h by W_h (A fragments packed as for the projection, read from L2;
 // two MFMA chains) and scales each output row by 1 / den_h: (U_h W_h) / den_h,
 // the same quotient as (U_h / den_h) W_h, with one scaling per output row and
-// head instead of one per summed feature.  Split rows: one wave per chunk sums its edges from
-// the exact row max (per-chunk maxima of k_split_prescan) into scratch, and
-// one wave per row adds the chunks in chunk order and projects the row on
-// the VALU with the FP32 W.
+// head instead of one per summed feature.  Split rows: one wave per chunk sums
+// its edges into scratch against maxima of its own (the lazy reference max
+// and the exact max, as a tile row keeps them), and one wave per row scales
+// the chunks to a common reference, adds them in chunk order and projects the
+// row on the VALU with the FP32 W.
 #include <type_traits>
 
 #include "internal.hpp"
@@ -81,8 +82,10 @@ constexpr int kTRowBytes = 2 * 2 * kTile * 4;             // the tile's node ids
 constexpr int kTDenBytes = 2 * 8 * (2 * kTile + 1) * 4;   // their denominators (2 x 8 heads x 33)
 constexpr int kLdsBytes = kSBytes + kTRowBytes + kTDenBytes;  // S, node ids, denominators
 constexpr uint32_t kNoRow = 0xffffffffu;
-constexpr int kPart = 8 * 128 + 8;         // floats per chunk partial (U_h rows of 128, then den)
-constexpr int kDenOff = 8 * 128;
+constexpr int kPart = 8 * 128 + 24;        // floats per chunk partial: U_h rows of 128, den, m, mx
+constexpr int kDenOff = 8 * 128;           // den_h against the chunk's reference max m_h
+constexpr int kMOff = kDenOff + 8;         // the reference max m_h
+constexpr int kMxOff = kDenOff + 16;       // the chunk's exact max of the scores
 constexpr int kChunkThreads = 256;
 
 static_assert(32 <= int(kPcolPad), "an id request may read 31 entries past the row");
@@ -624,29 +627,18 @@ __global__ void __launch_bounds__(kChunkThreads) k_afs_chunks(AfsArgs a) {
     const uint64_t rbeg = a.prow[k], rend = a.prow[k + 1];
     const uint32_t i = a.perm[k];
     if (i >= a.n || rbeg > rend || rend > a.e) return;
-    const uint32_t nch = uint32_t((rend - rbeg + a.chunk_edges - 1) / a.chunk_edges);
     const uint64_t beg = rbeg + uint64_t(c - first) * a.chunk_edges;
     const uint64_t end = beg + a.chunk_edges < rend ? beg + a.chunk_edges : rend;
+    // The chunk's edges as a row's (lazy reference max, exact max beside it);
+    // the merge scales the chunks to a common reference.
+    const bool rsep = a.in > kXRFeat;
     Sums s;
     zero_sums(s);
-    s.L = 0.0f;
-    s.m = 0.0f;
-    // Row max over the chunk maxima: lane l reads head l % 8 of chunks l / 8,
-    // l / 8 + 8, ... (independent loads), then the 8 lanes of each head reduce.
-    float mc = -INFINITY;
-    for (uint32_t q = uint32_t(l / 8); q < nch; q += 8) mc = fmaxf(mc, a.mchunk[(first + q) * 8 + l % 8]);
-    mc = fmaxf(mc, __shfl_xor(mc, 8));
-    mc = fmaxf(mc, __shfl_xor(mc, 16));
-    mc = fmaxf(mc, __shfl_xor(mc, 32));
-    if (head) {
-        const int h = n;  // = l % 8
-        s.L = a.L[uint64_t(i) * 8 + h];
-        s.m = s.mx = leaky(s.L + mc);
-    }
-    const bool rsep = a.in > kXRFeat;
+    s.L = head || !rsep ? a.L[uint64_t(i) * 8 + n % 8] : 0.0f;  // (lanes h + 8 score half of head h's edges)
+    s.m = s.mx = -INFINITY;
     Batch<kEPL> b;
-    if (rsep) gather_sums<true, true>(a.pcol, a.xr, a.R, beg, end, l, s, a.pcol[beg + uint32_t(l % 32)], 0, b);
-    else gather_sums<true, false>(a.pcol, a.xr, a.R, beg, end, l, s, a.pcol[beg + uint32_t(l % 32)], 0, b);
+    if (rsep) gather_sums<false, true>(a.pcol, a.xr, a.R, beg, end, l, s, a.pcol[beg + uint32_t(l % 32)], 0, b);
+    else gather_sums<false, false>(a.pcol, a.xr, a.R, beg, end, l, s, a.pcol[beg + uint32_t(l % 32)], 0, b);
     const float den = total_den(s.den);
     float* part = a.part + c * kPart;
     {
@@ -663,11 +655,18 @@ __global__ void __launch_bounds__(kChunkThreads) k_afs_chunks(AfsArgs a) {
                                 fold_pair(s.d[2 * sb + 1][q], s.d[2 * sb + 1][q + 1]));
         }
     }
-    if (head && g == 0) part[kDenOff + n] = den;
+    if (head && g == 0) {
+        part[kDenOff + n] = den;
+        part[kMOff + n] = s.m;
+        part[kMxOff + n] = s.mx;
+    }
 }
 
-// One wave per split row (found at its first chunk): adds the chunks' sums
-// and denominators in chunk order, then out_h = (U_h W_h) / den_h on the VALU
+// One wave per split row (found at its first chunk): scales each chunk's sums
+// and denominator by e^(m_c - M_ref), M_ref the largest of the chunks'
+// reference maxima, and adds them in chunk order (the chunk merge of the
+// running maximum, gat_tfs_online.cpp:86-117); then out_h = (U_h W_h) / den_h
+// on the VALU
 // with the FP32 (bf16-rounded) W; lane l computes columns 32 cb + 4 (l % 8)
 // .. + 3 of head l / 8, for each 32-column block cb of the head.
 __global__ void __launch_bounds__(kChunkThreads) k_afs_merge(AfsArgs a) {
@@ -681,23 +680,32 @@ __global__ void __launch_bounds__(kChunkThreads) k_afs_merge(AfsArgs a) {
     if (i >= a.n || rbeg > rend || rend > a.e) return;
     const uint32_t nch = uint32_t((rend - rbeg + a.chunk_edges - 1) / a.chunk_edges);
     if (c + nch > a.chunks) return;
-    // denominators and the exact max (lanes 0..7)
-    float d = 0.0f;
+    // The common reference M_ref and the exact max M (lanes 0..7, head l),
+    // then the denominators scaled to M_ref in chunk order.
+    float d = 0.0f, mref = -INFINITY;
     if (l < 8) {
-        float mc = -INFINITY;
+        float mx = -INFINITY;
 #pragma unroll 16
         for (uint32_t q = 0; q < nch; ++q) {
-            d += a.part[(c + q) * kPart + kDenOff + l];
-            mc = fmaxf(mc, a.mchunk[(c + q) * 8 + l]);
+            mref = fmaxf(mref, a.part[(c + q) * kPart + kMOff + l]);
+            mx = fmaxf(mx, a.part[(c + q) * kPart + kMxOff + l]);
         }
-        a.mx[uint64_t(i) * 8 + l] = leaky(a.L[uint64_t(i) * 8 + l] + mc);
-        a.den[uint64_t(i) * 8 + l] = d;
+#pragma unroll 16
+        for (uint32_t q = 0; q < nch; ++q) {
+            const float* pq = a.part + (c + q) * kPart;
+            d += pq[kDenOff + l] * exp_w(pq[kMOff + l] - mref);
+        }
+        a.mx[uint64_t(i) * 8 + l] = mx;
+        a.den[uint64_t(i) * 8 + l] = d * exp_w(mref - mx);  // against the exact max
     }
     // U_h[f] into LDS (lane l adds features 2l, 2l + 1); the projected row is
     // scaled by 1 / den_h afterwards, as in the tile path.
-    float dall[8];  // read before any lane is masked off
+    float dall[8], rall[8];  // read before any lane is masked off
 #pragma unroll
-    for (int h = 0; h < 8; ++h) dall[h] = lane_f(d, h);
+    for (int h = 0; h < 8; ++h) {
+        dall[h] = lane_f(d, h);
+        rall[h] = lane_f(mref, h);
+    }
     if (l < (a.in > kXRFeat ? kRowWords : kXRFeat / 2)) {
         // Chunk by chunk (the order of the sums); the loads of kMergeAhead
         // chunks are requested together, so the chain of partials runs at
@@ -709,17 +717,22 @@ __global__ void __launch_bounds__(kChunkThreads) k_afs_merge(AfsArgs a) {
         auto add_chunks = [&](uint32_t q0, auto count) {
             constexpr uint32_t CNT = decltype(count)::value;
             float2 v[CNT][8];
-#pragma unroll
-            for (uint32_t u = 0; u < CNT; ++u)
-#pragma unroll
-                for (int h = 0; h < 8; ++h)
-                    v[u][h] = *reinterpret_cast<const float2*>(a.part + (c + q0 + u) * kPart + 2 * l + h * 128);
+            float mq[CNT][8];
 #pragma unroll
             for (uint32_t u = 0; u < CNT; ++u)
 #pragma unroll
                 for (int h = 0; h < 8; ++h) {
-                    t[h][0] += v[u][h].x;
-                    t[h][1] += v[u][h].y;
+                    const float* pq = a.part + (c + q0 + u) * kPart;
+                    v[u][h] = *reinterpret_cast<const float2*>(pq + 2 * l + h * 128);
+                    mq[u][h] = pq[kMOff + h];
+                }
+#pragma unroll
+            for (uint32_t u = 0; u < CNT; ++u)
+#pragma unroll
+                for (int h = 0; h < 8; ++h) {
+                    const float f = exp_w(mq[u][h] - rall[h]);
+                    t[h][0] = __builtin_fmaf(v[u][h].x, f, t[h][0]);
+                    t[h][1] = __builtin_fmaf(v[u][h].y, f, t[h][1]);
                 }
         };
         uint32_t q = 0;
@@ -814,8 +827,7 @@ hipError_t launch_aggregate_afsum(const AfsArgs& a, const SplitTable& t, hipStre
         !a.wq || !a.R)
         return hipErrorInvalidValue;
     if (a.chunks) {
-        hipError_t e = launch_split_prescan(a.prow, a.pcol, a.R, 8, t, a.e, s);
-        if (e != hipSuccess) return e;
+        hipError_t e = hipSuccess;
         const dim3 grid(uint32_t((a.chunks + kChunkThreads / kWave - 1) / (kChunkThreads / kWave)));
         k_afs_chunks<<<grid, kChunkThreads, 0, s>>>(a);
         if ((e = hipGetLastError()) != hipSuccess) return e;

@@ -5,12 +5,12 @@
 // row max, den = sum p, out = ELU?(sum p Z / den).
 //
 // Work items, one wave each, in this order:
-//   * chunks of split rows (in-degree >= split_min), C edges each.
-//     k_split_prescan stores every chunk's per-head maximum first, so every
-//     chunk starts from the exact row max and its partial (sum p Z, sum p)
-//     needs no rescaling.  Partials go to scratch; the last chunk to arrive
-//     (agent-scope release/acquire around a relaxed counter) adds them in
-//     chunk order, which is deterministic, and finishes the row.
+//   * chunks of split rows (in-degree >= split_min), C edges each.  A chunk
+//     runs the online softmax over its edges as a whole row does and leaves
+//     its partial (sum p Z, sum p) with its own max m_c in scratch; the last
+//     chunk to arrive (agent-scope release/acquire around a relaxed counter)
+//     scales each partial by e^(m_c - M), M the row max, adds them in chunk
+//     order, which is deterministic, and finishes the row.
 //   * whole rows below split_min, heaviest first.
 //
 // Lane layout.  A source row is LPR 16-byte vectors.  Lane (slot, sub), with
@@ -420,9 +420,18 @@ __device__ inline void init_lane(const VArgs<ZT>& a, int sub, Lane<C>& st) {
     st.smask = sm;
 }
 
-// Chunk c of a split row: its edges from the exact row max, the partial sums
-// to scratch; the last chunk of the row to arrive adds the partials in chunk
-// order and finishes the row.
+// Floats per chunk partial: W sums, then 8 denominators and 8 maxima.
+template <class C>
+constexpr int part_floats() {
+    return C::W + 16;
+}
+
+// Chunk c of a split row: its edges with the online softmax (as a whole row),
+// the partial sums, denominators and the chunk's row max m_c to scratch; the
+// last chunk of the row to arrive takes M = max_c m_c (the exact row max, as
+// each m_c is exact over its chunk) and adds the partials in chunk order,
+// each scaled by e^(m_c - M) -- the merge of tfs_online_fused's running
+// maximum (implementation/src/gat_tfs_online.cpp:86-117) over chunks.
 template <class C, class ZT, bool RZ, bool O32>
 __device__ inline void run_chunk(const VArgs<ZT>& a, uint64_t c, int lane, int slot, int sub) {
     Lane<C> st;
@@ -436,13 +445,12 @@ __device__ inline void run_chunk(const VArgs<ZT>& a, uint64_t c, int lane, int s
     const uint64_t end = beg + a.sp.chunk_edges < rend ? beg + a.sp.chunk_edges : rend;
 #pragma unroll
     for (int v = 0; v < C::VPL; ++v) {
-        float m = -INFINITY;
-        for (uint32_t q = 0; q < nch; ++q) m = fmaxf(m, a.sp.mchunk[(first + q) * 8 + st.h[v]]);
         st.L[v] = a.L[uint64_t(i) * C::K + st.h[v]];
-        st.m[v] = leaky(st.L[v] + m);  // exact row max: no rescale happens in this chunk
+        st.m[v] = -INFINITY;
     }
-    aggregate<C, ZT, RZ, O32, true>(beg, end, a.pcol, a.R, a.Z, slot, sub, st);
-    float* part = a.sp.part + c * (C::W + 8);
+    aggregate<C, ZT, RZ, O32>(beg, end, a.pcol, a.R, a.Z, slot, sub, st);
+    constexpr int PF = part_floats<C>();
+    float* part = a.sp.part + c * PF;
     if (slot == 0) {
 #pragma unroll
         for (int v = 0; v < C::VPL; ++v) {
@@ -452,7 +460,10 @@ __device__ inline void run_chunk(const VArgs<ZT>& a, uint64_t c, int lane, int s
                 *reinterpret_cast<float4*>(part + f0 + x) =
                     make_float4(st.acc[v * C::VEC + x], st.acc[v * C::VEC + x + 1], st.acc[v * C::VEC + x + 2],
                                 st.acc[v * C::VEC + x + 3]);
-            if (f0 % C::DIM == 0) part[C::W + st.h[v]] = st.den[v];
+            if (f0 % C::DIM == 0) {
+                part[C::W + st.h[v]] = st.den[v];
+                part[C::W + 8 + st.h[v]] = st.m[v];
+            }
         }
     }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
@@ -462,7 +473,14 @@ __device__ inline void run_chunk(const VArgs<ZT>& a, uint64_t c, int lane, int s
     old = __shfl(old, 0);
     if (old + 1 != nch) return;  // not the last chunk of this row
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-    // Last arrival: add the partials of every chunk in chunk order.
+    // Last arrival: the row max over the chunks, then the partials of every
+    // chunk in chunk order, scaled to it.
+    float M[C::VPL];
+#pragma unroll
+    for (int v = 0; v < C::VPL; ++v) {
+        M[v] = -INFINITY;
+        for (uint32_t q = 0; q < nch; ++q) M[v] = fmaxf(M[v], a.sp.part[uint64_t(first + q) * PF + C::W + 8 + st.h[v]]);
+    }
     float tot[C::ACC];
     float dtot[C::VPL];
 #pragma unroll
@@ -470,23 +488,25 @@ __device__ inline void run_chunk(const VArgs<ZT>& a, uint64_t c, int lane, int s
 #pragma unroll
     for (int v = 0; v < C::VPL; ++v) dtot[v] = 0.0f;
     for (uint32_t q = 0; q < nch; ++q) {
-        const float* pq = a.sp.part + uint64_t(first + q) * (C::W + 8);
+        const float* pq = a.sp.part + uint64_t(first + q) * PF;
 #pragma unroll
         for (int v = 0; v < C::VPL; ++v) {
+            const float mq = pq[C::W + 8 + st.h[v]];
+            const float f = mq == M[v] ? 1.0f : exp_w(mq - M[v]);  // a chunk of only -inf scores: 0
             const int f0 = (sub + kWave * v) * C::VEC;
 #pragma unroll
             for (int x = 0; x < C::VEC; x += 4) {
                 const float4 t = *reinterpret_cast<const float4*>(pq + f0 + x);
-                tot[v * C::VEC + x] += t.x;
-                tot[v * C::VEC + x + 1] += t.y;
-                tot[v * C::VEC + x + 2] += t.z;
-                tot[v * C::VEC + x + 3] += t.w;
+                tot[v * C::VEC + x] += t.x * f;
+                tot[v * C::VEC + x + 1] += t.y * f;
+                tot[v * C::VEC + x + 2] += t.z * f;
+                tot[v * C::VEC + x + 3] += t.w * f;
             }
-            dtot[v] += pq[C::W + st.h[v]];
+            dtot[v] += pq[C::W + st.h[v]] * f;
         }
     }
     if (lane == 0) a.sp.counter[first] = 0;  // ready for the next launch
-    finish_row<C>(i, tot, dtot, st.m, st.h, slot, sub, a.hidden, a.mx, a.den, a.out32, a.outbf);
+    finish_row<C>(i, tot, dtot, M, st.h, slot, sub, a.hidden, a.mx, a.den, a.out32, a.outbf);
 }
 
 template <class C, class ZT, bool RZ, bool O32>
@@ -671,10 +691,6 @@ hipError_t run(const AggArgs& g, const RowBins& bins, const SplitTable& t, hipSt
     VArgs<ZT> a{g.prow, g.pcol, g.perm, g.left, g.right, static_cast<const ZT*>(g.feat), g.hidden, g.mx, g.den,
                 g.out32, g.outbf, g.n, g.e, bins.split_begin,
                 SplitArgs{t.chunks, t.chunk_k, t.chunk_first, t.chunk_edges, t.mchunk, t.part, t.counter}, g.ar};
-    if (t.chunks) {
-        hipError_t e = launch_split_prescan(g.prow, g.pcol, g.right, C::K, t, g.e, s);
-        if (e != hipSuccess) return e;
-    }
     const uint64_t items = t.chunks + bins.split_begin;
     if (!items) return hipSuccess;
     const dim3 grid(uint32_t((items + kWavesPerBlock - 1) / kWavesPerBlock));
@@ -727,10 +743,6 @@ hipError_t launch_aggregate_vec_next(const AggArgs& g, const RowBins& bins, cons
                       g.mx, g.den, g.out32, g.outbf, g.n, g.e, bins.split_begin,
                       SplitArgs{t.chunks, t.chunk_k, t.chunk_first, t.chunk_edges, t.mchunk, t.part, t.counter},
                       g.ar};
-    if (t.chunks) {
-        hipError_t e = launch_split_prescan(g.prow, g.pcol, g.right, C::K, t, g.e, s);
-        if (e != hipSuccess) return e;
-    }
     f.tiles = (bins.split_begin + kNextTile - 1) / kNextTile;
     const uint64_t chunk_blocks = (t.chunks + kWavesPerBlock - 1) / kWavesPerBlock;
     const uint64_t blocks = chunk_blocks + f.tiles;

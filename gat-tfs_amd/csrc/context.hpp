@@ -91,8 +91,8 @@ constexpr uint64_t kSmallGraphEdges = 16u << 20;
 constexpr uint32_t kSmallPlanMin = 512, kSmallPlanChunk = 256;
 constexpr uint64_t kMaxChunksPerRow = 96;
 // Floats per split chunk in SplitTable::part: the widest partial row of the
-// transform-first kernels (512 features + 8 denominators).
-constexpr uint64_t kTfPartFloats = 512 + 8;
+// transform-first kernels (512 features, 8 denominators, 8 chunk maxima).
+constexpr uint64_t kTfPartFloats = 512 + 16;
 struct SplitPlan {
     uint32_t min = 0, chunk = 0;
     RowBins bins;        // split_begin: first split row (sorted position)

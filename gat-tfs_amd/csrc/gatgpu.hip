@@ -126,7 +126,7 @@ int compute_bins(gatgpu_ctx* c) {
             HIPCHECK(c, P.k.ensure(ck.size() * 4));
             HIPCHECK(c, P.first.ensure(cf.size() * 4));
             HIPCHECK(c, P.mchunk.ensure(ck.size() * 8 * 4));
-            HIPCHECK(c, P.part.ensure(ck.size() * (8 * 128 + 8) * 4));  // largest partial: aggregate-first U
+            HIPCHECK(c, P.part.ensure(ck.size() * (8 * 128 + 24) * 4));  // largest partial: aggregate-first U
             HIPCHECK(c, P.counter.ensure(ck.size() * 4));
             HIPCHECK(c, hipMemcpy(P.k.p, ck.data(), ck.size() * 4, hipMemcpyHostToDevice));
             HIPCHECK(c, hipMemcpy(P.first.p, cf.data(), cf.size() * 4, hipMemcpyHostToDevice));
