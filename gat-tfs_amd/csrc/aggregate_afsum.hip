@@ -48,11 +48,13 @@
 // tile's U_h by W_h (A fragments packed as for the projection, read from L2;
 // two MFMA chains) and scales each output row by 1 / den_h: (U_h W_h) / den_h,
 // the same quotient as (U_h / den_h) W_h, with one scaling per output row and
-// head instead of one per summed feature.  Split rows: one wave per chunk sums
-// its edges into scratch against maxima of its own (the lazy reference max
-// and the exact max, as a tile row keeps them), and one wave per row scales
-// the chunks to a common reference, adds them in chunk order and projects the
-// row on the VALU with the FP32 W.
+// head instead of one per summed feature.  Split rows: the first blocks of the
+// same launch take one chunk per wave and sum its edges into scratch against
+// maxima of its own (the lazy reference max and the exact max, as a tile row
+// keeps them); the row's last chunk to arrive scales the chunks to a common
+// reference, adds them in chunk order and projects the row on the VALU with
+// the FP32 W.  The tile blocks take tiles from a counter, so those that start
+// after the chunk blocks take fewer.
 #include <type_traits>
 
 #include "internal.hpp"
@@ -80,13 +82,14 @@ constexpr int kHalfOff = 64;
 constexpr int kSBytes = 8 * kMaxKS * 2 * kBlk + kHalfOff;
 constexpr int kTRowBytes = 2 * 2 * kTile * 4;             // the tile's node ids (up to 2 x 32)
 constexpr int kTDenBytes = 2 * 8 * (2 * kTile + 1) * 4;   // their denominators (2 x 8 heads x 33)
-constexpr int kLdsBytes = kSBytes + kTRowBytes + kTDenBytes;  // S, node ids, denominators
+constexpr int kTQBytes = 4 * 4;                                // ring of the block's next tile indices
+constexpr int kLdsBytes = kSBytes + kTRowBytes + kTDenBytes + kTQBytes;  // S, node ids, denominators, tiles
 constexpr uint32_t kNoRow = 0xffffffffu;
 constexpr int kPart = 8 * 128 + 24;        // floats per chunk partial: U_h rows of 128, den, m, mx
 constexpr int kDenOff = 8 * 128;           // den_h against the chunk's reference max m_h
 constexpr int kMOff = kDenOff + 8;         // the reference max m_h
 constexpr int kMxOff = kDenOff + 16;       // the chunk's exact max of the scores
-constexpr int kChunkThreads = 256;
+constexpr int kMergeFloats = 8 * kRowWords * 2;  // LDS floats of a wave that merges a split row
 
 static_assert(32 <= int(kPcolPad), "an id request may read 31 entries past the row");
 static_assert(kRowWords == 16 * kSB && kXRFeat == 112, "XR row: 4 super-blocks, R in words 56..63 (D <= 112)");
@@ -362,6 +365,186 @@ __device__ inline float fold_pair(float x, float y) {
 // after the projection.
 // DIM: head width, 32 or 64 (wave h then multiplies U_h by the two 32-column
 // blocks of W_h in turn).  KS = 8 (D_in > 112): R from its own array.
+// The merge of split row c (its first chunk), by the wave of its last chunk
+// to arrive: scales each chunk's sums and denominator by e^(m_c - M_ref),
+// M_ref the largest of the chunks' reference maxima, and adds them in chunk
+// order (the chunk merge of the running maximum, gat_tfs_online.cpp:86-117);
+// then out_h = (U_h W_h) / den_h on the VALU with the FP32 (bf16-rounded) W;
+// lane l computes columns 32 cb + 4 (l % 8) .. + 3 of head l / 8, for each
+// 32-column block cb of the head.  sw: the wave's kMergeFloats of LDS.
+__device__ void afs_merge_row(const AfsArgs& a, uint64_t c, int l, float* sw) {
+    const uint32_t k = a.chunk_k[c];
+    const uint64_t rbeg = a.prow[k], rend = a.prow[k + 1];
+    const uint32_t i = a.perm[k];
+    if (i >= a.n || rbeg > rend || rend > a.e) return;
+    const uint32_t nch = uint32_t((rend - rbeg + a.chunk_edges - 1) / a.chunk_edges);
+    if (c + nch > a.chunks) return;
+    // The common reference M_ref and the exact max M (lanes 0..7, head l),
+    // then the denominators scaled to M_ref in chunk order.
+    float d = 0.0f, mref = -INFINITY;
+    if (l < 8) {
+        float mx = -INFINITY;
+#pragma unroll 16
+        for (uint32_t q = 0; q < nch; ++q) {
+            mref = fmaxf(mref, a.part[(c + q) * kPart + kMOff + l]);
+            mx = fmaxf(mx, a.part[(c + q) * kPart + kMxOff + l]);
+        }
+#pragma unroll 16
+        for (uint32_t q = 0; q < nch; ++q) {
+            const float* pq = a.part + (c + q) * kPart;
+            d += pq[kDenOff + l] * exp_w(pq[kMOff + l] - mref);
+        }
+        a.mx[uint64_t(i) * 8 + l] = mx;
+        a.den[uint64_t(i) * 8 + l] = d * exp_w(mref - mx);  // against the exact max
+    }
+    // U_h[f] into LDS (lane l adds features 2l, 2l + 1); the projected row is
+    // scaled by 1 / den_h afterwards, as in the tile path.
+    float dall[8], rall[8];  // read before any lane is masked off
+#pragma unroll
+    for (int h = 0; h < 8; ++h) {
+        dall[h] = lane_f(d, h);
+        rall[h] = lane_f(mref, h);
+    }
+    if (l < (a.in > kXRFeat ? kRowWords : kXRFeat / 2)) {
+        // Chunk by chunk (the order of the sums); the loads of kMergeAhead
+        // chunks are requested together, so the chain of partials runs at
+        // L2 bandwidth rather than one round trip per chunk.
+        constexpr uint32_t kMergeAhead = 2;
+        float t[8][2];
+#pragma unroll
+        for (int h = 0; h < 8; ++h) t[h][0] = t[h][1] = 0.0f;
+        auto add_chunks = [&](uint32_t q0, auto count) {
+            constexpr uint32_t CNT = decltype(count)::value;
+            float2 v[CNT][8];
+            float mq[CNT][8];
+#pragma unroll
+            for (uint32_t u = 0; u < CNT; ++u)
+#pragma unroll
+                for (int h = 0; h < 8; ++h) {
+                    const float* pq = a.part + (c + q0 + u) * kPart;
+                    v[u][h] = *reinterpret_cast<const float2*>(pq + 2 * l + h * 128);
+                    mq[u][h] = pq[kMOff + h];
+                }
+#pragma unroll
+            for (uint32_t u = 0; u < CNT; ++u)
+#pragma unroll
+                for (int h = 0; h < 8; ++h) {
+                    const float f = exp_w(mq[u][h] - rall[h]);
+                    t[h][0] = __builtin_fmaf(v[u][h].x, f, t[h][0]);
+                    t[h][1] = __builtin_fmaf(v[u][h].y, f, t[h][1]);
+                }
+        };
+        uint32_t q = 0;
+        for (; q + kMergeAhead <= nch; q += kMergeAhead) add_chunks(q, std::integral_constant<uint32_t, kMergeAhead>{});
+        for (; q < nch; ++q) add_chunks(q, std::integral_constant<uint32_t, 1>{});
+        // bf16-stored hidden outputs: U enters the projection as one bf16, as
+        // in the tile path (the rounding of a bf16 projection input).
+        const bool round_s = a.outbf != nullptr;
+#pragma unroll
+        for (int h = 0; h < 8; ++h) {
+            float s0 = t[h][0], s1 = t[h][1];
+            if (round_s) {
+                s0 = bf16_widen(bf16_hw(s0));
+                s1 = bf16_widen(bf16_hw(s1));
+            }
+            sw[h * 128 + 2 * l] = s0;
+            sw[h * 128 + 2 * l + 1] = s1;
+        }
+    }
+    wave_sync();
+    const int h = l / 8, width = 8 * a.dim;
+    float inv = 0.0f;
+#pragma unroll
+    for (int q = 0; q < 8; ++q)
+        if (q == h) inv = dall[q] > 0.0f ? 1.0f / dall[q] : 0.0f;
+    for (int cb = 0; cb < a.dim / 32; ++cb) {
+        const int c0 = a.dim * h + 32 * cb + 4 * (l % 8);
+        float o[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        const float* wcol = a.wq + c0;
+        auto fma4 = [&](float sv, const float4& wv) {
+            o[0] = __builtin_fmaf(sv, wv.x, o[0]);
+            o[1] = __builtin_fmaf(sv, wv.y, o[1]);
+            o[2] = __builtin_fmaf(sv, wv.z, o[2]);
+            o[3] = __builtin_fmaf(sv, wv.w, o[3]);
+        };
+        // 16 rows of W requested at a time (L2-resident), then their FMAs in order.
+        int f = 0;
+        for (; f + 16 <= a.in; f += 16) {
+            float4 wv[16];
+#pragma unroll
+            for (int x = 0; x < 16; ++x) wv[x] = *reinterpret_cast<const float4*>(wcol + uint64_t(f + x) * width);
+#pragma unroll
+            for (int x = 0; x < 16; ++x) fma4(sw[h * 128 + f + x], wv[x]);
+        }
+        for (; f < a.in; ++f) fma4(sw[h * 128 + f], *reinterpret_cast<const float4*>(wcol + uint64_t(f) * width));
+#pragma unroll
+        for (int x = 0; x < 4; ++x) o[x] *= inv;
+        if (a.hidden)
+#pragma unroll
+            for (int x = 0; x < 4; ++x) o[x] = elu_bf16(o[x]);
+        const uint64_t off = uint64_t(i) * width + c0;
+        if (a.outbf)
+            *reinterpret_cast<uint2*>(a.outbf + off) = make_uint2(bf16x2(o[0], o[1]), bf16x2(o[2], o[3]));
+        if (a.out32) *reinterpret_cast<float4*>(a.out32 + off) = make_float4(o[0], o[1], o[2], o[3]);
+    }
+}
+
+// Chunk c of a split row, one wave: sums against maxima of its own (the lazy
+// reference max and the exact max) into part[c][h * 128 + f], the
+// denominators and both maxima after them; the last chunk of the row to
+// arrive (agent-scope release/acquire around a relaxed counter) merges the
+// row.  sw: the wave's kMergeFloats of LDS.
+__device__ void afs_chunk(const AfsArgs& a, uint64_t c, int l, float* sw) {
+    const int g = l / 16, n = l % 16;
+    const bool head = n < 8;
+    if (c >= a.chunks) return;
+    const uint32_t k = a.chunk_k[c], first = a.chunk_first[c];
+    const uint64_t rbeg = a.prow[k], rend = a.prow[k + 1];
+    const uint32_t i = a.perm[k];
+    if (i >= a.n || rbeg > rend || rend > a.e) return;
+    const uint64_t beg = rbeg + uint64_t(c - first) * a.chunk_edges;
+    const uint64_t end = beg + a.chunk_edges < rend ? beg + a.chunk_edges : rend;
+        const bool rsep = a.in > kXRFeat;
+    Sums s;
+    zero_sums(s);
+    s.L = head || !rsep ? a.L[uint64_t(i) * 8 + n % 8] : 0.0f;  // (lanes h + 8 score half of head h's edges)
+    s.m = s.mx = -INFINITY;
+    Batch<kEPL> b;
+    if (rsep) gather_sums<false, true>(a.pcol, a.xr, a.R, beg, end, l, s, a.pcol[beg + uint32_t(l % 32)], 0, b);
+    else gather_sums<false, false>(a.pcol, a.xr, a.R, beg, end, l, s, a.pcol[beg + uint32_t(l % 32)], 0, b);
+    const float den = total_den(s.den);
+    float* part = a.part + c * kPart;
+    {
+        // lane (g, n): head 4 (g % 2) + q + (g >= 2) after fold_pair, q = 0, 2
+        const int hb = 4 * (g & 1) + (g >> 1);
+#pragma unroll
+        for (int sb = 0; sb < kSB; ++sb) {
+            const int P = 16 * sb + n;
+            if (P >= (rsep ? kRowWords : kXRFeat / 2)) continue;
+#pragma unroll
+            for (int q = 0; q < 4; q += 2)
+                *reinterpret_cast<float2*>(part + (hb + q) * 128 + 2 * P) =
+                    make_float2(fold_pair(s.d[2 * sb][q], s.d[2 * sb][q + 1]),
+                                fold_pair(s.d[2 * sb + 1][q], s.d[2 * sb + 1][q + 1]));
+        }
+    }
+    if (head && g == 0) {
+        part[kDenOff + n] = den;
+        part[kMOff + n] = s.m;
+        part[kMxOff + n] = s.mx;
+    }
+    const uint32_t nch = uint32_t((rend - rbeg + a.chunk_edges - 1) / a.chunk_edges);
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+    uint32_t old = 0;
+    if (l == 0) old = __hip_atomic_fetch_add(a.counter + first, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    old = __shfl(old, 0);
+    if (old + 1 != nch) return;  // not the last chunk of this row
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    if (l == 0) a.counter[first] = 0;  // ready for the next launch
+    afs_merge_row(a, first, l, sw);
+}
+
+
 template <int KS, bool HL, int TR, int DIM>
 __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) k_afs_tiles(AfsArgs a) {
     static_assert(TR == 16 || (TR == 32 && !HL), "16-row tiles, or 32-row tiles of one bf16");
@@ -384,7 +567,26 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4
     const int l = threadIdx.x % kWave;
     const int g = l / 16, n = l % 16;
     const bool head = n < 8;
+    const uint32_t chunk_blocks = gridDim.x - a.tile_blocks;
+    if (blockIdx.x < chunk_blocks) {
+        // Split-row chunks, one per wave, in the first blocks: they start with
+        // the launch, and the tile blocks that wait for their slots take fewer
+        // tiles.
+        static_assert(kWaves * kMergeFloats * 4 <= kSBytes, "merge scratch fits");
+        afs_chunk(a, uint64_t(blockIdx.x) * kWaves + w, l, reinterpret_cast<float*>(slds) + w * kMergeFloats);
+        return;
+    }
+    // Tiles in a dynamic order: the block's first three are tb, tb + G and
+    // tb + 2G (G tile blocks); tile j + 3 is taken from the launch's counter
+    // during tile j and published in the ring tq for tile j + 1, which
+    // requests its bounds two tiles ahead.  The last tile block to finish
+    // clears the counters for the next launch.
+    const uint32_t tb = blockIdx.x - chunk_blocks, G = a.tile_blocks;
+    uint32_t* const tq = reinterpret_cast<uint32_t*>(slds + kSBytes + kTRowBytes + kTDenBytes);
+    uint32_t* const tctr = a.counter + a.chunks;  // [0] tiles taken past 3G, [1] tile blocks done
     const uint64_t tiles = (a.rows + TR - 1) / TR;
+    if (threadIdx.x == 0) tq[2] = tb + 2 * G;
+    __syncthreads();
     // Bounds of the wave's rows of tile t (lane q < RPW: tile row w + 8 q),
     // requested one tile ahead (during the previous tile's projection).
     auto fetch_bounds = [&](uint64_t t, uint32_t& fi, uint64_t& fb, uint64_t& fe) {
@@ -421,10 +623,15 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4
     uint64_t mb, me, nmb, nme;
     uint32_t idr[NID], nidr[NID];
     float Lall, nLall;
-    fetch_bounds(blockIdx.x, mi, mb, me);
-    fetch_bounds(blockIdx.x + gridDim.x, nmi, nmb, nme);
+    fetch_bounds(tb, mi, mb, me);
+    fetch_bounds(tb + uint64_t(G), nmi, nmb, nme);
     fetch_ids(mi, mb, me, idr, Lall);
-    for (uint64_t tile = blockIdx.x; tile < tiles; tile += gridDim.x, buf ^= DB ? 1 : 0) {
+    uint64_t tile = tb, tnext = tb + uint64_t(G);
+    for (uint32_t j = 0; tile < tiles; ++j, buf ^= DB ? 1 : 0) {
+        const uint64_t t2 = uint32_t(__builtin_amdgcn_readfirstlane(int(tq[(j + 2) & 3])));
+        uint32_t taken = 0;
+        if (threadIdx.x == 0)
+            taken = 3 * G + __hip_atomic_fetch_add(tctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         uint32_t* const trow = trow_all + buf * TR;
         float* const tden = tden_all + buf * 8 * (TR + 1);
         // ---- RPW rows per wave (tile rows w + 8 q): bounds in lane q, L in
@@ -432,7 +639,7 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4
         uint32_t n2mi;
         uint64_t n2mb, n2me;
         fetch_ids(nmi, nmb, nme, nidr, nLall);
-        fetch_bounds(tile + 2 * uint64_t(gridDim.x), n2mi, n2mb, n2me);
+        fetch_bounds(t2, n2mi, n2mb, n2me);
         // Row q of the wave: node, edge range and first ids.
         auto row_of = [&](int q, uint32_t& qi, uint64_t& qb, uint64_t& qe, uint32_t& qids) {
             qi = uint32_t(__builtin_amdgcn_readlane(int(mi), q));
@@ -534,6 +741,7 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4
                     bf16x8, *reinterpret_cast<const uint4*>(wb + uint64_t(ks) * a.nmb * kWave * sizeof(uint4) + lo));
         };
         load_w(0);
+        if (threadIdx.x == 0) tq[(j + 3) & 3] = taken;
         __syncthreads();
         // 1 / den of the lane's output row (tile row l % 32) and head w; an
         // empty row has U = 0 and den = 0, and gives 0.
@@ -611,195 +819,34 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4
 #pragma unroll
         for (int c = 0; c < NID; ++c) idr[c] = nidr[c];
         Lall = nLall;
+        tile = tnext;
+        tnext = t2;
+    }
+    if (threadIdx.x == 0) {
+        const uint32_t done = __hip_atomic_fetch_add(tctr + 1, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+        if (done + 1 == G) {
+            __hip_atomic_store(tctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(tctr + 1, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
     }
 }
 
-// One wave per chunk of a split row: sums from the exact row max into
-// part[c][h * 128 + f] and the denominators into part[c][1024 + h].
-__global__ void __launch_bounds__(kChunkThreads) k_afs_chunks(AfsArgs a) {
-    const int w = __builtin_amdgcn_readfirstlane(int(threadIdx.x) / kWave);
-    const int l = threadIdx.x % kWave;
-    const int g = l / 16, n = l % 16;
-    const bool head = n < 8;
-    const uint64_t c = uint64_t(blockIdx.x) * (kChunkThreads / kWave) + w;
-    if (c >= a.chunks) return;
-    const uint32_t k = a.chunk_k[c], first = a.chunk_first[c];
-    const uint64_t rbeg = a.prow[k], rend = a.prow[k + 1];
-    const uint32_t i = a.perm[k];
-    if (i >= a.n || rbeg > rend || rend > a.e) return;
-    const uint64_t beg = rbeg + uint64_t(c - first) * a.chunk_edges;
-    const uint64_t end = beg + a.chunk_edges < rend ? beg + a.chunk_edges : rend;
-    // The chunk's edges as a row's (lazy reference max, exact max beside it);
-    // the merge scales the chunks to a common reference.
-    const bool rsep = a.in > kXRFeat;
-    Sums s;
-    zero_sums(s);
-    s.L = head || !rsep ? a.L[uint64_t(i) * 8 + n % 8] : 0.0f;  // (lanes h + 8 score half of head h's edges)
-    s.m = s.mx = -INFINITY;
-    Batch<kEPL> b;
-    if (rsep) gather_sums<false, true>(a.pcol, a.xr, a.R, beg, end, l, s, a.pcol[beg + uint32_t(l % 32)], 0, b);
-    else gather_sums<false, false>(a.pcol, a.xr, a.R, beg, end, l, s, a.pcol[beg + uint32_t(l % 32)], 0, b);
-    const float den = total_den(s.den);
-    float* part = a.part + c * kPart;
-    {
-        // lane (g, n): head 4 (g % 2) + q + (g >= 2) after fold_pair, q = 0, 2
-        const int hb = 4 * (g & 1) + (g >> 1);
-#pragma unroll
-        for (int sb = 0; sb < kSB; ++sb) {
-            const int P = 16 * sb + n;
-            if (P >= (rsep ? kRowWords : kXRFeat / 2)) continue;
-#pragma unroll
-            for (int q = 0; q < 4; q += 2)
-                *reinterpret_cast<float2*>(part + (hb + q) * 128 + 2 * P) =
-                    make_float2(fold_pair(s.d[2 * sb][q], s.d[2 * sb][q + 1]),
-                                fold_pair(s.d[2 * sb + 1][q], s.d[2 * sb + 1][q + 1]));
-        }
-    }
-    if (head && g == 0) {
-        part[kDenOff + n] = den;
-        part[kMOff + n] = s.m;
-        part[kMxOff + n] = s.mx;
-    }
-}
-
-// One wave per split row (found at its first chunk): scales each chunk's sums
-// and denominator by e^(m_c - M_ref), M_ref the largest of the chunks'
-// reference maxima, and adds them in chunk order (the chunk merge of the
-// running maximum, gat_tfs_online.cpp:86-117); then out_h = (U_h W_h) / den_h
-// on the VALU
-// with the FP32 (bf16-rounded) W; lane l computes columns 32 cb + 4 (l % 8)
-// .. + 3 of head l / 8, for each 32-column block cb of the head.
-__global__ void __launch_bounds__(kChunkThreads) k_afs_merge(AfsArgs a) {
-    __shared__ float s[kChunkThreads / kWave][8 * kRowWords * 2];
-    const int w = threadIdx.x / kWave, l = threadIdx.x % kWave;
-    const uint64_t c = uint64_t(blockIdx.x) * (kChunkThreads / kWave) + w;
-    if (c >= a.chunks || a.chunk_first[c] != c) return;
-    const uint32_t k = a.chunk_k[c];
-    const uint64_t rbeg = a.prow[k], rend = a.prow[k + 1];
-    const uint32_t i = a.perm[k];
-    if (i >= a.n || rbeg > rend || rend > a.e) return;
-    const uint32_t nch = uint32_t((rend - rbeg + a.chunk_edges - 1) / a.chunk_edges);
-    if (c + nch > a.chunks) return;
-    // The common reference M_ref and the exact max M (lanes 0..7, head l),
-    // then the denominators scaled to M_ref in chunk order.
-    float d = 0.0f, mref = -INFINITY;
-    if (l < 8) {
-        float mx = -INFINITY;
-#pragma unroll 16
-        for (uint32_t q = 0; q < nch; ++q) {
-            mref = fmaxf(mref, a.part[(c + q) * kPart + kMOff + l]);
-            mx = fmaxf(mx, a.part[(c + q) * kPart + kMxOff + l]);
-        }
-#pragma unroll 16
-        for (uint32_t q = 0; q < nch; ++q) {
-            const float* pq = a.part + (c + q) * kPart;
-            d += pq[kDenOff + l] * exp_w(pq[kMOff + l] - mref);
-        }
-        a.mx[uint64_t(i) * 8 + l] = mx;
-        a.den[uint64_t(i) * 8 + l] = d * exp_w(mref - mx);  // against the exact max
-    }
-    // U_h[f] into LDS (lane l adds features 2l, 2l + 1); the projected row is
-    // scaled by 1 / den_h afterwards, as in the tile path.
-    float dall[8], rall[8];  // read before any lane is masked off
-#pragma unroll
-    for (int h = 0; h < 8; ++h) {
-        dall[h] = lane_f(d, h);
-        rall[h] = lane_f(mref, h);
-    }
-    if (l < (a.in > kXRFeat ? kRowWords : kXRFeat / 2)) {
-        // Chunk by chunk (the order of the sums); the loads of kMergeAhead
-        // chunks are requested together, so the chain of partials runs at
-        // L2 bandwidth rather than one round trip per chunk.
-        constexpr uint32_t kMergeAhead = 4;
-        float t[8][2];
-#pragma unroll
-        for (int h = 0; h < 8; ++h) t[h][0] = t[h][1] = 0.0f;
-        auto add_chunks = [&](uint32_t q0, auto count) {
-            constexpr uint32_t CNT = decltype(count)::value;
-            float2 v[CNT][8];
-            float mq[CNT][8];
-#pragma unroll
-            for (uint32_t u = 0; u < CNT; ++u)
-#pragma unroll
-                for (int h = 0; h < 8; ++h) {
-                    const float* pq = a.part + (c + q0 + u) * kPart;
-                    v[u][h] = *reinterpret_cast<const float2*>(pq + 2 * l + h * 128);
-                    mq[u][h] = pq[kMOff + h];
-                }
-#pragma unroll
-            for (uint32_t u = 0; u < CNT; ++u)
-#pragma unroll
-                for (int h = 0; h < 8; ++h) {
-                    const float f = exp_w(mq[u][h] - rall[h]);
-                    t[h][0] = __builtin_fmaf(v[u][h].x, f, t[h][0]);
-                    t[h][1] = __builtin_fmaf(v[u][h].y, f, t[h][1]);
-                }
-        };
-        uint32_t q = 0;
-        for (; q + kMergeAhead <= nch; q += kMergeAhead) add_chunks(q, std::integral_constant<uint32_t, kMergeAhead>{});
-        for (; q < nch; ++q) add_chunks(q, std::integral_constant<uint32_t, 1>{});
-        // bf16-stored hidden outputs: U enters the projection as one bf16, as
-        // in the tile path (the rounding of a bf16 projection input).
-        const bool round_s = a.outbf != nullptr;
-#pragma unroll
-        for (int h = 0; h < 8; ++h) {
-            float s0 = t[h][0], s1 = t[h][1];
-            if (round_s) {
-                s0 = bf16_widen(bf16_hw(s0));
-                s1 = bf16_widen(bf16_hw(s1));
-            }
-            s[w][h * 128 + 2 * l] = s0;
-            s[w][h * 128 + 2 * l + 1] = s1;
-        }
-    }
-    wave_sync();
-    const int h = l / 8, width = 8 * a.dim;
-    float inv = 0.0f;
-#pragma unroll
-    for (int q = 0; q < 8; ++q)
-        if (q == h) inv = dall[q] > 0.0f ? 1.0f / dall[q] : 0.0f;
-    for (int cb = 0; cb < a.dim / 32; ++cb) {
-        const int c0 = a.dim * h + 32 * cb + 4 * (l % 8);
-        float o[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-        const float* wcol = a.wq + c0;
-        auto fma4 = [&](float sv, const float4& wv) {
-            o[0] = __builtin_fmaf(sv, wv.x, o[0]);
-            o[1] = __builtin_fmaf(sv, wv.y, o[1]);
-            o[2] = __builtin_fmaf(sv, wv.z, o[2]);
-            o[3] = __builtin_fmaf(sv, wv.w, o[3]);
-        };
-        // 16 rows of W requested at a time (L2-resident), then their FMAs in order.
-        int f = 0;
-        for (; f + 16 <= a.in; f += 16) {
-            float4 wv[16];
-#pragma unroll
-            for (int x = 0; x < 16; ++x) wv[x] = *reinterpret_cast<const float4*>(wcol + uint64_t(f + x) * width);
-#pragma unroll
-            for (int x = 0; x < 16; ++x) fma4(s[w][h * 128 + f + x], wv[x]);
-        }
-        for (; f < a.in; ++f) fma4(s[w][h * 128 + f], *reinterpret_cast<const float4*>(wcol + uint64_t(f) * width));
-#pragma unroll
-        for (int x = 0; x < 4; ++x) o[x] *= inv;
-        if (a.hidden)
-#pragma unroll
-            for (int x = 0; x < 4; ++x) o[x] = elu_bf16(o[x]);
-        const uint64_t off = uint64_t(i) * width + c0;
-        if (a.outbf)
-            *reinterpret_cast<uint2*>(a.outbf + off) = make_uint2(bf16x2(o[0], o[1]), bf16x2(o[2], o[3]));
-        if (a.out32) *reinterpret_cast<float4*>(a.out32 + off) = make_float4(o[0], o[1], o[2], o[3]);
-    }
-}
-
+// One block per kWaves chunks of split rows, then a resident grid of tile
+// blocks (two per CU).  a.counter holds chunks + 2 entries, zero between
+// launches.
 template <int KS, bool HL, int TR, int DIM>
-hipError_t launch_tiles_hl(const AfsArgs& a, hipStream_t s, int cus) {
+hipError_t launch_tiles_hl(AfsArgs a, hipStream_t s, int cus) {
     const uint64_t tiles = (a.rows + TR - 1) / TR;
-    if (!tiles) return hipSuccess;
+    uint64_t blocks = uint64_t(cus) * 2;
+    if (blocks > tiles) blocks = tiles;
+    const uint64_t chunk_blocks = (a.chunks + kWaves - 1) / kWaves;
+    if (blocks + chunk_blocks == 0) return hipSuccess;
+    if (tiles >= (uint64_t(1) << 31) || blocks + chunk_blocks > 0x7fffffffu) return hipErrorInvalidValue;
     hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_afs_tiles<KS, HL, TR, DIM>),
                                        hipFuncAttributeMaxDynamicSharedMemorySize, kLdsBytes);
     if (e != hipSuccess) return e;
-    uint64_t blocks = uint64_t(cus) * 2;
-    if (blocks > tiles) blocks = tiles;
-    k_afs_tiles<KS, HL, TR, DIM><<<dim3(uint32_t(blocks)), kThreads, kLdsBytes, s>>>(a);
+    a.tile_blocks = uint32_t(blocks);
+    k_afs_tiles<KS, HL, TR, DIM><<<dim3(uint32_t(chunk_blocks + blocks)), kThreads, kLdsBytes, s>>>(a);
     return hipGetLastError();
 }
 
@@ -826,12 +873,7 @@ hipError_t launch_aggregate_afsum(const AfsArgs& a, const SplitTable& t, hipStre
     if (!aggregate_afsum_supported(a.in, 8, a.dim, a.n) || a.nmb < 8 || a.ksteps != (a.in + 15) / 16 || !a.xr ||
         !a.wq || !a.R)
         return hipErrorInvalidValue;
-    if (a.chunks) {
-        hipError_t e = hipSuccess;
-        const dim3 grid(uint32_t((a.chunks + kChunkThreads / kWave - 1) / (kChunkThreads / kWave)));
-        k_afs_chunks<<<grid, kChunkThreads, 0, s>>>(a);
-        if ((e = hipGetLastError()) != hipSuccess) return e;
-    }
+    if (!a.counter) return hipErrorInvalidValue;
     hipError_t e = hipSuccess;
     switch (a.ksteps) {
         case 1: e = launch_tiles<1>(a, s, cus); break;
@@ -843,12 +885,7 @@ hipError_t launch_aggregate_afsum(const AfsArgs& a, const SplitTable& t, hipStre
         case 7: e = launch_tiles<7>(a, s, cus); break;
         default: e = launch_tiles<8>(a, s, cus); break;
     }
-    if (e != hipSuccess) return e;
-    if (a.chunks) {
-        const dim3 grid(uint32_t((a.chunks + kChunkThreads / kWave - 1) / (kChunkThreads / kWave)));
-        k_afs_merge<<<grid, kChunkThreads, 0, s>>>(a);
-    }
-    return hipGetLastError();
+    return e;
 }
 
 }  // namespace gatgpu

@@ -127,16 +127,18 @@ int compute_bins(gatgpu_ctx* c) {
             HIPCHECK(c, P.first.ensure(cf.size() * 4));
             HIPCHECK(c, P.mchunk.ensure(ck.size() * 8 * 4));
             HIPCHECK(c, P.part.ensure(ck.size() * (8 * 128 + 24) * 4));  // largest partial: aggregate-first U
-            HIPCHECK(c, P.counter.ensure(ck.size() * 4));
             HIPCHECK(c, hipMemcpy(P.k.p, ck.data(), ck.size() * 4, hipMemcpyHostToDevice));
             HIPCHECK(c, hipMemcpy(P.first.p, cf.data(), cf.size() * 4, hipMemcpyHostToDevice));
-            HIPCHECK(c, hipMemset(P.counter.p, 0, ck.size() * 4));
             t.chunk_k = P.k.as<uint32_t>();
             t.chunk_first = P.first.as<uint32_t>();
             t.mchunk = P.mchunk.as<float>();
             t.part = P.part.as<float>();
-            t.counter = P.counter.as<uint32_t>();
         }
+        // Arrivals of the split rows at their first chunks, then the two tile
+        // counters of the aggregate-first sum form.
+        HIPCHECK(c, P.counter.ensure((ck.size() + 2) * 4));
+        HIPCHECK(c, hipMemset(P.counter.p, 0, (ck.size() + 2) * 4));
+        t.counter = P.counter.as<uint32_t>();
     }
     return GATGPU_OK;
 }
@@ -318,6 +320,7 @@ int run_layer_af(gatgpu_ctx* c, int l, bool hidden, const float* src32, const ui
         a.chunk_edges = P.table.chunk_edges;
         a.mchunk = P.table.mchunk;
         a.part = P.table.part;
+        a.counter = P.table.counter;
         HIPCHECK(c, launch_aggregate_afsum(a, P.table, c->stream, c->cus));
     } else {
     AfArgs a{};

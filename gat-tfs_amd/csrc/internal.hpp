@@ -357,7 +357,9 @@ struct AfsArgs {
     const uint32_t* chunk_first;
     uint32_t chunk_edges;
     float* mchunk;
-    float* part;         // [chunks][8*128 + 8]
+    float* part;         // [chunks][8*128 + 24]
+    uint32_t* counter;   // [chunks + 2]: row arrivals (at a row's first chunk), tiles taken, tile blocks done; zero between launches
+    uint32_t tile_blocks;  // set by the launch: the blocks after the chunk blocks
 };
 // (n * 256 bytes must stay below 4 GiB: the gather uses 32-bit row offsets)
 bool aggregate_afsum_supported(int in, int heads, int dim, uint64_t n);
