@@ -27,13 +27,13 @@ SCHEDULES = [{}, {gatgpu.OPT_BLOCK_ROW_MIN_DEGREE: 1},
              {gatgpu.OPT_SPLIT_ROW_MIN_DEGREE: 16, gatgpu.OPT_SPLIT_CHUNK_EDGES: 64}]
 
 
-def run_layer(ctx, row, col, x, p, hidden, precision, options=None):
+def run_layer(ctx, row, col, x, p, hidden, precision, options=None, dataflow=gatgpu.TRANSFORM_FIRST):
     ctx.set_graph(row, col)
     for k, v in (options or {}).items():
         ctx.set_option(k, v)
     ctx.set_layer(0, p)
     ctx.set_input(x)
-    ctx.layer_forward(0, precision, gatgpu.TRANSFORM_FIRST, hidden)
+    ctx.layer_forward(0, precision, dataflow, hidden)
     out = {k: ctx.stage(0, k) for k in ("left", "right", "max", "den", "out")}
     for k in options or {}:
         ctx.set_option(k, DEFAULT_OPTIONS[k])
@@ -41,18 +41,46 @@ def run_layer(ctx, row, col, x, p, hidden, precision, options=None):
 
 
 # ---------------------------------------------------------------- schedule
-def schedule_graphs():
-    yield "boundary35", oracle.boundary_graph(17)["row"], oracle.boundary_graph(17)["col"]
-    g = smoke1024()
-    yield "smoke1024", g["row"], g["col"]
-    for name in ("smoke", "arxiv", "large"):
-        row, col = inputs.WORKLOADS[name].graph()
-        yield name, row, col
+def four_digit_graph():
+    """4 096 rows whose degrees need all four 8-bit digits of the radix sort:
+    two rows of more than 2^24 edges that differ only in their low digit, a
+    row of 2^17 + 3 and rows of 65 535, 65 536, 65 792 (0x10100) and twice
+    70 000 (equal degrees: ascending ids), among rows of 0..23 edges.  About
+    34M edges, sources uniform."""
+    rng = np.random.default_rng(5)
+    n = 4096
+    deg = rng.integers(0, 24, n).astype(np.uint64)
+    for i, d in {17: (1 << 24) + 5, 3000: (1 << 24) + 1, 5: (1 << 17) + 3, 900: 70000, 901: 70000,
+                 77: 65536, 4095: 65535, 1000: 0x10100}.items():
+        deg[i] = d
+    row = np.zeros(n + 1, np.uint64)
+    np.cumsum(deg, out=row[1:])
+    col = rng.integers(0, n, int(row[-1]), dtype=np.uint32)
+    return row, col
 
 
-@pytest.mark.parametrize("case", ["boundary35", "smoke1024", "smoke", "arxiv", "large"])
+def schedule_graph(case):
+    if case == "boundary35":
+        g = oracle.boundary_graph(17)
+        return g["row"], g["col"]
+    if case == "smoke1024":
+        g = smoke1024()
+        return g["row"], g["col"]
+    if case == "four_digits":
+        return four_digit_graph()
+    return inputs.WORKLOADS[case].graph()
+
+
+# Radix passes the sort needs (one per 8-bit digit of the maximum degree):
+# boundary35..large 1-2, skew (max in-degree 132 270) 3, four_digits 4.
+@pytest.mark.parametrize("case", ["boundary35", "smoke1024", "smoke", "arxiv", "large", "skew", "four_digits"])
 def test_degree_schedule_bit_exact(gpu_ctx, case):
-    row, col = next((r, c) for n, r, c in schedule_graphs() if n == case)
+    row, col = schedule_graph(case)
+    maxdeg = int(np.diff(row).max())
+    if case == "skew":
+        assert (1 << 16) <= maxdeg < (1 << 24)
+    if case == "four_digits":
+        assert maxdeg >= (1 << 24)
     gpu_ctx.set_graph(row, col)
     perm, steps = gpu_ctx.degree_schedule()
     operm, osteps = oracle.degree_schedule(row)
@@ -128,6 +156,170 @@ def test_adversarial_scores(gpu_ctx):
         r = oracle.ref_layer(g["row"], g["col"], x, p, False)
         scale = max(1.0, float(np.abs(r["out"]).max()))
         assert oracle.errors(r["out"], got["out"])["max_abs"] < FP32_MAX_ABS * scale, scenario
+
+
+def peak_graph():
+    """250 nodes; node 249 is the score peak of the late-peak scenario.  Row
+    degrees cycle through 0..249 edges (one to four 64-edge chunks); rows
+    i % 3 == 0 list the peak as their last source (in their last chunk),
+    rows i % 3 == 1 as their first, rows i % 3 == 2 not at all."""
+    n = 250
+    degs = [0, 1, 2, 15, 16, 17, 63, 64, 65, 127, 128, 129, 130, 191, 192, 193, 200, 249]
+    row, col = [0], []
+    for i in range(n):
+        c = degs[i % len(degs)]
+        if c:
+            base = [(i * 3 + k * 7) % (n - 1) for k in range(c - 1)]
+            col.extend({0: base + [n - 1], 1: [n - 1] + base}.get(i % 3, base + [(i * 3 + 5) % (n - 1)]))
+        row.append(len(col))
+    return np.array(row, np.uint64), np.array(col, np.uint32)
+
+
+def adversarial_layer_bf16_exact(n, scenario, K, d):
+    """The score scenarios of baseline/tests/boundaries.cpp:46-48 with every
+    input, weight and projected value exact in bf16, so the bf16 paths see
+    the same scores as the FP32 oracle: x = [1, t], W = 1, Z[i,:] = 1 + t_i,
+    L[i,h] = (1 + t_i) aL[h,0], R[j,h] = (1 + t_j) aR[h,1].
+    0: equal scores (aR = 0); 1: late peak (t = -255 except the last node,
+    +255: non-peak weights underflow to 0); 2: ramp t = i - 17; 3/4: L offset
+    +-8192 (t = 0 / t = round(8 sin i))."""
+    t = np.zeros(n, np.float32)
+    if scenario == 1:
+        t[:] = -255.0
+        t[-1] = 255.0
+    elif scenario == 2:
+        t = np.arange(n, dtype=np.float32) - 17
+    elif scenario == 4:
+        t = np.round(np.sin(np.arange(n)) * 8).astype(np.float32)
+    x = np.stack([np.ones(n, np.float32), t], axis=1)
+    w = np.ones((2, K * d), np.float32)
+    al = np.zeros(K * d, np.float32)
+    ar = np.zeros(K * d, np.float32)
+    for h in range(K):
+        al[h * d] = {3: 8192.0, 4: -8192.0}.get(scenario, float(h) - 4)
+        ar[h * d + 1] = 0.0 if scenario == 0 else 1.0
+    assert np.array_equal(oracle.quantize_bf16(x), x) and np.array_equal(oracle.quantize_bf16(x @ w), x @ w)
+    return x, {"in": 2, "heads": K, "dim": d, "w": w, "al": al, "ar": ar}
+
+
+ADVERSARIAL_PATHS = [("fp32_tf", gatgpu.FP32, gatgpu.TRANSFORM_FIRST), ("bf16_tf", gatgpu.BF16, gatgpu.TRANSFORM_FIRST),
+                     ("bf16_af", gatgpu.BF16, gatgpu.AGGREGATE_FIRST)]
+
+
+@pytest.mark.parametrize("K,d", [(8, 32), (8, 64)])
+@pytest.mark.parametrize("path", [p[0] for p in ADVERSARIAL_PATHS])
+def test_adversarial_scores_split_rows(gpu_ctx, K, d, path):
+    """boundaries.cpp:44-52 on the 8-head kernels: the transform-first 8 x 32 /
+    8 x 64 aggregation (FP32 and bf16) and the aggregate-first sum form,
+    under every schedule; with rows >= 16 split into 64-edge chunks, the
+    multi-chunk rows take each chunk's own maximum and the last chunk to
+    arrive rescales the partials, and the peak sits in a row's last chunk,
+    its first, or nowhere.  Every non-empty row has den >= 1, empty rows have
+    den 0 and output 0, outputs are finite, the row max equals the scalar max
+    of LeakyReLU(L + R) over the GPU's own L/R bit for bit, and the output
+    agrees with R0 (inputs exact in bf16, so bf16 and FP32 see one set of
+    scores)."""
+    _, precision, flow = next(p for p in ADVERSARIAL_PATHS if p[0] == path)
+    row, col = peak_graph()
+    n = row.size - 1
+    deg = np.diff(row).astype(np.int64)
+    dst = np.repeat(np.arange(n), deg)
+    for scenario in range(5):
+        x, p = adversarial_layer_bf16_exact(n, scenario, K, d)
+        r = oracle.ref_layer(row, col, x, p, False)
+        scale = max(1.0, float(np.abs(r["out"]).max()))
+        for opts in SCHEDULES:
+            got = run_layer(gpu_ctx, row, col, x, p, False, precision, opts, flow)
+            tag = (scenario, opts)
+            assert np.isfinite(got["out"]).all(), tag
+            assert np.all(got["den"][deg == 0] == 0) and np.all(got["out"][deg == 0] == 0), tag
+            assert np.all(got["den"][deg > 0] >= 1), tag
+            s = got["left"][dst] + got["right"][col]
+            s = np.where(s >= 0, s, np.float32(0.2) * s).astype(np.float32)
+            m = np.full((n, K), -np.inf, np.float32)
+            np.maximum.at(m, dst, s)
+            assert np.array_equal(got["max"], np.where(deg[:, None] > 0, m, 0).astype(np.float32)), tag
+            e = oracle.errors(r["out"], got["out"])
+            assert e["max_abs"] < 1e-3 * scale and e["relative_l2"] < 1e-4, (tag, e)
+
+
+# ---------------------------------------------------------------- repeated runs on one graph
+SPLIT_16_64 = {gatgpu.OPT_SPLIT_ROW_MIN_DEGREE: 16, gatgpu.OPT_SPLIT_CHUNK_EDGES: 64}
+
+
+@pytest.mark.parametrize("flow", [gatgpu.AGGREGATE_FIRST, gatgpu.TRANSFORM_FIRST])
+@pytest.mark.parametrize("split", [False, True])
+def test_rerun_without_set_graph(gpu_ctx, flow, split):
+    """The sum form takes its tiles from counters (169 343 rows: 5 292 tiles,
+    beyond the statically assigned ones) and split rows are merged by the
+    last chunk to arrive; each launch must leave those counters at zero for
+    the next one.  On the arxiv-sized graph a bf16 128 -> 8 x 32 layer runs on
+    inputs x1, x2, x1 with no set_graph in between: the second run equals a
+    run of x2 right after set_graph bit for bit, the third equals the first,
+    and the second is within tolerance of R0 on bf16-rounded x2 and W."""
+    w = inputs.WORKLOADS["arxiv"]
+    row, col = w.graph()
+    p = inputs.glorot_param(128, 8, 32, 41)
+    xs = [inputs.normal((w.n, 128), 42), inputs.normal((w.n, 128), 43)]
+    opts = SPLIT_16_64 if split else {}
+
+    def fresh():
+        gpu_ctx.set_graph(row, col)
+        for k, v in opts.items():
+            gpu_ctx.set_option(k, v)
+        gpu_ctx.set_layer(0, p)
+
+    def run(x):
+        gpu_ctx.layer_forward(0, gatgpu.BF16, flow, False, input=x)
+        return gpu_ctx.stage(0, "out"), gpu_ctx.stage(0, "den")
+
+    try:
+        fresh()
+        runs = [run(xs[0]), run(xs[1]), run(xs[0])]
+        fresh()
+        ref2 = run(xs[1])
+    finally:
+        for k in opts:
+            gpu_ctx.set_option(k, DEFAULT_OPTIONS[k])
+    assert not np.array_equal(runs[0][0], runs[1][0])
+    for a, b in zip(runs[1], ref2):
+        assert np.array_equal(a, b)
+    for a, b in zip(runs[2], runs[0]):
+        assert np.array_equal(a, b)
+    qp = dict(p, w=oracle.quantize_bf16(p["w"]))
+    r = oracle.ref_layer(row, col, oracle.quantize_bf16(xs[1]), qp, False)
+    e = oracle.errors(r["out"], runs[1][0])
+    assert e["finite"] and e["relative_l2"] < BF16_REL_L2, e
+
+
+def test_model_rerun_without_set_graph(gpu_ctx):
+    """Chained bf16 forwards on the arxiv-sized graph (layer 1 aggregate-first,
+    layer 2 transform-first with the output layer's projection in its
+    epilogue, split rows on every layer) with set_input between them and no
+    set_graph: the logits of x2 after x1 equal those of x2 on a fresh graph
+    bit for bit, and x1 again gives x1's logits."""
+    w = inputs.WORKLOADS["arxiv"]
+    row, col = w.graph()
+    m = w.model()
+    xs = [w.features(), inputs.normal((w.n, w.din), 44)]
+
+    def fresh():
+        gpu_ctx.set_graph(row, col)
+        gpu_ctx.set_model(m)
+
+    def run(x):
+        gpu_ctx.set_input(x)
+        return gpu_ctx.model_forward(gatgpu.BF16, gatgpu.AGGREGATE_FIRST)[0]
+
+    fresh()
+    l1, l2, l3 = run(xs[0]), run(xs[1]), run(xs[0])
+    fresh()
+    ref2 = run(xs[1])
+    assert not np.array_equal(l1, l2)
+    assert np.array_equal(l2, ref2) and np.array_equal(l3, l1)
+    ref = oracle.ref_model(row, col, xs[1], m)[2]["out"]
+    e = oracle.errors(ref, l2)
+    assert e["finite"] and e["relative_l2"] < BF16_REL_L2, e
 
 
 # ---------------------------------------------------------------- full models
