@@ -9,12 +9,16 @@ softmax/accumulation).  Prints ONE JSON line (rank 0).
   python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload large|skew|arxiv|smoke]
                   [--precision bf16|fp32] [--dataflow auto|transform_first|aggregate_first]
                   [--no-cpu-baseline] [--cpu-threads T] [--cpu-warmups 2] [--cpu-repeats 7]
+                  [--no-arxiv] [--arxiv-steps 50]
 
 Besides the contract fields the line carries, per layer, the aggregation's
 and the projection's time and fraction of the HBM (and MFMA) peaks
 ("layers"), the dominant projection against both peaks ("roofline_gemm"),
 the cold-start times ("cold_start_ms") and the host CPU baseline with its
-protocol and host description ("cpu_baseline").
+protocol and host description ("cpu_baseline").  With the default workload
+it also times the 2.5M-edge graph of the metric (169,343 nodes, 2,484,941
+edges, 128 -> 8x32 -> 8x32 -> 1x40) in bf16 and FP32, beside its own host
+CPU baseline ("arxiv"; --no-arxiv skips it).
 """
 from __future__ import annotations
 
@@ -46,17 +50,33 @@ def agg_bytes(n, e, heads, dim, s_z, s_out, r_gather=True):
     return 8 * (n + 1) + 4 * e + r + 4 * heads * n + e * heads * dim * s_z + n * heads * dim * s_out
 
 
+def source_digest(paths):
+    """SHA-256 over the given source files (repository-relative), in order."""
+    import hashlib
+
+    h = hashlib.sha256()
+    for rel in paths:
+        h.update((ROOT / rel).read_bytes())
+    return h.hexdigest()
+
+
 def pmc_traffic(workload, precision):
     """HBM bytes per launch of the layer-2 aggregation, measured with
     rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE and calibrated against a device
-    copy of known size; read from the committed summary (None if absent)."""
+    copy of known size; read from the committed summary.  The summary names
+    the kernel sources it was measured on and their digest: if those sources
+    have changed since, the figure is stale and is not reported (None, with
+    the reason)."""
     for f in sorted((ROOT / "profiles").glob("*pmc*.md")):
         for line in f.read_text().splitlines():
             if line.startswith("bench-traffic: "):
                 rec = json.loads(line[len("bench-traffic: "):])
                 if rec.get("workload") == workload and rec.get("precision") == precision:
-                    return rec
-    return None
+                    srcs = rec.get("sources")
+                    if not srcs or source_digest(srcs) != rec.get("sources_sha256"):
+                        return None, f"{f.name}: measured on other kernel sources than this tree's"
+                    return rec, f.name
+    return None, "no counter summary for this workload"
 
 
 def cpu_baseline(workload, precision, threads, warmups, repeats):
@@ -71,77 +91,42 @@ def cpu_baseline(workload, precision, threads, warmups, repeats):
     return json.loads(r.stdout.strip().splitlines()[-1])
 
 
-def main():
-    ap = argparse.ArgumentParser()
-    ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--workload", default="large")
-    ap.add_argument("--precision", default="bf16", choices=["bf16", "fp32"])
-    ap.add_argument("--dataflow", default="auto", choices=["auto", "transform_first", "aggregate_first"],
-                    help="per-layer dataflow; aggregate_first applies where the layer supports it")
-    ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--cpu-threads", type=int, default=0,
-                    help="CPU baseline threads (default: the first socket's physical cores, at most OMP_NUM_THREADS)")
-    ap.add_argument("--cpu-warmups", type=int, default=2)
-    ap.add_argument("--cpu-repeats", type=int, default=7)
-    ap.add_argument("--calibrate-copy", action="store_true",
-                    help="run one 1 GiB device-to-device copy first (counter calibration under rocprofv3 --pmc)")
-    args = ap.parse_args()
-    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print("bench.py measures one GPU: this build has no multi-GPU path (run with --gpus 1).", file=sys.stderr)
-        sys.exit(2)
-
-    cpu = None
-    if not args.no_cpu_baseline:
-        print("# CPU baseline (child process) ...", file=sys.stderr, flush=True)
-        cpu = cpu_baseline(args.workload, args.precision, args.cpu_threads, args.cpu_warmups, args.cpu_repeats)
-
-    import torch
-    import gatgpu
-    from gatgpu import inputs
-
-    w = inputs.WORKLOADS[args.workload]
+def run_forwards(gatgpu, torch, w, precision, flow, steps, warmup, calibrate_copy=False):
+    """Uploads workload w, runs `warmup` untimed forwards (the first one, which
+    allocates the per-layer buffers, timed as the cold forward) and `steps`
+    timed forwards.  Returns the HIP-event times and the cold-start record."""
     t0 = time.perf_counter()
     row, col = w.graph()
     x = w.features()
     model = w.model()
     gen_s = time.perf_counter() - t0
-    n, e = w.n, int(row[-1])
-    prec = gatgpu.BF16 if args.precision == "bf16" else gatgpu.FP32
-    flow = {"auto": gatgpu.AUTO, "transform_first": gatgpu.TRANSFORM_FIRST,
-            "aggregate_first": gatgpu.AGGREGATE_FIRST}[args.dataflow]
-
+    prec = gatgpu.BF16 if precision == "bf16" else gatgpu.FP32
     ctx = gatgpu.Context(0)
     ctx.set_graph(row, col)
     ctx.set_model(model)
     ctx.set_input(x)
     static = ctx.static_times()
-    print(f"# workload {w.name}: N={n} E={e} gen {gen_s:.1f}s", file=sys.stderr, flush=True)
-
-    if args.calibrate_copy:
+    print(f"# workload {w.name} {precision}: N={w.n} E={int(row[-1])} gen {gen_s:.1f}s", file=sys.stderr, flush=True)
+    if calibrate_copy:
         src = torch.ones(1 << 28, dtype=torch.float32, device="cuda")  # 1 GiB
         dst = torch.empty_like(src)
         dst.copy_(src)
         torch.cuda.synchronize()
         del src, dst
-    # The first forward allocates the per-layer device buffers: the cold forward.
     _, _, cold_ms = ctx.model_forward(prec, flow, want_logits=False, timed=True)
-    for _ in range(max(args.warmup - 1, 0)):
+    for _ in range(max(warmup - 1, 0)):
         ctx.model_forward(prec, flow, want_logits=False, timed=False)
     torch.cuda.synchronize()
     ctx.synchronize()
     step_ms, layer_times = [], []
     t0 = time.perf_counter()
-    for _ in range(args.steps):
+    for _ in range(steps):
         _, times, total = ctx.model_forward(prec, flow, want_logits=False, timed=True)
         step_ms.append(total)
         layer_times.append(times)
     ctx.synchronize()
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
-    ms = float(np.mean(step_ms))  # HIP-event model time (first kernel of layer 1 to last of layer 3)
-    value = 3 * e / (ms * 1e-3) / 1e9
     # Cold-start: the static steps (graph checks, uploads, degree schedule,
     # weight preparation, feature permutation), the first forward, and the
     # logits copied back to the host after a forward.
@@ -149,24 +134,39 @@ def main():
     cold = {k: round(v, 3) for k, v in ctx.static_times().items()}
     cold.update({k: round(static[k], 3) for k in static if k != "logits_d2h_ms"})
     cold["first_forward_ms"] = round(cold_ms, 3)
-
-    bf16 = prec == gatgpu.BF16
-    s_z = 2 if bf16 else 4
     # The output layer's projection ran inside layer 2's aggregation (its
     # output rows never stored): layer 2's kernel writes layer 3's Z rows and
     # L/R instead of its own output rows.
     fused23 = not ctx.has_stage(1, "out")
+    ctx.close()
+    ms = float(np.mean(step_ms))  # HIP-event model time (first kernel of layer 1 to last of layer 3)
+    return {"row": row, "model": model, "n": w.n, "e": int(row[-1]), "ms": ms, "wall_s": wall,
+            "layer_times": layer_times, "cold": cold, "fused23": fused23, "bf16": prec == gatgpu.BF16}
+
+
+def layer_records(r):
+    """Per-layer aggregation and projection times with their bytes, FLOP and
+    fractions of the HBM and MFMA peaks."""
+    n, e, model, bf16, fused23 = r["n"], r["e"], r["model"], r["bf16"], r["fused23"]
+    s_z = 2 if bf16 else 4
     layers = []
     for l, p in enumerate(model):
         K, d, D = p["heads"], p["dim"], p["in"]
         W = K * d
-        t = {k: float(np.mean([lt[l][k] for lt in layer_times])) for k in layer_times[0][l]}
+        t = {k: float(np.mean([lt[l][k] for lt in r["layer_times"]])) for k in r["layer_times"][0][l]}
         af = t["lr_ms"] > 0  # aggregate-first layers report the L/R front end as lr_ms
         hidden = l < 2
         s_out = 2 if (bf16 and hidden) else 4
         s_x = 4 if (l == 0 or not bf16) else 2  # layer 1 reads the FP32 features; later layers the bf16 output
+        gather_b = None
         if af:
+            # Algorithmic (B_AF): the bf16 input rows of D features per edge.
             agg_b = 8 * (n + 1) + 4 * e + 4 * K * e + 4 * K * n + e * D * 2 + n * W * s_out
+            # As read: the sum form gathers 256-byte table rows (128 bf16
+            # slots; R in the row tail up to 112 inputs, else from its own
+            # array: 4K bytes more per edge) and keeps L, max and den per node.
+            r_arr = 4 * K * e if D > 112 else 0
+            gather_b = 8 * (n + 1) + 4 * e + 256 * e + r_arr + 12 * K * n + n * W * s_out
         else:
             no_r = bf16 and ((K, d) == (8, 32) or (K, d) == (1, 64))  # R formed from the gathered Z row
             agg_b = agg_bytes(n, e, K, d, s_z, s_out, r_gather=not no_r)
@@ -178,6 +178,10 @@ def main():
                "aggregate_gbs": round(agg_b / (t["aggregate_ms"] * 1e-3) / 1e9, 1),
                "aggregate_frac": round(agg_b / (t["aggregate_ms"] * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
                "total_ms": round(t["total_ms"], 4)}
+        if gather_b is not None:
+            rec.update({"aggregate_bytes_basis": "algorithmic: D bf16 input features per edge",
+                        "gather_table_bytes": int(gather_b),
+                        "gather_table_frac": round(gather_b / (t["aggregate_ms"] * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)})
         if fused23 and l == 1:
             rec["fused"] = "layer-3 projection in the epilogue (32-row tiles on MFMA); layer-2 output rows not stored"
         if af:
@@ -194,10 +198,64 @@ def main():
                         "projection_bytes": int(gb),
                         "projection_hbm_frac": round(gb / (pm * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)})
         layers.append(rec)
+    return layers
+
+
+# The reference's published B0 forwards on this graph size (ogbn-arxiv,
+# 16 Sapphire Rapids cores; baseline/docs/FOUR_PATHS_GITHUB_INDEX.md:7-8).
+REFERENCE_ARXIV_B0_MS = {"bf16": 68.437, "fp32": 73.996}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--workload", default="large")
+    ap.add_argument("--precision", default="bf16", choices=["bf16", "fp32"])
+    ap.add_argument("--dataflow", default="auto", choices=["auto", "transform_first", "aggregate_first"],
+                    help="per-layer dataflow; aggregate_first applies where the layer supports it")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-threads", type=int, default=0,
+                    help="CPU baseline threads (default: the first socket's physical cores, at most OMP_NUM_THREADS)")
+    ap.add_argument("--cpu-warmups", type=int, default=2)
+    ap.add_argument("--cpu-repeats", type=int, default=7)
+    ap.add_argument("--no-arxiv", action="store_true",
+                    help="skip the 2.5M-edge graph's bf16 and FP32 forwards (run only with the default workload)")
+    ap.add_argument("--arxiv-steps", type=int, default=50)
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="run one 1 GiB device-to-device copy first (counter calibration under rocprofv3 --pmc)")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path (run with --gpus 1).", file=sys.stderr)
+        sys.exit(2)
+    with_arxiv = args.workload == "large" and not args.no_arxiv
+
+    # CPU baselines first, each in a child process, before the GPU is touched.
+    cpu, cpu_arxiv = None, {}
+    if not args.no_cpu_baseline:
+        print("# CPU baseline (child process) ...", file=sys.stderr, flush=True)
+        cpu = cpu_baseline(args.workload, args.precision, args.cpu_threads, args.cpu_warmups, args.cpu_repeats)
+        if with_arxiv:
+            for prec in ("bf16", "fp32"):
+                cpu_arxiv[prec] = cpu_baseline("arxiv", prec, args.cpu_threads, args.cpu_warmups, args.cpu_repeats)
+
+    import torch
+    import gatgpu
+    from gatgpu import inputs
+
+    flow = {"auto": gatgpu.AUTO, "transform_first": gatgpu.TRANSFORM_FIRST,
+            "aggregate_first": gatgpu.AGGREGATE_FIRST}[args.dataflow]
+    w = inputs.WORKLOADS[args.workload]
+    r = run_forwards(gatgpu, torch, w, args.precision, flow, args.steps, args.warmup, args.calibrate_copy)
+    n, e, model, bf16 = r["n"], r["e"], r["model"], r["bf16"]
+    ms = r["ms"]
+    value = 3 * e / (ms * 1e-3) / 1e9
+    layers = layer_records(r)
     # Dominant kernel: the layer-2 aggregation (fused prescan/softmax/SpMM/ELU).
     dom = layers[1]
-    pmc = pmc_traffic(w.name, args.precision)
-    gemm = max((r for r in layers if "projection_ms" in r), key=lambda r: r["projection_ms"])
+    pmc, pmc_src = pmc_traffic(w.name, args.precision)
+    gemm = max((x for x in layers if "projection_ms" in x), key=lambda x: x["projection_ms"])
     out = {
         "metric": METRIC,
         "value": round(value, 4),
@@ -212,11 +270,12 @@ def main():
         "dtype": "bf16" if bf16 else "f32",
         "data": "synthetic",
         "config": {"workload": f"{w.name}: 3-layer GAT {w.din}->{w.heads}x{w.dim}->{w.heads}x{w.dim}->1x{w.classes}, "
-                               f"N={n}, E={e} (incl. self-loops), max in-degree {int(np.diff(row).max())}",
-                   "precision": args.precision, "wall_ms_per_step": round(wall / args.steps * 1e3, 4)},
+                               f"N={n}, E={e} (incl. self-loops), max in-degree {int(np.diff(r['row']).max())}",
+                   "precision": args.precision, "wall_ms_per_step": round(r["wall_s"] / args.steps * 1e3, 4)},
         "roofline": {"bound": "hbm", "achieved": dom["aggregate_gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": dom["aggregate_frac"],
                      "traffic": int(pmc["bytes_per_launch"]) if pmc else None,
+                     "traffic_source": pmc_src,
                      "kernel": "layer-2 aggregation", "algorithmic_bytes": dom["aggregate_bytes"],
                      "avg_ms": dom["aggregate_ms"]},
         "roofline_gemm": {"kernel": f"layer-{gemm['layer']} projection", "bound": "hbm",
@@ -227,11 +286,31 @@ def main():
                           "mfma_frac": gemm["projection_mfma_frac"], "hbm_bytes": gemm["projection_bytes"],
                           "hbm_frac": gemm["projection_hbm_frac"]},
         "layers": layers,
-        "cold_start_ms": cold,
+        "cold_start_ms": r["cold"],
     }
-    ctx.close()
     if cpu is not None:
         out["cpu_baseline"] = cpu
+    if with_arxiv:
+        wa = inputs.WORKLOADS["arxiv"]
+        rec = {"workload": f"arxiv: 3-layer GAT {wa.din}->{wa.heads}x{wa.dim}->{wa.heads}x{wa.dim}->1x{wa.classes}, "
+                           f"N={wa.n}, E={wa.edges} (incl. self-loops), max in-degree {wa.max_degree}",
+               "note": "Z (87-173 MB) fits the 256 MB Infinity Cache at this size: the fractions are of the HBM "
+                       "peak but the gathers are served from that cache"}
+        for prec in ("bf16", "fp32"):
+            ra = run_forwards(gatgpu, torch, wa, prec, gatgpu.AUTO, args.arxiv_steps, 5)
+            ea = ra["e"]
+            entry = {"ms_per_forward": round(ra["ms"], 4), "gedge_s": round(3 * ea / (ra["ms"] * 1e-3) / 1e9, 4),
+                     "steps": args.arxiv_steps, "warmup": 5,
+                     "layers": [{k: x[k] for k in ("layer", "dataflow", "aggregate_ms", "aggregate_bytes",
+                                                   "aggregate_frac", "projection_ms", "total_ms") if k in x}
+                                for x in layer_records(ra)],
+                     "reference_published_b0_ms": REFERENCE_ARXIV_B0_MS[prec]}
+            if prec in cpu_arxiv:
+                c = cpu_arxiv[prec]
+                entry["cpu_b0"] = {k: c[k] for k in ("ms_per_forward", "p95_ms", "cores", "kind", "sample")}
+                entry["speedup_vs_cpu_b0"] = round(c["ms_per_forward"] / ra["ms"], 1)
+            rec[prec] = entry
+        out["arxiv"] = rec
     print(json.dumps(out), flush=True)
 
 
