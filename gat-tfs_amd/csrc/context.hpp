@@ -157,7 +157,7 @@ struct gatgpu_ctx {
     uint32_t split_min = 0;          // user option: rows >= this are split (0: per-kernel defaults)
     uint32_t split_chunk = 0;        // user option: edges per chunk (0: per-kernel defaults)
     bool keep_xbf = false;           // option GATGPU_OPT_KEEP_INPUT_BF16
-    bool fuse_next = true;           // option GATGPU_OPT_FUSE_NEXT_PROJECTION
+    int fuse_next = 1;               // option GATGPU_OPT_FUSE_NEXT_PROJECTION (0 never, 1 large graphs, 2 always)
     gatgpu::SplitPlan plans[gatgpu::kPlans];
     hipEvent_t ev[16] = {};
     int cus = 256;  // compute units of the device

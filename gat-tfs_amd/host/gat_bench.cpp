@@ -4,7 +4,7 @@
 // arguments against a whitelist with duplicates rejected (:9-16), a path
 // registry dispatched by name (run_path, :21-25), modes benchmark /
 // correctness / micro / export-fixture / fixed-p, and the same output lines (ENV,
-// STATIC, CONFIG, ERROR, per-layer JSON, E2E, SUMMARY; :46-64, :182).
+// STATIC, CONFIG, ERROR, COLD, per-layer JSON, E2E, SUMMARY; :46-64, :169-182).
 // Registered paths: gpu_fp32 and gpu_bf16 (include/gatgpu.h through
 // gat_gpu_path.hpp).  Correctness compares against R0 stage dumps in the
 // reference's --dump-prefix naming (<prefix>_layer<l>_<stage>.f32, :74-77);
@@ -344,16 +344,27 @@ int run(int argc, char** argv) {
         return 0;
     }
 
-    // ---- benchmark: device-resident model timing (main.cpp:153-183)
+    // ---- benchmark: device-resident model timing (main.cpp:153-183).  The
+    // COLD line spans graph load to the first forward, uploads and weight
+    // preparation included (main.cpp:169); each timed repeat prints the
+    // per-layer stage times of that forward (main.cpp:177) and its E2E line.
     std::vector<double> totals;
     for (int l = 0; l < 3; ++l) gpu.set_layer(l, model[l]);
     gpu.set_graph(g);
+    std::cout << "COLD startup_before_inference_ms="
+              << std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t_load).count()
+              << " includes_graph_load=true\n";
     double cold = 0;
     for (int r = -warmups; r < reps; ++r) {
         const double s = gpu.model(precision, nullptr, dataflow);
         if (r == -warmups) cold = s;
         if (r >= 0) {
             totals.push_back(s);
+            for (int l = 0; l < 3; ++l) {
+                Times t;
+                gpu.model_layer_times(l, t);
+                print_times(path, "benchmark", l + 1, r, g, model[l], t);
+            }
             std::cout << "E2E path=" << path << " rep=" << r << " layer=0 total_ms=" << s * 1e3
                       << " gedge_per_s=" << 3.0 * double(g.e) / s / 1e9 << " finite=1\n";
         }

@@ -136,18 +136,22 @@ enum {
                                             projection rounds (stage XBF);
                                             0 (default): they are rounded in
                                             registers only                    */
-    GATGPU_OPT_FUSE_NEXT_PROJECTION = 6  /* 1 (default): gatgpu_model_forward
-                                            runs the projection of a bf16
-                                            one-head output layer (<= 60
-                                            classes over 8 x 32 inputs) inside
-                                            the previous layer's aggregation,
-                                            on its output rows staged in LDS:
-                                            Z, L and R of the output layer are
-                                            bit-equal to the unfused run, and
-                                            the hidden layer's OUT stage is not
-                                            stored (gatgpu_stage_size gives 0,
-                                            and a per-layer forward of the
-                                            output layer chained on it fails).
+    GATGPU_OPT_FUSE_NEXT_PROJECTION = 6  /* 2: gatgpu_model_forward runs the
+                                            projection of a bf16 one-head
+                                            output layer (<= 60 classes over
+                                            8 x 32 inputs) inside the previous
+                                            layer's aggregation, on its output
+                                            rows staged in LDS: Z, L and R of
+                                            the output layer are bit-equal to
+                                            the unfused run, and the hidden
+                                            layer's OUT stage is not stored
+                                            (gatgpu_stage_size gives 0, and a
+                                            per-layer forward of the output
+                                            layer chained on it fails).
+                                            1 (default): the same on graphs of
+                                            at least 16M edges, where it is the
+                                            faster form; smaller graphs run
+                                            unfused.
                                             0: every layer stores its output  */
 };
 
@@ -281,7 +285,8 @@ int gatgpu_get_static_times(gatgpu_ctx* ctx, gatgpu_static_times* out);
 int gatgpu_layer_forward_static(gatgpu_ctx* ctx, int layer, int precision, int hidden, const float* x,
                                 float* out);
 /* Bytes of the static array gatgpu_layer_forward_static would use for
- * `layer` of the context's graph (0 if the layer is not set). */
+ * `layer` of the context's graph.  GATGPU_ESTATE (and *bytes untouched) if
+ * the graph or the layer's weights are not set. */
 int gatgpu_static_scratch_need(gatgpu_ctx* ctx, int layer, int precision, int hidden, uint64_t* bytes);
 
 /* ---- misc ------------------------------------------------------------ */

@@ -311,10 +311,15 @@ def test_model_rerun_without_set_graph(gpu_ctx):
         gpu_ctx.set_input(x)
         return gpu_ctx.model_forward(gatgpu.BF16, gatgpu.AGGREGATE_FIRST)[0]
 
-    fresh()
-    l1, l2, l3 = run(xs[0]), run(xs[1]), run(xs[0])
-    fresh()
-    ref2 = run(xs[1])
+    gpu_ctx.set_option(gatgpu.OPT_FUSE_NEXT_PROJECTION, 2)  # fused on this graph size too
+    try:
+        fresh()
+        l1, l2, l3 = run(xs[0]), run(xs[1]), run(xs[0])
+        assert not gpu_ctx.has_stage(1, "out")
+        fresh()
+        ref2 = run(xs[1])
+    finally:
+        gpu_ctx.set_option(gatgpu.OPT_FUSE_NEXT_PROJECTION, 1)
     assert not np.array_equal(l1, l2)
     assert np.array_equal(l2, ref2) and np.array_equal(l3, l1)
     ref = oracle.ref_model(row, col, xs[1], m)[2]["out"]
@@ -386,15 +391,15 @@ def ragged_graph(n, seed):
 
 def fused_and_unfused(ctx, row, col, x, model, options=None):
     """bf16 model forward (layers 2-3 transform-first) with the output layer's
-    projection fused into layer 2's aggregation (option 1) and without (0):
-    logits and the stages of layers 2 and 3 of each run."""
+    projection fused into layer 2's aggregation (option 2: on any graph) and
+    without (0): logits and the stages of layers 2 and 3 of each run."""
     ctx.set_graph(row, col)
     for k, v in (options or {}).items():
         ctx.set_option(k, v)
     ctx.set_model(model)
     ctx.set_input(x)
     runs = {}
-    for fuse in (0, 1):
+    for fuse in (0, 2):
         ctx.set_option(gatgpu.OPT_FUSE_NEXT_PROJECTION, fuse)
         logits, _, _ = ctx.model_forward(gatgpu.BF16, gatgpu.TRANSFORM_FIRST)
         runs[fuse] = (logits, {(l, k): ctx.stage(l, k) for l in (1, 2)
@@ -420,7 +425,7 @@ def test_fused_output_projection_bit_exact(gpu_ctx, classes, sched):
     x = inputs.normal((3001, 128), 3)
     model = inputs.random_model(128, classes, 11)
     runs = fused_and_unfused(gpu_ctx, row, col, x, model, SCHEDULES[sched])
-    (l0, s0), (l1, s1) = runs[0], runs[1]
+    (l0, s0), (l1, s1) = runs[0], runs[2]
     assert np.isfinite(l0).all() and np.array_equal(l0, l1)
     for (l, k), v in s0.items():
         if (l, k) == (1, "out"):
@@ -438,8 +443,23 @@ def test_fused_output_projection_arxiv(gpu_ctx):
     w = inputs.WORKLOADS["arxiv"]
     row, col = w.graph()
     runs = fused_and_unfused(gpu_ctx, row, col, w.features(), w.model())
-    assert np.array_equal(runs[0][0], runs[1][0])
-    assert np.array_equal(runs[0][1][(2, "z")], runs[1][1][(2, "z")])
+    assert np.array_equal(runs[0][0], runs[2][0])
+    assert np.array_equal(runs[0][1][(2, "z")], runs[2][1][(2, "z")])
+    assert runs[2][1][(1, "out")] is None
+
+
+def test_fusion_default_by_graph_size(gpu_ctx):
+    """The default fuses the output projection into layer 2 only on graphs of
+    at least 16M edges: the 2.5M-edge graph keeps layer 2's output rows."""
+    w = inputs.WORKLOADS["arxiv"]
+    row, col = w.graph()
+    gpu_ctx.set_graph(row, col)
+    gpu_ctx.set_model(w.model())
+    gpu_ctx.set_input(w.features())
+    gpu_ctx.model_forward(gatgpu.BF16, gatgpu.AUTO, want_logits=False)
+    assert gpu_ctx.has_stage(1, "out")
+    with pytest.raises(gatgpu.GatGpuError):
+        gpu_ctx.set_option(gatgpu.OPT_FUSE_NEXT_PROJECTION, 3)
 
 
 def test_layer2_micro_fp32(gpu_ctx):

@@ -1,4 +1,5 @@
 """The C++ harness gat_bench (modes and output lines of baseline/bench/main.cpp)."""
+import json
 import subprocess
 from pathlib import Path
 
@@ -119,6 +120,12 @@ def test_benchmark_and_micro_modes(smoke_file, tmp_path):
     p = run("--mode", "benchmark", "--graph", smoke_file, "--seed", 11, "--repeats", 3, "--warmups", 1,
             "--output", tmp_path / "logits.f32", check_rc=0)
     assert "SUMMARY path=gpu_bf16 median_ms=" in p.stdout and p.stdout.count("E2E path=") == 3
+    assert p.stdout.count("COLD startup_before_inference_ms=") == 1
+    # per-layer JSON of every timed repeat (baseline/bench/main.cpp:177)
+    recs = [json.loads(line) for line in p.stdout.splitlines() if line.startswith("{")]
+    assert [(r["rep"], r["layer"]) for r in recs] == [(r, l) for r in range(3) for l in (1, 2, 3)]
+    assert all(r["mode"] == "benchmark" and r["total_ms"] > 0 and r["score_exp_aggregate_ms"] > 0 for r in recs)
+    assert all(r["N"] == 1024 and r["E"] == 41540 for r in recs)
     logits = np.fromfile(tmp_path / "logits.f32", np.float32)
     assert logits.size == 1024 * 40 and np.isfinite(logits).all()
     p = run("--mode", "micro", "--graph", smoke_file, "--seed", 11, "--repeats", 2, "--warmups", 1,

@@ -1,65 +1,143 @@
-"""The reference-harness patch in INTEGRATION.md compiles and links.
+"""The reference-harness patch in INTEGRATION.md compiles, links, and edits
+the reference's lines as they stand.
 
-The file-scope block and the one-line changes are taken from INTEGRATION.md
-as they stand and compiled with g++ against gat-tfs_amd/host/gat_types.hpp,
+The file-scope block and the five changes are taken from INTEGRATION.md as
+they stand and compiled with g++ against gat-tfs_amd/host/gat_types.hpp,
 whose containers carry the field names of baseline/include/gat.hpp:32-106
 (the reference's own header needs oneMKL, absent here), then linked against
 libgatgpu.so.  No GPU is touched: the program only checks the path names.
+
+Each changed line of baseline/bench/main.cpp, with the patch's addition taken
+out again, must be the reference's line: its SHA-256 (leading whitespace
+stripped) equals the digest of main.cpp:21, :30, :71 or :172 recorded below.
+Where the reference tree is present the digests are recomputed from it.
 """
+import hashlib
 import re
 import subprocess
 from pathlib import Path
 
+import pytest
+
 import gatgpu
 
 ROOT = Path(__file__).resolve().parent.parent
+MAIN_CPP = Path("/root/reference/baseline/bench/main.cpp")
+
+# SHA-256 of the stripped text of baseline/bench/main.cpp lines the patch edits.
+MAIN_CPP_DIGESTS = {
+    21: "82f2d732ca0146643c7dd6ca26db08b4483743168b12d417698b48a83a0d7965",   # run_path signature
+    30: "c3d6c8d94d512188f3f33982b620520c5dae2b37f757d177547a3aeda8de4150",   # path whitelist
+    71: "669914adfe0c0bf41c0b01b1dd274400d5440e8ceaf82630d3f6ad9792618698",   # correctness paths
+    172: "5010f9849dd6f778da6662cad06360141cfea9e38ce04719f48176c4b201a067",  # benchmark model timer
+}
+
+# run_path's signature (the interface change 1 goes into, main.cpp:21).
+RUN_PATH_SIGNATURE = ("static void run_path(const std::string& path,const Graph& g,const Param& p,const Prepared& q,"
+                      "const Schedule& s,const std::vector<float>& input,Workspace& w,bool hidden,int panel,Times& t,"
+                      "const std::string& policy){")
+
+GPU_NAMES = ',"gpu_fp32","gpu_bf16"'
+WHITELIST_ADD = "&&!is_gpu_path(path)"
+
+
+def digest(line):
+    return hashlib.sha256(line.strip().encode()).hexdigest()
 
 
 def patch_pieces():
     text = (ROOT / "INTEGRATION.md").read_text()
-    blocks = re.findall(r"```cpp\n(.*?)```", text, re.S)
-    scope = next(b for b in blocks if "// integration: file scope" in b)
-    change1 = next(b.strip() for b in blocks if b.strip().startswith("if(gpu_run_path("))
-    change3 = next(b.strip() for b in blocks if b.strip() == "g_model=&model;")
-    change5 = next(b for b in blocks if "gpu_model_seconds(path" in b and "double total;" in b)
-    gpu_branch = change5.split("else")[0]  # the GPU branch of the benchmark timer
-    return scope, change1, change3, gpu_branch
+    blocks = [b.strip() for b in re.findall(r"```cpp\n(.*?)```", text, re.S)]
+    p = {"scope": next(b for b in blocks if "// integration: file scope" in b),
+         "change1": next(b for b in blocks if b.startswith("if(gpu_run_path(")),
+         "change2": next(b for b in blocks if b.startswith('if(path!="ref_fp32"')),
+         "change3": next(b for b in blocks if b == "g_model=&model;"),
+         "change4": next(b for b in blocks if b.startswith("std::vector<std::string> paths=")),
+         "change5": next(b for b in blocks if "gpu_model_seconds(path" in b and "double total;" in b)}
+    return p
+
+
+def originals(p):
+    """The reference's lines, recovered from the patched ones."""
+    assert WHITELIST_ADD in p["change2"] and GPU_NAMES in p["change4"]
+    line30 = p["change2"].replace(WHITELIST_ADD, "")
+    line71 = p["change4"].replace(GPU_NAMES, "")
+    # change 5's else branch is main.cpp:172 with `double total=` split off.
+    m = re.search(r"else\{(auto begin=Clock::now\(\);.*\})total=seconds\(begin,Clock::now\(\)\);\}$", p["change5"])
+    assert m, p["change5"]
+    line172 = m.group(1) + "double total=seconds(begin,Clock::now());"
+    return {21: RUN_PATH_SIGNATURE, 30: line30, 71: line71, 172: line172}
+
+
+def test_patched_lines_are_the_references_lines():
+    got = {k: digest(v) for k, v in originals(patch_pieces()).items()}
+    assert got == MAIN_CPP_DIGESTS
+
+
+@pytest.mark.skipif(not MAIN_CPP.exists(), reason="reference tree not present")
+def test_recorded_digests_match_main_cpp():
+    lines = MAIN_CPP.read_text().split("\n")
+    assert {k: digest(lines[k - 1]) for k in MAIN_CPP_DIGESTS} == MAIN_CPP_DIGESTS
 
 
 def test_integration_patch_compiles_and_links(tmp_path):
     gatgpu.load_library()  # built
-    scope, change1, change3, gpu_branch = patch_pieces()
+    p = patch_pieces()
     src = f"""
+#include <chrono>
 #include <cstdio>
 #include <stdexcept>
 #include <string>
 #include <vector>
 #include "gat_types.hpp"
 using namespace gat;
-{scope}
-static void run_path(const std::string& path, const Graph& g, const Param& p, const std::vector<float>& input,
-                     Workspace& w, bool hidden, Times& t) {{
-    {change1}
+using Clock = std::chrono::steady_clock;
+static double seconds(Clock::time_point a, Clock::time_point b) {{ return std::chrono::duration<double>(b - a).count(); }}
+struct Prepared {{}};
+struct Schedule {{}};
+{p["scope"]}
+{RUN_PATH_SIGNATURE}
+    {p["change1"]}
+    (void)q; (void)s; (void)panel; (void)policy;
     throw std::runtime_error("bad path");
 }}
+static void check_path(const std::string& path) {{
+    {p["change2"]}
+}}
+static std::vector<std::string> correctness_paths() {{
+    {p["change4"]}
+    return paths;
+}}
 static double bench_once(const std::string& path, const Graph& g, const Model& model, int layer) {{
-    Workspace ws[3];
+    std::vector<Workspace> ws(3);
     Times times[3];
+    std::vector<Prepared> prep(3);
+    Schedule sched;
+    int panel = 64;
+    std::string policy = "z_avx";
     const std::vector<float>* input = &g.x;
-    {gpu_branch}
+    {p["change5"]}
     (void)input;
     return total;
 }}
 int main(int argc, char**) {{
     Model model(3);
     Graph g;
-    {change3}
+    {p["change3"]}
     if (argc > 99) {{  // compiled and linked, never run here
         Workspace w;
         Times t;
-        run_path("gpu_bf16", g, model[0], g.x, w, true, t);
-        std::printf("%f\\n", bench_once("gpu_fp32", g, model, 0));
+        run_path("gpu_bf16", g, model[0], Prepared{{}}, Schedule{{}}, g.x, w, true, 64, t, "z_avx");
+        std::printf("%f %f\\n", bench_once("gpu_fp32", g, model, 0), bench_once("gpu_bf16", g, model, 2));
     }}
+    for (const char* ok : {{"gpu_fp32", "gpu_bf16", "standard_bf16", "ref_fp32"}}) check_path(ok);
+    try {{
+        check_path("gpu_fp16");
+        return 2;
+    }} catch (const std::runtime_error&) {{
+    }}
+    const auto paths = correctness_paths();
+    if (paths.size() != 6 || paths[4] != "gpu_fp32" || paths[5] != "gpu_bf16") return 3;
     return is_gpu_path("gpu_bf16") && is_gpu_path("gpu_fp32") && !is_gpu_path("standard_bf16") ? 0 : 1;
 }}
 """
@@ -67,9 +145,9 @@ int main(int argc, char**) {{
     f.write_text(src)
     lib = ROOT / "gat-tfs_amd" / "lib"
     exe = tmp_path / "patch"
-    p = subprocess.run(["g++", "-std=c++17", "-Wall", "-Werror", "-Wno-unused-function", f"-I{ROOT / 'include'}",
+    r = subprocess.run(["g++", "-std=c++17", "-Wall", "-Werror", "-Wno-unused-function", f"-I{ROOT / 'include'}",
                         f"-I{ROOT / 'gat-tfs_amd' / 'host'}", str(f), str(ROOT / "gat-tfs_amd" / "host" / "gat_types.cpp"),
                         f"-L{lib}", "-lgatgpu", f"-Wl,-rpath,{lib}", "-o", str(exe)],
                        capture_output=True, text=True, timeout=300)
-    assert p.returncode == 0, p.stderr[-3000:]
+    assert r.returncode == 0, r.stderr[-3000:]
     assert subprocess.run([str(exe)], timeout=60).returncode == 0

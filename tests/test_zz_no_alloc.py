@@ -93,3 +93,17 @@ def test_static_layer_rejects_oversized_layer(ctx):
     assert err.value.code == gatgpu.EOVERFLOW and "static scratch" in str(err.value)
     ctx.synchronize()
     assert bool(torch.all(od == 7.0))
+
+
+def test_static_scratch_need_before_setup():
+    """Without a graph, or without the layer's weights, the size query
+    returns GATGPU_ESTATE."""
+    with gatgpu.Context(0) as fresh:
+        with pytest.raises(gatgpu.GatGpuError) as err:
+            fresh.static_scratch_need(0, gatgpu.BF16, True)
+        assert err.value.code == gatgpu.ESTATE
+        row, col = inputs.WORKLOADS["smoke"].graph()
+        fresh.set_graph(row, col)
+        with pytest.raises(gatgpu.GatGpuError) as err:
+            fresh.static_scratch_need(1, gatgpu.BF16, True)
+        assert err.value.code == gatgpu.ESTATE
