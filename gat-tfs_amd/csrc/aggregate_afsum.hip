@@ -83,7 +83,8 @@ constexpr int kSBytes = 8 * kMaxKS * 2 * kBlk + kHalfOff;
 constexpr int kTRowBytes = 2 * 2 * kTile * 4;             // the tile's node ids (up to 2 x 32)
 constexpr int kTDenBytes = 2 * 8 * (2 * kTile + 1) * 4;   // their denominators (2 x 8 heads x 33)
 constexpr int kTQBytes = 4 * 4;                                // ring of the block's next tile indices
-constexpr int kLdsBytes = kSBytes + kTRowBytes + kTDenBytes + kTQBytes;  // S, node ids, denominators, tiles
+constexpr int kTMdBytes = 2 * 8 * 2 * kTile * 4;               // the tile rows' max and den stages (up to 32 rows)
+constexpr int kLdsBytes = kSBytes + kTRowBytes + kTDenBytes + kTQBytes + kTMdBytes;  // S, ids, dens, tiles, stages
 constexpr uint32_t kNoRow = 0xffffffffu;
 constexpr int kPart = 8 * 128 + 24;        // floats per chunk partial: U_h rows of 128, den, m, mx
 constexpr int kDenOff = 8 * 128;           // den_h against the chunk's reference max m_h
@@ -583,6 +584,10 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4
     // clears the counters for the next launch.
     const uint32_t tb = blockIdx.x - chunk_blocks, G = a.tile_blocks;
     uint32_t* const tq = reinterpret_cast<uint32_t*>(slds + kSBytes + kTRowBytes + kTDenBytes);
+    // The tile rows' max (8 per row) and den stages, written out as whole
+    // lines after the tile's barrier.
+    float* const smd = reinterpret_cast<float*>(slds + kSBytes + kTRowBytes + kTDenBytes + kTQBytes);
+    static_assert(2 * 8 * TR * 4 <= kTMdBytes, "stage rows fit");
     uint32_t* const tctr = a.counter + a.chunks;  // [0] tiles taken past 3G, [1] tile blocks done
     const uint64_t tiles = (a.rows + TR - 1) / TR;
     if (threadIdx.x == 0) tq[2] = tb + 2 * G;
@@ -682,8 +687,8 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4
             if (head && g == 0) {
                 // empty row: max 0, denominator 0 (ref_fp32.cpp:11); else the
                 // denominator against the row max, sum e^(s - M) = den e^(m - M)
-                a.mx[uint64_t(i) * 8 + n] = end > beg ? s.mx : 0.0f;
-                a.den[uint64_t(i) * 8 + n] = end > beg ? den * exp_w(s.m - s.mx) : 0.0f;
+                smd[r * 8 + n] = end > beg ? s.mx : 0.0f;
+                smd[(TR + r) * 8 + n] = end > beg ? den * exp_w(s.m - s.mx) : 0.0f;
                 tden[n * (TR + 1) + r] = den;  // against the reference max, as U
             }
             {
@@ -743,6 +748,21 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4
         load_w(0);
         if (threadIdx.x == 0) tq[(j + 3) & 3] = taken;
         __syncthreads();
+        if (w == kWaves - 1) {
+            // The tile's max and den stages: tile row r is sorted position
+            // rows - 1 - (tile TR + r), so lane l takes row TR - 1 - l / 2 and
+            // the lanes store consecutive 16-byte pieces (whole lines) where
+            // each head lane used to store 4 bytes per row.
+            const int r = TR - 1 - l / 2, q = 4 * (l % 2);
+            if (r >= 0) {
+                const uint32_t i = trow[r];
+                if (i != kNoRow) {
+                    *reinterpret_cast<float4*>(a.mx + uint64_t(i) * 8 + q) = *reinterpret_cast<const float4*>(smd + r * 8 + q);
+                    *reinterpret_cast<float4*>(a.den + uint64_t(i) * 8 + q) =
+                        *reinterpret_cast<const float4*>(smd + (TR + r) * 8 + q);
+                }
+            }
+        }
         // 1 / den of the lane's output row (tile row l % 32) and head w; an
         // empty row has U = 0 and den = 0, and gives 0.
         float inv;

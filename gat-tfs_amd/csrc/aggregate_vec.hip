@@ -296,7 +296,7 @@ struct Flag {
 
 // Edges [beg, end) of a row or chunk, then the edge slots merged.  EXACT: m
 // holds a chunk's exact (finite) row max already.  O32: see batch.
-template <class C, class ZT, bool RZ, bool O32 = false, bool EXACT = false>
+template <class C, class ZT, bool RZ, bool O32 = false, bool EXACT = false, bool MERGE = true>
 __device__ inline void aggregate(uint64_t beg, uint64_t end, const uint32_t* __restrict__ pcol,
                                  const float* __restrict__ R, const ZT* __restrict__ Z, int slot, int sub,
                                  Lane<C>& st) {
@@ -319,7 +319,7 @@ __device__ inline void aggregate(uint64_t beg, uint64_t end, const uint32_t* __r
     // least EPI edges) or from a finite max (chunks).
     if (RZ && (EXACT || total >= uint32_t(C::EPI))) edges(Flag<RZ>{});
     else edges(Flag<false>{});
-    merge_slots<C>(st);
+    if constexpr (MERGE) merge_slots<C>(st);
 }
 
 // Normalise, ELU and store one output row from the slot-0 lanes; the first
@@ -560,34 +560,63 @@ constexpr int kURz = 4;
 // v_mfma_f32_32x32x16_bf16 exactly as k_proj_fast does it (Z^T = W^T H^T,
 // the same fragments, k steps in the same order into zeroed accumulators), so
 // Z, L and R of the next layer carry the bits of the unfused projection.
-// Wave 0 forms Z columns 0..31; wave 1 columns 32..63 (HB = 2) and the L/R
-// block, so each 128-byte Z row is written by two waves together, and L / R
-// of the tile as whole lines.  Split rows store their output rows as usual;
-// the caller projects them afterwards.
+// Wave 0 forms Z columns 0..31, wave 1 columns 32..63 (HB = 2), wave HB the
+// L/R block, so each 128-byte Z row is written by two waves together, and L
+// / R of the tile as whole lines.  The rows' max and den go to LDS too, and
+// the wave left idle by the projection writes the tile's 32 x 8 of each as
+// whole lines: written per row they were 32-byte pieces, and those partial
+// lines, mixed into the gather's reads, cost 0.09 ms more per launch on the
+// 64.3M-edge graph.  The row epilogue (normalise, ELU, bf16) is split
+// between the two edge slots, 4 features each.  Split rows store their
+// output rows as usual; the caller projects them afterwards.
 constexpr int kNextTile = 32;
 constexpr int kNextRowBytes = 512 + 16;  // padded: the 32 lanes of a B read hit distinct bank groups
 
+// The two edge slots' states merged, the features split between them: on
+// exit m and den are the row's in every lane, and lane (slot, sub) holds in
+// tot the totals of features 4 slot .. 4 slot + 3 of vector sub.  One
+// v_permlane32_swap per feature pair (x of the lower half with x + 4 of the
+// upper) and one add, lower half's value first as in merge_step.
 template <class C>
-__device__ inline void finish_row_tile(uint32_t i, const Lane<C>& st, int slot, int sub, float* mx, float* dn,
-                                       unsigned char* trow) {
+__device__ inline void merge_slots_split(Lane<C>& st, float (&tot)[4]) {
+    static_assert(C::EPI == 2 && C::VPL == 1 && C::VEC == 8, "two edge slots of 8 features");
+    const float M = pair_max<32>(st.m[0]);
+    const float f = st.m[0] == M ? 1.0f : exp_w(st.m[0] - M);
+    st.m[0] = M;
+    st.den[0] = pair_add<32>(st.den[0] * f);
+#pragma unroll
+    for (int x = 0; x < 4; ++x) {
+        const auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(st.acc[x] * f), __float_as_uint(st.acc[x + 4] * f),
+                                                        false, false);
+        tot[x] = __uint_as_float(p[0]) + __uint_as_float(p[1]);
+    }
+}
+
+template <class C>
+__device__ inline void finish_row_tile(const Lane<C>& st, const float (&tot)[4], int slot, int sub,
+                                       float* smd, unsigned char* trow) {
     static_assert(C::VEC == 8 && C::VPL == 1 && C::W == 256, "bf16 8 x 32 rows");
-    if (slot != 0) return;
-    if ((sub * C::VEC) % C::DIM == 0) {
-        mx[uint64_t(i) * C::K + st.h[0]] = st.m[0];
-        dn[uint64_t(i) * C::K + st.h[0]] = st.den[0];
+    if (slot == 0 && (sub * C::VEC) % C::DIM == 0) {
+        smd[st.h[0]] = st.m[0];
+        smd[kNextTile * C::K + st.h[0]] = st.den[0];
     }
     const float scale = st.den[0] > 0.0f ? 1.0f / st.den[0] : 0.0f;
-    uint32_t wv[4];
-#pragma unroll
-    for (int x = 0; x < 4; ++x) wv[x] = bf16x2(elu_bf16(st.acc[2 * x] * scale), elu_bf16(st.acc[2 * x + 1] * scale));
-    *reinterpret_cast<uint4*>(trow + 16 * sub) = make_uint4(wv[0], wv[1], wv[2], wv[3]);
+    const uint32_t w0 = bf16x2(elu_bf16(tot[0] * scale), elu_bf16(tot[1] * scale));
+    const uint32_t w1 = bf16x2(elu_bf16(tot[2] * scale), elu_bf16(tot[3] * scale));
+    *reinterpret_cast<uint2*>(trow + 16 * sub + 8 * slot) = make_uint2(w0, w1);
 }
 
 template <class C, int HB, bool O32>
 __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(8)))
 k_agg_vec_next(VArgs<uint16_t> a, NextProj f, uint64_t chunk_blocks) {
     static_assert(HB == 1 || HB == 2, "one head of at most 64 columns");
-    __shared__ __attribute__((aligned(16))) unsigned char tile[kNextTile * kNextRowBytes + kNextTile * 4];
+    // Rows of H (bf16), then R of the next layer per row, the rows' max and
+    // den (written out by the idle wave as whole lines), and which rows ran.
+    constexpr int kMdOff = kNextTile * kNextRowBytes + kNextTile * 4;
+    constexpr int kOkOff = kMdOff + 2 * kNextTile * C::K * 4;
+    __shared__ __attribute__((aligned(16))) unsigned char tile[kOkOff + kNextTile];
+    float* const smd = reinterpret_cast<float*>(tile + kMdOff);
+    unsigned char* const tok = tile + kOkOff;
     const int w = __builtin_amdgcn_readfirstlane(int(threadIdx.x) / kWave);
     const int lane = threadIdx.x % kWave;
     const int slot = lane / C::LPR, sub = lane % C::LPR;
@@ -610,13 +639,16 @@ k_agg_vec_next(VArgs<uint16_t> a, NextProj f, uint64_t chunk_blocks) {
                 init_lane<C, uint16_t, true>(a, sub, st);
                 st.L[0] = a.L[k * C::K + st.h[0]];
                 st.m[0] = -INFINITY;
-                aggregate<C, uint16_t, true, O32>(beg, end, a.pcol, a.R, a.Z, slot, sub, st);
+                aggregate<C, uint16_t, true, O32, false, false>(beg, end, a.pcol, a.R, a.Z, slot, sub, st);
+                float tot[4];
+                merge_slots_split<C>(st, tot);
                 if (end == beg) st.m[0] = 0.0f;  // empty row: max 0, den 0, output 0
-                finish_row_tile<C>(uint32_t(k), st, slot, sub, a.mx, a.den, trow);
+                finish_row_tile<C>(st, tot, slot, sub, smd + r * C::K, trow);
                 stored = true;
             }
         }
-        if (!stored && slot == 0) *reinterpret_cast<uint4*>(trow + 16 * sub) = make_uint4(0, 0, 0, 0);
+        if (lane == 0) tok[r] = stored;
+        if (!stored) *reinterpret_cast<uint2*>(trow + 16 * sub + 8 * slot) = make_uint2(0, 0);
     }
     __syncthreads();
     // ---- the tile's Z^T = W^T H^T: lane (half, col) supplies H[col][16 ks + 8 half .. + 7].
@@ -630,6 +662,17 @@ k_agg_vec_next(VArgs<uint16_t> a, NextProj f, uint64_t chunk_blocks) {
     const bool ok = col < cnt;
     float* const rsh = reinterpret_cast<float*>(tile + kNextTile * kNextRowBytes);
     uint32_t zp[8] = {};
+    if (w == kWavesPerBlock - 1) {
+        // The tile's max and den (sorted rows p0 .. p0 + 31, 8 heads): 1 KB
+        // each, lane l rows l / 2, whole lines instead of 32-byte pieces.
+        static_assert(HB + 1 < kWavesPerBlock && C::K == 8 && kNextTile * C::K == 4 * kWave, "layout");
+        const int r = lane / 2;
+        if (r < cnt && tok[r]) {
+            const float4* s = reinterpret_cast<const float4*>(smd);
+            reinterpret_cast<float4*>(a.mx + p0 * C::K)[lane] = s[lane];
+            reinterpret_cast<float4*>(a.den + p0 * C::K)[lane] = s[kWave + lane];
+        }
+    }
     if (w <= HB) {
         const unsigned char* bsrc = tile + col * kNextRowBytes + 16 * half;
         const uint4* wsrc = f.wpk + size_t(w) * kWave + lane;
