@@ -52,6 +52,7 @@ struct K1Args {
     uint32_t* counter;
     const uint32_t* operm;  // output row of sorted position k: operm[k] (null: the node index)
     const float* ar;        // aR [W] when R is recomputed from the gathered rows
+    int os;                 // out32 row stride: W, or G * VEC with operm (whole padded rows)
 };
 
 __device__ inline void unpack(const uint4& v, float (&f)[8]) {
@@ -200,16 +201,34 @@ __device__ inline void group_online(uint64_t beg, uint64_t end, const uint32_t* 
 }
 
 template <class C>
-__device__ inline void store_row(uint32_t i, int W, int sub, const float (&acc)[C::VEC], float d, bool hidden,
+__device__ inline void store_row(uint32_t i, int W, int os, int sub, const float (&acc)[C::VEC], float d, bool hidden,
                                  float* out32, uint16_t* outbf) {
     const float scale = d > 0.0f ? 1.0f / d : 0.0f;
+    if (out32 && os == C::G * C::VEC) {
+        // Padded FP32 rows (the logits in original node order): each lane
+        // stores its 16-byte pieces whole, zeros past W, so the scattered
+        // rows are written as whole lines.
+        static_assert(C::VEC % 4 == 0, "16-byte pieces");
+#pragma unroll
+        for (int x = 0; x < C::VEC; x += 4) {
+            float y[4];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int f = sub * C::VEC + x + q;
+                y[q] = f < W ? acc[x + q] * scale : 0.0f;
+                if (hidden) y[q] = elu(y[q]);
+            }
+            *reinterpret_cast<float4*>(out32 + uint64_t(i) * os + sub * C::VEC + x) = make_float4(y[0], y[1], y[2], y[3]);
+        }
+        if (!outbf) return;
+    }
 #pragma unroll
     for (int x = 0; x < C::VEC; ++x) {
         const int f = sub * C::VEC + x;
         if (f >= W) continue;
         float y = acc[x] * scale;
         if (hidden) y = elu(y);
-        if (out32) out32[uint64_t(i) * W + f] = y;
+        if (out32 && os != C::G * C::VEC) out32[uint64_t(i) * W + f] = y;
         if (outbf) outbf[uint64_t(i) * W + f] = bf16_hw(y);
     }
 }
@@ -276,7 +295,7 @@ __global__ void __launch_bounds__(kThreads) k_agg_k1(K1Args<ZT> a) {
             a.den[i] = dtot;
             a.counter[first] = 0;
         }
-        if (g == 0) store_row<C>(a.operm ? a.operm[k] : i, a.W, sub, tot, dtot, a.hidden, a.out32, a.outbf);
+        if (g == 0) store_row<C>(a.operm ? a.operm[k] : i, a.W, a.os, sub, tot, dtot, a.hidden, a.out32, a.outbf);
         return;
     }
     // ---------------- 64/G whole rows per wave, heaviest first
@@ -305,7 +324,7 @@ __global__ void __launch_bounds__(kThreads) k_agg_k1(K1Args<ZT> a) {
         a.mx[i] = Mi;
         a.den[i] = dloc;
     }
-    store_row<C>(a.operm ? a.operm[k] : i, a.W, sub, acc, dloc, a.hidden, a.out32, a.outbf);
+    store_row<C>(a.operm ? a.operm[k] : i, a.W, a.os, sub, acc, dloc, a.hidden, a.out32, a.outbf);
 }
 
 template <int G, class ZT>
@@ -318,7 +337,9 @@ hipError_t run(const AggArgs& g, const RowBins& bins, const SplitTable& t, hipSt
     const int rs = g.r_in_feat ? int(g.fstride * sizeof(ZT) / 4) : 1;
     K1Args<ZT> a{g.prow, g.pcol, g.perm, g.left, rptr, static_cast<const ZT*>(g.feat), g.heads * g.dim,
                  g.fstride, rs, g.hidden, g.mx, g.den, g.out32, g.outbf, g.n, g.e, bins.split_begin, t.chunks,
-                 t.chunk_k, t.chunk_first, t.chunk_edges, t.mchunk, t.part, t.counter, g.out_perm, g.ar};
+                 t.chunk_k, t.chunk_first, t.chunk_edges, t.mchunk, t.part, t.counter, g.out_perm, g.ar,
+                 g.out_perm && g.ostride ? g.ostride : g.heads * g.dim};
+    if (a.os != a.W && (!a.operm || a.os != C::G * C::VEC)) return hipErrorInvalidValue;
     if (t.chunks) {
         hipError_t e = launch_split_prescan(g.prow, g.pcol, g.right, 1, t, g.e, s);
         if (e != hipSuccess) return e;
@@ -344,6 +365,11 @@ hipError_t run(const AggArgs& g, const RowBins& bins, const SplitTable& t, hipSt
 }
 
 }  // namespace
+
+int k1_out_stride(bool feat_bf16, int W) {
+    if (feat_bf16) return K1<uint16_t, 8>::MAXW;
+    return W <= 32 ? K1<float, 8>::MAXW : K1<float, 16>::MAXW;
+}
 
 bool aggregate_k1_supported(const AggArgs& g) {
     const int W = g.dim;

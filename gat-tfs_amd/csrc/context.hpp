@@ -47,6 +47,7 @@ struct LayerState {
     // What the last forward of this layer produced.
     bool ran = false, z_valid = false, out32_valid = false, outbf_valid = false;
     bool out_original = false;  // out32 rows in original node order (else sorted order)
+    int out_stride = 0;         // out32 row stride (floats): the width, or k1_out_stride when out_original
     bool xbf_valid = false;     // inbf holds the rounded layer input rows
     int xbf_stride = 0;         // their row stride (bf16 elements)
     int precision = -1;
@@ -118,6 +119,7 @@ struct TfBufs {
     bool fused_convert_ok = false;   // the FP32 input carries kF32Pad floats past its last row
     bool keep_xbf = false;           // write the rounded input rows to xbf even when the convert is fused
     const uint32_t* out_perm = nullptr;  // one-head kernel: output row of sorted position k
+    int ostride = 0;                     // its out32 row stride (floats)
     // The next layer's projection in this layer's aggregation epilogue
     // (launch_aggregate_vec_next); the next layer then runs with projected.
     const NextProj* next = nullptr;

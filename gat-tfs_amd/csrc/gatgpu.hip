@@ -219,6 +219,21 @@ float ms_between(hipEvent_t a, hipEvent_t b) {
     return ms;
 }
 
+// Rows of `width` floats at `stride` on the device to the dense host array
+// [n][width]: one copy, or, for padded rows (the one-head kernel's logits),
+// packed on the device first (identity gather into the logits buffer).
+int download_rows_dense(gatgpu_ctx* c, float* host, const void* src, uint64_t stride, uint32_t width) {
+    if (stride != width) {
+        HIPCHECK(c, c->logits.ensure(c->n * uint64_t(width) * 4));
+        HIPCHECK(c, launch_gather_rows(src, stride, c->logits.p, width, c->ident.as<uint32_t>(), c->n, c->n, width,
+                                       c->stream));
+        src = c->logits.p;
+    }
+    HIPCHECK(c, hipMemcpyAsync(host, src, c->n * uint64_t(width) * 4, hipMemcpyDeviceToHost, c->stream));
+    HIPCHECK(c, hipStreamSynchronize(c->stream));
+    return GATGPU_OK;
+}
+
 // Aggregate-first bf16 layer: convert the input to bf16 rows of 128, the
 // L/R-only MFMA front end (reordered contraction), then the aggregate-first
 // kernels (tiles of 32 rows + split-row chunks).
@@ -360,6 +375,7 @@ int run_layer_af(gatgpu_ctx* c, int l, bool hidden, const float* src32, const ui
     }
     if (ev_base >= 0) HIPCHECK(c, hipEventRecord(c->ev[ev_base + 3], c->stream));
     Ls.out_original = false;
+    Ls.out_stride = W;
     Ls.xbf_valid = rounds_input;
     Ls.xbf_stride = xs;
     Ls.ran = true;
@@ -476,8 +492,11 @@ int run_layer(gatgpu_ctx* c, int l, int precision, int dataflow, bool hidden, co
     HIPCHECK(c, Ls.den.ensure(n * K * 4));
     const bool bf16 = precision == GATGPU_BF16;
     const bool want_outbf = bf16 && hidden && !fixed;
+    // FP32 rows written to original node order by the one-head kernel take
+    // the kernel's padded stride: whole lines per scattered row.
+    const int ostride = orig_out && !want_outbf && !fixed && K == 1 && W <= 64 ? k1_out_stride(bf16, W) : W;
     if (want_outbf) HIPCHECK(c, Ls.outbf.ensure(n * W * 2));
-    else HIPCHECK(c, Ls.out32.ensure((n * W + kF32Pad) * 4));
+    else HIPCHECK(c, Ls.out32.ensure((n * uint64_t(ostride > W ? ostride : W) + kF32Pad) * 4));
     // bf16 path: X as [n][xs] bf16 (xs = ksteps*16, zero-padded), Z as [n][zs]
     // bf16 (zs = W rounded up to 8 for aligned vector stores).
     const int xs = Ls.ksteps * 16;
@@ -508,7 +527,10 @@ int run_layer(gatgpu_ctx* c, int l, int precision, int dataflow, bool hidden, co
     b.fused_convert_ok = true;  // the context's FP32 buffers carry kF32Pad floats of padding
     b.keep_xbf = c->keep_xbf;
     // Layer 3's one-head kernel writes its FP32 rows straight to original rows.
-    if (orig_out && b.out32 && !fixed) b.out_perm = c->perm;
+    if (orig_out && b.out32 && !fixed) {
+        b.out_perm = c->perm;
+        b.ostride = ostride;
+    }
     NextProj nx;
     if (fuse == kFuseNext) {
         LayerState& N = c->L[l + 1];
@@ -534,6 +556,7 @@ int run_layer(gatgpu_ctx* c, int l, int precision, int dataflow, bool hidden, co
     Ls.out32_valid = !want_outbf;
     Ls.outbf_valid = want_outbf && fuse != kFuseNext;
     Ls.out_original = done.out_perm_used;
+    Ls.out_stride = done.out_perm_used ? ostride : W;
     Ls.xbf_valid = bf16 && src32 && (!done.fused_convert || c->keep_xbf);
     Ls.xbf_stride = xs;
     return GATGPU_OK;
@@ -651,7 +674,10 @@ int run_tf(gatgpu_ctx* c, int l, int precision, bool hidden, const float* src32,
     a.r_from_z = pa.r_from_z;
     a.ar = Ls.ar.as<float>();
     const bool one_head = !fixed && !aggregate_vec_supported(a) && aggregate_k1_supported(a);
-    if (one_head && a.out32) a.out_perm = b.out_perm;
+    if (one_head && a.out32) {
+        a.out_perm = b.out_perm;
+        a.ostride = b.ostride;
+    }
     if (done) done->out_perm_used = a.out_perm != nullptr;
     // The one-head kernel takes its own split plan; the 8-head, generic and
     // fixed-p kernels the 8-head one.
@@ -1074,7 +1100,8 @@ int gatgpu_model_forward(gatgpu_ctx* c, int precision, int dataflow, float* logi
     if (total_ms) *total_ms = ms_between(c->ev[0], c->ev[12]);
     if (logits) {
         const auto t0 = Clock::now();
-        HIPCHECK(c, hipMemcpy(logits, logits_dev, c->n * C * 4, hipMemcpyDeviceToHost));
+        if (int r = download_rows_dense(c, logits, logits_dev, L2.out_original ? uint64_t(L2.out_stride) : C, C))
+            return r;
         c->st.logits_d2h_ms = ms_wall(t0, Clock::now());
     }
     return GATGPU_OK;
@@ -1149,7 +1176,7 @@ int gatgpu_get_stage(gatgpu_ctx* c, int layer, int which, float* host) {
                             : which == GATGPU_STAGE_XBF ? uint64_t(L.xbf_stride)
                                                         : uint64_t(width);
     if (which == GATGPU_STAGE_OUT && !bf && L.out_original) {
-        HIPCHECK(c, hipMemcpy(host, src, count * 4, hipMemcpyDeviceToHost));
+        if (int r = download_rows_dense(c, host, src, uint64_t(L.out_stride), uint32_t(W))) return r;
     } else if (bf) {
         std::vector<uint16_t> rows;
         if (int r = download_rows_original(c, src, stride, width, rows)) return r;

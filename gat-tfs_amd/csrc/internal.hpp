@@ -265,6 +265,9 @@ struct AggArgs {
     // Output row of sorted position k (one-head kernel only): out_perm[k]
     // instead of the node index perm[k].  Null: the node index.
     const uint32_t* out_perm = nullptr;
+    // Row stride of out32 (floats) where out_perm is set: k1_out_stride, so
+    // that every scattered row is whole 128-byte lines.  0: W.
+    int ostride = 0;
 };
 // The permuted column array carries kPcolPad zero entries past its e
 // edges, so that kernels may load a whole batch of wave-uniform source ids
@@ -296,6 +299,10 @@ hipError_t launch_aggregate_fixed(const AggArgs& a, const float* p_sorted, const
                                   const RowBins& bins, const SplitTable& split, hipStream_t s);
 // aggregate_k1.hip: one head, rows of at most 64 features.
 bool aggregate_k1_supported(const AggArgs& a);
+// Row stride (floats) of the one-head kernel's FP32 rows written to original
+// node order: the kernel's widest row (G lanes x 16 bytes, 128 or 256 bytes),
+// padded with zeros past the W classes.
+int k1_out_stride(bool feat_bf16, int W);
 hipError_t launch_aggregate_k1(const AggArgs& a, const RowBins& bins, const SplitTable& split,
                                hipStream_t s);
 // aggregate_af.hip: aggregate-first bf16 layer (input rows <= 128, 32 features per head).
