@@ -144,6 +144,29 @@ def run_forwards(gatgpu, torch, w, precision, flow, steps, warmup, calibrate_cop
             "layer_times": layer_times, "cold": cold, "fused23": fused23, "bf16": prec == gatgpu.BF16}
 
 
+def device_copy_gbs(torch, nbytes, reps=5):
+    """Rate of a device-to-device copy of nbytes (the runtime's blit kernel,
+    as torch's copy_ issues it): 2 nbytes moved per copy, median of reps,
+    timed with events on torch's stream.  The streaming reference for the
+    projections, which read one table and write another."""
+    n = nbytes // 4
+    src = torch.ones(n, dtype=torch.float32, device="cuda")
+    dst = torch.empty_like(src)
+    dst.copy_(src)
+    ts = []
+    for _ in range(reps):
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        dst.copy_(src)
+        b.record()
+        b.synchronize()
+        ts.append(a.elapsed_time(b))
+    del src, dst
+    torch.cuda.empty_cache()
+    ms = float(np.median(ts))
+    return {"bytes_per_copy": 2 * 4 * n, "ms": round(ms, 4), "gbs": round(2 * 4 * n / (ms * 1e-3) / 1e9, 1)}
+
+
 def layer_records(r):
     """Per-layer aggregation and projection times with their bytes, FLOP and
     fractions of the HBM and MFMA peaks."""
@@ -256,6 +279,9 @@ def main():
     dom = layers[1]
     pmc, pmc_src = pmc_traffic(w.name, args.precision)
     gemm = max((x for x in layers if "projection_ms" in x), key=lambda x: x["projection_ms"])
+    # A device copy of the projection's input table size: the rate a stream of
+    # reads and writes of that size reaches on this part.
+    copy = device_copy_gbs(torch, int(n * model[gemm["layer"] - 1]["in"] * (2 if bf16 else 4)))
     out = {
         "metric": METRIC,
         "value": round(value, 4),
@@ -284,7 +310,8 @@ def main():
                           "avg_ms": gemm["projection_ms"], "achieved_tflops": gemm["projection_tflops"],
                           "peak_tflops": MFMA_BF16_PEAK_TFLOPS if bf16 else MFMA_FP32_PEAK_TFLOPS,
                           "mfma_frac": gemm["projection_mfma_frac"], "hbm_bytes": gemm["projection_bytes"],
-                          "hbm_frac": gemm["projection_hbm_frac"]},
+                          "hbm_frac": gemm["projection_hbm_frac"], "device_copy": copy,
+                          "copy_frac": round(gemm["projection_bytes"] / (gemm["projection_ms"] * 1e-3) / 1e9 / copy["gbs"], 4)},
         "layers": layers,
         "cold_start_ms": r["cold"],
     }
