@@ -374,6 +374,38 @@ def test_workload_model_parity(gpu_ctx, name, precision):
         assert e["finite"] and e["relative_l2"] < BF16_REL_L2, e
 
 
+@pytest.mark.parametrize("classes", [20, 32, 47, 64])
+@pytest.mark.parametrize("precision", [gatgpu.FP32, gatgpu.BF16])
+def test_model_logits_rows_in_original_order(gpu_ctx, classes, precision):
+    """The last layer writes its FP32 rows straight to original node order
+    with the one-head kernel's padded stride (32 or 64 floats, zeros past the
+    classes); the logits copied back, the OUT stage of layer 3 and a per-layer
+    forward chained on the model's own layer-2 output agree bit for bit, and
+    the logits match R0 (FP32 max-abs 1e-4, bf16 rel-L2 1e-2).  A ragged
+    graph (empty rows, split rows), 128 -> 8 x 32 -> 8 x 32 -> 1 x classes."""
+    row, col = ragged_graph(3001, 40 + classes)
+    x = inputs.normal((3001, 128), 7)
+    model = inputs.random_model(128, classes, 13)
+    gpu_ctx.set_graph(row, col)
+    gpu_ctx.set_model(model)
+    gpu_ctx.set_input(x)
+    gpu_ctx.set_option(gatgpu.OPT_FUSE_NEXT_PROJECTION, 0)  # keep layer 2's output for the chained check
+    try:
+        logits, _, _ = gpu_ctx.model_forward(precision, gatgpu.TRANSFORM_FIRST)
+        out = gpu_ctx.stage(2, "out")
+        assert logits.shape == (3001, classes) and np.array_equal(logits, out)
+        gpu_ctx.layer_forward(2, precision, gatgpu.TRANSFORM_FIRST, False)
+        assert np.array_equal(gpu_ctx.stage(2, "out"), logits)
+    finally:
+        gpu_ctx.set_option(gatgpu.OPT_FUSE_NEXT_PROJECTION, 1)
+    ref = oracle.ref_model(row, col, x, model)[2]["out"]
+    e = oracle.errors(ref, logits)
+    if precision == gatgpu.FP32:
+        assert e["finite"] and e["max_abs"] < FP32_MAX_ABS, e
+    else:
+        assert e["finite"] and e["relative_l2"] < BF16_REL_L2, e
+
+
 # ---------------------------------------------------------------- output projection fused into layer 2
 def ragged_graph(n, seed):
     """CSR with empty rows, rows of one to a few hundred edges and two rows
