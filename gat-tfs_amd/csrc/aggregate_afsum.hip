@@ -588,6 +588,7 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4
     // lines after the tile's barrier.
     float* const smd = reinterpret_cast<float*>(slds + kSBytes + kTRowBytes + kTDenBytes + kTQBytes);
     static_assert(2 * 8 * TR * 4 <= kTMdBytes, "stage rows fit");
+    static_assert(!DB, "the stage rows are single-buffered: the next tile writes them after the closing barrier");
     uint32_t* const tctr = a.counter + a.chunks;  // [0] tiles taken past 3G, [1] tile blocks done
     const uint64_t tiles = (a.rows + TR - 1) / TR;
     if (threadIdx.x == 0) tq[2] = tb + 2 * G;
