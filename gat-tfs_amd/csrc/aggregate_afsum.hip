@@ -798,35 +798,54 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4
                     else dl = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wf[ks], bv, dl, 0, 0, 0);
                 }
             }
+            // Lane (half, r) holds features DIM h + 32 b + 16 half + {0..15} of
+            // tile row r (permuted packing).
             const int r = l % 32, half = l / 32;
-            const uint32_t i = trow[r % TR];
-            if (r < TR) {
-                if (i != kNoRow) {
-                    // Lane (half, r) holds features DIM h + 32 b + 16 half + {0..15}
-                    // (permuted packing).
-                    float o[16];
+            if constexpr (!HL) {
+                // bf16 hidden rows (ELU).  Each store leaves the head block's 64
+                // contiguous bytes of 16 rows, where one 16-byte piece per row
+                // and lane half left before (3.171 -> 3.137 ms on the 64.3M-edge
+                // layer): inside the lane quad (rows 4a .. 4a + 3), store j
+                // takes rows 4a + 2j and 4a + 2j + 1, lane c writing piece
+                // 2 half + c % 2 of row 4a + 2j + c / 2, read from quad lane
+                // 2j + c / 2 by DPP.
+                static_assert(TR == 32, "bf16 tiles hold 32 rows");
+                uint32_t P[2][4];  // the lane's two 16-byte pieces (2 half, 2 half + 1)
 #pragma unroll
-                    for (int x = 0; x < 16; ++x) {
-                        const float y = (dh[x] + dl[x]) * inv;
-                        o[x] = HL ? y : elu_bf16(y);  // FP32 outputs: the last layer; bf16: hidden
+                for (int q = 0; q < 2; ++q)
+#pragma unroll
+                    for (int x = 0; x < 4; ++x)
+                        P[q][x] = bf16x2(elu_bf16((dh[8 * q + 2 * x] + dl[8 * q + 2 * x]) * inv),
+                                         elu_bf16((dh[8 * q + 2 * x + 1] + dl[8 * q + 2 * x + 1]) * inv));
+                const int c = l & 3;
+                auto store_pair = [&](auto J) {
+                    constexpr int j = decltype(J)::value;
+                    constexpr int kSel = j ? 0xFA : 0x50;  // quad_perm [2j, 2j, 2j + 1, 2j + 1]
+                    uint32_t T[4];
+#pragma unroll
+                    for (int x = 0; x < 4; ++x) {
+                        const uint32_t a0 = uint32_t(__builtin_amdgcn_mov_dpp(int(P[0][x]), kSel, 0xF, 0xF, false));
+                        const uint32_t a1 = uint32_t(__builtin_amdgcn_mov_dpp(int(P[1][x]), kSel, 0xF, 0xF, false));
+                        T[x] = (c & 1) ? a1 : a0;
                     }
+                    const uint32_t ij = trow[(r & ~3) + 2 * j + (c >> 1)];
+                    if (ij != kNoRow)
+                        *reinterpret_cast<uint4*>(a.outbf + uint64_t(ij) * (8 * DIM) + DIM * h + 32 * b + 16 * half +
+                                                  8 * (c & 1)) = make_uint4(T[0], T[1], T[2], T[3]);
+                };
+                store_pair(std::integral_constant<int, 0>{});
+                store_pair(std::integral_constant<int, 1>{});
+            } else {
+                // FP32 outputs (the last layer, no ELU): 16 tile rows, 64 bytes
+                // per lane.
+                const uint32_t i = trow[r % TR];
+                if (r < TR && i != kNoRow) {
                     const uint64_t off = uint64_t(i) * (8 * DIM) + DIM * h + 32 * b + 16 * half;
-                    if (a.outbf) {
 #pragma unroll
-                        for (int q = 0; q < 2; ++q) {
-                            uint32_t v[4];
-#pragma unroll
-                            for (int x = 0; x < 4; ++x)
-                                v[x] = bf16x2(o[8 * q + 2 * x], o[8 * q + 2 * x + 1]);
-                            *reinterpret_cast<uint4*>(a.outbf + off + 8 * q) = make_uint4(v[0], v[1], v[2], v[3]);
-                        }
-                    }
-                    if (a.out32) {
-#pragma unroll
-                        for (int q = 0; q < 4; ++q)
-                            *reinterpret_cast<float4*>(a.out32 + off + 4 * q) =
-                                make_float4(o[4 * q], o[4 * q + 1], o[4 * q + 2], o[4 * q + 3]);
-                    }
+                    for (int q = 0; q < 4; ++q)
+                        *reinterpret_cast<float4*>(a.out32 + off + 4 * q) =
+                            make_float4((dh[4 * q] + dl[4 * q]) * inv, (dh[4 * q + 1] + dl[4 * q + 1]) * inv,
+                                        (dh[4 * q + 2] + dl[4 * q + 2]) * inv, (dh[4 * q + 3] + dl[4 * q + 3]) * inv);
                 }
             }
         }

@@ -127,9 +127,10 @@ __global__ void __launch_bounds__(kThreads) k_proj_mfma(ProjArgs a) {
 // unconditionally (rows past n re-read row n - 1 and are not stored).
 // Head blocks use the permuted packing (pack_projection_weights): lane
 // (half, col) ends with features 32 mb + 16 half + {0..15} of row col, so
-// Z leaves as two 16-byte stores per block.  FULL: 0 any shape; 1 a layer of
-// 8 heads x 32 with every store unconditional; 2 the same with R = Z_bf16 aR
-// (what the aggregation recomputes from the gathered row).
+// Z leaves as two 16-byte stores per block, or, in FULL layers, as whole
+// 128-byte lines after a transpose inside each lane quad.  FULL: 0 any shape;
+// 1 a layer of 8 heads x 32 with every store unconditional; 2 the same with
+// R = Z_bf16 aR (what the aggregation recomputes from the gathered row).
 // L/R-only launches (HB = 0: the aggregate-first front end, a streaming pass
 // with KS KB of W) take a full grid, one tile per wave, and W is cheap to
 // refetch; their LDS request holds them to two blocks (16 waves) per CU.
@@ -251,41 +252,88 @@ __global__ void __launch_bounds__(kThreads) k_proj_fast(ProjArgs a) {
         // bounds tests either.
         const bool full = FULL;
         float rz4[4] = {};  // R from the stored (bf16) Z of the lane's 4 heads (4 half + q)
+        if constexpr (FULL != 0) {
+            // Z rows leave as whole 128-byte lines.  Lane (half, col) holds 32
+            // bytes of row col per head block: bytes 64 mb + 32 half + {0..31}.
+            // Line k of the row is blocks 2k and 2k + 1, so the lane quad
+            // (rows 4a .. 4a + 3, both halves) holds 4 rows x 8 pieces of 16
+            // bytes of it, 4 pieces per lane (slot p: block 2k + p / 2, piece p
+            // % 2).  A 4 x 4 transpose inside the quad (two DPP exchange stages,
+            // lane c taking slot p from quad lane c ^ 1, then c ^ 2) leaves lane
+            // c with slot c of the 4 rows, so store j writes row 4a + j whole
+            // from the 8 lanes of quad a: 8 lines per instruction where the
+            // direct stores wrote 16-byte pieces of 32 rows (0.565 -> 0.555 ms on
+            // the 2.45M-row 256 -> 8 x 32 layer).
+            const int c = l & 3;
 #pragma unroll
-        for (int mb = 0; mb < HB; ++mb) {
-            float zr[16];
-            uint32_t zp[8];  // the stored bf16 pairs
+            for (int k = 0; k < HB / 2; ++k) {
+                uint32_t S[4][4];
 #pragma unroll
-            for (int x = 0; x < 8; ++x) zp[x] = bf16x2(acc[mb][2 * x], acc[mb][2 * x + 1]);
+                for (int m2 = 0; m2 < 2; ++m2) {
+                    const int mb = 2 * k + m2;
+                    uint32_t zp[8];  // the stored bf16 pairs
 #pragma unroll
-            for (int x = 0; x < 8; ++x) {
-                zr[2 * x] = __builtin_bit_cast(float, zp[x] << 16);
-                zr[2 * x + 1] = __builtin_bit_cast(float, zp[x] & 0xffff0000u);
+                    for (int x = 0; x < 8; ++x) zp[x] = bf16x2(acc[mb][2 * x], acc[mb][2 * x + 1]);
+#pragma unroll
+                    for (int x = 0; x < 8; ++x) S[2 * m2 + x / 4][x % 4] = zp[x];
+                    if constexpr (FULL == 2) {
+                        // R = Z_bf16 . aR with the summation the aggregation kernel
+                        // uses: an FMA chain over each 8 features, then
+                        // (s0 + s1) + (s2 + s3).
+                        float s8[2];
+#pragma unroll
+                        for (int q8 = 0; q8 < 2; ++q8) {
+                            float t = 0.0f;
+#pragma unroll
+                            for (int x = 0; x < 8; ++x) {
+                                const uint32_t pr = zp[4 * q8 + x / 2];
+                                const float zv = __builtin_bit_cast(float, (x & 1) ? (pr & 0xffff0000u) : (pr << 16));
+                                t = __builtin_fmaf(zv, arl[32 * mb + 16 * half + 8 * q8 + x], t);
+                            }
+                            s8[q8] = t;
+                        }
+                        const float part = s8[0] + s8[1];
+                        const float r = part + __shfl_xor(part, 32);
+                        rz4[mb & 3] = (mb >> 2) == half ? r : rz4[mb & 3];
+                    }
+                }
+                uint32_t U[4][4], T[4][4];
+#pragma unroll
+                for (int p = 0; p < 4; ++p)
+#pragma unroll
+                    for (int v = 0; v < 4; ++v) {
+                        const uint32_t o = uint32_t(__builtin_amdgcn_mov_dpp(int(S[p ^ 1][v]), 0xB1, 0xF, 0xF, false));
+                        U[p][v] = (c & 1) == (p & 1) ? S[p][v] : o;  // quad_perm [1, 0, 3, 2]
+                    }
+#pragma unroll
+                for (int p = 0; p < 4; ++p)
+#pragma unroll
+                    for (int v = 0; v < 4; ++v) {
+                        const uint32_t o = uint32_t(__builtin_amdgcn_mov_dpp(int(U[p ^ 2][v]), 0x4E, 0xF, 0xF, false));
+                        T[p][v] = (c & 2) == (p & 2) ? U[p][v] : o;  // quad_perm [2, 3, 0, 1]
+                    }
+                // T[j]: slot c (line bytes 64 (c / 2) + 32 half + 16 (c % 2)) of
+                // quad row j; rows past n repeat row n - 1, as that row's lane did.
+                const int off = 64 * k + 32 * (c / 2) + 16 * half + 8 * (c % 2);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const uint64_t rj = tile * 32 + uint64_t((col & ~3) + j);
+                    const uint64_t rsj = rj < a.n ? rj : a.n - 1;
+                    *reinterpret_cast<uint4*>(a.z + rsj * a.zs + off) = make_uint4(T[j][0], T[j][1], T[j][2], T[j][3]);
+                }
             }
+        } else {
 #pragma unroll
-            for (int q8 = 0; q8 < 2; ++q8) {
-                const int f0 = 32 * mb + 16 * half + 8 * q8;
-                if (!full && f0 >= a.width) continue;
-                uint32_t w4[4];
-#pragma unroll
-                for (int x = 0; x < 4; ++x) w4[x] = zp[4 * q8 + x];
-                *reinterpret_cast<uint4*>(a.z + rs * a.zs + f0) = make_uint4(w4[0], w4[1], w4[2], w4[3]);
-            }
-            if constexpr (FULL == 2) {
-                // R = Z_bf16 . aR with the summation the aggregation kernel uses:
-                // an FMA chain over each 8 features, then (s0 + s1) + (s2 + s3).
-                float s8[2];
+            for (int mb = 0; mb < HB; ++mb) {
 #pragma unroll
                 for (int q8 = 0; q8 < 2; ++q8) {
-                    float t = 0.0f;
+                    const int f0 = 32 * mb + 16 * half + 8 * q8;
+                    if (f0 >= a.width) continue;
+                    uint32_t w4[4];
 #pragma unroll
-                    for (int x = 0; x < 8; ++x)
-                        t = __builtin_fmaf(zr[8 * q8 + x], arl[32 * mb + 16 * half + 8 * q8 + x], t);
-                    s8[q8] = t;
+                    for (int x = 0; x < 4; ++x) w4[x] = bf16x2(acc[mb][8 * q8 + 2 * x], acc[mb][8 * q8 + 2 * x + 1]);
+                    *reinterpret_cast<uint4*>(a.z + rs * a.zs + f0) = make_uint4(w4[0], w4[1], w4[2], w4[3]);
                 }
-                const float part = s8[0] + s8[1];
-                const float r = part + __shfl_xor(part, 32);
-                rz4[mb & 3] = (mb >> 2) == half ? r : rz4[mb & 3];
             }
         }
         // L/R block: lane half h4 holds heads 4 h4 + {0..3} of each quarter
@@ -344,16 +392,30 @@ __global__ void __launch_bounds__(kThreads) k_proj_fast(ProjArgs a) {
 // 512 -> 8 x 64 projection: 2.73 ms with the fragments staged through
 // registers, 2.63 ms with the direct loads; six-wave blocks at three waves
 // per SIMD (168 registers, two-step read-ahead, spilled addresses) 3.04 ms.
+//
+// The step barrier orders LDS only (each wave first waits for its own loads
+// into the next slot), so Z stores stay in flight across it; where every head
+// block is full (DEL) a block's Z stores are also issued one step late,
+// behind the next block's fragment loads, so the wait for those loads does
+// not wait for them.  The one-head 512 -> 64 projection went 0.977 -> 0.94 ms;
+// the 8 x 64 one is unchanged by both (and by fragments staged through
+// registers after the MFMAs, whose fragment reads the compiler then waits for
+// in order where it waits for every LDS-DMA load: 2.81 ms).
 constexpr int kWideThreads = 256;  // the FP32 projection's block (k_proj_f32)
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 constexpr int kWideWaves = kWideThreads / kWave;
 constexpr int kWideBW = 4;  // waves per block of the bf16 wide path
 typedef __attribute__((address_space(3))) void* lds_ptr;
 
-template <int KS, bool F32IN, bool RZ>
+template <int KS, bool F32IN, bool RZ, bool DEL>
 __global__ void __launch_bounds__(kWideBW * kWave) __attribute__((amdgpu_waves_per_eu(2))) k_proj_wide(ProjArgs a) {
     __shared__ __attribute__((aligned(16))) u32x4 slot0[KS * kWave];
     __shared__ __attribute__((aligned(16))) u32x4 slot1[KS * kWave];
+    // aR of the one head of 64 (RZ), read by the epilogue from LDS: a global
+    // load there would sit behind the delayed Z stores in the in-order counter.
+    __shared__ float arl[RZ ? 64 : 1];
+    if constexpr (RZ)
+        for (int q = threadIdx.x; q < 64; q += kWideBW * kWave) arl[q] = a.ar[q];
     const int w = __builtin_amdgcn_readfirstlane(int(threadIdx.x) / kWave), l = threadIdx.x % kWave;
     const int half = l / 32, col = l % 32;
     const uint64_t row = (uint64_t(blockIdx.x) * kWideBW + w) * 32 + col;
@@ -412,6 +474,11 @@ __global__ void __launch_bounds__(kWideBW * kWave) __attribute__((amdgpu_waves_p
     // 8 features (p0..p7), then ((p0 + p1) + (p2 + p3)) + ((p4 + p5) + (p6 + p7)).
     // Lane half 0 holds p0, p1 (block 0) and p4, p5 (block 1); half 1 the others.
     float rlo = 0.0f, rhi = 0.0f;  // pair sums of head blocks 0 and 1
+    // DEL (every head block full): block ob's Z pieces leave at the top of
+    // step ob + 1, after block ob + 2's fragment loads are issued, so the wait
+    // for those loads at the end of step ob + 1 (vmcnt(2)) leaves the two
+    // stores in flight instead of waiting for them.
+    uint32_t pend[2][4] = {};
     dma(0, slot0);
     __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the tile's input and block 0's fragments
     __syncthreads();
@@ -420,6 +487,14 @@ __global__ void __launch_bounds__(kWideBW * kWave) __attribute__((amdgpu_waves_p
     // MFMAs and before this block's stores, so the barrier then publishes wr.
     auto step = [&](int ob, const u32x4* rd, u32x4* wr) {
         if (ob + 1 < nob) dma(ob + 1, wr);
+        if constexpr (DEL) {
+            if (ob > 0) {
+#pragma unroll
+                for (int q8 = 0; q8 < 2; ++q8)
+                    *reinterpret_cast<uint4*>(a.z + rs * a.zs + 32 * (ob - 1) + 16 * half + 8 * q8) =
+                        make_uint4(pend[q8][0], pend[q8][1], pend[q8][2], pend[q8][3]);
+            }
+        }
         f32x16 acc;
 #pragma unroll
         for (int r = 0; r < 16; ++r) acc[r] = 0.0f;
@@ -444,7 +519,8 @@ __global__ void __launch_bounds__(kWideBW * kWave) __attribute__((amdgpu_waves_p
             __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
         }
         __builtin_amdgcn_sched_group_barrier(0x008, kAhead, 0);
-        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's loads into wr
+        if (DEL && ob > 0) __builtin_amdgcn_s_waitcnt(0x0F72);  // vmcnt(2): the loads into wr, not the 2 stores after them
+        else __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's loads into wr
         __builtin_amdgcn_sched_barrier(0);
         if (ob < a.head_blocks) {
             // Permuted packing: lane (half, col) holds features 32 ob + 16 half + {0..15}.
@@ -463,8 +539,8 @@ __global__ void __launch_bounds__(kWideBW * kWave) __attribute__((amdgpu_waves_p
                         float t = 0.0f;
 #pragma unroll
                         for (int x = 0; x < 4; ++x) {
-                            t = __builtin_fmaf(__builtin_bit_cast(float, w4[q8][x] << 16), a.ar[f0 + 2 * x], t);
-                            t = __builtin_fmaf(__builtin_bit_cast(float, w4[q8][x] & 0xffff0000u), a.ar[f0 + 2 * x + 1],
+                            t = __builtin_fmaf(__builtin_bit_cast(float, w4[q8][x] << 16), arl[f0 + 2 * x], t);
+                            t = __builtin_fmaf(__builtin_bit_cast(float, w4[q8][x] & 0xffff0000u), arl[f0 + 2 * x + 1],
                                                t);
                         }
                         if (ob == 0) rlo = q8 == 0 ? t : rlo + t;
@@ -472,12 +548,19 @@ __global__ void __launch_bounds__(kWideBW * kWave) __attribute__((amdgpu_waves_p
                     }
                 }
             }
+            if constexpr (DEL) {
 #pragma unroll
-            for (int q8 = 0; q8 < 2; ++q8) {
-                const int f0 = 32 * ob + 16 * half + 8 * q8;
-                if (f0 < a.width)
-                    *reinterpret_cast<uint4*>(a.z + rs * a.zs + f0) =
-                        make_uint4(w4[q8][0], w4[q8][1], w4[q8][2], w4[q8][3]);
+                for (int q8 = 0; q8 < 2; ++q8)
+#pragma unroll
+                    for (int x = 0; x < 4; ++x) pend[q8][x] = w4[q8][x];
+            } else {
+#pragma unroll
+                for (int q8 = 0; q8 < 2; ++q8) {
+                    const int f0 = 32 * ob + 16 * half + 8 * q8;
+                    if (f0 < a.width)
+                        *reinterpret_cast<uint4*>(a.z + rs * a.zs + f0) =
+                            make_uint4(w4[q8][0], w4[q8][1], w4[q8][2], w4[q8][3]);
+                }
             }
         } else {
             float rz = 0.0f;
@@ -506,7 +589,11 @@ __global__ void __launch_bounds__(kWideBW * kWave) __attribute__((amdgpu_waves_p
                 }
             }
         }
-        __syncthreads();
+        // The slots are LDS only, and each wave has waited for its own loads
+        // into wr: an LDS-scoped barrier, which leaves the Z stores in flight.
+        __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
     };
     for (int ob = 0; ob < nob; ob += 2) {
         step(ob, slot0, slot1);
@@ -518,8 +605,14 @@ template <int KS, bool F32IN>
 hipError_t launch_wide_io(const ProjArgs& a, hipStream_t s) {
     const uint64_t blocks = (a.tiles + kWideBW - 1) / kWideBW;
     if (blocks < 1 || blocks > 0x7fffffffu) return hipErrorInvalidValue;
-    if (a.r_from_z) k_proj_wide<KS, F32IN, true><<<dim3(uint32_t(blocks)), kWideBW * kWave, 0, s>>>(a);
-    else k_proj_wide<KS, F32IN, false><<<dim3(uint32_t(blocks)), kWideBW * kWave, 0, s>>>(a);
+    const bool del = a.width % 32 == 0;  // every head block full: its stores are unconditional
+    if (a.r_from_z) {
+        if (del) k_proj_wide<KS, F32IN, true, true><<<dim3(uint32_t(blocks)), kWideBW * kWave, 0, s>>>(a);
+        else k_proj_wide<KS, F32IN, true, false><<<dim3(uint32_t(blocks)), kWideBW * kWave, 0, s>>>(a);
+    } else {
+        if (del) k_proj_wide<KS, F32IN, false, true><<<dim3(uint32_t(blocks)), kWideBW * kWave, 0, s>>>(a);
+        else k_proj_wide<KS, F32IN, false, false><<<dim3(uint32_t(blocks)), kWideBW * kWave, 0, s>>>(a);
+    }
     return hipGetLastError();
 }
 
