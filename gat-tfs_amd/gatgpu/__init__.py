@@ -228,16 +228,19 @@ class Context:
         self._check(self.lib.gatgpu_fixed_p_forward(self.h, layer, precision, dataflow, _ptr(inp), ctypes.byref(t)))
         return t.as_dict()
 
-    def model_forward(self, precision=FP32, dataflow=AUTO, want_logits=True, timed=True):
+    def model_forward(self, precision=FP32, dataflow=AUTO, want_logits=True, timed=True, stages=True):
+        """timed: the model time (HIP events, first kernel to last); stages:
+        also the per-layer times, which add an event at every stage boundary."""
         logits = None
         if want_logits:
             logits = np.empty((self.n, self.layers[2][1] * self.layers[2][2]), np.float32)
-        times = (Times * 3)() if timed else None
+        per_layer = timed and stages
+        times = (Times * 3)() if per_layer else None
         total = ctypes.c_double(0.0)
         self._check(self.lib.gatgpu_model_forward(self.h, precision, dataflow, _ptr(logits),
-                                                  times if timed else None,
+                                                  times if per_layer else None,
                                                   ctypes.byref(total) if timed else None))
-        return logits, ([t.as_dict() for t in times] if timed else None), total.value
+        return logits, ([t.as_dict() for t in times] if per_layer else None), total.value
 
     def has_stage(self, layer, which):
         """True when the last forward left this stage (gatgpu_stage_size > 0)."""

@@ -214,6 +214,8 @@ int gatgpu_layer_forward(gatgpu_ctx* ctx, int layer, int precision, int dataflow
  * timer of baseline/bench/main.cpp:171-174).  logits (NULL allowed) receives
  * layer 2's FP32 [n][dim] output after the timer stops.  times (NULL allowed)
  * points at 3 per-layer records; total_ms (NULL allowed) gets the model time.
+ * The per-stage events are recorded only when times is given: with total_ms
+ * alone the forward carries two events, its first and its last.
  * dataflow applies to every layer (AUTO decides per layer; AGGREGATE_FIRST
  * falls back to transform-first on layers it does not support). */
 int gatgpu_model_forward(gatgpu_ctx* ctx, int precision, int dataflow, float* logits,

@@ -359,6 +359,26 @@ def test_smoke1024_model_bf16(gpu_ctx):
     assert e["finite"] and e["relative_l2"] < BF16_REL_L2, e
 
 
+@pytest.mark.parametrize("precision", [gatgpu.FP32, gatgpu.BF16])
+def test_model_time_without_stage_events(gpu_ctx, precision):
+    """total_ms alone (no per-layer records): the forward records only its
+    first and last events and still returns the model time; the logits and
+    stages equal those of a forward with every stage timed."""
+    g = smoke1024()
+    gpu_ctx.set_graph(g["row"], g["col"])
+    gpu_ctx.set_model(oracle.random_model(128, 40, 11))
+    gpu_ctx.set_input(g["x"])
+    staged, times, t_staged = gpu_ctx.model_forward(precision, gatgpu.AUTO)
+    den_staged = gpu_ctx.stage(1, "den").copy()
+    bare, none, t_bare = gpu_ctx.model_forward(precision, gatgpu.AUTO, stages=False)
+    assert none is None and len(times) == 3
+    assert 0 < t_bare < 1e3 and 0 < t_staged < 1e3
+    assert np.array_equal(bare, staged)
+    assert np.array_equal(gpu_ctx.stage(1, "den"), den_staged)
+    # untimed forwards still return no time
+    assert gpu_ctx.model_forward(precision, gatgpu.AUTO, want_logits=False, timed=False)[2] == 0.0
+
+
 @pytest.mark.parametrize("name", ["smoke", "arxiv"])
 @pytest.mark.parametrize("precision", [gatgpu.FP32, gatgpu.BF16])
 def test_workload_model_parity(gpu_ctx, name, precision):
