@@ -134,6 +134,8 @@ __global__ void __launch_bounds__(kThreads) k_proj_mfma(ProjArgs a) {
 // L/R-only launches (HB = 0: the aggregate-first front end, a streaming pass
 // with KS KB of W) take a full grid, one tile per wave, and W is cheap to
 // refetch; their LDS request holds them to two blocks (16 waves) per CU.
+// With 7 k steps they write the gather-table rows as whole lines, after the
+// same in-quad transpose (0.329 -> 0.309 ms on the 2.45M-row 100-input layer).
 template <int KS, int HB, bool F32IN, int FULL>
 __global__ void __launch_bounds__(kThreads) k_proj_fast(ProjArgs a) {
     static_assert(!FULL || HB == 8, "FULL layers are 8 heads x 32");
@@ -213,11 +215,61 @@ __global__ void __launch_bounds__(kThreads) k_proj_fast(ProjArgs a) {
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[mb][r] = 0.0f;
         const uint64_t rs = row < a.n ? row : a.n - 1;  // lanes past n repeat row n - 1
+        // XRL: the aggregate-first front end writing 7 k steps of rounded input
+        // and R into 256-byte gather-table rows.  Lane (half, col) holds 16
+        // bytes per k step, bytes 32 (ks % 4) + 16 half of line ks / 4; R of
+        // its 4 heads is the fourth slot of line 1.  Each line leaves whole:
+        // a 4 x 4 transpose of the slots inside the lane quad (two DPP
+        // exchange stages) gives lane c slot c of the quad's 4 rows.
+        constexpr bool XRL_OK = ONE && F32IN && KS == 7;
+        const bool xrl = XRL_OK && a.xout && a.r_in_z && a.xout == a.z && a.xouts == kXRStride &&
+                         a.zs == kXRStride && a.r_off == kXRFeat && a.heads == 8;
+        uint4 xo[XRL_OK ? KS : 1];
+        auto line_out = [&](const uint4 (&slot)[4], int line) {
+            const int c = l & 3;
+            uint32_t S[4][4], U[4][4];
+#pragma unroll
+            for (int p = 0; p < 4; ++p) {
+                S[p][0] = slot[p].x;
+                S[p][1] = slot[p].y;
+                S[p][2] = slot[p].z;
+                S[p][3] = slot[p].w;
+            }
+#pragma unroll
+            for (int p = 0; p < 4; ++p)
+#pragma unroll
+                for (int v = 0; v < 4; ++v) {
+                    const uint32_t o = uint32_t(__builtin_amdgcn_mov_dpp(int(S[p ^ 1][v]), 0xB1, 0xF, 0xF, false));
+                    U[p][v] = (c & 1) == (p & 1) ? S[p][v] : o;  // quad_perm [1, 0, 3, 2]
+                }
+#pragma unroll
+            for (int p = 0; p < 4; ++p)
+#pragma unroll
+                for (int v = 0; v < 4; ++v) {
+                    const uint32_t o = uint32_t(__builtin_amdgcn_mov_dpp(int(U[p ^ 2][v]), 0x4E, 0xF, 0xF, false));
+                    S[p][v] = (c & 2) == (p & 2) ? U[p][v] : o;  // quad_perm [2, 3, 0, 1]
+                }
+            // S[j]: slot c (bytes 32 c + 16 half of the line) of quad row j;
+            // rows past n repeat row n - 1, as that row's lane did.
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const uint64_t rj = tile * 32 + uint64_t((col & ~3) + j);
+                const uint64_t rsj = rj < a.n ? rj : a.n - 1;
+                *reinterpret_cast<uint4*>(a.xout + rsj * kXRStride + 64 * line + 16 * c + 8 * half) =
+                    make_uint4(S[j][0], S[j][1], S[j][2], S[j][3]);
+            }
+        };
         auto kstep = [&](int ks) {
             const bf16x8 b = operand(ks);
             if constexpr (F32IN) {
-                if (a.xout)
+                if constexpr (XRL_OK) {
+                    if (xrl) xo[ks] = __builtin_bit_cast(uint4, b);
+                    else if (a.xout)
+                        *reinterpret_cast<uint4*>(a.xout + rs * a.xouts + 16 * ks + 8 * half) =
+                            __builtin_bit_cast(uint4, b);
+                } else if (a.xout) {
                     *reinterpret_cast<uint4*>(a.xout + rs * a.xouts + 16 * ks + 8 * half) = __builtin_bit_cast(uint4, b);
+                }
             }
             const uint4* wk = wlds + size_t(ks) * NB * kWave + l;
 #pragma unroll
@@ -233,6 +285,12 @@ __global__ void __launch_bounds__(kThreads) k_proj_fast(ProjArgs a) {
         // the stores.  Every load is unconditional, so each wait is exact.
 #pragma unroll
         for (int ks = 0; ks < KA; ++ks) kstep(ks);
+        if constexpr (XRL_OK) {
+            if (xrl) {
+                const uint4 l0[4] = {xo[0], xo[1], xo[2], xo[3]};
+                line_out(l0, 0);
+            }
+        }
         if constexpr (!ONE) {
 #pragma unroll
             for (int ks = 0; ks < KA; ++ks) load_ks(next, ks);
@@ -354,7 +412,18 @@ __global__ void __launch_bounds__(kThreads) k_proj_fast(ProjArgs a) {
                     FULL == 2 ? make_float4(rz4[0], rz4[1], rz4[2], rz4[3]) : rv;
             } else {
                 *reinterpret_cast<float4*>(a.right + rs * 8 + 4 * half) = rv;
-                if (a.r_in_z) *reinterpret_cast<float4*>(a.z + rs * a.zs + a.r_off + 8 * half) = rv;
+                if constexpr (XRL_OK) {
+                    if (xrl) {
+                        const uint4 l1[4] = {xo[4], xo[5], xo[6],
+                                             make_uint4(__float_as_uint(rv.x), __float_as_uint(rv.y),
+                                                        __float_as_uint(rv.z), __float_as_uint(rv.w))};
+                        line_out(l1, 1);
+                    } else if (a.r_in_z) {
+                        *reinterpret_cast<float4*>(a.z + rs * a.zs + a.r_off + 8 * half) = rv;
+                    }
+                } else if (a.r_in_z) {
+                    *reinterpret_cast<float4*>(a.z + rs * a.zs + a.r_off + 8 * half) = rv;
+                }
             }
         } else {
 #pragma unroll
