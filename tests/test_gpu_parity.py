@@ -726,7 +726,51 @@ def test_bf16_projection_stages(gpu_ctx, D, K, d):
     gathers): that R is
     checked against the float64 dot of the GPU's own Z stage to FP32
     summation accuracy, and against R0 to the bf16 rounding of Z."""
-    w = inputs.WORKLOADS["smoke"]
+    check_bf16_projection(gpu_ctx, inputs.WORKLOADS["smoke"], D, K, d)
+
+
+# 1021 rows: the last 32-row tile holds 29 rows and its last lane quad one, so
+# the stores that leave whole lines after an in-quad transpose (rows 4a + j
+# written by lane quad a, rows past n repeating row n - 1) meet partial tiles.
+ODD_ROWS = inputs.Workload("odd1021", "uniform", 1021, 16, 0, 128, 8, 32, 40)
+
+
+@pytest.mark.parametrize("D", [100, 256])
+def test_projection_partial_tiles(gpu_ctx, D):
+    """The 8 x 32 projection (whole-line Z stores, R from the stored Z) on a
+    graph whose row count is not a multiple of 32 or 4: the same bounds as on
+    whole tiles."""
+    check_bf16_projection(gpu_ctx, ODD_ROWS, D, 8, 32)
+
+
+@pytest.mark.parametrize("D", [100, 64])
+def test_aggregate_first_partial_tiles(gpu_ctx, D):
+    """The aggregate-first front end writes the gather-table rows (rounded X and
+    R) as whole lines; on 1021 rows every row, including the last partial
+    tile's, feeds the sum form as on whole tiles: outputs and L equal R0 on
+    bf16-rounded X and W."""
+    w = ODD_ROWS
+    row, col = w.graph()
+    x = inputs.normal((w.n, D), 23)
+    p = inputs.glorot_param(D, 8, 32, 24)
+    qp = dict(p, w=oracle.quantize_bf16(p["w"]))
+    xq = oracle.quantize_bf16(x)
+    gpu_ctx.set_graph(row, col)
+    gpu_ctx.set_layer(0, p)
+    gpu_ctx.set_input(x)
+    for hidden in (False, True):
+        r = oracle.ref_layer(row, col, xq, qp, hidden)
+        gpu_ctx.layer_forward(0, gatgpu.BF16, gatgpu.AGGREGATE_FIRST, hidden)
+        out = gpu_ctx.stage(0, "out")
+        e = oracle.errors(oracle.quantize_bf16(r["out"]) if hidden else r["out"], out)
+        assert e["finite"] and e["relative_l2"] < (4e-3 if hidden else 1e-4), (hidden, e)
+        assert oracle.errors(r["left"], gpu_ctx.stage(0, "left"))["relative_l2"] < 1e-5
+        assert oracle.errors(r["right"], gpu_ctx.stage(0, "right"))["relative_l2"] < 1e-5
+        for k_ in ("max", "den"):
+            assert oracle.errors(r[k_], gpu_ctx.stage(0, k_))["relative_l2"] < 1e-4, (hidden, k_)
+
+
+def check_bf16_projection(gpu_ctx, w, D, K, d):
     row, col = w.graph()
     x = inputs.normal((w.n, D), 3)
     p = inputs.glorot_param(D, K, d, 4)
