@@ -546,9 +546,10 @@ __device__ void afs_chunk(const AfsArgs& a, uint64_t c, int l, float* sw) {
 }
 
 
-template <int KS, bool HL, int TR, int DIM>
+template <int KS, bool HL, int TR, int DIM, bool SHORT>
 __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) k_afs_tiles(AfsArgs a) {
     static_assert(TR == 16 || (TR == 32 && !HL), "16-row tiles, or 32-row tiles of one bf16");
+    static_assert(!SHORT || !HL, "short rows: 32-row tiles of bf16-stored rows");
     static_assert(DIM == 32 || DIM == 64, "heads of 32 or 64");
     constexpr bool RSEP = KS == 8;
     constexpr int RPW = TR / kWaves;          // rows per wave and tile
@@ -569,7 +570,7 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4
     const int g = l / 16, n = l % 16;
     const bool head = n < 8;
     const uint32_t chunk_blocks = gridDim.x - a.tile_blocks;
-    if (blockIdx.x < chunk_blocks) {
+    if (!SHORT && blockIdx.x < chunk_blocks) {
         // Split-row chunks, one per wave, in the first blocks: they start with
         // the launch, and the tile blocks that wait for their slots take fewer
         // tiles.
@@ -590,7 +591,7 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4
     static_assert(2 * 8 * TR * 4 <= kTMdBytes, "stage rows fit");
     static_assert(!DB, "the stage rows are single-buffered: the next tile writes them after the closing barrier");
     uint32_t* const tctr = a.counter + a.chunks;  // [0] tiles taken past 3G, [1] tile blocks done
-    const uint64_t tiles = (a.rows + TR - 1) / TR;
+    const uint64_t span = a.rows - a.row_lo, tiles = (span + TR - 1) / TR;
     if (threadIdx.x == 0) tq[2] = tb + 2 * G;
     __syncthreads();
     // Bounds of the wave's rows of tile t (lane q < RPW: tile row w + 8 q),
@@ -599,7 +600,7 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4
         fi = kNoRow;
         fb = fe = 0;
         const uint64_t tpos = t * TR + w + kWaves * l;
-        if (l < RPW && t < tiles && tpos < a.rows) {
+        if (l < RPW && t < tiles && tpos < span) {
             const uint64_t k = a.rows - 1 - tpos;
             fi = a.perm[k];
             fb = a.prow[k];
@@ -655,73 +656,186 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4
                  uint32_t(__builtin_amdgcn_readlane(int(uint32_t(me)), q));
             qids = q / 2 == 0 ? idr[0] : idr[(RPW + 1) / 2 - 1];
         };
-        // Each row's first batch is requested before the previous row's
-        // epilogue (its loads then travel while that row's sums are staged).
-        Batch<kEPL> pre;
-        bool have_pre = false;  // wave-uniform
-#pragma unroll 1
-        for (int rr = 0; rr < RPW; ++rr) {
-            const int r = w + kWaves * rr;
-            uint32_t i, ids;
-            uint64_t beg, end;
-            row_of(rr, i, beg, end, ids);
-            const float Lr = __shfl(Lall, 8 * rr + n % 8);
-            if (l == 0) trow[r] = i;
-            if (i == kNoRow) continue;
-            Sums s;
-            zero_sums(s);
-            s.L = head || !RSEP ? Lr : 0.0f;  // (lanes h + 8 score half of head h's edges)
-            s.m = s.mx = -INFINITY;
-            if (!have_pre && beg < end) first_batch<RSEP>(a.xr, a.R, beg, end, l, ids, 32 * (rr % 2), pre);
-            gather_sums<false, RSEP, kEPL, true>(a.pcol, a.xr, a.R, beg, end, l, s, ids, 32 * (rr % 2), pre);
-            have_pre = false;
-            if (rr + 1 < RPW) {
-                uint32_t ni, nids;
-                uint64_t nb, ne;
-                row_of(rr + 1, ni, nb, ne, nids);
-                if (ni != kNoRow && nb < ne) {
-                    first_batch<RSEP>(a.xr, a.R, nb, ne, l, nids, 32 * ((rr + 1) % 2), pre);
-                    have_pre = true;
+        if constexpr (SHORT) {
+            // ---- Short rows (this instance takes the sorted positions whose
+            // rows have at most kShortDeg = 4 edges: on the 2^22-node R-MAT
+            // graph 3.0M of the 4.2M rows).  The wave's four rows share one
+            // 16-edge batch, k group g taking the edges of row g: one round trip
+            // for four rows, where a row took one of its own.  Such a row has one
+            // batch: its max is the batch's, nothing is rescaled, and its weights
+            // p, max and denominator are those of a one-row batch bit for bit.
+            // Row m = 4 v + x of the MFMA's A is row v's head 4 hf + x in pass hf:
+            // that row's weights in k group v and zeros in the others.  U = (hi
+            // parts' sum) + (lo parts' sum) from two MFMAs, the two sums a one-row
+            // batch keeps in D rows h and 8 + h and fold_pair adds.
+            static_assert(kShortDeg == kEPL && RPW == 4 && NID == 2, "one k group (4 edges) per row, four rows");
+            uint32_t cnt = 0;  // edges of the lane's row g (0 for none)
+#pragma unroll
+            for (int q = 0; q < RPW; ++q) {
+                uint32_t qi, qids;
+                uint64_t qb, qe;
+                row_of(q, qi, qb, qe, qids);
+                if (l == 0) trow[w + kWaves * q] = qi;
+                if (g == q) cnt = qi == kNoRow ? 0u : uint32_t(qe - qb);
+            }
+            // Sources: id t of row g (lane 32 (g % 2) + t of idr[g / 2]); past
+            // the row's end its last edge again (weight 0), and an empty row
+            // reads its first id slot (padding or the next row's).
+            uint32_t jl[kEPL];
+#pragma unroll
+            for (int t = 0; t < kEPL; ++t) {
+                const int src = 4 * (32 * (g & 1) + max(min(t, int(cnt) - 1), 0));
+                const uint32_t v0 = uint32_t(__builtin_amdgcn_ds_bpermute(src, int(idr[0])));
+                const uint32_t v1 = uint32_t(__builtin_amdgcn_ds_bpermute(src, int(idr[1])));
+                jl[t] = (g >> 1) ? v1 : v0;
+            }
+            uint32_t raw[kSB][kEPL];
+            float rsep[kEPL];
+            load_batch<RSEP, kEPL>(a.xr, a.R, jl, l, raw, rsep);
+            // Head lanes score their row's edges for head n: the row max, the
+            // weights and their hi / lo parts, the denominator.
+            const float Lq = __shfl(Lall, 8 * g + n % 8);
+            float sc[kEPL];
+            float mq = -INFINITY;
+#pragma unroll
+            for (int t = 0; t < kEPL; ++t) {
+                const float r = RSEP ? rsep[t]
+                                     : __builtin_bit_cast(
+                                           float, __builtin_amdgcn_mov_dpp(int(raw[3][t]), 0x128, 0xF, 0xF, false));
+                sc[t] = (head && t < int(cnt)) ? leaky(Lq + r) : -INFINITY;
+                mq = fmaxf(mq, sc[t]);
+            }
+            const float mz = cnt > 0 ? mq : 0.0f;  // (an empty row: every weight 0)
+            uint32_t hw[2], lw[2];
+            float ps = 0.0f;
+#pragma unroll
+            for (int q2 = 0; q2 < 2; ++q2) {
+                const float p0 = exp_w(sc[2 * q2] - mz);  // -inf past the end: 0
+                const float p1 = exp_w(sc[2 * q2 + 1] - mz);
+                ps += p0 + p1;
+                hw[q2] = bf16x2(p0, p1);
+                lw[q2] = bf16x2(p0 - __builtin_bit_cast(float, hw[q2] << 16),
+                                p1 - __builtin_bit_cast(float, hw[q2] & 0xffff0000u));
+            }
+            const int r = w + kWaves * g;  // the lane's tile row
+            if (head) {
+                smd[r * 8 + n] = cnt > 0 ? mq : 0.0f;
+                smd[(TR + r) * 8 + n] = cnt > 0 ? ps : 0.0f;
+                tden[n * (TR + 1) + r] = ps;
+            }
+            // Pass hf: lane (g, n) supplies A row n at k = 4 g .. 4 g + 3, the
+            // weights of head 4 hf + n % 4 from its k group's head lane where
+            // row n / 4 is its own (g), zeros elsewhere.
+#pragma unroll
+            for (int hf = 0; hf < 2; ++hf) {
+                const int srcl = 4 * (16 * g + 4 * hf + n % 4);
+                const bool mine = n / 4 == g;
+                uint32_t ah[2], al[2];
+#pragma unroll
+                for (int q2 = 0; q2 < 2; ++q2) {
+                    const uint32_t th = uint32_t(__builtin_amdgcn_ds_bpermute(srcl, int(hw[q2])));
+                    const uint32_t tl = uint32_t(__builtin_amdgcn_ds_bpermute(srcl, int(lw[q2])));
+                    ah[q2] = mine ? th : 0u;
+                    al[q2] = mine ? tl : 0u;
                 }
-            }
-            const float den = total_den(s.den);  // against the reference max s.m
-            if (head && g == 0) {
-                // empty row: max 0, denominator 0 (ref_fp32.cpp:11); else the
-                // denominator against the row max, sum e^(s - M) = den e^(m - M)
-                smd[r * 8 + n] = end > beg ? s.mx : 0.0f;
-                smd[(TR + r) * 8 + n] = end > beg ? den * exp_w(s.m - s.mx) : 0.0f;
-                tden[n * (TR + 1) + r] = den;  // against the reference max, as U
-            }
-            {
-                // After fold_pair, lane (g, n) holds U of head 4 (g % 2) + q + (g >= 2)
-                // for q = 0, 2.  Element (head h, feature pair P = 16 sb + n) of tile
-                // row r sits at block (h, P / 8[, hl]) + 32 r + 4 (P % 8): a per-lane
-                // base plus a compile-time offset for each (q, sb, hl); block index
-                // ((h * kMaxKS + ks) * 2 + hl) with hi + lo, (buf * 8 + h) * kMaxKS + ks
-                // without.  (With KS <= 7 the words of R, 56..63, fall in k step 7.)
-                const int gh = g & 1, up = g >> 1;
-                unsigned char* base =
-                    slds + 32 * r + 4 * (n % 8) + kHalfOff * gh +
-                    (HL ? 8 * kMaxKS * gh + 2 * kMaxKS * up + 2 * (n / 8)
-                        : buf * 8 * kMaxKS + 4 * kMaxKS * gh + kMaxKS * up + n / 8) *
-                        BLK;
 #pragma unroll
                 for (int sb = 0; sb < kSB; ++sb) {
+                    uint32_t ev[2], od[2];
+#pragma unroll
+                    for (int q2 = 0; q2 < 2; ++q2) {
+                        const uint32_t w0 = raw[sb][2 * q2], w1 = raw[sb][2 * q2 + 1];
+                        ev[q2] = __builtin_amdgcn_perm(w1, w0, 0x05040100u);
+                        od[q2] = __builtin_amdgcn_perm(w1, w0, 0x07060302u);
+                    }
+                    const f32x4 z = {0.0f, 0.0f, 0.0f, 0.0f};
+                    const f32x4 eh = Mfma<kEPL>::run(ah, ev, z), el = Mfma<kEPL>::run(al, ev, z);
+                    const f32x4 oh = Mfma<kEPL>::run(ah, od, z), ol = Mfma<kEPL>::run(al, od, z);
+                    // D register x of lane (g, n): A row 4 g + x, i.e. row g's head
+                    // 4 hf + x, feature pair 16 sb + n; an empty row stages +0.
                     const int ks = 2 * sb + n / 8;
                     if (ks >= KS) continue;
 #pragma unroll
-                    for (int q = 0; q < 4; q += 2) {
-                        const float s0 = fold_pair(s.d[2 * sb][q], s.d[2 * sb][q + 1]);
-                        const float s1 = fold_pair(s.d[2 * sb + 1][q], s.d[2 * sb + 1][q + 1]);
-                        const uint32_t hw = bf16x2(s0, s1);
-                        if constexpr (HL) {
-                            const uint32_t lw = bf16x2(s0 - __builtin_bit_cast(float, hw << 16),
-                                                       s1 - __builtin_bit_cast(float, hw & 0xffff0000u));
-                            unsigned char* e = base + (2 * kMaxKS * q + 4 * sb) * BLK;
-                            *reinterpret_cast<uint32_t*>(e) = hw;
-                            *reinterpret_cast<uint32_t*>(e + BLK) = lw;
-                        } else {
-                            *reinterpret_cast<uint32_t*>(base + (kMaxKS * q + 2 * sb) * BLK) = hw;
+                    for (int x = 0; x < 4; ++x) {
+                        const int h = 4 * hf + x;
+                        const float s0 = eh[x] + el[x], s1 = oh[x] + ol[x];
+                        *reinterpret_cast<uint32_t*>(slds + 32 * r + 4 * (n % 8) + (h >= 4 ? kHalfOff : 0) +
+                                                     ((buf * 8 + h) * kMaxKS + ks) * BLK) =
+                            cnt > 0 ? bf16x2(s0, s1) : 0u;
+                    }
+                }
+            }
+            // (the projection's W fragment loads stay below: hoisted into the
+            // batch they would hold their registers across its MFMAs)
+            __builtin_amdgcn_sched_barrier(0);
+        } else {
+            // Each row's first batch is requested before the previous row's
+            // epilogue (its loads then travel while that row's sums are staged).
+            Batch<kEPL> pre;
+            bool have_pre = false;  // wave-uniform
+#pragma unroll 1
+            for (int rr = 0; rr < RPW; ++rr) {
+                const int r = w + kWaves * rr;
+                uint32_t i, ids;
+                uint64_t beg, end;
+                row_of(rr, i, beg, end, ids);
+                const float Lr = __shfl(Lall, 8 * rr + n % 8);
+                if (l == 0) trow[r] = i;
+                if (i == kNoRow) continue;
+                Sums s;
+                zero_sums(s);
+                s.L = head || !RSEP ? Lr : 0.0f;  // (lanes h + 8 score half of head h's edges)
+                s.m = s.mx = -INFINITY;
+                if (!have_pre && beg < end) first_batch<RSEP>(a.xr, a.R, beg, end, l, ids, 32 * (rr % 2), pre);
+                gather_sums<false, RSEP, kEPL, true>(a.pcol, a.xr, a.R, beg, end, l, s, ids, 32 * (rr % 2), pre);
+                have_pre = false;
+                if (rr + 1 < RPW) {
+                    uint32_t ni, nids;
+                    uint64_t nb, ne;
+                    row_of(rr + 1, ni, nb, ne, nids);
+                    if (ni != kNoRow && nb < ne) {
+                        first_batch<RSEP>(a.xr, a.R, nb, ne, l, nids, 32 * ((rr + 1) % 2), pre);
+                        have_pre = true;
+                    }
+                }
+                const float den = total_den(s.den);  // against the reference max s.m
+                if (head && g == 0) {
+                    // empty row: max 0, denominator 0 (ref_fp32.cpp:11); else the
+                    // denominator against the row max, sum e^(s - M) = den e^(m - M)
+                    smd[r * 8 + n] = end > beg ? s.mx : 0.0f;
+                    smd[(TR + r) * 8 + n] = end > beg ? den * exp_w(s.m - s.mx) : 0.0f;
+                    tden[n * (TR + 1) + r] = den;  // against the reference max, as U
+                }
+                {
+                    // After fold_pair, lane (g, n) holds U of head 4 (g % 2) + q + (g >= 2)
+                    // for q = 0, 2.  Element (head h, feature pair P = 16 sb + n) of tile
+                    // row r sits at block (h, P / 8[, hl]) + 32 r + 4 (P % 8): a per-lane
+                    // base plus a compile-time offset for each (q, sb, hl); block index
+                    // ((h * kMaxKS + ks) * 2 + hl) with hi + lo, (buf * 8 + h) * kMaxKS + ks
+                    // without.  (With KS <= 7 the words of R, 56..63, fall in k step 7.)
+                    const int gh = g & 1, up = g >> 1;
+                    unsigned char* base =
+                        slds + 32 * r + 4 * (n % 8) + kHalfOff * gh +
+                        (HL ? 8 * kMaxKS * gh + 2 * kMaxKS * up + 2 * (n / 8)
+                            : buf * 8 * kMaxKS + 4 * kMaxKS * gh + kMaxKS * up + n / 8) *
+                            BLK;
+#pragma unroll
+                    for (int sb = 0; sb < kSB; ++sb) {
+                        const int ks = 2 * sb + n / 8;
+                        if (ks >= KS) continue;
+#pragma unroll
+                        for (int q = 0; q < 4; q += 2) {
+                            const float s0 = fold_pair(s.d[2 * sb][q], s.d[2 * sb][q + 1]);
+                            const float s1 = fold_pair(s.d[2 * sb + 1][q], s.d[2 * sb + 1][q + 1]);
+                            const uint32_t hw = bf16x2(s0, s1);
+                            if constexpr (HL) {
+                                const uint32_t lw = bf16x2(s0 - __builtin_bit_cast(float, hw << 16),
+                                                           s1 - __builtin_bit_cast(float, hw & 0xffff0000u));
+                                unsigned char* e = base + (2 * kMaxKS * q + 4 * sb) * BLK;
+                                *reinterpret_cast<uint32_t*>(e) = hw;
+                                *reinterpret_cast<uint32_t*>(e + BLK) = lw;
+                            } else {
+                                *reinterpret_cast<uint32_t*>(base + (kMaxKS * q + 2 * sb) * BLK) = hw;
+                            }
                         }
                     }
                 }
@@ -872,32 +986,48 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4
 }
 
 // One block per kWaves chunks of split rows, then a resident grid of tile
-// blocks (two per CU).  a.counter holds chunks + 2 entries, zero between
-// launches.
-template <int KS, bool HL, int TR, int DIM>
+// blocks (two per CU) over the sorted positions [a.row_lo, a.rows).  a.counter
+// holds chunks + 2 entries, zero between launches.  SHORT: tile blocks only.
+template <int KS, bool HL, int TR, int DIM, bool SHORT>
 hipError_t launch_tiles_hl(AfsArgs a, hipStream_t s, int cus) {
-    const uint64_t tiles = (a.rows + TR - 1) / TR;
+    if (a.row_lo > a.rows) return hipErrorInvalidValue;
+    const uint64_t tiles = (a.rows - a.row_lo + TR - 1) / TR;
     uint64_t blocks = uint64_t(cus) * 2;
     if (blocks > tiles) blocks = tiles;
-    const uint64_t chunk_blocks = (a.chunks + kWaves - 1) / kWaves;
+    const uint64_t chunk_blocks = SHORT ? 0 : (a.chunks + kWaves - 1) / kWaves;
     if (blocks + chunk_blocks == 0) return hipSuccess;
     if (tiles >= (uint64_t(1) << 31) || blocks + chunk_blocks > 0x7fffffffu) return hipErrorInvalidValue;
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_afs_tiles<KS, HL, TR, DIM>),
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_afs_tiles<KS, HL, TR, DIM, SHORT>),
                                        hipFuncAttributeMaxDynamicSharedMemorySize, kLdsBytes);
     if (e != hipSuccess) return e;
     a.tile_blocks = uint32_t(blocks);
-    k_afs_tiles<KS, HL, TR, DIM><<<dim3(uint32_t(chunk_blocks + blocks)), kThreads, kLdsBytes, s>>>(a);
+    k_afs_tiles<KS, HL, TR, DIM, SHORT><<<dim3(uint32_t(chunk_blocks + blocks)), kThreads, kLdsBytes, s>>>(a);
     return hipGetLastError();
 }
 
 // FP32 outputs (the last layer, no ELU) keep U as hi + lo; bf16-stored hidden
-// outputs stage one bf16.
+// outputs stage one bf16, and their rows of at most kShortDeg edges (positions
+// [0, a.short_rows)) go to the short-row instance in a launch of their own
+// after the others (the two launches share the tile counters, which each
+// leaves at zero).
 template <int KS>
 hipError_t launch_tiles(const AfsArgs& a, hipStream_t s, int cus) {
     if (a.hidden != (a.out32 == nullptr) || (a.out32 == nullptr) == (a.outbf == nullptr)) return hipErrorInvalidValue;
-    if (a.dim == 64)
-        return a.out32 ? launch_tiles_hl<KS, true, 16, 64>(a, s, cus) : launch_tiles_hl<KS, false, kTileBf16, 64>(a, s, cus);
-    return a.out32 ? launch_tiles_hl<KS, true, 16, 32>(a, s, cus) : launch_tiles_hl<KS, false, kTileBf16, 32>(a, s, cus);
+    if (a.short_rows > a.rows) return hipErrorInvalidValue;
+    AfsArgs al = a;
+    al.row_lo = 0;
+    if (a.out32)
+        return a.dim == 64 ? launch_tiles_hl<KS, true, 16, 64, false>(al, s, cus)
+                           : launch_tiles_hl<KS, true, 16, 32, false>(al, s, cus);
+    al.row_lo = a.short_rows;
+    hipError_t e = a.dim == 64 ? launch_tiles_hl<KS, false, kTileBf16, 64, false>(al, s, cus)
+                               : launch_tiles_hl<KS, false, kTileBf16, 32, false>(al, s, cus);
+    if (e != hipSuccess || a.short_rows == 0) return e;
+    AfsArgs as = a;
+    as.rows = a.short_rows;
+    as.row_lo = 0;
+    return a.dim == 64 ? launch_tiles_hl<KS, false, kTileBf16, 64, true>(as, s, cus)
+                       : launch_tiles_hl<KS, false, kTileBf16, 32, true>(as, s, cus);
 }
 
 }  // namespace

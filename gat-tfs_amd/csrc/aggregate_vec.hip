@@ -113,6 +113,45 @@ struct Lane {
     uint32_t smask;    // all ones in the lanes of edge slot 1 (batch, O32)
 };
 
+// The weights and sums of a batch whose rows z and scores s are in (the form
+// without R from Z; z is 0 and s unused for the edges outside the row, ok
+// false): the batch max moves m (the sums rescaled by e^(m_old - m_new)),
+// then each edge adds p = e^(s - m) to den and p z to the sums, in edge order.
+// Products fuse into FMAs only within a statement, so the operations, and the
+// bits, do not depend on the code around the sums (k_agg_vec, k_agg_vec_short).
+template <class C>
+__device__ inline void batch_sums(const uint4 (&z)[C::U][C::VPL], const float (&s)[C::U][C::VPL],
+                                  const bool (&ok)[C::U], Lane<C>& st) {
+#pragma clang fp contract(on)
+#pragma unroll
+    for (int v = 0; v < C::VPL; ++v) {
+        float mb = -INFINITY;
+#pragma unroll
+        for (int u = 0; u < C::U; ++u) {
+            const float mx = max_quiet(mb, s[u][v]);
+            mb = ok[u] ? mx : mb;
+        }
+        const float mn = max_quiet(st.m[v], mb);
+        const float sc = mn > st.m[v] ? exp_w(st.m[v] - mn) : 1.0f;  // exp(-inf) = 0 on a slot's first edge
+        st.m[v] = mn;
+        st.den[v] *= sc;
+#pragma unroll
+        for (int x = 0; x < C::VEC; ++x) st.acc[v * C::VEC + x] *= sc;
+    }
+#pragma unroll
+    for (int u = 0; u < C::U; ++u) {
+#pragma unroll
+        for (int v = 0; v < C::VPL; ++v) {
+            const float p = ok[u] ? exp_w(s[u][v] - st.m[v]) : 0.0f;
+            st.den[v] += p;
+            float f[C::VEC];
+            unpack(z[u][v], f);
+#pragma unroll
+            for (int x = 0; x < C::VEC; ++x) st.acc[v * C::VEC + x] += p * f[x];
+        }
+    }
+}
+
 // One batch of edges [base, base + BATCH) clipped to end.  RZ (bf16 8 x 32):
 // R of the source is recomputed from the gathered row, R = Z_bf16 . aR, as an
 // FMA chain over the lane's 8 features and (s0 + s1) + (s2 + s3) over the 4
@@ -224,33 +263,7 @@ __device__ inline void batch(uint32_t left, const uint32_t (&js)[C::BATCH], cons
         }
         return;
     }
-#pragma unroll
-    for (int v = 0; v < C::VPL; ++v) {
-        float mb = -INFINITY;
-#pragma unroll
-        for (int u = 0; u < C::U; ++u) {
-            const float mx = max_quiet(mb, s[u][v]);
-            mb = ok[u] ? mx : mb;
-        }
-        const float mn = max_quiet(st.m[v], mb);
-        const float sc = mn > st.m[v] ? exp_w(st.m[v] - mn) : 1.0f;  // exp(-inf) = 0 on a slot's first edge
-        st.m[v] = mn;
-        st.den[v] *= sc;
-#pragma unroll
-        for (int x = 0; x < C::VEC; ++x) st.acc[v * C::VEC + x] *= sc;
-    }
-#pragma unroll
-    for (int u = 0; u < C::U; ++u) {
-#pragma unroll
-        for (int v = 0; v < C::VPL; ++v) {
-            const float p = ok[u] ? exp_w(s[u][v] - st.m[v]) : 0.0f;
-            st.den[v] += p;
-            float f[C::VEC];
-            unpack(z[u][v], f);
-#pragma unroll
-            for (int x = 0; x < C::VEC; ++x) st.acc[v * C::VEC + x] += p * f[x];
-        }
-    }
+    batch_sums<C>(z, s, ok, st);
 }
 
 // The edge slots' states merged: afterwards every lane holds its heads'
@@ -509,8 +522,9 @@ __device__ inline void run_chunk(const VArgs<ZT>& a, uint64_t c, int lane, int s
     finish_row<C>(i, tot, dtot, M, st.h, slot, sub, a.hidden, a.mx, a.den, a.out32, a.outbf);
 }
 
+// short_rows: the positions [0, short_rows) are k_agg_vec_short's.
 template <class C, class ZT, bool RZ, bool O32>
-__global__ void __launch_bounds__(kThreads) k_agg_vec(VArgs<ZT> a) {
+__global__ void __launch_bounds__(kThreads) k_agg_vec(VArgs<ZT> a, uint64_t short_rows) {
     // The wave index is made wave-uniform so that row bounds and source ids
     // come in through scalar loads.
     const int w = __builtin_amdgcn_readfirstlane(int(threadIdx.x) / kWave);
@@ -524,7 +538,7 @@ __global__ void __launch_bounds__(kThreads) k_agg_vec(VArgs<ZT> a) {
     }
     // ---------------- whole row, heaviest first
     const uint64_t widx = item - a.sp.chunks;
-    if (widx >= a.rows) return;
+    if (widx >= a.rows - short_rows) return;
     const uint64_t k = a.rows - 1 - widx;
     const uint32_t i = a.perm[k];
     const uint64_t beg = a.prow[k], end = a.prow[k + 1];
@@ -542,6 +556,87 @@ __global__ void __launch_bounds__(kThreads) k_agg_vec(VArgs<ZT> a) {
 #pragma unroll
         for (int v = 0; v < C::VPL; ++v) st.m[v] = 0.0f;
     finish_row<C>(i, st.acc, st.den, st.m, st.h, slot, sub, a.hidden, a.mx, a.den, a.out32, a.outbf);
+}
+
+// Rows of at most kShortDeg edges, the sorted positions [0, a.short_rows), for
+// bf16 rows with R in its own array: four consecutive positions per wave.  One
+// round trip brings the four rows' bounds, one their ids and L, and one every
+// edge's row and R, where a wave per row waits for those three round trips
+// for each row (a 2^22-node R-MAT graph has 3.0M such rows, 4.6 % of its
+// edges, which took 1.8 ms of its 8 x 64 layer that way).  Every load is
+// issued, so that they leave together: edges past a row's end read its last
+// edge again (an empty row its first id slot: padding or the next row's first
+// id), and their rows and R are replaced by 0 before the sums, which so take
+// the values and the operations of batch() on that row (U = 4 where the
+// one-row-per-wave kernel has 8: the loads it skips add +0, which leaves its
+// sums, never -0, unchanged).
+template <class C>
+__global__ void __launch_bounds__(kThreads) k_agg_vec_short(VArgs<uint16_t> a, uint64_t short_rows) {
+    static_assert(C::VPL == 1 && C::BATCH >= int(kShortDeg), "one vector per lane and edge, one batch per row");
+    constexpr int RW = 4;  // rows per wave
+    constexpr uint32_t kNone = 0xffffffffu;
+    const int w = __builtin_amdgcn_readfirstlane(int(threadIdx.x) / kWave);
+    const int lane = threadIdx.x % kWave;
+    const int slot = C::EPI > 1 ? lane / C::LPR : 0;
+    const int sub = C::EPI > 1 ? lane % C::LPR : lane;
+    const uint64_t k0 = (uint64_t(blockIdx.x) * kWavesPerBlock + w) * RW;
+    if (k0 >= short_rows) return;
+    const auto* perm = read_only(a.perm);
+    const auto* prow = read_only(a.prow);
+    uint32_t ri[RW], cnt[RW];
+    uint64_t rb[RW];
+#pragma unroll
+    for (int r = 0; r < RW; ++r) {
+        const bool in = k0 + r < short_rows;
+        const uint64_t k = in ? k0 + r : k0;
+        const uint32_t i = perm[k];
+        const uint64_t b = prow[k], e = prow[k + 1];
+        // (the launch hands over rows of at most kShortDeg edges only)
+        const bool good = in && i < a.n && b <= e && e <= a.e && e - b <= uint64_t(kShortDeg);
+        ri[r] = good ? i : kNone;
+        rb[r] = good ? b : 0;  // (a row not stored reads ids from pcol[0]: valid sources)
+        cnt[r] = good ? uint32_t(e - b) : 0u;
+    }
+    Lane<C> st[RW];
+    uint4 z[RW][C::U];
+    float rv[RW][C::U];
+#pragma unroll
+    for (int r = 0; r < RW; ++r) {
+        init_lane<C, uint16_t, false>(a, sub, st[r]);
+        st[r].L[0] = a.L[uint64_t(ri[r] == kNone ? 0u : ri[r]) * C::K + st[r].h[0]];
+        st[r].m[0] = -INFINITY;
+        uint32_t js[C::BATCH], jc[C::BATCH];
+        load_ids<C>(a.pcol, rb[r], js);
+        jc[0] = js[0];
+#pragma unroll
+        for (int t = 1; t < C::BATCH; ++t) jc[t] = uint32_t(t) < cnt[r] ? js[t] : jc[t - 1];
+#pragma unroll
+        for (int u = 0; u < C::U; ++u) {
+            uint32_t j = jc[u * C::EPI];
+#pragma unroll
+            for (int q = 1; q < C::EPI; ++q) j = slot == q ? jc[u * C::EPI + q] : j;
+            z[r][u] = *reinterpret_cast<const uint4*>(a.Z + uint64_t(j) * C::W + sub * C::VEC);
+            rv[r][u] = a.R[uint64_t(j) * C::K + st[r].h[0]];
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < RW; ++r) {
+        bool ok[C::U];
+        uint4 zz[C::U][1];
+        float sc[C::U][1];
+#pragma unroll
+        for (int u = 0; u < C::U; ++u) {
+            ok[u] = slot < int(cnt[r]) - u * C::EPI;
+            zz[u][0] = ok[u] ? z[r][u] : make_uint4(0, 0, 0, 0);
+            sc[u][0] = leaky(st[r].L[0] + (ok[u] ? rv[r][u] : 0.0f));
+        }
+        if (cnt[r] > 0) batch_sums<C>(zz, sc, ok, st[r]);
+        merge_slots<C>(st[r]);
+        if (cnt[r] == 0) st[r].m[0] = 0.0f;  // empty row: max 0, denominator 0, output 0
+        if (ri[r] != kNone)
+            finish_row<C>(ri[r], st[r].acc, st[r].den, st[r].m, st[r].h, slot, sub, a.hidden, a.mx, a.den, a.out32,
+                          a.outbf);
+    }
 }
 
 // Edge loads per lane and batch of the R-from-Z form.
@@ -729,24 +824,40 @@ bool offsets32(uint64_t n) {
     return n <= (uint64_t(1) << 32) / (uint64_t(C::W) * sizeof(ZT));
 }
 
+// Split-row chunks and rows, one wave each, then (bf16 rows with R in its own
+// array) the rows of at most kShortDeg edges four to a wave in a launch of
+// their own.
 template <class C, class ZT>
 hipError_t run(const AggArgs& g, const RowBins& bins, const SplitTable& t, hipStream_t s) {
     VArgs<ZT> a{g.prow, g.pcol, g.perm, g.left, g.right, static_cast<const ZT*>(g.feat), g.hidden, g.mx, g.den,
                 g.out32, g.outbf, g.n, g.e, bins.split_begin,
                 SplitArgs{t.chunks, t.chunk_k, t.chunk_first, t.chunk_edges, t.mchunk, t.part, t.counter}, g.ar};
-    const uint64_t items = t.chunks + bins.split_begin;
+    uint64_t short_rows = 0;
+    if constexpr (sizeof(ZT) == 2) {
+        if (!g.r_from_z) short_rows = std::min(bins.short_end, bins.split_begin);
+    }
+    const uint64_t items = t.chunks + bins.split_begin - short_rows;
+    if constexpr (sizeof(ZT) == 2) {
+        if (short_rows) {
+            using CS = Cfg<uint16_t, C::W, C::K, 4>;
+            const uint64_t waves = (short_rows + 3) / 4;
+            k_agg_vec_short<CS>
+                <<<dim3(uint32_t((waves + kWavesPerBlock - 1) / kWavesPerBlock)), kThreads, 0, s>>>(a, short_rows);
+            if (hipError_t e = hipGetLastError(); e != hipSuccess || !items) return e;
+        }
+    }
     if (!items) return hipSuccess;
     const dim3 grid(uint32_t((items + kWavesPerBlock - 1) / kWavesPerBlock));
     if constexpr (sizeof(ZT) == 2 && C::W == 256) {
         if (g.r_from_z) {
             if (!g.ar) return hipErrorInvalidValue;
             using CR = Cfg<ZT, C::W, C::K, kURz>;
-            if (offsets32<CR, ZT>(g.n)) k_agg_vec<CR, ZT, true, true><<<grid, kThreads, 0, s>>>(a);
-            else k_agg_vec<CR, ZT, true, false><<<grid, kThreads, 0, s>>>(a);
+            if (offsets32<CR, ZT>(g.n)) k_agg_vec<CR, ZT, true, true><<<grid, kThreads, 0, s>>>(a, 0);
+            else k_agg_vec<CR, ZT, true, false><<<grid, kThreads, 0, s>>>(a, 0);
             return hipGetLastError();
         }
     }
-    k_agg_vec<C, ZT, false, false><<<grid, kThreads, 0, s>>>(a);
+    k_agg_vec<C, ZT, false, false><<<grid, kThreads, 0, s>>>(a, short_rows);
     return hipGetLastError();
 }
 

@@ -67,8 +67,9 @@ int bind(gatgpu_ctx* c) {
 
 // Sorted-position boundaries of the degree bins.
 int compute_bins(gatgpu_ctx* c) {
-    // Thresholds: block bin, then each plan's split degree.
-    uint32_t thr[1 + kPlans] = {c->block_min ? c->block_min - 1 : 0};
+    // Thresholds: block bin, each plan's split degree, then the short rows.
+    uint32_t thr[2 + kPlans] = {c->block_min ? c->block_min - 1 : 0};
+    thr[1 + kPlans] = kShortDeg;
     uint32_t maxdeg = 0;  // degrees are sorted ascending
     if (c->n) HIPCHECK(c, hipMemcpy(&maxdeg, c->sorted_deg + (c->n - 1), 4, hipMemcpyDeviceToHost));
     const bool small = c->e < kSmallGraphEdges;
@@ -84,17 +85,18 @@ int compute_bins(gatgpu_ctx* c) {
     }
     // block_min 0 means every row takes a block.
     HIPCHECK(c, c->small.ensure(128));
-    // small[]: [0,4) max degree, [8,16) neighbor steps, [16,32) thresholds, [40,72) positions
+    // small[]: [0,4) max degree, [8,16) neighbor steps, [16,36) thresholds, [40,80) positions
     uint32_t* dthr = reinterpret_cast<uint32_t*>(c->small.as<char>() + 16);
     uint64_t* dpos = reinterpret_cast<uint64_t*>(c->small.as<char>() + 40);
     HIPCHECK(c, hipMemcpyAsync(dthr, thr, sizeof(thr), hipMemcpyHostToDevice, c->stream));
-    HIPCHECK(c, launch_count_le(c->sorted_deg, c->n, dthr, 1 + kPlans, dpos, c->stream));
-    uint64_t pos[1 + kPlans];
+    HIPCHECK(c, launch_count_le(c->sorted_deg, c->n, dthr, 2 + kPlans, dpos, c->stream));
+    uint64_t pos[2 + kPlans];
     HIPCHECK(c, hipMemcpyAsync(pos, dpos, sizeof(pos), hipMemcpyDeviceToHost, c->stream));
     HIPCHECK(c, hipStreamSynchronize(c->stream));
     RowBins b;
     b.n = c->n;
     b.block_begin = c->block_min ? pos[0] : 0;
+    b.short_end = pos[1 + kPlans];
     c->bins = b;
     std::vector<uint64_t> prow;
     for (int q = 0; q < kPlans; ++q) {
@@ -329,6 +331,7 @@ int run_layer_af(gatgpu_ctx* c, int l, bool hidden, const float* src32, const ui
         a.e = c->e;
         const SplitPlan& P = c->plans[kPlanAf];
         a.rows = P.bins.split_begin;
+        a.short_rows = std::min(P.bins.short_end, a.rows);
         a.chunks = P.table.chunks;
         a.chunk_k = P.table.chunk_k;
         a.chunk_first = P.table.chunk_first;

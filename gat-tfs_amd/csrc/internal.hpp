@@ -237,11 +237,14 @@ hipError_t launch_projection_f32(const ProjF32Args& a, hipStream_t s);
 void pack_projection_f32(const float* w, const float* blr, int in, int heads, int dim, std::vector<float>& out);
 
 // aggregate.hip
+// Rows of at most this many edges share the sum form's 16-edge batches (four
+// rows a batch).
+constexpr uint32_t kShortDeg = 4;
 struct RowBins {
     // Sorted positions [0, n) split by degree: [0, block_begin) one wave per
     // row, [block_begin, split_begin) one block per row, [split_begin, n)
-    // several blocks per row.
-    uint64_t block_begin = 0, split_begin = 0, n = 0;
+    // several blocks per row.  [0, short_end): rows of at most kShortDeg edges.
+    uint64_t block_begin = 0, split_begin = 0, n = 0, short_end = 0;
 };
 struct AggArgs {
     const uint64_t* prow;
@@ -359,6 +362,8 @@ struct AfsArgs {
     uint16_t* outbf;
     uint64_t n, e;
     uint64_t rows;       // non-split rows: sorted positions [0, rows)
+    uint64_t short_rows; // of them [0, short_rows) have at most kShortDeg edges (bf16-stored outputs: shared batches)
+    uint64_t row_lo;     // set by the launch: the positions [row_lo, rows) one kernel launch takes
     uint64_t chunks;
     const uint32_t* chunk_k;
     const uint32_t* chunk_first;

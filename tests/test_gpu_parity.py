@@ -770,6 +770,93 @@ def test_aggregate_first_partial_tiles(gpu_ctx, D):
             assert oracle.errors(r[k_], gpu_ctx.stage(0, k_))["relative_l2"] < 1e-4, (hidden, k_)
 
 
+def short_row_graph(n, seed, heavy):
+    """Rows of 0..4 edges (a third of them one edge), and with `heavy` a tenth
+    of the rows with 5..40; distinct random sources."""
+    rng = np.random.default_rng(seed)
+    deg = rng.choice(np.array([0, 1, 1, 2, 3, 4]), size=n)
+    if heavy:
+        pick = rng.choice(n, n // 10, replace=False)
+        deg[pick] = rng.integers(5, 41, pick.size)
+    row = np.zeros(n + 1, np.uint64)
+    row[1:] = np.cumsum(deg)
+    col = np.concatenate([rng.choice(n, int(k), replace=False) for k in deg]).astype(np.uint32)
+    return row, col
+
+
+@pytest.mark.parametrize("D,d,heavy", [(100, 32, True), (128, 64, True), (100, 32, False)])
+def test_sum_form_short_rows(gpu_ctx, D, d, heavy):
+    """Rows of at most 4 edges share one 16-edge batch four at a time, in a
+    launch of their own (without heavier rows, the only one).  On a graph of
+    mostly such rows, empty rows included: the row max equals max_j
+    LeakyReLU(L_i + R_j) over the GPU's own L and R bit for bit, an empty row
+    gives max, den and output 0, and den and the bf16 outputs equal R0 on
+    bf16-rounded X and W, over all rows and over the short rows alone."""
+    n = 2011
+    row, col = short_row_graph(n, 5, heavy)
+    deg = np.diff(row.astype(np.int64))
+    assert np.mean(deg <= 4) > 0.85 and np.any(deg == 0)
+    x = inputs.normal((n, D), 41)
+    p = inputs.glorot_param(D, 8, d, 42)
+    qp = dict(p, w=oracle.quantize_bf16(p["w"]))
+    r = oracle.ref_layer(row, col, oracle.quantize_bf16(x), qp, True)
+    gpu_ctx.set_graph(row, col)
+    gpu_ctx.set_layer(0, p)
+    gpu_ctx.set_input(x)
+    gpu_ctx.layer_forward(0, gatgpu.BF16, gatgpu.AGGREGATE_FIRST, True)
+    out, den, M = (gpu_ctx.stage(0, k) for k in ("out", "den", "max"))
+    L, R = gpu_ctx.stage(0, "left"), gpu_ctx.stage(0, "right")
+    want = np.zeros_like(M)
+    for i in np.nonzero(deg)[0]:  # FP32 as the kernel forms it: L + R, then max(s, 0.2 s)
+        s = L[i] + R[col[int(row[i]):int(row[i + 1])]]
+        want[i] = np.max(np.maximum(s, np.float32(0.2) * s), axis=0)
+    assert np.array_equal(M.view(np.uint32), want.view(np.uint32))
+    empty = deg == 0
+    assert np.all(M[empty] == 0) and np.all(den[empty] == 0) and np.all(out[empty] == 0)
+    ref_out = oracle.quantize_bf16(r["out"])
+    short = deg <= 4
+    for sel in (slice(None), short):
+        e = oracle.errors(ref_out[sel], out[sel])
+        assert e["finite"] and e["relative_l2"] < 4e-3, e
+        assert oracle.errors(r["den"][sel], den[sel])["relative_l2"] < 1e-5
+
+
+@pytest.mark.parametrize("heavy", [True, False])
+def test_transform_first_short_rows(gpu_ctx, heavy):
+    """8 x 64 bf16 rows (R in its own array): rows of at most 4 edges go four
+    to a wave in a launch of their own (without heavier rows, the only one).
+    Over the GPU's own Z, L and R: the row max bit for bit, den and the FP32
+    output rows against a float64 softmax within FP32 summation error, empty
+    rows 0; and the outputs against R0."""
+    n = 2011
+    row, col = short_row_graph(n, 7, heavy)
+    deg = np.diff(row.astype(np.int64))
+    x = inputs.normal((n, 100), 43)
+    p = inputs.glorot_param(100, 8, 64, 44)
+    got = run_layer(gpu_ctx, row, col, x, p, False, gatgpu.BF16)
+    Z = gpu_ctx.stage(0, "z").astype(np.float64).reshape(n, 8, 64)
+    L, R, M, den, out = (got[k] for k in ("left", "right", "max", "den", "out"))
+    out = out.reshape(n, 8, 64)
+    for i in range(n):
+        b, e_ = int(row[i]), int(row[i + 1])
+        if b == e_:
+            assert np.all(M[i] == 0) and np.all(den[i] == 0) and np.all(out[i] == 0), i
+            continue
+        src = col[b:e_]
+        s = L[i][None, :] + R[src]
+        s = np.maximum(s, np.float32(0.2) * s)
+        assert np.array_equal(s.max(axis=0), M[i]), i
+        w = np.exp(s.astype(np.float64) - M[i].astype(np.float64))  # [edges][heads]
+        d64 = w.sum(axis=0)
+        assert np.all(np.abs(den[i] - d64) <= 1e-5 * d64), i
+        acc = np.einsum("eh,ehf->hf", w, Z[src])
+        mag = np.einsum("eh,ehf->hf", w, np.abs(Z[src])) / d64[:, None]
+        assert np.all(np.abs(out[i] - acc / d64[:, None]) <= 1e-5 * mag + 1e-30), i
+    r = oracle.ref_layer(row, col, x, p, False)
+    e = oracle.errors(r["out"], got["out"])
+    assert e["finite"] and e["relative_l2"] < BF16_REL_L2, e
+
+
 def check_bf16_projection(gpu_ctx, w, D, K, d):
     row, col = w.graph()
     x = inputs.normal((w.n, D), 3)
