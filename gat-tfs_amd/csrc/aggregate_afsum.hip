@@ -887,6 +887,7 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4
         }
         // ---- wave h: the tile's U_h W_h / den_h.  B lane l reads tile row l % 16 (lanes
         // with l % 32 >= 16 repeat rows 0..15; their output columns are dropped).
+        uint32_t P0[2][4];  // heads of 64: block 0's stored pieces, kept for the whole-line stores
 #pragma unroll
         for (int b = 0; b < NBH; ++b) {
             if (b > 0) load_w(b);
@@ -905,10 +906,11 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4
                     dh = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wf[ks], bh, dh, 0, 0, 0);
                     dl = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wf[ks], bl, dl, 0, 0, 0);
                 } else {
-                    // even / odd k steps in two chains
+                    // even / odd k steps in two chains; heads of 64 one chain
+                    // (the registers of the second hold block 0's stored pieces)
                     const bf16x8 bv = __builtin_bit_cast(
                         bf16x8, *reinterpret_cast<const uint4*>(slds + ((buf * 8 + h) * kMaxKS + ks) * BLK + boff));
-                    if (ks % 2 == 0) dh = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wf[ks], bv, dh, 0, 0, 0);
+                    if (NBH == 2 || ks % 2 == 0) dh = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wf[ks], bv, dh, 0, 0, 0);
                     else dl = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wf[ks], bv, dl, 0, 0, 0);
                 }
             }
@@ -929,8 +931,9 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4
                 for (int q = 0; q < 2; ++q)
 #pragma unroll
                     for (int x = 0; x < 4; ++x)
-                        P[q][x] = bf16x2(elu_bf16((dh[8 * q + 2 * x] + dl[8 * q + 2 * x]) * inv),
-                                         elu_bf16((dh[8 * q + 2 * x + 1] + dl[8 * q + 2 * x + 1]) * inv));
+                        P[q][x] = NBH == 2 ? bf16x2(elu_bf16(dh[8 * q + 2 * x] * inv), elu_bf16(dh[8 * q + 2 * x + 1] * inv))
+                                           : bf16x2(elu_bf16((dh[8 * q + 2 * x] + dl[8 * q + 2 * x]) * inv),
+                                                    elu_bf16((dh[8 * q + 2 * x + 1] + dl[8 * q + 2 * x + 1]) * inv));
                 const int c = l & 3;
                 auto store_pair = [&](auto J) {
                     constexpr int j = decltype(J)::value;
@@ -947,8 +950,55 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4
                         *reinterpret_cast<uint4*>(a.outbf + uint64_t(ij) * (8 * DIM) + DIM * h + 32 * b + 16 * half +
                                                   8 * (c & 1)) = make_uint4(T[0], T[1], T[2], T[3]);
                 };
-                store_pair(std::integral_constant<int, 0>{});
-                store_pair(std::integral_constant<int, 1>{});
+                if constexpr (NBH == 1) {
+                    store_pair(std::integral_constant<int, 0>{});
+                    store_pair(std::integral_constant<int, 1>{});
+                } else if (b == 0) {
+#pragma unroll
+                    for (int q = 0; q < 2; ++q)
+#pragma unroll
+                        for (int x = 0; x < 4; ++x) P0[q][x] = P[q][x];
+                } else {
+                    // Heads of 64: the head's 128 bytes of a row are one line,
+                    // block b's piece q of half `half` at bytes 64 b + 32 half +
+                    // 16 q.  Slot p of a lane is block p / 2, piece p % 2; a 4 x
+                    // 4 transpose inside the lane quad (two DPP exchange stages,
+                    // lane c taking slot p from quad lane c ^ 1, then c ^ 2)
+                    // leaves lane c with slot c of rows 4a .. 4a + 3, so store j
+                    // writes row 4a + j whole from the 8 lanes of quad a (both
+                    // halves): 8 lines per instruction, where each block's
+                    // stores wrote half lines of 16 rows.
+                    uint32_t S[4][4], U[4][4], T[4][4];
+#pragma unroll
+                    for (int x = 0; x < 4; ++x) {
+                        S[0][x] = P0[0][x];
+                        S[1][x] = P0[1][x];
+                        S[2][x] = P[0][x];
+                        S[3][x] = P[1][x];
+                    }
+#pragma unroll
+                    for (int p = 0; p < 4; ++p)
+#pragma unroll
+                        for (int v = 0; v < 4; ++v) {
+                            const uint32_t o = uint32_t(__builtin_amdgcn_mov_dpp(int(S[p ^ 1][v]), 0xB1, 0xF, 0xF, false));
+                            U[p][v] = (c & 1) == (p & 1) ? S[p][v] : o;  // quad_perm [1, 0, 3, 2]
+                        }
+#pragma unroll
+                    for (int p = 0; p < 4; ++p)
+#pragma unroll
+                        for (int v = 0; v < 4; ++v) {
+                            const uint32_t o = uint32_t(__builtin_amdgcn_mov_dpp(int(U[p ^ 2][v]), 0x4E, 0xF, 0xF, false));
+                            T[p][v] = (c & 2) == (p & 2) ? U[p][v] : o;  // quad_perm [2, 3, 0, 1]
+                        }
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        const uint32_t ij = trow[(r & ~3) + j];
+                        if (ij != kNoRow)
+                            *reinterpret_cast<uint4*>(a.outbf + uint64_t(ij) * (8 * DIM) + DIM * h + 32 * (c / 2) +
+                                                      16 * half + 8 * (c % 2)) =
+                                make_uint4(T[j][0], T[j][1], T[j][2], T[j][3]);
+                    }
+                }
             } else {
                 // FP32 outputs (the last layer, no ELU): 16 tile rows, 64 bytes
                 // per lane.
