@@ -821,6 +821,50 @@ def test_sum_form_short_rows(gpu_ctx, D, d, heavy):
         assert oracle.errors(r["den"][sel], den[sel])["relative_l2"] < 1e-5
 
 
+TINY_GRAPHS = {
+    "one_node": ([0, 1], [0]),
+    "one_empty_node": ([0, 0], []),
+    "three_nodes_one_empty": ([0, 2, 2, 5], [0, 2, 1, 2, 0]),
+    "seven_nodes": ([0, 1, 3, 3, 7, 8, 12, 17], [0, 0, 1, 0, 1, 2, 3, 4, 0, 2, 4, 5, 6, 5, 4, 3, 2]),
+}
+
+
+@pytest.mark.parametrize("name", sorted(TINY_GRAPHS))
+def test_short_rows_tiny_graphs(gpu_ctx, name):
+    """Fewer rows than one tile or one four-row group, empty rows among them
+    (a graph with no edges at all included): the sum form (100 -> 8 x 32,
+    hidden) and the 8 x 64 bf16 transform-first layer equal R0 (on bf16-rounded
+    X and W for the sum form), the row max equals max_j LeakyReLU(L_i + R_j)
+    over the GPU's own L and R bit for bit and den a float64 softmax over them,
+    and an empty row gives max, den and output 0."""
+    row = np.array(TINY_GRAPHS[name][0], np.uint64)
+    col = np.array(TINY_GRAPHS[name][1], np.uint32)
+    n = row.size - 1
+    empty = np.diff(row.astype(np.int64)) == 0
+    for D, d, flow, hidden in ((100, 32, gatgpu.AGGREGATE_FIRST, True), (100, 64, gatgpu.TRANSFORM_FIRST, False)):
+        x = inputs.normal((n, D), 51)
+        p = inputs.glorot_param(D, 8, d, 52)
+        qp = dict(p, w=oracle.quantize_bf16(p["w"]))
+        got = run_layer(gpu_ctx, row, col, x, p, hidden, gatgpu.BF16, dataflow=flow)
+        if flow == gatgpu.AGGREGATE_FIRST:
+            r = oracle.ref_layer(row, col, oracle.quantize_bf16(x), qp, hidden)
+            ref, tol = oracle.quantize_bf16(r["out"]), 4e-3
+        else:
+            r = oracle.ref_layer(row, col, x, p, hidden)
+            ref, tol = r["out"], BF16_REL_L2
+        assert np.all(got["max"][empty] == 0) and np.all(got["den"][empty] == 0) and np.all(got["out"][empty] == 0)
+        if (~empty).any():
+            e = oracle.errors(ref[~empty], got["out"][~empty])
+            assert e["finite"] and e["relative_l2"] < tol, (name, flow, e)
+        L, R = got["left"], got["right"]
+        for i in np.nonzero(~empty)[0]:
+            s = L[i][None, :] + R[col[int(row[i]):int(row[i + 1])]]
+            s = np.maximum(s, np.float32(0.2) * s)
+            assert np.array_equal(s.max(axis=0), got["max"][i]), (flow, i)
+            d64 = np.exp(s.astype(np.float64) - got["max"][i].astype(np.float64)).sum(axis=0)
+            assert np.all(np.abs(got["den"][i] - d64) <= 1e-5 * d64), (flow, i)
+
+
 @pytest.mark.parametrize("heavy", [True, False])
 def test_transform_first_short_rows(gpu_ctx, heavy):
     """8 x 64 bf16 rows (R in its own array): rows of at most 4 edges go four
