@@ -292,6 +292,52 @@ def test_rerun_without_set_graph(gpu_ctx, flow, split):
     assert e["finite"] and e["relative_l2"] < BF16_REL_L2, e
 
 
+@pytest.mark.parametrize("flow", [gatgpu.AGGREGATE_FIRST, gatgpu.TRANSFORM_FIRST])
+def test_short_rows_rerun_without_set_graph(gpu_ctx, flow):
+    """The rows of at most 4 edges run in a launch of their own after the
+    others; the sum form's two launches take tiles from the same counters, each
+    leaving them at zero.  On 140 000 rows, half of them with 1..4 edges and
+    half with 5..40 (about 2 200 tiles each, beyond the statically assigned
+    ones), a bf16 100 -> 8 x 64 layer runs on x1, x2, x1 with no set_graph in
+    between: the second run equals x2 on a fresh graph bit for bit, the third
+    equals the first, and the second is within tolerance of R0."""
+    n = 140_000
+    rng = np.random.default_rng(61)
+    deg = np.where(rng.random(n) < 0.5, rng.integers(1, 5, n), rng.integers(5, 41, n))
+    row = np.zeros(n + 1, np.uint64)
+    row[1:] = np.cumsum(deg)
+    col = rng.integers(0, n, int(row[-1])).astype(np.uint32)
+    p = inputs.glorot_param(100, 8, 64, 62)
+    xs = [inputs.normal((n, 100), 63), inputs.normal((n, 100), 64)]
+
+    def fresh():
+        gpu_ctx.set_graph(row, col)
+        gpu_ctx.set_layer(0, p)
+
+    def run(x):
+        gpu_ctx.layer_forward(0, gatgpu.BF16, flow, True, input=x)
+        return gpu_ctx.stage(0, "out"), gpu_ctx.stage(0, "den"), gpu_ctx.stage(0, "max")
+
+    fresh()
+    runs = [run(xs[0]), run(xs[1]), run(xs[0])]
+    fresh()
+    ref2 = run(xs[1])
+    assert not np.array_equal(runs[0][0], runs[1][0])
+    for a, b in zip(runs[1], ref2):
+        assert np.array_equal(a, b)
+    for a, b in zip(runs[2], runs[0]):
+        assert np.array_equal(a, b)
+    if flow == gatgpu.AGGREGATE_FIRST:
+        qp = dict(p, w=oracle.quantize_bf16(p["w"]))
+        r = oracle.ref_layer(row, col, oracle.quantize_bf16(xs[1]), qp, True)
+        ref, tol = oracle.quantize_bf16(r["out"]), 4e-3
+    else:
+        r = oracle.ref_layer(row, col, xs[1], p, True)
+        ref, tol = r["out"], BF16_REL_L2
+    e = oracle.errors(ref, runs[1][0])
+    assert e["finite"] and e["relative_l2"] < tol, e
+
+
 def test_model_rerun_without_set_graph(gpu_ctx):
     """Chained bf16 forwards on the arxiv-sized graph (layer 1 aggregate-first,
     layer 2 transform-first with the output layer's projection in its
