@@ -10,7 +10,7 @@ row by row against a float64 evaluation of the exact-max softmax over the
 GPU's own stages on sampled rows (the heaviest included).
 
 The R-MAT graph (2^22 nodes, 100.6M edges, 128 -> 8x64 -> 8x64 -> 1x64) gets
-the same R0 logits check for its bf16 forward.
+the same R0 check of every layer for its bf16 and FP32 forwards.
 """
 import numpy as np
 import pytest
@@ -149,19 +149,34 @@ def test_large_layers_2_3_sampled_rows(gpu_ctx, large):
         check_tf_layer_rows(gpu_ctx, layer, hidden, large["m"][layer], row, col, rows)
 
 
-def test_skew_bf16_logits_vs_r0(gpu_ctx):
-    """R-MAT forward (layer 1 aggregate-first with heads of 64, layers 2-3
-    transform-first, 9 109 split rows) within relative L2 1e-2 of R0."""
+@pytest.fixture(scope="module")
+def skew():
     w = inputs.WORKLOADS["skew"]
-    g = dict(row=None, col=None)
-    g["row"], g["col"] = w.graph()
-    g["x"] = w.features()
-    g["m"] = w.model()
-    logits = forward(gpu_ctx, g, gatgpu.BF16)
-    h = g["x"]
-    for l, p in enumerate(g["m"]):
-        h = oracle.ref_layer(g["row"], g["col"], h, p, hidden=l < 2)["out"]
+    row, col = w.graph()
+    x = w.features()
+    m = w.model()
+    return dict(w=w, row=row, col=col, x=x, m=m, r0=r0_chain(row, col, x, m))
+
+
+def test_skew_bf16_logits_vs_r0(gpu_ctx, skew):
+    """R-MAT forward (layer 1 aggregate-first with heads of 64, layers 2-3
+    transform-first, 9 109 split rows, 3.0M rows of at most 4 edges) within
+    relative L2 1e-2 of R0."""
+    logits = forward(gpu_ctx, skew, gatgpu.BF16)
+    for l, h in enumerate(skew["r0"]):
         got = logits if l == 2 else gpu_ctx.stage(l, "out")
         e = oracle.errors(h, got)
         report("skew_bf16_gpu_vs_r0", l + 1, e)
         assert e["finite"] and e["relative_l2"] < BF16_REL_L2, (l, e)
+
+
+def test_skew_fp32_logits_vs_r0(gpu_ctx, skew):
+    """R-MAT FP32 forward (FP32 MFMA projections, 8 x 64 FP32 rows, the
+    one-head output layer; every layer transform-first) within max-abs 1e-4 of
+    R0 on every layer, as the 64.3M-edge graph's."""
+    logits = forward(gpu_ctx, skew, gatgpu.FP32)
+    for l, h in enumerate(skew["r0"]):
+        got = logits if l == 2 else gpu_ctx.stage(l, "out")
+        e = oracle.errors(h, got)
+        report("skew_fp32_gpu_vs_r0", l + 1, e)
+        assert e["finite"] and e["max_abs"] < FP32_MAX_ABS, (l, e)
