@@ -600,6 +600,7 @@ int run_tf(gatgpu_ctx* c, int l, int precision, bool hidden, const float* src32,
     pa.r_in_z = r_in_z;
     pa.r_off = zs - 2;
     pa.ar = Ls.ar.as<float>();
+    pa.al = Ls.al.as<float>();
     pa.r_from_z = bf16 && !fixed && r_from_z_supported(pa);
     // ---- convert (bf16 path, FP32 source only; a bf16 source was rounded in
     // the previous layer's epilogue, which equals convert() of that output).

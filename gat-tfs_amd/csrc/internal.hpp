@@ -201,6 +201,7 @@ struct ProjArgs {
     int xouts;           // rows, features [0, 16 ksteps), at xout[row * xouts]
     bool r_from_z;       // bf16 8 x 32 or one head x 64: R = Z_bf16 . aR (the aggregation recomputes it)
     const float* ar;     // aR [256] when r_from_z
+    const float* al;     // aL [heads * dim]: the W-stationary path forms L and R from FP32 Z
 };
 // R from the stored bf16 Z: the fast projection writes R = Z_bf16 . aR and
 // the 8-head aggregation recomputes it from each gathered row instead of

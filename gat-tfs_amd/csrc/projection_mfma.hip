@@ -21,7 +21,10 @@
 // are cut into groups of up to 8 blocks of 32; the last group also carries the
 // L/R block.  Where W does not fit LDS (several groups, or one group of many
 // k steps) the wide path keeps each tile's input in registers and streams W
-// through LDS instead.
+// through LDS instead; for 8 heads x 64 the W-stationary path keeps W in
+// registers and streams the tiles' input through LDS.
+#include <utility>
+
 #include "internal.hpp"
 
 namespace gatgpu {
@@ -685,6 +688,239 @@ hipError_t launch_wide_io(const ProjArgs& a, hipStream_t s) {
     return hipGetLastError();
 }
 
+// s_waitcnt vmcnt(N), N < 64 (the counter's high bits sit at [15:14]).
+template <int N>
+__device__ __forceinline__ void wait_vm_const() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x0F70);
+}
+
+// f(integral_constant<int, I>) for I = 0 .. N - 1, in order.
+template <class F, int... I>
+__device__ __forceinline__ void for_each_const(F&& f, std::integer_sequence<int, I...>) {
+    (f(std::integral_constant<int, I>{}), ...);
+}
+template <int N, class F>
+__device__ __forceinline__ void unroll_const(F&& f) {
+    for_each_const(f, std::make_integer_sequence<int, N>{});
+}
+
+// W-stationary wide path: 8 heads x 64 (16 head blocks), bf16 input, L and R
+// in their own arrays (e.g. 512 -> 8 x 64).  Each wave keeps one head block's
+// W^T fragments in registers for the whole launch (KS x 16 bytes per lane),
+// and the tiles' input comes to it through LDS: blocks come in pairs, block
+// p taking head blocks 0..7 and block pairs + p blocks 8..15 of the same
+// tiles (the two share an XCD, so one of them finds each tile in L2), and
+// every tile's input is requested kWsRing - 1 tiles ahead into an LDS ring
+// (global_load_lds, the block's 8 waves sharing the k steps).  k_proj_wide
+// instead streams W's fragments from L2 at every output block, and on a CU
+// with HBM reads in flight those L2 hits wait as long as the reads.  Z is
+// bit-equal to the other bf16 paths (each block's k steps in one chain, in
+// order).  L and R are the FP32 Z row of the head against a_L and a_R, as
+// lr_from_z forms them (baseline_standard.cpp:7-20), where the other paths
+// multiply X by the hi/lo parts of W a: the two agree to FP32 rounding, not
+// bit for bit.
+constexpr int kWsWaves = 8;
+constexpr int kWsRing = 4;  // tile inputs in LDS: the one multiplied and 3 requested ahead
+
+template <int KS>
+__global__ void __launch_bounds__(kWsWaves * kWave) __attribute__((amdgpu_waves_per_eu(2))) k_proj_ws(ProjArgs a,
+                                                                                                   uint32_t pairs) {
+    // The ring's slots are distinct arrays and the tile loop is unrolled by
+    // kWsRing, so the compiler can tell the requests into one slot from the
+    // reads of another and leaves them in flight.
+    __shared__ __attribute__((aligned(16))) u32x4 ring0[KS * kWave];
+    __shared__ __attribute__((aligned(16))) u32x4 ring1[KS * kWave];
+    __shared__ __attribute__((aligned(16))) u32x4 ring2[KS * kWave];
+    __shared__ __attribute__((aligned(16))) u32x4 ring3[KS * kWave];
+    // L and R shares per tile row of the block's 4 heads (two head blocks
+    // each), two tiles: [tile & 1][L, R][head][row][head block].
+    __shared__ float plr[2][2][4][32][2];
+    static_assert(kWsRing == 4 && KS % kWsWaves == 0, "four slots; the waves share the k steps evenly");
+    const int w = __builtin_amdgcn_readfirstlane(int(threadIdx.x) / kWave), l = threadIdx.x % kWave;
+    const int half = l / 32, col = l % 32;
+    const uint32_t g = blockIdx.x / pairs, p = blockIdx.x % pairs;
+    const int ob = int(8 * g) + w;  // head block: head ob / 2, its features 32 (ob % 2) .. + 31
+    const uint64_t nt = a.tiles > p ? (a.tiles - 1 - p) / pairs + 1 : 0;
+    if (nt == 0) return;  // (the launch gives every pair a tile)
+    // W^T fragments of head block ob (group g, block w of the packing).
+    bf16x8 wr[KS];
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks)
+        wr[ks] = __builtin_bit_cast(bf16x8, a.wpk[((size_t(g) * KS + ks) * a.nmb + w) * kWave + l]);
+    // a_L and a_R of the lane's 16 features (32 ob + 16 half + j).
+    float alv[16], arv[16];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+        alv[j] = a.al[32 * ob + 16 * half + j];
+        arv[j] = a.ar[32 * ob + 16 * half + j];
+    }
+    // Lanes past n recompute row n - 1 and store its own values to it.
+    auto row_of = [&](uint64_t i) -> uint64_t {
+        const uint64_t r = (p + i * pairs) * 32 + col;
+        return r < a.n ? r : a.n - 1;
+    };
+    // Tile i's input into dst: this wave's k steps w, w + 8, ...  Past the
+    // last tile the last one is requested again (into a slot no tile reads),
+    // so every tile issues the same vector-memory instructions: kDma requests
+    // and 3 stores (two Z pieces and one L or R value per row).
+    constexpr int kDma = KS / kWsWaves;
+    auto request = [&](uint64_t i, u32x4* dst) {
+        const unsigned char* src =
+            reinterpret_cast<const unsigned char*>(a.x + row_of(i < nt ? i : nt - 1) * a.xs + 8 * half);
+#pragma unroll
+        for (int q = 0; q < kDma; ++q) {
+            const int ks = w + kWsWaves * q;
+            __builtin_amdgcn_global_load_lds(src + 32 * ks, (lds_ptr)(dst + ks * kWave), 16, 0, 0);
+        }
+    };
+    // Wave w's value of the tile before: L (w < 4) or R of head 4 g + w % 4,
+    // the shares of its two head blocks added.
+    const int hw = w % 4;
+    auto lr_value = [&](uint64_t i) -> float {
+        const float2 v = *reinterpret_cast<const float2*>(&plr[i & 1][w < 4 ? 0 : 1][hw][l % 32][0]);
+        return v.x + v.y;
+    };
+    float* const lr_out = (w < 4 ? a.left : a.right) + 4 * g + hw;
+    request(0, ring0);
+    request(1, ring1);
+    request(2, ring2);
+    wait_vm_const<2 * kDma>();  // tile 0's input (tiles 1 and 2 requested after it)
+    __syncthreads();
+    uint64_t prs = 0;  // the previous tile's row
+    // Tile i from rd; tile i + 3 requested into rq.  At its end the wait for
+    // tile i + 1's input: AFTER instructions were issued after that request.
+    auto tile = [&](uint64_t i, const u32x4* rd, u32x4* rq, auto AFTER) {
+        const uint64_t rs = row_of(i);
+        request(i + 3, rq);  // into the slot tile i - 1 read
+        if (l < 32) {
+            // The tile before's L or R; tile 0 stores 0 to its own rows, which
+            // tile 1 overwrites (same wave, same address).
+            if (i > 0) lr_out[prs * 8] = lr_value(i - 1);
+            else lr_out[rs * 8] = 0.0f;
+        }
+        f32x16 acc;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[r] = 0.0f;
+        // The tile's B fragments, read by ds_read_b128 written out here: the
+        // compiler, which cannot tell the slots apart once several requests
+        // are in flight, would wait for all of them before a compiled LDS
+        // read.  The slot was filled and published before this tile (the
+        // previous tile's vmcnt wait and barrier); each read is waited for
+        // with lgkmcnt(kAhead - 1) -- LDS reads complete in order, so that
+        // holds whatever else the counter carries.
+        const uint32_t xaddr = uint32_t(reinterpret_cast<uintptr_t>(rd + l));
+        constexpr int kAhead = 4;
+        u32x4 fb[kAhead];
+        auto rd_frag = [&](auto KSC) {
+            constexpr int k = decltype(KSC)::value;
+            u32x4 v;
+            asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(v) : "v"(xaddr), "i"(k * kWave * 16));
+            fb[k % kAhead] = v;
+        };
+        unroll_const<kAhead>(rd_frag);
+        auto step = [&](auto KSC) {
+            constexpr int k = decltype(KSC)::value;
+            u32x4 v = fb[k % kAhead];
+            if constexpr (k + kAhead <= KS) {
+                asm volatile("s_waitcnt lgkmcnt(%1)" : "+v"(v) : "i"(kAhead - 1));
+            } else {
+                asm volatile("s_waitcnt lgkmcnt(%1)" : "+v"(v) : "i"(KS - 1 - k));
+            }
+            acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wr[k], __builtin_bit_cast(bf16x8, v), acc, 0, 0, 0);
+            if constexpr (k + kAhead < KS) rd_frag(std::integral_constant<int, k + kAhead>{});
+        };
+        unroll_const<KS>(step);
+        // Z: lane (half, col) holds features 32 ob + 16 half + {0..15} of row
+        // col, two 16-byte pieces.  Each store writes the head block's 64
+        // bytes of 16 rows: inside the lane quad (rows 4 a .. 4 a + 3), store
+        // j takes rows 4 a + 2 j and 4 a + 2 j + 1, lane c writing piece
+        // 2 half + c % 2 of row 4 a + 2 j + c / 2, read from quad lane
+        // 2 j + c / 2 by DPP.
+        {
+            uint32_t P[2][4];
+#pragma unroll
+            for (int q8 = 0; q8 < 2; ++q8)
+#pragma unroll
+                for (int x = 0; x < 4; ++x) P[q8][x] = bf16x2(acc[8 * q8 + 2 * x], acc[8 * q8 + 2 * x + 1]);
+            const int c = l & 3;
+            const uint64_t tbase = (p + i * pairs) * 32;
+            auto store_pair = [&](auto J) {
+                constexpr int j = decltype(J)::value;
+                constexpr int kSel = j ? 0xFA : 0x50;  // quad_perm [2j, 2j, 2j + 1, 2j + 1]
+                uint32_t T[4];
+#pragma unroll
+                for (int x = 0; x < 4; ++x) {
+                    const uint32_t a0 = uint32_t(__builtin_amdgcn_mov_dpp(int(P[0][x]), kSel, 0xF, 0xF, false));
+                    const uint32_t a1 = uint32_t(__builtin_amdgcn_mov_dpp(int(P[1][x]), kSel, 0xF, 0xF, false));
+                    T[x] = (c & 1) ? a1 : a0;
+                }
+                const uint64_t rj = tbase + uint64_t((col & ~3) + 2 * j + (c >> 1));
+                const uint64_t rsj = rj < a.n ? rj : a.n - 1;
+                *reinterpret_cast<uint4*>(a.z + rsj * a.zs + 32 * ob + 16 * half + 8 * (c & 1)) =
+                    make_uint4(T[0], T[1], T[2], T[3]);
+            };
+            store_pair(std::integral_constant<int, 0>{});
+            store_pair(std::integral_constant<int, 1>{});
+        }
+        // The head block's share of L and R from FP32 Z: an FMA chain over the
+        // lane's 16 features, the two lane halves added.
+        float pl = 0.0f, pr = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+            pl = __builtin_fmaf(acc[j], alv[j], pl);
+            pr = __builtin_fmaf(acc[j], arv[j], pr);
+        }
+        pl += __shfl_xor(pl, 32);
+        pr += __shfl_xor(pr, 32);
+        if (l < 32) {
+            plr[i & 1][0][w / 2][l][w % 2] = pl;
+            plr[i & 1][1][w / 2][l][w % 2] = pr;
+        }
+        wait_vm_const<decltype(AFTER)::value>();
+        __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
+        prs = rs;
+    };
+    // After tile 1's request: tile 2's, then tile 0's request and stores.
+    tile(0, ring0, ring3, std::integral_constant<int, 2 * kDma + 3>{});
+    if (nt > 1) {
+        // After tile 2's request: tiles 0 and 1's requests and stores.
+        tile(1, ring1, ring0, std::integral_constant<int, 2 * kDma + 6>{});
+        // After tile i + 1's request (made in tile i - 2): the stores of tiles
+        // i - 2 .. i and the requests of tiles i - 1 and i.
+        constexpr int kAfter = 2 * kDma + 9;
+        for (uint64_t i = 2; i < nt; i += kWsRing) {
+            tile(i, ring2, ring1, std::integral_constant<int, kAfter>{});
+            if (i + 1 < nt) {
+                tile(i + 1, ring3, ring2, std::integral_constant<int, kAfter>{});
+                if (i + 2 < nt) {
+                    tile(i + 2, ring0, ring3, std::integral_constant<int, kAfter>{});
+                    if (i + 3 < nt) tile(i + 3, ring1, ring0, std::integral_constant<int, kAfter>{});
+                }
+            }
+        }
+    }
+    if (l < 32) lr_out[prs * 8] = lr_value(nt - 1);
+}
+
+// The W-stationary path's shapes: bf16 input, 8 heads x 64 (two groups of 8
+// full head blocks), L and R in their own arrays, 16 to 32 k steps.
+bool ws_ok(const ProjArgs& a) {
+    return !a.x32 && !a.r_from_z && !a.r_in_z && a.al && a.ar && a.heads == 8 && a.width == 512 &&
+           a.head_blocks == 16 && a.groups == 2 && a.nmb == 9 && (a.ksteps == 16 || a.ksteps == 24 || a.ksteps == 32);
+}
+
+template <int KS>
+hipError_t launch_ws(const ProjArgs& a, hipStream_t s, int cus) {
+    uint64_t pairs = uint64_t(cus) / 2;
+    if (pairs > a.tiles) pairs = a.tiles;
+    if (pairs < 1) return hipErrorInvalidValue;
+    k_proj_ws<KS><<<dim3(uint32_t(2 * pairs)), kWsWaves * kWave, 0, s>>>(a, uint32_t(pairs));
+    return hipGetLastError();
+}
+
 // FP32 projection (the FP32 path's Z = X W and L/R = X B_LR) on
 // v_mfma_f32_32x32x2_f32: FP32 products, FP32 accumulation.  Same work split
 // as the wide path: a wave keeps the FP32 input of its 32-row tile in
@@ -908,7 +1144,15 @@ bool wide_supported_impl(const ProjArgs& a) {
     return wide_ks(a) && !fast_supported_impl(a) && (a.groups > 1 || group_lds > 160 * 1024);
 }
 
-hipError_t launch_wide(const ProjArgs& a, hipStream_t s) {
+hipError_t launch_wide(const ProjArgs& a, hipStream_t s, int cus) {
+    if (ws_ok(a) && cus >= 2) {
+        switch (a.ksteps) {
+            case 16: return launch_ws<16>(a, s, cus);
+            case 24: return launch_ws<24>(a, s, cus);
+            case 32: return launch_ws<32>(a, s, cus);
+            default: break;
+        }
+    }
     switch (a.ksteps) {
         case 8: return a.x32 ? launch_wide_io<8, true>(a, s) : launch_wide_io<8, false>(a, s);
         case 16: return a.x32 ? hipErrorInvalidValue : launch_wide_io<16, false>(a, s);
@@ -937,7 +1181,7 @@ bool projection_fp32_input(const ProjArgs& a) {
 
 hipError_t launch_projection_mfma(const ProjArgs& a, hipStream_t s, int cus) {
     if (a.x32 && !projection_fp32_input(a)) return hipErrorInvalidValue;
-    if (a.r_from_z && a.heads == 1) return rz_one_head(a) && a.ar ? launch_wide(a, s) : hipErrorInvalidValue;
+    if (a.r_from_z && a.heads == 1) return rz_one_head(a) && a.ar ? launch_wide(a, s, cus) : hipErrorInvalidValue;
     if (fast_supported_impl(a)) {
         switch (a.head_blocks) {
             case 0: return launch_fast_ks<0>(a, s, cus);
@@ -946,7 +1190,7 @@ hipError_t launch_projection_mfma(const ProjArgs& a, hipStream_t s, int cus) {
             default: return launch_fast_ks<8>(a, s, cus);
         }
     }
-    if (wide_supported_impl(a)) return launch_wide(a, s);
+    if (wide_supported_impl(a)) return launch_wide(a, s, cus);
     switch (a.nmb) {
         case 2: return launch_nmb<2>(a, s, cus);
         case 3: return launch_nmb<3>(a, s, cus);

@@ -789,6 +789,49 @@ def test_projection_partial_tiles(gpu_ctx, D):
     check_bf16_projection(gpu_ctx, ODD_ROWS, D, 8, 32)
 
 
+# Row counts for the W-stationary 8 x 64 projection: its blocks come in pairs
+# (half the CUs, 128 on MI355X) and each pair takes every pairs-th 32-row
+# tile, so 32 t - 7 rows give the pairs t // 128 or t // 128 + 1 tiles each:
+# 1 to 9 tiles per pair across these graphs, every tail of its 4-tile loop,
+# and a partial last tile.
+WS_TILES = [192, 320, 448, 576, 832, 1088]
+
+
+@pytest.mark.parametrize("tiles", WS_TILES)
+def test_ws_projection_tile_counts(gpu_ctx, tiles):
+    """The 512 -> 8 x 64 projection (W held in registers, the tiles' input in an
+    LDS ring) on graphs that give its block pairs 1 to 9 tiles: Z within one
+    bf16 ulp plus the FP32 accumulation-order bound of the float64 product of
+    the bf16-rounded operands, and L and R (dots of the FP32 Z row with a_L and
+    a_R, lr_from_z, baseline_standard.cpp:7-20) within the FP32 bounds of that
+    product's dots."""
+    n, D, K, d = 32 * tiles - 7, 512, 8, 64
+    row, col = inputs.uniform_graph(n, 2, 5)
+    x = inputs.normal((n, D), 17)
+    p = inputs.glorot_param(D, K, d, 18)
+    xq = oracle.quantize_bf16(x).astype(np.float64)
+    wq = oracle.quantize_bf16(p["w"]).astype(np.float64)
+    gpu_ctx.set_graph(row, col)
+    gpu_ctx.set_layer(0, p)
+    gpu_ctx.set_input(x)
+    gpu_ctx.layer_forward(0, gatgpu.BF16, gatgpu.TRANSFORM_FIRST, False)
+    z64 = xq @ wq
+    absdot = np.abs(xq) @ np.abs(wq)
+    zref = oracle.quantize_bf16(z64.astype(np.float32)).astype(np.float64)
+    z = gpu_ctx.stage(0, "z").astype(np.float64)
+    ulp = np.ldexp(1.0, np.frexp(np.abs(zref))[1] - 8)
+    assert np.all(np.abs(z - zref) <= ulp + 4 * D * 2.0 ** -24 * absdot)
+    for key, att in (("left", p["al"]), ("right", p["ar"])):
+        a64 = att.astype(np.float64).reshape(K, d)
+        want = (z64.reshape(n, K, d) * a64).sum(axis=2)
+        # FP32 Z (the Z check's accumulation-order bound) times a, then
+        # 64-term FP32 sums; a factor 2 of margin.
+        bound = ((4 * D + 2 * d) * 2.0 ** -24 * (absdot.reshape(n, K, d) * np.abs(a64)).sum(axis=2)) * 2 + 1e-30
+        got = gpu_ctx.stage(0, key).astype(np.float64).reshape(n, K)
+        bad = np.abs(got - want) > bound
+        assert not bad.any(), (key, int(bad.sum()), np.argwhere(bad)[0])
+
+
 @pytest.mark.parametrize("D", [100, 64])
 def test_aggregate_first_partial_tiles(gpu_ctx, D):
     """The aggregate-first front end writes the gather-table rows (rounded X and
