@@ -561,10 +561,28 @@ __global__ void __launch_bounds__(kWideBW * kWave) __attribute__((amdgpu_waves_p
         if (ob + 1 < nob) dma(ob + 1, wr);
         if constexpr (DEL) {
             if (ob > 0) {
+                // Each store writes block ob - 1's 64 bytes of 16 rows: in the
+                // lane quad (rows 4 a .. 4 a + 3), store j takes rows 4 a + 2 j
+                // and 4 a + 2 j + 1, lane c writing piece 2 half + c % 2 of row
+                // 4 a + 2 j + c / 2, read from quad lane 2 j + c / 2 by DPP.
+                const int c = l & 3;
+                const uint64_t tbase = (uint64_t(blockIdx.x) * kWideBW + w) * 32;
 #pragma unroll
-                for (int q8 = 0; q8 < 2; ++q8)
-                    *reinterpret_cast<uint4*>(a.z + rs * a.zs + 32 * (ob - 1) + 16 * half + 8 * q8) =
-                        make_uint4(pend[q8][0], pend[q8][1], pend[q8][2], pend[q8][3]);
+                for (int j = 0; j < 2; ++j) {
+                    uint32_t T[4];
+#pragma unroll
+                    for (int x = 0; x < 4; ++x) {
+                        const uint32_t a0 = uint32_t(j ? __builtin_amdgcn_mov_dpp(int(pend[0][x]), 0xFA, 0xF, 0xF, false)
+                                                       : __builtin_amdgcn_mov_dpp(int(pend[0][x]), 0x50, 0xF, 0xF, false));
+                        const uint32_t a1 = uint32_t(j ? __builtin_amdgcn_mov_dpp(int(pend[1][x]), 0xFA, 0xF, 0xF, false)
+                                                       : __builtin_amdgcn_mov_dpp(int(pend[1][x]), 0x50, 0xF, 0xF, false));
+                        T[x] = (c & 1) ? a1 : a0;
+                    }
+                    const uint64_t rj = tbase + uint64_t((col & ~3) + 2 * j + (c >> 1));
+                    const uint64_t rsj = rj < a.n ? rj : a.n - 1;
+                    *reinterpret_cast<uint4*>(a.z + rsj * a.zs + 32 * (ob - 1) + 16 * half + 8 * (c & 1)) =
+                        make_uint4(T[0], T[1], T[2], T[3]);
+                }
             }
         }
         f32x16 acc;
