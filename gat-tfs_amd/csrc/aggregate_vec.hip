@@ -152,11 +152,12 @@ __device__ inline void batch_sums(const uint4 (&z)[C::U][C::VPL], const float (&
     }
 }
 
-// One batch of edges [base, base + BATCH) clipped to end.  RZ (bf16 8 x 32):
-// R of the source is recomputed from the gathered row, R = Z_bf16 . aR, as an
-// FMA chain over the lane's 8 features and (s0 + s1) + (s2 + s3) over the 4
-// lanes of the head -- the summation the projection used to store R -- so no
-// R line is fetched.
+// One batch of edges [base, base + BATCH) clipped to end.  RZ (bf16 8 x 32
+// or 8 x 64): R of the source is recomputed from the gathered row, R =
+// Z_bf16 . aR, as an FMA chain over the lane's 8 features, (s0 + s1) + (s2 +
+// s3) over the 4 lanes of a head of 32, and for a head of 64 the two quads'
+// sums added -- the summation the projection used to store R -- so no R line
+// is fetched.
 // Source ids of edges [base, base + BATCH): wave-uniform scalar loads, which
 // may run up to 2 BATCH - 1 entries past the last edge (pcol is padded).
 template <class C>
@@ -228,7 +229,7 @@ __device__ inline void batch(uint32_t left, const uint32_t (&js)[C::BATCH], cons
         // (the unpacked row is used twice, so it is not kept for a batch):
         // online per edge, the accumulators rescaled only when some lane of
         // the wave raised its max.
-        static_assert(C::VEC == 8 && C::DIM == 32 && C::VPL == 1, "R from Z: bf16 8 x 32 rows");
+        static_assert(C::VEC == 8 && (C::DIM == 32 || C::DIM == 64) && C::VPL == 1, "R from Z: bf16 8 x 32 or 8 x 64 rows");
 #pragma unroll
         for (int u = 0; u < C::U; ++u) {
             float f[C::VEC];
@@ -238,6 +239,12 @@ __device__ inline void batch(uint32_t left, const uint32_t (&js)[C::BATCH], cons
             for (int x = 0; x < C::VEC; ++x) t = __builtin_fmaf(f[x], st.ar[x], t);
             t += quad_xor1(t);
             t += quad_xor2(t);
+            if constexpr (C::DIM == 64) {
+                // the other quad of the head's 8 lanes (DPP row_half_mirror:
+                // lane i of each 8 takes lane 7 - i)
+                t += __builtin_bit_cast(float,
+                                        __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, t), 0x141, 0xF, 0xF, false));
+            }
             const float sc_ = leaky(st.L[0] + t);
             float mn, scale, p;
             if constexpr (FREE) {
@@ -832,9 +839,12 @@ hipError_t run(const AggArgs& g, const RowBins& bins, const SplitTable& t, hipSt
     VArgs<ZT> a{g.prow, g.pcol, g.perm, g.left, g.right, static_cast<const ZT*>(g.feat), g.hidden, g.mx, g.den,
                 g.out32, g.outbf, g.n, g.e, bins.split_begin,
                 SplitArgs{t.chunks, t.chunk_k, t.chunk_first, t.chunk_edges, t.mchunk, t.part, t.counter}, g.ar};
+    // (With R from Z the rows of 8 x 64 layers still take the short launch,
+    // which gathers R: the projection stored R = Z_bf16 . aR in the summation
+    // order the main kernel recomputes it in, so both see the same scores.)
     uint64_t short_rows = 0;
     if constexpr (sizeof(ZT) == 2) {
-        if (!g.r_from_z) short_rows = std::min(bins.short_end, bins.split_begin);
+        if (!g.r_from_z || C::W == 512) short_rows = std::min(bins.short_end, bins.split_begin);
     }
     const uint64_t items = t.chunks + bins.split_begin - short_rows;
     if constexpr (sizeof(ZT) == 2) {
@@ -854,6 +864,13 @@ hipError_t run(const AggArgs& g, const RowBins& bins, const SplitTable& t, hipSt
             using CR = Cfg<ZT, C::W, C::K, kURz>;
             if (offsets32<CR, ZT>(g.n)) k_agg_vec<CR, ZT, true, true><<<grid, kThreads, 0, s>>>(a, 0);
             else k_agg_vec<CR, ZT, true, false><<<grid, kThreads, 0, s>>>(a, 0);
+            return hipGetLastError();
+        }
+    }
+    if constexpr (sizeof(ZT) == 2 && C::W == 512) {
+        if (g.r_from_z) {  // one edge slot: whole 1 KB rows, R from each
+            if (!g.ar) return hipErrorInvalidValue;
+            k_agg_vec<C, ZT, true, false><<<grid, kThreads, 0, s>>>(a, short_rows);
             return hipGetLastError();
         }
     }

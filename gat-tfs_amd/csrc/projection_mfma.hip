@@ -741,7 +741,7 @@ __device__ __forceinline__ void unroll_const(F&& f) {
 constexpr int kWsWaves = 8;
 constexpr int kWsRing = 4;  // tile inputs in LDS: the one multiplied and 3 requested ahead
 
-template <int KS>
+template <int KS, bool RZ>
 __global__ void __launch_bounds__(kWsWaves * kWave) __attribute__((amdgpu_waves_per_eu(2))) k_proj_ws(ProjArgs a,
                                                                                                    uint32_t pairs) {
     // The ring's slots are distinct arrays and the tile loop is unrolled by
@@ -759,7 +759,9 @@ __global__ void __launch_bounds__(kWsWaves * kWave) __attribute__((amdgpu_waves_
     const int half = l / 32, col = l % 32;
     const uint32_t g = blockIdx.x / pairs, p = blockIdx.x % pairs;
     const int ob = int(8 * g) + w;  // head block: head ob / 2, its features 32 (ob % 2) .. + 31
-    const uint64_t nt = a.tiles > p ? (a.tiles - 1 - p) / pairs + 1 : 0;
+    // Row indices in 32 bits (the path takes fewer than 2^31 rows).
+    const uint32_t nt = a.tiles > p ? uint32_t((a.tiles - 1 - p) / pairs + 1) : 0;
+    const uint32_t n = uint32_t(a.n);
     if (nt == 0) return;  // (the launch gives every pair a tile)
     // W^T fragments of head block ob (group g, block w of the packing).
     bf16x8 wr[KS];
@@ -774,18 +776,18 @@ __global__ void __launch_bounds__(kWsWaves * kWave) __attribute__((amdgpu_waves_
         arv[j] = a.ar[32 * ob + 16 * half + j];
     }
     // Lanes past n recompute row n - 1 and store its own values to it.
-    auto row_of = [&](uint64_t i) -> uint64_t {
-        const uint64_t r = (p + i * pairs) * 32 + col;
-        return r < a.n ? r : a.n - 1;
+    auto row_of = [&](uint32_t i) -> uint32_t {
+        const uint32_t r = (p + i * pairs) * 32 + col;
+        return r < n ? r : n - 1;
     };
     // Tile i's input into dst: this wave's k steps w, w + 8, ...  Past the
     // last tile the last one is requested again (into a slot no tile reads),
     // so every tile issues the same vector-memory instructions: kDma requests
     // and 3 stores (two Z pieces and one L or R value per row).
     constexpr int kDma = KS / kWsWaves;
-    auto request = [&](uint64_t i, u32x4* dst) {
+    auto request = [&](uint32_t i, u32x4* dst) {
         const unsigned char* src =
-            reinterpret_cast<const unsigned char*>(a.x + row_of(i < nt ? i : nt - 1) * a.xs + 8 * half);
+            reinterpret_cast<const unsigned char*>(a.x + size_t(row_of(i < nt ? i : nt - 1)) * a.xs + 8 * half);
 #pragma unroll
         for (int q = 0; q < kDma; ++q) {
             const int ks = w + kWsWaves * q;
@@ -795,7 +797,7 @@ __global__ void __launch_bounds__(kWsWaves * kWave) __attribute__((amdgpu_waves_
     // Wave w's value of the tile before: L (w < 4) or R of head 4 g + w % 4,
     // the shares of its two head blocks added.
     const int hw = w % 4;
-    auto lr_value = [&](uint64_t i) -> float {
+    auto lr_value = [&](uint32_t i) -> float {
         const float2 v = *reinterpret_cast<const float2*>(&plr[i & 1][w < 4 ? 0 : 1][hw][l % 32][0]);
         return v.x + v.y;
     };
@@ -805,17 +807,17 @@ __global__ void __launch_bounds__(kWsWaves * kWave) __attribute__((amdgpu_waves_
     request(2, ring2);
     wait_vm_const<2 * kDma>();  // tile 0's input (tiles 1 and 2 requested after it)
     __syncthreads();
-    uint64_t prs = 0;  // the previous tile's row
+    uint32_t prs = 0;  // the previous tile's row
     // Tile i from rd; tile i + 3 requested into rq.  At its end the wait for
     // tile i + 1's input: AFTER instructions were issued after that request.
-    auto tile = [&](uint64_t i, const u32x4* rd, u32x4* rq, auto AFTER) {
-        const uint64_t rs = row_of(i);
+    auto tile = [&](uint32_t i, const u32x4* rd, u32x4* rq, auto AFTER) {
+        const uint32_t rs = row_of(i);
         request(i + 3, rq);  // into the slot tile i - 1 read
         if (l < 32) {
             // The tile before's L or R; tile 0 stores 0 to its own rows, which
             // tile 1 overwrites (same wave, same address).
-            if (i > 0) lr_out[prs * 8] = lr_value(i - 1);
-            else lr_out[rs * 8] = 0.0f;
+            if (i > 0) lr_out[size_t(prs) * 8] = lr_value(i - 1);
+            else lr_out[size_t(rs) * 8] = 0.0f;
         }
         f32x16 acc;
 #pragma unroll
@@ -855,14 +857,42 @@ __global__ void __launch_bounds__(kWsWaves * kWave) __attribute__((amdgpu_waves_
         // j takes rows 4 a + 2 j and 4 a + 2 j + 1, lane c writing piece
         // 2 half + c % 2 of row 4 a + 2 j + c / 2, read from quad lane
         // 2 j + c / 2 by DPP.
+        uint32_t P[2][4];
+#pragma unroll
+        for (int q8 = 0; q8 < 2; ++q8)
+#pragma unroll
+            for (int x = 0; x < 4; ++x) P[q8][x] = bf16x2(acc[8 * q8 + 2 * x], acc[8 * q8 + 2 * x + 1]);
+        // The head block's share of L (and of R unless RZ) from FP32 Z: an
+        // FMA chain over the lane's 16 features, the two lane halves added.
+        // RZ: R = Z_bf16 . aR in the order the 8-head aggregation recomputes
+        // it from a gathered row -- an FMA chain over each 8 stored features
+        // (chunks c, c + 1 of the head), their sum, the lane halves' sums
+        // added, then (below) the head's two blocks -- so both give R the same
+        // bits.
+        float pl = 0.0f, pr = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 16; ++j) pl = __builtin_fmaf(acc[j], alv[j], pl);
+        if constexpr (RZ) {
+            float t8[2];
+#pragma unroll
+            for (int q8 = 0; q8 < 2; ++q8) {
+                float t = 0.0f;
+#pragma unroll
+                for (int x = 0; x < 8; ++x) {
+                    const uint32_t pr2 = P[q8][x / 2];
+                    const float zv = __builtin_bit_cast(float, (x & 1) ? (pr2 & 0xffff0000u) : (pr2 << 16));
+                    t = __builtin_fmaf(zv, arv[8 * q8 + x], t);
+                }
+                t8[q8] = t;
+            }
+            pr = t8[0] + t8[1];
+        } else {
+#pragma unroll
+            for (int j = 0; j < 16; ++j) pr = __builtin_fmaf(acc[j], arv[j], pr);
+        }
         {
-            uint32_t P[2][4];
-#pragma unroll
-            for (int q8 = 0; q8 < 2; ++q8)
-#pragma unroll
-                for (int x = 0; x < 4; ++x) P[q8][x] = bf16x2(acc[8 * q8 + 2 * x], acc[8 * q8 + 2 * x + 1]);
             const int c = l & 3;
-            const uint64_t tbase = (p + i * pairs) * 32;
+            const uint32_t tbase = (p + i * pairs) * 32;
             auto store_pair = [&](auto J) {
                 constexpr int j = decltype(J)::value;
                 constexpr int kSel = j ? 0xFA : 0x50;  // quad_perm [2j, 2j, 2j + 1, 2j + 1]
@@ -873,21 +903,13 @@ __global__ void __launch_bounds__(kWsWaves * kWave) __attribute__((amdgpu_waves_
                     const uint32_t a1 = uint32_t(__builtin_amdgcn_mov_dpp(int(P[1][x]), kSel, 0xF, 0xF, false));
                     T[x] = (c & 1) ? a1 : a0;
                 }
-                const uint64_t rj = tbase + uint64_t((col & ~3) + 2 * j + (c >> 1));
-                const uint64_t rsj = rj < a.n ? rj : a.n - 1;
-                *reinterpret_cast<uint4*>(a.z + rsj * a.zs + 32 * ob + 16 * half + 8 * (c & 1)) =
+                const uint32_t rj = tbase + uint32_t((col & ~3) + 2 * j + (c >> 1));
+                const uint32_t rsj = rj < n ? rj : n - 1;
+                *reinterpret_cast<uint4*>(a.z + size_t(rsj) * a.zs + 32 * ob + 16 * half + 8 * (c & 1)) =
                     make_uint4(T[0], T[1], T[2], T[3]);
             };
             store_pair(std::integral_constant<int, 0>{});
             store_pair(std::integral_constant<int, 1>{});
-        }
-        // The head block's share of L and R from FP32 Z: an FMA chain over the
-        // lane's 16 features, the two lane halves added.
-        float pl = 0.0f, pr = 0.0f;
-#pragma unroll
-        for (int j = 0; j < 16; ++j) {
-            pl = __builtin_fmaf(acc[j], alv[j], pl);
-            pr = __builtin_fmaf(acc[j], arv[j], pr);
         }
         pl += __shfl_xor(pl, 32);
         pr += __shfl_xor(pr, 32);
@@ -909,7 +931,7 @@ __global__ void __launch_bounds__(kWsWaves * kWave) __attribute__((amdgpu_waves_
         // After tile i + 1's request (made in tile i - 2): the stores of tiles
         // i - 2 .. i and the requests of tiles i - 1 and i.
         constexpr int kAfter = 2 * kDma + 9;
-        for (uint64_t i = 2; i < nt; i += kWsRing) {
+        for (uint32_t i = 2; i < nt; i += kWsRing) {
             tile(i, ring2, ring1, std::integral_constant<int, kAfter>{});
             if (i + 1 < nt) {
                 tile(i + 1, ring3, ring2, std::integral_constant<int, kAfter>{});
@@ -920,14 +942,15 @@ __global__ void __launch_bounds__(kWsWaves * kWave) __attribute__((amdgpu_waves_
             }
         }
     }
-    if (l < 32) lr_out[prs * 8] = lr_value(nt - 1);
+    if (l < 32) lr_out[size_t(prs) * 8] = lr_value(nt - 1);
 }
 
 // The W-stationary path's shapes: bf16 input, 8 heads x 64 (two groups of 8
-// full head blocks), L and R in their own arrays, 16 to 32 k steps.
+// full head blocks), L and R in their own arrays, 16 to 32 k steps; with or
+// without R from the stored Z.
 bool ws_ok(const ProjArgs& a) {
-    return !a.x32 && !a.r_from_z && !a.r_in_z && a.al && a.ar && a.heads == 8 && a.width == 512 &&
-           a.head_blocks == 16 && a.groups == 2 && a.nmb == 9 && (a.ksteps == 16 || a.ksteps == 24 || a.ksteps == 32);
+    return !a.x32 && !a.r_in_z && a.al && a.ar && a.heads == 8 && a.width == 512 && a.head_blocks == 16 &&
+           a.groups == 2 && a.nmb == 9 && (a.ksteps == 16 || a.ksteps == 24 || a.ksteps == 32) && a.n < (1ull << 31);
 }
 
 template <int KS>
@@ -935,7 +958,8 @@ hipError_t launch_ws(const ProjArgs& a, hipStream_t s, int cus) {
     uint64_t pairs = uint64_t(cus) / 2;
     if (pairs > a.tiles) pairs = a.tiles;
     if (pairs < 1) return hipErrorInvalidValue;
-    k_proj_ws<KS><<<dim3(uint32_t(2 * pairs)), kWsWaves * kWave, 0, s>>>(a, uint32_t(pairs));
+    if (a.r_from_z) k_proj_ws<KS, true><<<dim3(uint32_t(2 * pairs)), kWsWaves * kWave, 0, s>>>(a, uint32_t(pairs));
+    else k_proj_ws<KS, false><<<dim3(uint32_t(2 * pairs)), kWsWaves * kWave, 0, s>>>(a, uint32_t(pairs));
     return hipGetLastError();
 }
 
@@ -1157,7 +1181,7 @@ bool wide_ks(const ProjArgs& a) {
 bool rz_one_head(const ProjArgs& a) { return wide_ks(a) && a.heads == 1 && a.width == 64 && !a.r_in_z; }
 
 bool wide_supported_impl(const ProjArgs& a) {
-    if (a.r_from_z) return rz_one_head(a);
+    if (a.r_from_z) return rz_one_head(a) || ws_ok(a);
     const size_t group_lds = size_t(a.ksteps) * a.nmb * kWave * sizeof(uint4);
     return wide_ks(a) && !fast_supported_impl(a) && (a.groups > 1 || group_lds > 160 * 1024);
 }
@@ -1171,6 +1195,7 @@ hipError_t launch_wide(const ProjArgs& a, hipStream_t s, int cus) {
             default: break;
         }
     }
+    if (a.r_from_z && !rz_one_head(a)) return hipErrorInvalidValue;  // (8 x 64: the W-stationary path only)
     switch (a.ksteps) {
         case 8: return a.x32 ? launch_wide_io<8, true>(a, s) : launch_wide_io<8, false>(a, s);
         case 16: return a.x32 ? hipErrorInvalidValue : launch_wide_io<16, false>(a, s);
@@ -1184,7 +1209,7 @@ bool projection_fast_path(const ProjArgs& a) { return fast_supported_impl(a); }
 
 bool r_from_z_supported(const ProjArgs& a) {
     return (fast_supported_impl(a) && a.head_blocks == 8 && a.width == 256 && a.heads == 8 && !a.r_in_z) ||
-           rz_one_head(a);
+           rz_one_head(a) || ws_ok(a);
 }
 
 // The FP32-input form holds 32 bytes per k step; at 16 k steps and 8 head
