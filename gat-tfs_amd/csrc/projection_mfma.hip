@@ -807,7 +807,30 @@ __global__ void __launch_bounds__(kWsWaves * kWave) __attribute__((amdgpu_waves_
     request(2, ring2);
     wait_vm_const<2 * kDma>();  // tile 0's input (tiles 1 and 2 requested after it)
     __syncthreads();
-    uint32_t prs = 0;  // the previous tile's row
+    uint32_t prs = 0, prs2 = 0;  // the rows of the previous two tiles
+    // RZ: the head block's share of R from the bf16 Z in the order the
+    // 8-head aggregation recomputes it from a gathered row -- an FMA chain
+    // over each 8 stored features (chunks c, c + 1 of the head), their sum,
+    // the lane halves' sums added, then (in lr_value) the head's two blocks --
+    // so both give R the same bits.  A tile's share is formed during the next
+    // tile's MFMA chain, from its packed Z (zp), and published by that tile's
+    // barrier; the R waves store R two tiles late.
+    uint32_t zp[2][4] = {};
+    auto r_share = [&]() -> float {
+        float u[2];
+#pragma unroll
+        for (int q8 = 0; q8 < 2; ++q8) {
+            float v = 0.0f;
+#pragma unroll
+            for (int x = 0; x < 8; ++x) {
+                const uint32_t pr2 = zp[q8][x / 2];
+                const float zv = __builtin_bit_cast(float, (x & 1) ? (pr2 & 0xffff0000u) : (pr2 << 16));
+                v = __builtin_fmaf(zv, arv[8 * q8 + x], v);
+            }
+            u[q8] = v;
+        }
+        return u[0] + u[1];  // (the lane halves are added by the caller)
+    };
     // Tile i from rd; tile i + 3 requested into rq.  At its end the wait for
     // tile i + 1's input: AFTER instructions were issued after that request.
     auto tile = [&](uint32_t i, const u32x4* rd, u32x4* rq, auto AFTER) {
@@ -816,9 +839,16 @@ __global__ void __launch_bounds__(kWsWaves * kWave) __attribute__((amdgpu_waves_
         if (l < 32) {
             // The tile before's L or R; tile 0 stores 0 to its own rows, which
             // tile 1 overwrites (same wave, same address).
-            if (i > 0) lr_out[size_t(prs) * 8] = lr_value(i - 1);
-            else lr_out[size_t(rs) * 8] = 0.0f;
+            // (RZ: the R waves store tile i - 2's R; tile 1 also stores 0.)
+            if (!RZ || w < 4) {
+                if (i > 0) lr_out[size_t(prs) * 8] = lr_value(i - 1);
+                else lr_out[size_t(rs) * 8] = 0.0f;
+            } else {
+                if (i > 1) lr_out[size_t(prs2) * 8] = lr_value(i - 2);
+                else lr_out[size_t(rs) * 8] = 0.0f;
+            }
         }
+        float prv = 0.0f;  // RZ: the tile before's R share, formed among this tile's MFMAs
         f32x16 acc;
 #pragma unroll
         for (int r = 0; r < 16; ++r) acc[r] = 0.0f;
@@ -849,6 +879,7 @@ __global__ void __launch_bounds__(kWsWaves * kWave) __attribute__((amdgpu_waves_
             }
             acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wr[k], __builtin_bit_cast(bf16x8, v), acc, 0, 0, 0);
             if constexpr (k + kAhead < KS) rd_frag(std::integral_constant<int, k + kAhead>{});
+            if constexpr (RZ && k == 1) prv = r_share();
         };
         unroll_const<KS>(step);
         // Z: lane (half, col) holds features 32 ob + 16 half + {0..15} of row
@@ -864,28 +895,14 @@ __global__ void __launch_bounds__(kWsWaves * kWave) __attribute__((amdgpu_waves_
             for (int x = 0; x < 4; ++x) P[q8][x] = bf16x2(acc[8 * q8 + 2 * x], acc[8 * q8 + 2 * x + 1]);
         // The head block's share of L (and of R unless RZ) from FP32 Z: an
         // FMA chain over the lane's 16 features, the two lane halves added.
-        // RZ: R = Z_bf16 . aR in the order the 8-head aggregation recomputes
-        // it from a gathered row -- an FMA chain over each 8 stored features
-        // (chunks c, c + 1 of the head), their sum, the lane halves' sums
-        // added, then (below) the head's two blocks -- so both give R the same
-        // bits.
         float pl = 0.0f, pr = 0.0f;
 #pragma unroll
         for (int j = 0; j < 16; ++j) pl = __builtin_fmaf(acc[j], alv[j], pl);
         if constexpr (RZ) {
-            float t8[2];
 #pragma unroll
-            for (int q8 = 0; q8 < 2; ++q8) {
-                float t = 0.0f;
+            for (int q8 = 0; q8 < 2; ++q8)
 #pragma unroll
-                for (int x = 0; x < 8; ++x) {
-                    const uint32_t pr2 = P[q8][x / 2];
-                    const float zv = __builtin_bit_cast(float, (x & 1) ? (pr2 & 0xffff0000u) : (pr2 << 16));
-                    t = __builtin_fmaf(zv, arv[8 * q8 + x], t);
-                }
-                t8[q8] = t;
-            }
-            pr = t8[0] + t8[1];
+                for (int x = 0; x < 4; ++x) zp[q8][x] = P[q8][x];
         } else {
 #pragma unroll
             for (int j = 0; j < 16; ++j) pr = __builtin_fmaf(acc[j], arv[j], pr);
@@ -912,15 +929,20 @@ __global__ void __launch_bounds__(kWsWaves * kWave) __attribute__((amdgpu_waves_
             store_pair(std::integral_constant<int, 1>{});
         }
         pl += __shfl_xor(pl, 32);
-        pr += __shfl_xor(pr, 32);
+        if constexpr (RZ) prv += __shfl_xor(prv, 32);
         if (l < 32) {
             plr[i & 1][0][w / 2][l][w % 2] = pl;
-            plr[i & 1][1][w / 2][l][w % 2] = pr;
+            if (RZ && i > 0) plr[(i - 1) & 1][1][w / 2][l][w % 2] = prv;
+        }
+        if constexpr (!RZ) {
+            pr += __shfl_xor(pr, 32);
+            if (l < 32) plr[i & 1][1][w / 2][l][w % 2] = pr;
         }
         wait_vm_const<decltype(AFTER)::value>();
         __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
         __builtin_amdgcn_s_barrier();
         asm volatile("" ::: "memory");
+        prs2 = prs;
         prs = rs;
     };
     // After tile 1's request: tile 2's, then tile 0's request and stores.
@@ -941,6 +963,14 @@ __global__ void __launch_bounds__(kWsWaves * kWave) __attribute__((amdgpu_waves_
                 }
             }
         }
+    }
+    if constexpr (RZ) {
+        // R of tile nt - 2 (formed during tile nt - 1), then the last tile's.
+        if (l < 32 && w >= 4 && nt > 1) lr_out[size_t(prs2) * 8] = lr_value(nt - 2);
+        float pr = r_share();
+        pr += __shfl_xor(pr, 32);
+        if (l < 32) plr[(nt - 1) & 1][1][w / 2][l][w % 2] = pr;
+        __syncthreads();
     }
     if (l < 32) lr_out[size_t(prs) * 8] = lr_value(nt - 1);
 }
