@@ -206,11 +206,17 @@ ADVERSARIAL_PATHS = [("fp32_tf", gatgpu.FP32, gatgpu.TRANSFORM_FIRST), ("bf16_tf
                      ("bf16_af", gatgpu.BF16, gatgpu.AGGREGATE_FIRST)]
 
 
-@pytest.mark.parametrize("K,d", [(8, 32), (8, 64)])
-@pytest.mark.parametrize("path", [p[0] for p in ADVERSARIAL_PATHS])
-def test_adversarial_scores_split_rows(gpu_ctx, K, d, path):
+# (K, d, D_in, path): D_in 256 takes the 8 x 64 bf16 layer onto the
+# W-stationary projection, whose aggregation recomputes R from gathered Z rows.
+SPLIT_ADVERSARIAL_CASES = ([(K, d, 2, p[0]) for K, d in ((8, 32), (8, 64)) for p in ADVERSARIAL_PATHS] +
+                           [(8, 64, 256, "bf16_tf")])
+
+
+@pytest.mark.parametrize("K,d,din,path", SPLIT_ADVERSARIAL_CASES)
+def test_adversarial_scores_split_rows(gpu_ctx, K, d, din, path):
     """boundaries.cpp:44-52 on the 8-head kernels: the transform-first 8 x 32 /
-    8 x 64 aggregation (FP32 and bf16) and the aggregate-first sum form,
+    8 x 64 aggregation (FP32 and bf16; 8 x 64 bf16 also with 256 inputs, R
+    recomputed from each gathered Z row) and the aggregate-first sum form,
     under every schedule; with rows >= 16 split into 64-edge chunks, the
     multi-chunk rows take each chunk's own maximum and the last chunk to
     arrive rescales the partials, and the peak sits in a row's last chunk,
@@ -226,6 +232,12 @@ def test_adversarial_scores_split_rows(gpu_ctx, K, d, path):
     dst = np.repeat(np.arange(n), deg)
     for scenario in range(5):
         x, p = adversarial_layer_bf16_exact(n, scenario, K, d)
+        if din > x.shape[1]:
+            # Zero inputs and weight rows: the same exact Z.
+            x = np.concatenate((x, np.zeros((n, din - x.shape[1]), np.float32)), axis=1)
+            w = np.zeros((din, K * d), np.float32)
+            w[:p["in"]] = p["w"]
+            p = dict(p, **{"in": din, "w": w})
         r = oracle.ref_layer(row, col, x, p, False)
         scale = max(1.0, float(np.abs(r["out"]).max()))
         for opts in SCHEDULES:
